@@ -1,0 +1,151 @@
+/*
+ * sparsecore_amd.h — C-ABI of the MI355X (gfx950) padded-CSR training path.
+ *
+ * This is the drop-in boundary that replaces the reference's pybind11 module
+ * `sparselab._core` (csrc/bindings.cpp:494-745) for the hot path: forward
+ * SpMM, the live-slot weight gradient (SDDMM), the CSR transpose build used
+ * for dX = W^T·dY, the transpose-cache value refresh, and the PaddedCSR
+ * invariant checker.
+ *
+ * Conventions
+ *   - Every pointer is a DEVICE pointer (HBM) unless the name ends in _host.
+ *   - No entry point allocates memory: callers pass outputs and workspaces
+ *     (the Python host layer allocates them through torch's caching
+ *     allocator).
+ *   - Every call is stream-ordered on `stream` (a hipStream_t passed as
+ *     void*; NULL means the legacy default stream) and returns without
+ *     synchronizing.
+ *   - Return value: SLK_OK (0) on success; on failure a non-zero code and a
+ *     thread-local message available from slk_last_error(). Messages keep
+ *     the substrings the reference raises as ValueError ("shape mismatch",
+ *     "ncols", "dY.shape", "X.shape", "shared inner dim N", ...).
+ *   - Shapes follow the reference: W is M x K (nrows x ncols), X is K x N
+ *     row-major, Y is M x N row-major, dY is M x N, dW has total_capacity
+ *     entries aligned with W.values.
+ */
+#ifndef SPARSECORE_AMD_H
+#define SPARSECORE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SLK_ABI_VERSION 1
+
+#if defined(__GNUC__)
+#define SLK_API __attribute__((visibility("default")))
+#else
+#define SLK_API
+#endif
+
+enum slk_status {
+    SLK_OK = 0,
+    SLK_EINVAL = 1,   /* bad shape / argument: the reference raises ValueError  */
+    SLK_EDEVICE = 2,  /* HIP runtime error (launch failure, bad device pointer) */
+};
+
+/* Order of the per-slot dot products in slk_sddmm.
+ *   SLK_DW_SIMD   — the reference AVX2 kernel's order: two 8-wide
+ *                   accumulators over 16-float steps, an 8-wide step, a
+ *                   3-level horizontal add, then a scalar tail
+ *                   (csrc/kernels/spmm_grad_avx2.cpp:112-258).
+ *   SLK_DW_SCALAR — the reference scalar kernel's single sequential chain
+ *                   (csrc/kernels/spmm_grad.cpp:89-108).                     */
+enum slk_dw_order { SLK_DW_SIMD = 0, SLK_DW_SCALAR = 1 };
+
+/* Device view of a PaddedCSR (reference struct: csrc/kernels/padded_csr.hpp:47-74).
+ * values/col_indices have total_capacity entries; the three row arrays have
+ * nrows entries. Within row i, slots [row_start[i], row_start[i]+row_nnz[i])
+ * are live with strictly ascending columns; the rest of the row's capacity is
+ * padding (col = -1).                                                        */
+typedef struct slk_csr {
+    int64_t nrows;
+    int64_t ncols;
+    int64_t total_capacity;
+    const float*   values;
+    const int32_t* col_indices;
+    const int32_t* row_start;
+    const int32_t* row_nnz;
+    const int32_t* row_capacity;
+} slk_csr;
+
+/* Thread-local description of the last failure of this thread ("" if none). */
+SLK_API const char* slk_last_error(void);
+
+/* SLK_ABI_VERSION of the loaded library. */
+SLK_API int slk_abi_version(void);
+
+/* Y = W·X. Replaces `spmm_simd` / `spmm_scalar` (csrc/bindings.cpp:243-272,
+ * kernels csrc/kernels/spmm_avx2.cpp:82-263 and spmm.cpp:20-105). Y is fully
+ * written (rows without live slots become 0), so it needs no pre-zeroing.
+ * Each Y element is the fused multiply-add chain over the row's live slots in
+ * slot order, starting from +0.0 — the same arithmetic as the reference.     */
+SLK_API int slk_spmm(const slk_csr* W, const float* X, int64_t K, int64_t N,
+             float* Y, void* stream);
+
+/* dW[s] = dot(dY[i,:], X[col[s],:]) for every live slot s of row i, and
+ * dW[s] = 0 for every padding slot. Replaces `spmm_grad_w_simd` /
+ * `spmm_grad_w` (csrc/bindings.cpp:318-431). `order` is an slk_dw_order.
+ * dY is M x N, X is K x N; dW has W->total_capacity entries.                */
+SLK_API int slk_sddmm(const slk_csr* W, const float* dY, int64_t dY_rows,
+              const float* X, int64_t X_rows, int64_t N, float* dW,
+              int order, void* stream);
+
+/* Transpose build, part 1 of 2 (replaces the index work of
+ * `transpose_with_perm`, sparselab/layout.py:460-536).
+ * Bytes of device workspace slk_transpose_count needs for W.                */
+SLK_API int64_t slk_transpose_workspace_bytes(const slk_csr* W);
+
+/* Counting pass: per-row-block column histograms, WT row_nnz, WT
+ * row_capacity = max(1, ceil(nnz * (1 + padding_ratio))) evaluated in
+ * float64 (layout.py:46-68), WT row_start = exclusive scan of the
+ * capacities, and *capT_dev = total WT capacity (one int64 on the device).
+ * WT arrays have W->ncols entries.                                          */
+SLK_API int slk_transpose_count(const slk_csr* W, double padding_ratio,
+                        void* workspace, int64_t workspace_bytes,
+                        int32_t* WT_row_start, int32_t* WT_row_nnz,
+                        int32_t* WT_row_capacity, int64_t* capT_dev,
+                        void* stream);
+
+/* Fill pass: stable scatter of W's live slots into WT (each WT row lists its
+ * source rows in ascending order), padding = (col -1, value 0, perm -1).
+ * perm[t] = slot of W whose value sits at WT slot t (int64, -1 on padding).
+ * `workspace` must be the one slk_transpose_count filled for this W.       */
+SLK_API int slk_transpose_fill(const slk_csr* W, const void* workspace,
+                       int64_t workspace_bytes,
+                       const int32_t* WT_row_start, const int32_t* WT_row_nnz,
+                       const int32_t* WT_row_capacity, int64_t capT,
+                       float* WT_values, int32_t* WT_col_indices,
+                       int64_t* perm, void* stream);
+
+/* Cache-hit refresh: WT_values[t] = W_values[perm[t]] where perm[t] >= 0;
+ * padding slots are left as they are. Replaces the numpy gather of
+ * `_cached_transpose` (sparselab/ops.py:83-94).                              */
+SLK_API int slk_transpose_refresh(const float* W_values, int64_t W_capacity,
+                          const int64_t* perm, int64_t capT,
+                          float* WT_values, void* stream);
+
+/* Invariant scan of a device PaddedCSR (the checks of
+ * csrc/kernels/padded_csr.cpp:79-196, invariants 3-7). Writes
+ * SLK_CHECK_WORDS int64 words to result_dev:
+ *   [0] sum of row_capacity
+ *   [1] first row violating invariant 3 (INT64_MAX if none)
+ *   [2] first row violating invariant 4 (INT64_MAX if none)
+ *   [3] first (row << 32 | slot-in-row) with a live-column violation
+ *       (invariant 6), INT64_MAX if none
+ *   [4] first (row << 32 | slot-in-row) with a padding column != -1
+ *       (invariants 5+7), INT64_MAX if none
+ * Slot checks are only evaluated for rows whose [row_start, row_start+cap)
+ * lies inside the arrays, so a malformed CSR never causes an out-of-bounds
+ * read. The caller formats the reference's message from these words.       */
+#define SLK_CHECK_WORDS 5
+SLK_API int slk_check_invariants(const slk_csr* W, int64_t col_indices_len,
+                         int64_t* result_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPARSECORE_AMD_H */

@@ -1,0 +1,186 @@
+"""ctypes binding of ``libsparsecore_amd.so`` (C-ABI: include/sparsecore_amd.h).
+
+This module is the only place that talks to the native library. It replaces
+the reference's pybind11 module ``sparselab._core`` (csrc/bindings.cpp) for
+the hot path. Every wrapper takes torch tensors that already live on a HIP
+device, passes their raw device pointers plus torch's current stream, and
+maps a non-zero status to ``ValueError`` (bad arguments, as the reference
+raises) or ``RuntimeError`` (HIP failure).
+
+There is no CPU fallback: if the library is missing, importing the package
+still works (so the host-side API and its error paths stay usable), but every
+kernel call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libsparsecore_amd.so"
+ABI_VERSION = 1
+
+SLK_OK, SLK_EINVAL, SLK_EDEVICE = 0, 1, 2
+SLK_DW_SIMD, SLK_DW_SCALAR = 0, 1
+SLK_CHECK_WORDS = 5
+
+# Every symbol include/sparsecore_amd.h declares.
+EXPORTS = (
+    "slk_last_error",
+    "slk_abi_version",
+    "slk_spmm",
+    "slk_sddmm",
+    "slk_transpose_workspace_bytes",
+    "slk_transpose_count",
+    "slk_transpose_fill",
+    "slk_transpose_refresh",
+    "slk_check_invariants",
+)
+
+
+class CsrView(ctypes.Structure):
+    """Mirror of ``slk_csr`` (include/sparsecore_amd.h)."""
+
+    _fields_ = [
+        ("nrows", ctypes.c_int64),
+        ("ncols", ctypes.c_int64),
+        ("total_capacity", ctypes.c_int64),
+        ("values", ctypes.c_void_p),
+        ("col_indices", ctypes.c_void_p),
+        ("row_start", ctypes.c_void_p),
+        ("row_nnz", ctypes.c_void_p),
+        ("row_capacity", ctypes.c_void_p),
+    ]
+
+
+_lib = None
+_load_error: str | None = None
+
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+_csrp = ctypes.POINTER(CsrView)
+
+
+def _declare(lib) -> None:
+    lib.slk_last_error.restype = ctypes.c_char_p
+    lib.slk_last_error.argtypes = []
+    lib.slk_abi_version.restype = ctypes.c_int
+    lib.slk_spmm.argtypes = [_csrp, _vp, _i64, _i64, _vp, _vp]
+    lib.slk_sddmm.argtypes = [_csrp, _vp, _i64, _vp, _i64, _i64, _vp, ctypes.c_int, _vp]
+    lib.slk_transpose_workspace_bytes.restype = _i64
+    lib.slk_transpose_workspace_bytes.argtypes = [_csrp]
+    lib.slk_transpose_count.argtypes = [_csrp, ctypes.c_double, _vp, _i64, _vp, _vp, _vp, _vp,
+                                        _vp]
+    lib.slk_transpose_fill.argtypes = [_csrp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp]
+    lib.slk_transpose_refresh.argtypes = [_vp, _i64, _vp, _i64, _vp, _vp]
+    lib.slk_check_invariants.argtypes = [_csrp, _i64, _vp, _vp]
+    for name in EXPORTS:
+        if name not in ("slk_last_error", "slk_abi_version", "slk_transpose_workspace_bytes"):
+            getattr(lib, name).restype = ctypes.c_int
+
+
+def load(path: str | os.PathLike | None = None):
+    """Load (once) and return the native library; raises RuntimeError if absent."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        _load_error = (f"sparsecore_amd: native library {p} is not built. Build it with "
+                       f"`python -m sparsecore_amd.build` (hipcc, gfx950). There is no CPU "
+                       f"fallback for the padded-CSR kernels.")
+        raise RuntimeError(_load_error)
+    # torch is imported first (module import above), so the HIP runtime torch
+    # loaded is the one this library binds to (same soname).
+    lib = ctypes.CDLL(str(p))
+    _declare(lib)
+    ver = lib.slk_abi_version()
+    if ver != ABI_VERSION:
+        raise RuntimeError(f"sparsecore_amd: library ABI {ver} != expected {ABI_VERSION}; "
+                           f"rebuild with `python -m sparsecore_amd.build`")
+    _lib = lib
+    return lib
+
+
+def available() -> bool:
+    try:
+        load()
+        return True
+    except (RuntimeError, OSError):
+        return False
+
+
+def _raise(rc: int) -> None:
+    msg = _lib.slk_last_error().decode(errors="replace")
+    if rc == SLK_EINVAL:
+        raise ValueError(msg)
+    raise RuntimeError(msg or f"sparsecore_amd: native call failed with status {rc}")
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None or t.numel() == 0 else t.data_ptr()
+
+
+def spmm(view: CsrView, X: torch.Tensor, Y: torch.Tensor) -> None:
+    lib = load()
+    rc = lib.slk_spmm(ctypes.byref(view), ptr(X), X.shape[0], X.shape[1], ptr(Y), stream_of(Y))
+    if rc:
+        _raise(rc)
+
+
+def sddmm(view: CsrView, dY: torch.Tensor, X: torch.Tensor, dW: torch.Tensor,
+          order: int) -> None:
+    lib = load()
+    rc = lib.slk_sddmm(ctypes.byref(view), ptr(dY), dY.shape[0], ptr(X), X.shape[0],
+                       X.shape[1], ptr(dW), order, stream_of(dW))
+    if rc:
+        _raise(rc)
+
+
+def transpose_workspace_bytes(view: CsrView) -> int:
+    return int(load().slk_transpose_workspace_bytes(ctypes.byref(view)))
+
+
+def transpose_count(view: CsrView, padding_ratio: float, ws: torch.Tensor,
+                    rs_t: torch.Tensor, nnz_t: torch.Tensor, cap_t: torch.Tensor,
+                    capT_dev: torch.Tensor) -> None:
+    lib = load()
+    rc = lib.slk_transpose_count(ctypes.byref(view), float(padding_ratio), ptr(ws), ws.numel(),
+                                 ptr(rs_t), ptr(nnz_t), ptr(cap_t), capT_dev.data_ptr(),
+                                 stream_of(capT_dev))
+    if rc:
+        _raise(rc)
+
+
+def transpose_fill(view: CsrView, ws: torch.Tensor, rs_t: torch.Tensor, nnz_t: torch.Tensor,
+                   cap_t: torch.Tensor, capT: int, val_t: torch.Tensor, col_t: torch.Tensor,
+                   perm: torch.Tensor) -> None:
+    lib = load()
+    rc = lib.slk_transpose_fill(ctypes.byref(view), ptr(ws), ws.numel(), ptr(rs_t), ptr(nnz_t),
+                                ptr(cap_t), capT, ptr(val_t), ptr(col_t), ptr(perm),
+                                stream_of(perm))
+    if rc:
+        _raise(rc)
+
+
+def transpose_refresh(W_values: torch.Tensor, perm: torch.Tensor, WT_values: torch.Tensor) -> None:
+    lib = load()
+    rc = lib.slk_transpose_refresh(ptr(W_values), W_values.numel(), ptr(perm), perm.numel(),
+                                   ptr(WT_values), stream_of(WT_values))
+    if rc:
+        _raise(rc)
+
+
+def check_invariants(view: CsrView, col_len: int, result: torch.Tensor) -> None:
+    lib = load()
+    rc = lib.slk_check_invariants(ctypes.byref(view), col_len, result.data_ptr(),
+                                  stream_of(result))
+    if rc:
+        _raise(rc)

@@ -1,0 +1,51 @@
+// Error state and argument validation shared by every entry point.
+#include "common.hpp"
+
+namespace slk {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+int check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        return fail(SLK_EDEVICE, std::string(what) + ": kernel launch failed: " +
+                                     hipGetErrorString(e));
+    }
+    return SLK_OK;
+}
+
+int validate_csr(const slk_csr* W, const char* who) {
+    if (W == nullptr) return fail(SLK_EINVAL, std::string(who) + ": W is NULL");
+    if (W->nrows < 0 || W->ncols < 0 || W->total_capacity < 0) {
+        return fail(SLK_EINVAL, std::string(who) + ": negative shape (" +
+                                    std::to_string(W->nrows) + ", " +
+                                    std::to_string(W->ncols) + ")");
+    }
+    if (W->total_capacity > INT32_MAX) {
+        return fail(SLK_EINVAL, std::string(who) +
+                                    ": total_capacity exceeds the int32 slot index range");
+    }
+    if (W->nrows > 0 &&
+        (W->row_start == nullptr || W->row_nnz == nullptr || W->row_capacity == nullptr)) {
+        return fail(SLK_EINVAL, std::string(who) + ": NULL row array");
+    }
+    if (W->total_capacity > 0 && (W->values == nullptr || W->col_indices == nullptr)) {
+        return fail(SLK_EINVAL, std::string(who) + ": NULL slot array");
+    }
+    return SLK_OK;
+}
+
+}  // namespace slk
+
+extern "C" const char* slk_last_error(void) { return slk::g_last_error.c_str(); }
+
+extern "C" int slk_abi_version(void) { return SLK_ABI_VERSION; }

@@ -1,0 +1,41 @@
+// Shared helpers for the gfx950 padded-CSR kernels: error reporting,
+// launch checking and small device utilities. Host and device code.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "sparsecore_amd.h"
+
+namespace slk {
+
+constexpr int kWave = 64;  // CDNA wavefront width
+
+// Records `msg` as this thread's last error and returns `code`.
+int fail(int code, const std::string& msg);
+
+// Clears this thread's last error (called at the start of every entry point).
+void clear_error();
+
+// Converts a pending launch error into SLK_EDEVICE with context `what`.
+int check_launch(const char* what);
+
+inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Validates the parts of a CSR view every kernel relies on.
+int validate_csr(const slk_csr* W, const char* who);
+
+// Wave index of the calling thread, made wave-uniform so that values derived
+// from it live in scalar registers (and row metadata loads become scalar).
+__device__ __forceinline__ int64_t wave_id() {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    return static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + w;
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+}  // namespace slk

@@ -1,0 +1,311 @@
+// On-device transpose of a padded-CSR matrix, plus the cache-hit refresh.
+//
+// Reference: sparselab/layout.py:460-536 (transpose_with_perm) builds WT
+// (ncols x nrows) with padding ratio pr and perm[t] = W slot feeding WT slot t
+// (-1 on padding). Each WT row lists its source rows in ascending order (a
+// stable argsort of the column stream), which — together with the capacity
+// rule max(1, ceil(nnz * (1 + pr))) in float64 (layout.py:46-68) — fixes
+// every output array uniquely. This file computes the same arrays as a
+// counting sort keyed by column:
+//
+//   T1 hist    one workgroup per block of B consecutive W rows counts the
+//              block's columns in LDS and writes bh[b][c].
+//   T2 colscan one thread per column turns bh[.][c] into the exclusive
+//              prefix over blocks (the block's starting rank inside WT row c)
+//              and writes WT row_nnz / row_capacity.
+//   T3 scan    exclusive scan of the WT capacities -> WT row_start, capT.
+//   (host)     reads capT, allocates the WT slot arrays.
+//   T4 pad     writes padding slots (col -1, value 0, perm -1).
+//   T5 scatter one wave per block walks its rows in ascending order and
+//              places every live slot at WT row_start[c] + rank, with the
+//              running rank kept per column in LDS. A row's columns are
+//              distinct, so one row's 64-slot batch never collides on a
+//              counter; rows are visited in order, which makes the scatter
+//              stable and the result deterministic.
+//
+// Integer atomics appear only in T1's LDS histogram (counts are
+// order-independent). Columns are processed in chunks of kColChunk so the LDS
+// footprint stays bounded for any ncols.
+#include "common.hpp"
+
+namespace slk {
+namespace {
+
+constexpr int kColChunk = 16384;          // LDS counters per pass (64 KiB)
+constexpr int64_t kHistBudget = 1 << 24;  // max bh entries (64 MiB)
+
+struct BlockPlan {
+    int64_t rows_per_block;
+    int64_t nblk;
+};
+
+BlockPlan plan_blocks(int64_t M, int64_t K) {
+    BlockPlan p{1, 0};
+    if (M <= 0) return p;
+    int64_t target = ceil_div(M, 4);
+    const int64_t cap_by_budget = K > 0 ? kHistBudget / K : target;
+    if (cap_by_budget < target) target = cap_by_budget;
+    if (target < 1) target = 1;
+    p.rows_per_block = ceil_div(M, target);
+    p.nblk = ceil_div(M, p.rows_per_block);
+    return p;
+}
+
+__global__ __launch_bounds__(256) void tr_hist_kernel(
+    int64_t M, int64_t K, int64_t B, const int32_t* __restrict__ row_start,
+    const int32_t* __restrict__ row_capacity, const int32_t* __restrict__ col,
+    int32_t* __restrict__ bh) {
+    extern __shared__ int32_t hist[];
+    const int64_t b = blockIdx.x;
+    const int64_t r0 = b * B;
+    const int64_t r1 = (r0 + B < M) ? r0 + B : M;
+    const int64_t lo = row_start[r0];
+    const int64_t hi = static_cast<int64_t>(row_start[r1 - 1]) + row_capacity[r1 - 1];
+    for (int64_t c0 = 0; c0 < K; c0 += kColChunk) {
+        const int64_t kc = (K - c0 < kColChunk) ? K - c0 : kColChunk;
+        for (int64_t t = threadIdx.x; t < kc; t += blockDim.x) hist[t] = 0;
+        __syncthreads();
+        // Padding slots carry col = -1 (PaddedCSR invariant 5+7), live slots
+        // carry their column, so the flat slot range of the block suffices.
+        for (int64_t s = lo + threadIdx.x; s < hi; s += blockDim.x) {
+            const int64_t c = col[s] - c0;
+            if (c >= 0 && c < kc) atomicAdd(&hist[c], 1);
+        }
+        __syncthreads();
+        for (int64_t t = threadIdx.x; t < kc; t += blockDim.x) bh[b * K + c0 + t] = hist[t];
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(256) void tr_colscan_kernel(int64_t K, int64_t nblk,
+                                                         double one_plus_pr,
+                                                         int32_t* __restrict__ bh,
+                                                         int32_t* __restrict__ nnz_t,
+                                                         int32_t* __restrict__ cap_t) {
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (c >= K) return;
+    int32_t run = 0;
+    int64_t b = 0;
+    for (; b + 4 <= nblk; b += 4) {
+        const int32_t t0 = bh[(b + 0) * K + c], t1 = bh[(b + 1) * K + c];
+        const int32_t t2 = bh[(b + 2) * K + c], t3 = bh[(b + 3) * K + c];
+        bh[(b + 0) * K + c] = run; run += t0;
+        bh[(b + 1) * K + c] = run; run += t1;
+        bh[(b + 2) * K + c] = run; run += t2;
+        bh[(b + 3) * K + c] = run; run += t3;
+    }
+    for (; b < nblk; ++b) {
+        const int32_t t = bh[b * K + c];
+        bh[b * K + c] = run;
+        run += t;
+    }
+    nnz_t[c] = run;
+    // layout.py:66-67: np.maximum(1, np.ceil(nnz.astype(float64) * (1 + pr))).astype(int32)
+    const double scaled = ceil(static_cast<double>(run) * one_plus_pr);
+    cap_t[c] = scaled < 1.0 ? 1 : static_cast<int32_t>(scaled);
+}
+
+constexpr int kScanThreads = 1024;
+
+__global__ __launch_bounds__(kScanThreads) void tr_scan_kernel(int64_t K,
+                                                               const int32_t* __restrict__ cap_t,
+                                                               int32_t* __restrict__ start_t,
+                                                               int64_t* __restrict__ cap_total) {
+    __shared__ int64_t part[kScanThreads];
+    const int t = threadIdx.x;
+    const int64_t per = ceil_div(K, kScanThreads);
+    const int64_t a = t * per;
+    const int64_t e = (a + per < K) ? a + per : K;
+    int64_t sum = 0;
+    for (int64_t c = a; c < e; ++c) sum += cap_t[c];
+    part[t] = sum;
+    __syncthreads();
+    // Hillis-Steele inclusive scan over the per-thread sums.
+    for (int off = 1; off < kScanThreads; off <<= 1) {
+        const int64_t add = (t >= off) ? part[t - off] : 0;
+        __syncthreads();
+        part[t] += add;
+        __syncthreads();
+    }
+    int64_t run = part[t] - sum;
+    for (int64_t c = a; c < e; ++c) {
+        start_t[c] = static_cast<int32_t>(run);
+        run += cap_t[c];
+    }
+    if (t == kScanThreads - 1) *cap_total = part[t];
+}
+
+__global__ __launch_bounds__(256) void tr_pad_kernel(int64_t K, const int32_t* __restrict__ start_t,
+                                                     const int32_t* __restrict__ nnz_t,
+                                                     const int32_t* __restrict__ cap_t,
+                                                     float* __restrict__ val_t,
+                                                     int32_t* __restrict__ col_t,
+                                                     int64_t* __restrict__ perm) {
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (c >= K) return;
+    const int64_t rs = start_t[c];
+    for (int64_t p = rs + nnz_t[c]; p < rs + cap_t[c]; ++p) {
+        col_t[p] = -1;
+        val_t[p] = 0.0f;
+        perm[p] = -1;
+    }
+}
+
+__global__ __launch_bounds__(kWave) void tr_scatter_kernel(
+    int64_t M, int64_t K, int64_t B, const int32_t* __restrict__ row_start,
+    const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ col,
+    const float* __restrict__ val, const int32_t* __restrict__ bh,
+    const int32_t* __restrict__ start_t, float* __restrict__ val_t,
+    int32_t* __restrict__ col_t, int64_t* __restrict__ perm) {
+    extern __shared__ int32_t cur[];
+    const int lane = threadIdx.x;
+    const int64_t b = blockIdx.x;
+    const int64_t r0 = b * B;
+    const int64_t r1 = (r0 + B < M) ? r0 + B : M;
+    for (int64_t c0 = 0; c0 < K; c0 += kColChunk) {
+        const int64_t kc = (K - c0 < kColChunk) ? K - c0 : kColChunk;
+        for (int64_t t = lane; t < kc; t += kWave) cur[t] = start_t[c0 + t] + bh[b * K + c0 + t];
+        __syncthreads();
+        for (int64_t r = r0; r < r1; ++r) {
+            const int64_t start = row_start[r];
+            const int32_t nnz = row_nnz[r];
+            for (int32_t k0 = 0; k0 < nnz; k0 += kWave) {
+                const int32_t k = k0 + lane;
+                if (k < nnz) {
+                    const int64_t s = start + k;
+                    const int64_t c = col[s] - c0;
+                    if (c >= 0 && c < kc) {
+                        const int32_t pos = cur[c];
+                        cur[c] = pos + 1;
+                        perm[pos] = s;
+                        col_t[pos] = static_cast<int32_t>(r);
+                        val_t[pos] = val[s];
+                    }
+                }
+                // Orders this batch's counter updates before the next batch
+                // (a later row may share a column with this one).
+                __syncthreads();
+            }
+        }
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(256) void tr_refresh_kernel(const float* __restrict__ w_val,
+                                                         int64_t w_cap,
+                                                         const int64_t* __restrict__ perm,
+                                                         int64_t cap_t, float* __restrict__ val_t) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; t < cap_t;
+         t += stride) {
+        const int64_t p = perm[t];
+        if (p >= 0 && p < w_cap) val_t[t] = w_val[p];
+    }
+}
+
+}  // namespace
+}  // namespace slk
+
+extern "C" int64_t slk_transpose_workspace_bytes(const slk_csr* W) {
+    if (W == nullptr || W->nrows <= 0 || W->ncols <= 0) return 0;
+    const slk::BlockPlan p = slk::plan_blocks(W->nrows, W->ncols);
+    return p.nblk * W->ncols * static_cast<int64_t>(sizeof(int32_t));
+}
+
+extern "C" int slk_transpose_count(const slk_csr* W, double padding_ratio, void* workspace,
+                                   int64_t workspace_bytes, int32_t* WT_row_start,
+                                   int32_t* WT_row_nnz, int32_t* WT_row_capacity,
+                                   int64_t* capT_dev, void* stream) {
+    using namespace slk;
+    clear_error();
+    if (int rc = validate_csr(W, "transpose")) return rc;
+    if (!(padding_ratio >= 0.0)) {
+        return fail(SLK_EINVAL,
+                    "padding_ratio must be >= 0, got " + std::to_string(padding_ratio));
+    }
+    const int64_t M = W->nrows, K = W->ncols;
+    if (capT_dev == nullptr) return fail(SLK_EINVAL, "transpose: NULL capT");
+    hipStream_t st = as_stream(stream);
+    if (K == 0) {
+        // WT has no rows: capT = 0. Written by a kernel (graph-capture safe).
+        hipLaunchKernelGGL(tr_scan_kernel, dim3(1), dim3(kScanThreads), 0, st, int64_t{0},
+                           WT_row_capacity, WT_row_start, capT_dev);
+        return check_launch("transpose_count");
+    }
+    if (WT_row_start == nullptr || WT_row_nnz == nullptr || WT_row_capacity == nullptr) {
+        return fail(SLK_EINVAL, "transpose: NULL WT row arrays");
+    }
+    const BlockPlan p = plan_blocks(M, K);
+    const int64_t need = p.nblk * K * static_cast<int64_t>(sizeof(int32_t));
+    if (workspace_bytes < need || (need > 0 && workspace == nullptr)) {
+        return fail(SLK_EINVAL, "transpose: workspace of " + std::to_string(workspace_bytes) +
+                                    " bytes is smaller than the required " +
+                                    std::to_string(need));
+    }
+    int32_t* bh = static_cast<int32_t*>(workspace);
+    const size_t lds = static_cast<size_t>(K < kColChunk ? K : kColChunk) * sizeof(int32_t);
+    if (p.nblk > 0) {
+        hipLaunchKernelGGL(tr_hist_kernel, dim3(static_cast<unsigned>(p.nblk)), dim3(256), lds, st,
+                           M, K, p.rows_per_block, W->row_start, W->row_capacity, W->col_indices,
+                           bh);
+        if (int rc = check_launch("transpose_count/hist")) return rc;
+    }
+    hipLaunchKernelGGL(tr_colscan_kernel, dim3(static_cast<unsigned>(ceil_div(K, 256))), dim3(256),
+                       0, st, K, p.nblk, 1.0 + padding_ratio, bh, WT_row_nnz, WT_row_capacity);
+    if (int rc = check_launch("transpose_count/colscan")) return rc;
+    hipLaunchKernelGGL(tr_scan_kernel, dim3(1), dim3(kScanThreads), 0, st, K, WT_row_capacity,
+                       WT_row_start, capT_dev);
+    return check_launch("transpose_count/scan");
+}
+
+extern "C" int slk_transpose_fill(const slk_csr* W, const void* workspace, int64_t workspace_bytes,
+                                  const int32_t* WT_row_start, const int32_t* WT_row_nnz,
+                                  const int32_t* WT_row_capacity, int64_t capT, float* WT_values,
+                                  int32_t* WT_col_indices, int64_t* perm, void* stream) {
+    using namespace slk;
+    clear_error();
+    if (int rc = validate_csr(W, "transpose")) return rc;
+    const int64_t M = W->nrows, K = W->ncols;
+    if (K == 0 || capT == 0) return SLK_OK;
+    if (capT > INT32_MAX) {
+        return fail(SLK_EINVAL, "transpose: WT capacity " + std::to_string(capT) +
+                                    " exceeds the int32 slot index range");
+    }
+    if (WT_values == nullptr || WT_col_indices == nullptr || perm == nullptr) {
+        return fail(SLK_EINVAL, "transpose: NULL WT slot arrays");
+    }
+    const BlockPlan p = plan_blocks(M, K);
+    const int64_t need = p.nblk * K * static_cast<int64_t>(sizeof(int32_t));
+    if (workspace_bytes < need || (need > 0 && workspace == nullptr)) {
+        return fail(SLK_EINVAL, "transpose: workspace too small");
+    }
+    hipStream_t st = as_stream(stream);
+    hipLaunchKernelGGL(tr_pad_kernel, dim3(static_cast<unsigned>(ceil_div(K, 256))), dim3(256), 0,
+                       st, K, WT_row_start, WT_row_nnz, WT_row_capacity, WT_values, WT_col_indices,
+                       perm);
+    if (int rc = check_launch("transpose_fill/pad")) return rc;
+    if (p.nblk == 0) return SLK_OK;
+    const size_t lds = static_cast<size_t>(K < kColChunk ? K : kColChunk) * sizeof(int32_t);
+    hipLaunchKernelGGL(tr_scatter_kernel, dim3(static_cast<unsigned>(p.nblk)), dim3(kWave), lds,
+                       st, M, K, p.rows_per_block, W->row_start, W->row_nnz, W->col_indices,
+                       W->values, static_cast<const int32_t*>(workspace), WT_row_start, WT_values,
+                       WT_col_indices, perm);
+    return check_launch("transpose_fill/scatter");
+}
+
+extern "C" int slk_transpose_refresh(const float* W_values, int64_t W_capacity,
+                                     const int64_t* perm, int64_t capT, float* WT_values,
+                                     void* stream) {
+    using namespace slk;
+    clear_error();
+    if (capT < 0 || W_capacity < 0) return fail(SLK_EINVAL, "transpose_refresh: negative size");
+    if (capT == 0) return SLK_OK;
+    if (perm == nullptr || WT_values == nullptr || (W_capacity > 0 && W_values == nullptr)) {
+        return fail(SLK_EINVAL, "transpose_refresh: NULL pointer");
+    }
+    int64_t blocks = ceil_div(capT, 256);
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(tr_refresh_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       as_stream(stream), W_values, W_capacity, perm, capT, WT_values);
+    return check_launch("transpose_refresh");
+}

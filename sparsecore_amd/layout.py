@@ -1,0 +1,639 @@
+"""sparsecore_amd.layout — the padded-CSR matrix, its factories and its transpose.
+
+Drop-in for the reference's C++ ``PaddedCSR`` class (csrc/kernels/padded_csr.hpp:47-143,
+exposed by csrc/bindings.cpp:596-743) together with the Python factories of
+``sparselab/layout.py``. The arrays live in torch tensors, normally on the HIP
+device (HBM); a matrix built on the CPU can be moved with ``.cuda()`` /
+``.to(device)``. Host-side work here is setup and validation only; the
+transpose used by the backward pass runs on the GPU
+(``transpose_with_perm`` → the ``slk_transpose_*`` kernels).
+
+Layout (unchanged from the reference, padded_csr.hpp:30-45):
+
+    values[total_capacity]        float32; live slots hold weights, padding 0.0
+    col_indices[total_capacity]   int32;   live slots hold their column, padding -1
+    row_start[nrows]              int32;   first slot of each row
+    row_nnz[nrows]                int32;   live slots per row (<= capacity)
+    row_capacity[nrows]           int32;   slots reserved per row
+    topology_version              int;     bumped by every rewrite_row
+
+Within a row the first ``row_nnz`` slots are live with strictly ascending
+columns and the rest are padding; rows tile ``[0, total_capacity)`` in order.
+"""
+
+from __future__ import annotations
+
+import math
+import weakref  # noqa: F401  (PaddedCSR objects are weak-referenceable)
+
+import numpy as np
+import torch
+
+from . import _lib
+
+__all__ = [
+    "PaddedCSR",
+    "from_dense",
+    "from_torch_sparse_csr",
+    "random",
+    "to_dense",
+    "transpose",
+    "transpose_with_perm",
+]
+
+_I32 = torch.int32
+_F32 = torch.float32
+_NONE = (1 << 63) - 1  # "no violation" word of the device checker
+
+
+# ─────────────────────────────────────────────────────────────────────
+#  Row-capacity rule
+# ─────────────────────────────────────────────────────────────────────
+
+def _compute_row_capacity(row_nnz: np.ndarray, padding_ratio: float) -> np.ndarray:
+    """capacity[i] = max(1, ceil(nnz[i] * (1 + padding_ratio))), in float64.
+
+    Same rule as sparselab/layout.py:46-68; the device transpose applies it in
+    the same float64 arithmetic (slk_transpose_count).
+    """
+    if padding_ratio < 0:
+        raise ValueError(f"padding_ratio must be >= 0, got {padding_ratio}")
+    scaled = np.ceil(np.asarray(row_nnz).astype(np.float64) * (1.0 + padding_ratio))
+    return np.maximum(1, scaled).astype(np.int32)
+
+
+def _as_tensor(x, dtype, device) -> torch.Tensor:
+    if isinstance(x, torch.Tensor):
+        t = x.detach()
+        if device is not None:
+            t = t.to(device)
+        return t.to(dtype).contiguous()
+    arr = np.asarray(x)
+    if arr.dtype == object:
+        arr = np.asarray(list(x))
+    t = torch.from_numpy(np.ascontiguousarray(arr).astype(
+        np.float32 if dtype == _F32 else np.int32))
+    return t.to(device) if device is not None else t
+
+
+def _wrap_i32(v: int) -> int:
+    return ((v + (1 << 31)) % (1 << 32)) - (1 << 31)
+
+
+# ─────────────────────────────────────────────────────────────────────
+#  Invariant messages (text of csrc/kernels/padded_csr.cpp:79-196; the
+#  reference tests match these substrings, so the wording is kept)
+# ─────────────────────────────────────────────────────────────────────
+
+def _msg_inv3_first(got: int) -> str:
+    return f"Invariant 3 violated: row_start[0] must be 0, got {got}."
+
+
+def _msg_inv3(i: int, got: int, expected: int) -> str:
+    return (f"Invariant 3 violated: row_start[{i}]={got} should equal row_start[{i - 1}] + "
+            f"row_capacity[{i - 1}] = {expected}.")
+
+
+def _msg_inv4(i: int, nnz: int, cap: int) -> str:
+    return f"Invariant 4 violated at row {i}: row_nnz={nnz} must be in [0, {cap}]."
+
+
+def _msg_inv6_range(i: int, k: int, c: int, ncols: int) -> str:
+    return (f"Invariant 6 violated at row {i}, slot {k}: col_indices={c} must be in "
+            f"[0, {ncols}).")
+
+
+def _msg_inv6_order(i: int, k: int, c: int, prev: int) -> str:
+    return (f"Invariant 6 violated at row {i}, slot {k}: col_indices={c} must be strictly "
+            f"greater than previous={prev} (live columns must be sorted ascending and "
+            f"distinct).")
+
+
+def _msg_inv57(i: int, k: int, c: int) -> str:
+    return (f"Invariants 5+7 violated at row {i}, slot {k}: padding col_indices={c} "
+            f"must be -1.")
+
+
+def _check_shape_and_lengths(nrows, ncols, n_values, n_col, n_rs, n_nnz, n_cap) -> str:
+    if nrows < 0 or ncols < 0:
+        return f"Invariant 1 violated: shape must be non-negative, got ({nrows}, {ncols})."
+    if not (n_rs == n_nnz == n_cap == nrows):
+        return (f"Metadata array length mismatch: row_start={n_rs}, row_nnz={n_nnz}, "
+                f"row_capacity={n_cap}, expected nrows={nrows}.")
+    if n_values != n_col:
+        return (f"Invariant 2 violated: values ({n_values}) and col_indices ({n_col}) must "
+                f"have the same length.")
+    return ""
+
+
+def _check_host(nrows, ncols, values, col, rs, nnz, cap) -> str:
+    """Vectorized host check of invariants 1-7 with the reference's first-violation order."""
+    msg = _check_shape_and_lengths(nrows, ncols, values.shape[0], col.shape[0], rs.shape[0],
+                                   nnz.shape[0], cap.shape[0])
+    if msg:
+        return msg
+    rs64, nnz64, cap64 = rs.astype(np.int64), nnz.astype(np.int64), cap.astype(np.int64)
+    total = int(cap64.sum())
+    if values.shape[0] != total:
+        return (f"Invariant 2 violated: values.size()={values.shape[0]} does not match "
+                f"total_capacity={total} (sum of row_capacity).")
+    if nrows == 0:
+        return ""
+    if rs64[0] != 0:
+        return _msg_inv3_first(int(rs64[0]))
+    if nrows > 1:
+        expected = (rs.astype(np.int32)[:-1].astype(np.int64) + cap64[:-1])
+        expected = ((expected + (1 << 31)) % (1 << 32)) - (1 << 31)
+        bad = np.flatnonzero(rs64[1:] != expected)
+        if bad.size:
+            i = int(bad[0]) + 1
+            return _msg_inv3(i, int(rs64[i]), int(expected[i - 1]))
+    bad = np.flatnonzero((nnz64 < 0) | (nnz64 > cap64))
+    if bad.size:
+        i = int(bad[0])
+        return _msg_inv4(i, int(nnz64[i]), int(cap64[i]))
+    # Rows tile [0, total) now; classify every slot.
+    row_of = np.repeat(np.arange(nrows, dtype=np.int64), cap64)
+    pos = np.arange(total, dtype=np.int64) - rs64[row_of]
+    live = pos < nnz64[row_of]
+    c = col.astype(np.int64)
+    prev = np.empty_like(c)
+    prev[0:1] = -1
+    prev[1:] = c[:-1]
+    prev[pos == 0] = -1
+    live_bad = live & ((c < 0) | (c >= ncols) | (c <= prev))
+    pad_bad = (~live) & (c != -1)
+    lb = np.flatnonzero(live_bad)
+    pb = np.flatnonzero(pad_bad)
+    if not lb.size and not pb.size:
+        return ""
+    lrow = int(row_of[lb[0]]) if lb.size else None
+    prow = int(row_of[pb[0]]) if pb.size else None
+    if lrow is not None and (prow is None or lrow <= prow):
+        s = int(lb[0])
+        i, k, cc = lrow, int(pos[s]), int(c[s])
+        if cc < 0 or cc >= ncols:
+            return _msg_inv6_range(i, k, cc, ncols)
+        return _msg_inv6_order(i, k, cc, int(prev[s]))
+    s = int(pb[0])
+    return _msg_inv57(prow, int(pos[s]), int(c[s]))
+
+
+# ─────────────────────────────────────────────────────────────────────
+#  PaddedCSR
+# ─────────────────────────────────────────────────────────────────────
+
+class PaddedCSR:
+    """Sparse matrix with padded-row CSR storage (reference padded_csr.hpp:47-143).
+
+    ``PaddedCSR(nrows, ncols)`` builds an empty zero-capacity matrix;
+    ``PaddedCSR(nrows, ncols, values, col_indices, row_start, row_nnz,
+    row_capacity)`` takes the five arrays (lists, numpy arrays or tensors),
+    validates all invariants and raises ``ValueError`` on the first violation,
+    as the reference constructor does (csrc/bindings.cpp:608-627).
+    ``device=`` places the arrays (default: where tensor inputs live, else CPU).
+    """
+
+    def __init__(self, nrows, ncols, values=None, col_indices=None, row_start=None,
+                 row_nnz=None, row_capacity=None, *, device=None):
+        nrows = int(nrows)
+        ncols = int(ncols)
+        parts = (values, col_indices, row_start, row_nnz, row_capacity)
+        if all(p is None for p in parts):
+            if nrows < 0 or ncols < 0:
+                raise ValueError(f"PaddedCSR: shape must be non-negative, got ({nrows}, {ncols})")
+            dev = torch.device(device) if device is not None else torch.device("cpu")
+            self._init(nrows, ncols, torch.zeros(0, dtype=_F32, device=dev),
+                       torch.zeros(0, dtype=_I32, device=dev),
+                       torch.zeros(nrows, dtype=_I32, device=dev),
+                       torch.zeros(nrows, dtype=_I32, device=dev),
+                       torch.zeros(nrows, dtype=_I32, device=dev), nnz=0)
+            return
+        if any(p is None for p in parts):
+            raise TypeError("PaddedCSR() takes either (nrows, ncols) or all of values, "
+                            "col_indices, row_start, row_nnz, row_capacity")
+        if device is None:
+            devs = {p.device for p in parts if isinstance(p, torch.Tensor)}
+            device = devs.pop() if len(devs) == 1 else None
+        v = _as_tensor(values, _F32, device)
+        c = _as_tensor(col_indices, _I32, device)
+        rs = _as_tensor(row_start, _I32, device)
+        nz = _as_tensor(row_nnz, _I32, device)
+        cp = _as_tensor(row_capacity, _I32, device)
+        for t in (v, c, rs, nz, cp):
+            if t.dim() != 1:
+                raise ValueError("PaddedCSR arrays must be 1-D")
+        self._init(nrows, ncols, v, c, rs, nz, cp, nnz=None)
+        msg = self._check()
+        if msg:
+            raise ValueError("PaddedCSR invariant check failed: " + msg)
+        self._nnz = int(nz.to(torch.int64).sum().item()) if nrows else 0
+
+    # internal constructor: trusted arrays (kernel outputs), no validation
+    @classmethod
+    def _from_parts(cls, nrows, ncols, values, col, rs, nnz_t, cap_t, nnz: int,
+                    topology_version: int = 0) -> "PaddedCSR":
+        self = cls.__new__(cls)
+        self._init(nrows, ncols, values, col, rs, nnz_t, cap_t, nnz=nnz)
+        self._topology_version = int(topology_version)
+        return self
+
+    def _init(self, nrows, ncols, values, col, rs, nnz_t, cap_t, nnz):
+        self._nrows = nrows
+        self._ncols = ncols
+        self._values = values
+        self._col = col
+        self._rs = rs
+        self._row_nnz = nnz_t
+        self._row_cap = cap_t
+        self._nnz = nnz
+        self._topology_version = 0
+        self._cview = None
+        self._host_rows = None  # cached numpy (row_start, row_nnz, row_capacity)
+
+    # ─── shape and aggregates (bindings.cpp:631-660) ────────────────
+    @property
+    def shape(self) -> tuple[int, int]:
+        return (self._nrows, self._ncols)
+
+    @property
+    def nrows(self) -> int:
+        return self._nrows
+
+    @property
+    def ncols(self) -> int:
+        return self._ncols
+
+    @property
+    def nnz(self) -> int:
+        return self._nnz
+
+    @property
+    def total_capacity(self) -> int:
+        return int(self._values.numel())
+
+    @property
+    def padding_slots(self) -> int:
+        return self.total_capacity - self._nnz
+
+    @property
+    def sparsity(self) -> float:
+        if self._nrows == 0 or self._ncols == 0:
+            return 1.0
+        return 1.0 - self._nnz / float(self._nrows * self._ncols)
+
+    @property
+    def topology_version(self) -> int:
+        return self._topology_version
+
+    @property
+    def device(self) -> torch.device:
+        return self._values.device
+
+    # ─── arrays (bindings.cpp:665-687) ──────────────────────────────
+    # `values` is the live weight buffer (an optimizer may update it in
+    # place); the structure arrays must only change through rewrite_row.
+    @property
+    def values(self) -> torch.Tensor:
+        return self._values
+
+    @property
+    def col_indices(self) -> torch.Tensor:
+        return self._col
+
+    @property
+    def row_start(self) -> torch.Tensor:
+        return self._rs
+
+    @property
+    def row_nnz(self) -> torch.Tensor:
+        return self._row_nnz
+
+    @property
+    def row_capacity(self) -> torch.Tensor:
+        return self._row_cap
+
+    def _bind_values(self, t: torch.Tensor) -> None:
+        """Point the matrix at another float32 buffer of the same size (aliasing)."""
+        if t.dtype != _F32 or t.numel() != self._values.numel() or not t.is_contiguous():
+            raise ValueError("values buffer must be a contiguous float32 tensor of "
+                             "total_capacity elements")
+        self._values = t
+        self._cview = None
+
+    def _on_device(self) -> bool:
+        return self._values.device.type == "cuda"
+
+    def _require_device(self, who: str) -> None:
+        if not self._on_device():
+            raise RuntimeError(
+                f"{who}: the PaddedCSR lives on {self._values.device}; the padded-CSR kernels run "
+                f"on the HIP device only — move it with .cuda() / .to('cuda')")
+
+    def _view(self) -> _lib.CsrView:
+        v = self._cview
+        if v is None:
+            v = _lib.CsrView(self._nrows, self._ncols, self._values.numel(),
+                             _lib.ptr(self._values), _lib.ptr(self._col), _lib.ptr(self._rs),
+                             _lib.ptr(self._row_nnz), _lib.ptr(self._row_cap))
+            self._cview = v
+        return v
+
+    def _rows_host(self):
+        h = self._host_rows
+        if h is None:
+            h = (self._rs.cpu().numpy().copy(), self._row_nnz.cpu().numpy().copy(),
+                 self._row_cap.cpu().numpy().copy())
+            self._host_rows = h
+        return h
+
+    # ─── invariants (padded_csr.cpp:79-196) ─────────────────────────
+    def _check(self) -> str:
+        if not self._on_device():
+            return _check_host(self._nrows, self._ncols, self._values.detach().numpy(),
+                               self._col.numpy(), self._rs.numpy(), self._row_nnz.numpy(),
+                               self._row_cap.numpy())
+        return self._check_device()
+
+    def _check_device(self) -> str:
+        M, K = self._nrows, self._ncols
+        msg = _check_shape_and_lengths(M, K, self._values.numel(), self._col.numel(),
+                                       self._rs.numel(), self._row_nnz.numel(),
+                                       self._row_cap.numel())
+        if msg:
+            return msg
+        res = torch.empty(_lib.SLK_CHECK_WORDS, dtype=torch.int64, device=self._values.device)
+        _lib.check_invariants(self._view(), self._col.numel(), res)
+        w = res.cpu().tolist()
+        total = w[0]
+        if self._values.numel() != total:
+            return (f"Invariant 2 violated: values.size()={self._values.numel()} does not "
+                    f"match total_capacity={total} (sum of row_capacity).")
+
+        def at(t, i):
+            return int(t[i].item())
+
+        if w[1] != _NONE:
+            i = w[1]
+            if i == 0:
+                return _msg_inv3_first(at(self._rs, 0))
+            return _msg_inv3(i, at(self._rs, i),
+                             _wrap_i32(at(self._rs, i - 1) + at(self._row_cap, i - 1)))
+        if w[2] != _NONE:
+            i = w[2]
+            return _msg_inv4(i, at(self._row_nnz, i), at(self._row_cap, i))
+        live, pad = w[3], w[4]
+        if live == _NONE and pad == _NONE:
+            return ""
+        if live != _NONE and (pad == _NONE or (live >> 32) <= (pad >> 32)):
+            i, k = live >> 32, live & 0xFFFFFFFF
+            s = at(self._rs, i) + k
+            c = at(self._col, s)
+            if c < 0 or c >= K:
+                return _msg_inv6_range(i, k, c, K)
+            return _msg_inv6_order(i, k, c, at(self._col, s - 1) if k > 0 else -1)
+        i, k = pad >> 32, pad & 0xFFFFFFFF
+        return _msg_inv57(i, k, at(self._col, at(self._rs, i) + k))
+
+    def assert_invariants(self) -> None:
+        """Raise ValueError describing the first violated invariant, if any."""
+        msg = self._check()
+        if msg:
+            raise ValueError("PaddedCSR invariant check failed: " + msg)
+
+    # ─── mutation (padded_csr.cpp:219-296, bindings.cpp:703-734) ────
+    def rewrite_row(self, row_idx, new_cols, new_values) -> None:
+        """Replace row ``row_idx``'s live set; trailing slots become padding.
+
+        ``new_cols`` must be strictly ascending, distinct, inside [0, ncols) and
+        no longer than the row's capacity. Bumps ``topology_version``.
+        """
+        cols = np.asarray(new_cols.detach().cpu() if isinstance(new_cols, torch.Tensor)
+                          else new_cols)
+        vals = np.asarray(new_values.detach().cpu() if isinstance(new_values, torch.Tensor)
+                          else new_values)
+        if cols.ndim != 1 or vals.ndim != 1:
+            raise ValueError("rewrite_row: new_cols and new_values must be 1-D arrays")
+        cols = cols.astype(np.int32)
+        vals = vals.astype(np.float32)
+        row_idx = int(row_idx)
+        if row_idx < 0 or row_idx >= self._nrows:
+            raise ValueError(f"rewrite_row: row_idx={row_idx} out of range [0, {self._nrows}).")
+        if cols.shape[0] != vals.shape[0]:
+            raise ValueError(f"rewrite_row: new_cols.size()={cols.shape[0]} must equal "
+                             f"new_values.size()={vals.shape[0]}")
+        rs, nz, cp = self._rows_host()
+        cap = int(cp[row_idx])
+        n = int(cols.shape[0])
+        if n > cap:
+            raise ValueError(f"rewrite_row: row {row_idx} has capacity {cap} but got {n} new "
+                             f"entries.")
+        prev = -1
+        for k in range(n):
+            c = int(cols[k])
+            if c < 0 or c >= self._ncols:
+                raise ValueError(f"rewrite_row: new_cols[{k}]={c} out of range "
+                                 f"[0, {self._ncols}).")
+            if c <= prev:
+                raise ValueError(f"rewrite_row: new_cols must be strictly ascending, got {prev} "
+                                 f"followed by {c} at position {k}.")
+            prev = c
+        full_c = np.full(cap, -1, dtype=np.int32)
+        full_v = np.zeros(cap, dtype=np.float32)
+        full_c[:n] = cols
+        full_v[:n] = vals
+        base = int(rs[row_idx])
+        with torch.no_grad():
+            self._col[base:base + cap].copy_(torch.from_numpy(full_c))
+            self._values[base:base + cap].copy_(torch.from_numpy(full_v))
+            self._row_nnz[row_idx:row_idx + 1].fill_(n)
+        self._nnz += n - int(nz[row_idx])
+        nz[row_idx] = n
+        self._topology_version += 1
+
+    # ─── device movement ───────────────────────────────────────────
+    def to(self, device) -> "PaddedCSR":
+        device = torch.device(device)
+        if device.type == "cuda" and device.index is None:
+            device = torch.device("cuda", torch.cuda.current_device())
+        if device == self._values.device:
+            return self
+        out = PaddedCSR._from_parts(self._nrows, self._ncols, self._values.to(device),
+                                    self._col.to(device), self._rs.to(device),
+                                    self._row_nnz.to(device), self._row_cap.to(device),
+                                    self._nnz, self._topology_version)
+        out._host_rows = self._host_rows
+        return out
+
+    def cuda(self, device=None) -> "PaddedCSR":
+        if device is None:
+            device = torch.device("cuda")
+        elif isinstance(device, int):
+            device = torch.device("cuda", device)
+        return self.to(device)
+
+    def cpu(self) -> "PaddedCSR":
+        return self.to("cpu")
+
+    def __repr__(self) -> str:
+        return (f"PaddedCSR(nrows={self._nrows}, ncols={self._ncols}, nnz={self._nnz}, "
+                f"capacity={self.total_capacity})")
+
+    # factories and conversions are attached below (as the reference attaches
+    # them in sparselab/__init__.py:56-60)
+
+
+# ─────────────────────────────────────────────────────────────────────
+#  Factories (sparselab/layout.py:75-255)
+# ─────────────────────────────────────────────────────────────────────
+
+def _build_from_rows(nrows, ncols, crow, col, vals, padding_ratio, device) -> PaddedCSR:
+    row_nnz = np.diff(crow).astype(np.int32)
+    cap = _compute_row_capacity(row_nnz, padding_ratio) if nrows else np.zeros(0, np.int32)
+    start = np.zeros(nrows, dtype=np.int64)
+    if nrows > 1:
+        start[1:] = np.cumsum(cap[:-1].astype(np.int64))
+    total = int(cap.astype(np.int64).sum())
+    values = np.zeros(total, dtype=np.float32)
+    cols = np.full(total, -1, dtype=np.int32)
+    n = int(crow[-1]) if nrows else 0
+    if n:
+        row_of = np.repeat(np.arange(nrows, dtype=np.int64), row_nnz.astype(np.int64))
+        dest = start[row_of] + (np.arange(n, dtype=np.int64) - crow[:-1].astype(np.int64)[row_of])
+        values[dest] = vals[:n]
+        cols[dest] = col[:n]
+    p = PaddedCSR(nrows, ncols, torch.from_numpy(values), torch.from_numpy(cols),
+                  torch.from_numpy(start.astype(np.int32)), torch.from_numpy(row_nnz),
+                  torch.from_numpy(cap))
+    return p.to(device) if device is not None else p
+
+
+def from_torch_sparse_csr(csr: torch.Tensor, *, padding_ratio: float = 0.2,
+                          device=None) -> PaddedCSR:
+    """PaddedCSR from a ``torch.sparse_csr`` tensor (layout.py:75-165).
+
+    The result lives on ``device`` (default: the input's device).
+    """
+    if csr.layout != torch.sparse_csr:
+        raise ValueError(f"from_torch_sparse_csr expected layout=torch.sparse_csr, "
+                         f"got layout={csr.layout}")
+    if csr.dim() != 2:
+        raise ValueError(f"from_torch_sparse_csr expected 2-D tensor, got {csr.dim()}-D")
+    if padding_ratio < 0:
+        raise ValueError(f"padding_ratio must be >= 0, got {padding_ratio}")
+    nrows, ncols = csr.size()
+    crow = csr.crow_indices().contiguous().cpu().numpy().astype(np.int64)
+    col = csr.col_indices().contiguous().cpu().numpy().astype(np.int32)
+    vals = csr.values().detach().contiguous().cpu().numpy().astype(np.float32)
+    target = device if device is not None else csr.device
+    return _build_from_rows(int(nrows), int(ncols), crow, col, vals, padding_ratio, target)
+
+
+def from_dense(W: torch.Tensor, *, threshold: float = 0.0, padding_ratio: float = 0.2,
+               device=None) -> PaddedCSR:
+    """PaddedCSR holding the entries of ``W`` with |W| > threshold (layout.py:172-208)."""
+    if W.dim() != 2:
+        raise ValueError(f"from_dense expected 2-D tensor, got {W.dim()}-D")
+    if padding_ratio < 0:
+        raise ValueError(f"padding_ratio must be >= 0, got {padding_ratio}")
+    target = device if device is not None else W.device
+    W_np = W.detach().to(dtype=_F32).cpu().contiguous().numpy()
+    if threshold > 0:
+        W_np = np.where(np.abs(W_np) > threshold, W_np, np.float32(0.0))
+    nrows, ncols = W_np.shape
+    # Row-major nonzeros, i.e. what W.to_sparse_csr() stores (entries != 0).
+    rows, cols = np.nonzero(W_np != 0)
+    crow = np.zeros(nrows + 1, dtype=np.int64)
+    if nrows:
+        crow[1:] = np.cumsum(np.bincount(rows, minlength=nrows))
+    return _build_from_rows(nrows, ncols, crow, cols.astype(np.int32), W_np[rows, cols],
+                            padding_ratio, target)
+
+
+def random(nrows: int, ncols: int, *, sparsity: float, padding_ratio: float = 0.2,
+           seed: int | None = None, device=None) -> PaddedCSR:
+    """Random pattern at the given sparsity with N(0, 1) values (layout.py:215-255).
+
+    Draws from a CPU torch.Generator in the reference's order (randn values,
+    then the rand keep-mask), so a seed selects the same matrix as there.
+    """
+    if not 0.0 <= sparsity < 1.0:
+        raise ValueError(f"sparsity must be in [0, 1), got {sparsity}")
+    gen = torch.Generator()
+    if seed is not None:
+        gen.manual_seed(seed)
+    W = torch.randn(nrows, ncols, generator=gen, dtype=_F32)
+    keep = torch.rand(nrows, ncols, generator=gen) < (1.0 - sparsity)
+    W = W * keep.float()
+    return from_dense(W, threshold=0.0, padding_ratio=padding_ratio, device=device)
+
+
+def _live_slots(p: PaddedCSR):
+    """(rows, slots) of every live entry, in row-major order, on p's device."""
+    dev = p.device
+    n = p.nnz
+    nnz64 = p.row_nnz.to(torch.int64)
+    rows = torch.repeat_interleave(torch.arange(p.nrows, device=dev), nnz64, output_size=n)
+    first = torch.cumsum(nnz64, 0) - nnz64
+    offs = torch.arange(n, device=dev) - first[rows]
+    slots = p.row_start.to(torch.int64)[rows] + offs
+    return rows, slots
+
+
+def to_dense(p: PaddedCSR) -> torch.Tensor:
+    """Dense float32 copy of p on p's device (layout.py:262-292)."""
+    dense = torch.zeros(p.nrows, p.ncols, dtype=_F32, device=p.device)
+    if p.nnz:
+        rows, slots = _live_slots(p)
+        dense[rows, p.col_indices[slots].to(torch.int64)] = p.values[slots]
+    return dense
+
+
+# ─────────────────────────────────────────────────────────────────────
+#  Transpose (layout.py:307-536) — on the HIP device
+# ─────────────────────────────────────────────────────────────────────
+
+def transpose_with_perm(p: PaddedCSR, *, padding_ratio: float = 0.2):
+    """(WT, perm): the transpose of p and, for each WT slot, the W slot it copies.
+
+    WT is ncols x nrows with capacities max(1, ceil(nnz*(1+padding_ratio))),
+    each row listing its source rows in ascending order; perm is int64 with -1
+    on padding (layout.py:460-536). Built on the GPU by a counting sort
+    (slk_transpose_count / slk_transpose_fill); one device->host read of the
+    WT capacity sizes the output arrays.
+    """
+    if padding_ratio < 0:
+        raise ValueError(f"padding_ratio must be >= 0, got {padding_ratio}")
+    p._require_device("transpose")
+    dev = p.device
+    M, K = p.nrows, p.ncols
+    view = p._view()
+    ws = torch.empty(_lib.transpose_workspace_bytes(view), dtype=torch.uint8, device=dev)
+    rs_t = torch.empty(K, dtype=_I32, device=dev)
+    nnz_t = torch.empty(K, dtype=_I32, device=dev)
+    cap_t = torch.empty(K, dtype=_I32, device=dev)
+    capT_dev = torch.empty(1, dtype=torch.int64, device=dev)
+    _lib.transpose_count(view, padding_ratio, ws, rs_t, nnz_t, cap_t, capT_dev)
+    capT = int(capT_dev.item())
+    if capT > np.iinfo(np.int32).max:
+        raise ValueError(f"transpose: capacity {capT} exceeds the int32 slot range")
+    val_t = torch.empty(capT, dtype=_F32, device=dev)
+    col_t = torch.empty(capT, dtype=_I32, device=dev)
+    perm = torch.empty(capT, dtype=torch.int64, device=dev)
+    _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, capT, val_t, col_t, perm)
+    WT = PaddedCSR._from_parts(K, M, val_t, col_t, rs_t, nnz_t, cap_t, p.nnz)
+    return WT, perm
+
+
+def transpose(p: PaddedCSR, *, padding_ratio: float = 0.2) -> PaddedCSR:
+    """The transpose of p as a new PaddedCSR (layout.py:307-434)."""
+    return transpose_with_perm(p, padding_ratio=padding_ratio)[0]
+
+
+PaddedCSR.from_dense = staticmethod(from_dense)
+PaddedCSR.from_torch_sparse_csr = staticmethod(from_torch_sparse_csr)
+PaddedCSR.random = staticmethod(random)
+PaddedCSR.to_dense = to_dense
+PaddedCSR.transpose = transpose
+
+del math

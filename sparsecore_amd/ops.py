@@ -1,0 +1,162 @@
+"""sparsecore_amd.ops — spmm, its autograd Function and the transpose cache.
+
+Drop-in for ``sparselab/ops.py``: same public ``spmm(W, X, *, kernel)``, same
+``_SpMMFunction.apply(W_values, W, X, kernel)`` contract, same
+``_transpose_cache`` / ``_cached_transpose`` / ``_clear_transpose_cache``
+(cache entries are ``(topology_version, (nrows, ncols), WT, perm)``).
+
+Every kernel runs on the HIP device through the C-ABI library:
+
+    forward  Y  = W·X               slk_spmm                 (ops.py:144-165)
+    backward dW = SDDMM(dY, X)      slk_sddmm                (ops.py:186-192)
+             WT = cached transpose  slk_transpose_refresh on a hit,
+                                    slk_transpose_count/fill on a miss (ops.py:70-99)
+             dX = WT·dY             slk_spmm on WT           (ops.py:201-203)
+
+Tensors on the CPU are rejected with RuntimeError (the reference rejected
+non-CPU tensors the same way; this build is GPU-only and has no CPU path).
+"""
+
+from __future__ import annotations
+
+import weakref
+
+import torch
+
+from . import _lib
+from .layout import PaddedCSR, transpose_with_perm
+
+__all__ = ["spmm"]
+
+_KERNELS = ("auto", "simd", "scalar")
+
+# Key: id(W). Value: (topology_version, (nrows, ncols), WT, perm).
+_transpose_cache: dict[int, tuple[int, tuple[int, int], PaddedCSR, torch.Tensor]] = {}
+
+
+def _drop_entry(key: int) -> None:
+    _transpose_cache.pop(key, None)
+
+
+def _cached_transpose(W: PaddedCSR) -> PaddedCSR:
+    """W's transpose, rebuilt only when W's topology changes (ops.py:70-99).
+
+    Hit (same id, topology_version and shape): refresh the live WT values from
+    W.values through perm on the device and return the same WT object.
+    Miss: rebuild on the device and store the entry. Entries are dropped when
+    W is garbage collected, so a recycled id() can never return a stale WT.
+    """
+    key = id(W)
+    cur_version = W.topology_version
+    cur_shape = (int(W.nrows), int(W.ncols))
+    cached = _transpose_cache.get(key)
+    if cached is not None and cached[0] == cur_version and cached[1] == cur_shape:
+        _, _, WT, perm = cached
+        _lib.transpose_refresh(W.values, perm, WT.values)
+        return WT
+    WT, perm = transpose_with_perm(W)
+    if cached is None:
+        weakref.finalize(W, _drop_entry, key)
+    _transpose_cache[key] = (cur_version, cur_shape, WT, perm)
+    return WT
+
+
+def _clear_transpose_cache() -> None:
+    """Testing utility: clear all cache entries. Not part of the public API."""
+    _transpose_cache.clear()
+
+
+def _launch_spmm(W: PaddedCSR, X: torch.Tensor) -> torch.Tensor:
+    Y = torch.empty((W.nrows, X.shape[1]), dtype=torch.float32, device=X.device)
+    _lib.spmm(W._view(), X, Y)
+    return Y
+
+
+def _launch_sddmm(W: PaddedCSR, dY: torch.Tensor, X: torch.Tensor, kernel: str) -> torch.Tensor:
+    dW = torch.empty(W.total_capacity, dtype=torch.float32, device=X.device)
+    order = _lib.SLK_DW_SCALAR if kernel == "scalar" else _lib.SLK_DW_SIMD
+    _lib.sddmm(W._view(), dY, X, dW, order)
+    return dW
+
+
+def _device_f32(t: torch.Tensor) -> torch.Tensor:
+    return t.to(dtype=torch.float32).contiguous()
+
+
+def _check_same_device(W: PaddedCSR, t: torch.Tensor, who: str, name: str) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"{who}: {name} must be on a HIP (ROCm) device (got device={t.device}). "
+            f"sparsecore_amd runs the padded-CSR kernels on the GPU only.")
+    W._require_device(who)
+    if W.device != t.device:
+        raise RuntimeError(f"{who}: W is on {W.device} but {name} is on {t.device}")
+
+
+class _SpMMFunction(torch.autograd.Function):
+    """Autograd bridge for Y = W @ X with W a PaddedCSR (ops.py:127-210).
+
+    The first input, ``W_values``, is the tensor autograd tracks (aliased with
+    ``W.values`` by SparseLinear); the kernels read the weights through W, as
+    the reference does. Backward returns dW aligned with W.values (length
+    total_capacity, padding exactly 0) and dX = Wᵀ·dY. A gradient nobody asked
+    for (``needs_input_grad`` False) is not computed.
+    """
+
+    @staticmethod
+    def forward(ctx, W_values, W, X, kernel):
+        ctx.save_for_backward(W_values, X)
+        ctx.W = W
+        ctx.kernel = kernel
+        if kernel not in _KERNELS:
+            raise ValueError(f"spmm: unknown kernel={kernel!r}. Expected one of: "
+                             f"{sorted(_KERNELS)}.")
+        _check_same_device(W, X, "spmm", "X")
+        return _launch_spmm(W, _device_f32(X))
+
+    @staticmethod
+    def backward(ctx, dY):
+        W_values, X = ctx.saved_tensors
+        W = ctx.W
+        dY_f32 = _device_f32(dY)
+        dW_values = dX = None
+        if ctx.needs_input_grad[0]:
+            dW_values = _launch_sddmm(W, dY_f32, _device_f32(X), ctx.kernel)
+        if ctx.needs_input_grad[2]:
+            WT = _cached_transpose(W)
+            dX = _launch_spmm(WT, dY_f32)
+        return dW_values, None, dX, None
+
+
+def spmm(W: PaddedCSR, X: torch.Tensor, *, kernel: str = "auto") -> torch.Tensor:
+    """Y = W @ X for a PaddedCSR W (M x K) and a dense 2-D X (K x N) on the GPU.
+
+    Same contract as sparselab.ops.spmm (ops.py:217-331) except for the
+    device: X (and W) must live on the HIP device. Any float dtype is
+    converted to float32. If X requires grad the call goes through the
+    autograd Function. ``kernel`` ("auto", "simd", "scalar") selects the dW
+    summation order of the reference kernel of that name; the forward result
+    is the same for all three.
+
+    Raises TypeError (wrong W / X type), RuntimeError (tensor not on the HIP
+    device) and ValueError (X not 2-D, shape mismatch, unknown kernel).
+    """
+    if not isinstance(W, PaddedCSR):
+        raise TypeError(f"spmm: W must be a sparselab.PaddedCSR, got {type(W).__name__}")
+    if not isinstance(X, torch.Tensor):
+        raise TypeError(f"spmm: X must be a torch.Tensor, got {type(X).__name__}")
+    if X.device.type != "cuda":
+        raise RuntimeError(
+            f"spmm: X must be on a HIP (ROCm) device (got device={X.device}). "
+            f"sparsecore_amd runs the padded-CSR kernels on the GPU only.")
+    if X.dim() != 2:
+        raise ValueError(f"spmm: X must be 2-D, got shape={tuple(X.shape)}")
+    if kernel not in _KERNELS:
+        raise ValueError(f"spmm: unknown kernel={kernel!r}. Expected one of: "
+                         f"{sorted(_KERNELS)}.")
+    _check_same_device(W, X, "spmm", "X")
+    X_f32 = _device_f32(X)
+    W_values_t = W.values
+    if X_f32.requires_grad or W_values_t.requires_grad:
+        return _SpMMFunction.apply(W_values_t, W, X_f32, kernel)
+    return _launch_spmm(W, X_f32)

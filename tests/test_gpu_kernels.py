@@ -1,0 +1,236 @@
+"""GPU parity of the HIP kernels against the oracle and the golden fixtures.
+
+Bar: bit-exact. Forward and dX reproduce the reference's fma chains, dW the
+reference's summation orders, and the transpose is pure integer/data movement
+whose layout the PaddedCSR invariants fix uniquely.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import (assert_bits_equal, c1_inputs, csr_arrays_equal, from_oracle, golden_cases,
+                     golden_csr, to_oracle)
+from sparsecore_amd import _lib, layout, ops
+
+pytestmark = pytest.mark.gpu
+
+N_SWEEP = [1, 2, 3, 4, 5, 7, 8, 9, 15, 16, 17, 31, 32, 33, 63, 64, 65, 100, 255, 256, 257, 1000]
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _spmm(W, X):
+    return ops._launch_spmm(W, X)
+
+
+def _sddmm(W, dY, X, kernel="simd"):
+    return ops._launch_sddmm(W, dY, X, kernel)
+
+
+# ───────────────────────── golden fixtures ─────────────────────────────
+
+@pytest.mark.parametrize("name", sorted(golden_cases()))
+def test_golden_fixture_bit_exact(dev, name):
+    print(f"[golden] {name}", flush=True)
+    case = golden_cases()[name]
+    c = golden_csr(case)
+    W = from_oracle(c, dev)
+    X, dY = _t(case["X"], dev), _t(case["dY"], dev)
+    assert_bits_equal(_spmm(W, X).cpu().numpy(), case["Y"], "Y")
+    assert_bits_equal(_sddmm(W, dY, X, "simd").cpu().numpy(), case["dW"], "dW")
+    assert_bits_equal(_sddmm(W, dY, X, "scalar").cpu().numpy(), case["dW_scalar"], "dW_scalar")
+    WT = ops._cached_transpose(W)
+    assert_bits_equal(_spmm(WT, dY).cpu().numpy(), case["dX"], "dX")
+
+
+def test_c1_config_matches_reference_digests(dev):
+    import gen
+
+    print("[golden] c1 512x784 N=256", flush=True)
+    meta, c, X_np, dY_np = c1_inputs()
+    W = from_oracle(c, dev)
+    X, dY = _t(X_np, dev), _t(dY_np, dev)
+    WT, _ = layout.transpose_with_perm(W)
+    outs = {"Y": _spmm(W, X), "dW": _sddmm(W, dY, X, "simd"),
+            "dW_scalar": _sddmm(W, dY, X, "scalar"), "dX": _spmm(WT, dY)}
+    for k, v in outs.items():
+        got = v.cpu().numpy()
+        s = meta["samples"][k]
+        flat = got.reshape(-1)
+        assert flat[s["index"]].view(np.uint32).tolist() == s["value_bits"], k
+        assert gen.digest(got) == meta["outputs_sha256"][k], k
+
+
+# ───────────────────────── forward / dW sweeps ─────────────────────────
+
+def _case(M, K, N, per_row, seed, pr=0.2):
+    c = oracle.uniform_rows(M, K, per_row, seed=seed, sigma=1.0, padding_ratio=pr)
+    rng = np.random.default_rng(seed + 1)
+    X = rng.standard_normal((K, N)).astype(np.float32)
+    dY = rng.standard_normal((M, N)).astype(np.float32)
+    return c, X, dY
+
+
+@pytest.mark.parametrize("N", N_SWEEP)
+def test_spmm_and_sddmm_bit_exact_over_N(dev, N):
+    print(f"[sweep] N={N}", flush=True)
+    c, X_np, dY_np = _case(48, 70, N, 11, seed=N)
+    W = from_oracle(c, dev)
+    X, dY = _t(X_np, dev), _t(dY_np, dev)
+    assert_bits_equal(_spmm(W, X).cpu().numpy(), oracle.spmm(c, X_np), "Y")
+    assert_bits_equal(_sddmm(W, dY, X).cpu().numpy(), oracle.sddmm(c, dY_np, X_np), "dW")
+    assert_bits_equal(_sddmm(W, dY, X, "scalar").cpu().numpy(),
+                      oracle.sddmm(c, dY_np, X_np, "scalar"), "dW scalar")
+
+
+@pytest.mark.parametrize("N", [8, 64, 256])
+def test_unaligned_inputs_take_the_scalar_load_path(dev, N):
+    """X / dY starting 4 bytes past a 16-byte boundary (views with an offset)."""
+    c, X_np, dY_np = _case(33, 41, N, 7, seed=5)
+    W = from_oracle(c, dev)
+    Xbuf = torch.empty(X_np.size + 1, device=dev)
+    Xbuf[1:] = _t(X_np.reshape(-1), dev)
+    dYbuf = torch.empty(dY_np.size + 1, device=dev)
+    dYbuf[1:] = _t(dY_np.reshape(-1), dev)
+    X = Xbuf[1:].view(X_np.shape)
+    dY = dYbuf[1:].view(dY_np.shape)
+    assert X.data_ptr() % 16 != 0
+    assert_bits_equal(_spmm(W, X).cpu().numpy(), oracle.spmm(c, X_np), "Y")
+    assert_bits_equal(_sddmm(W, dY, X).cpu().numpy(), oracle.sddmm(c, dY_np, X_np), "dW")
+
+
+@pytest.mark.parametrize("lanes", [1, 4, 16, 64])
+def test_spmm_every_tile_width(dev, monkeypatch, lanes):
+    monkeypatch.setenv("SLK_SPMM_LANES", str(lanes))
+    c, X_np, _ = _case(40, 50, 300, 9, seed=lanes)
+    W = from_oracle(c, dev)
+    assert_bits_equal(_spmm(W, _t(X_np, dev)).cpu().numpy(), oracle.spmm(c, X_np), "Y")
+
+
+@pytest.mark.parametrize("pr", [0.0, 0.2, 0.5, 1.0])
+def test_padding_slots_of_dW_are_exactly_zero(dev, pr):
+    c, X_np, dY_np = _case(20, 30, 9, 6, seed=11, pr=pr)
+    W = from_oracle(c, dev)
+    dW = _sddmm(W, _t(dY_np, dev), _t(X_np, dev)).cpu().numpy()
+    pads = oracle.padding_slots(c)
+    assert np.all(dW[pads].view(np.uint32) == 0)  # +0.0 exactly
+
+
+def test_skewed_rows_bit_exact(dev):
+    c = oracle.zipf_rows(256, 512, 0.05, 1.1, seed=3, sigma=0.5)
+    rng = np.random.default_rng(3)
+    X_np = rng.standard_normal((512, 96)).astype(np.float32)
+    dY_np = rng.standard_normal((256, 96)).astype(np.float32)
+    W = from_oracle(c, dev)
+    X, dY = _t(X_np, dev), _t(dY_np, dev)
+    assert int(c.row_nnz.max()) == 512  # a fully dense row
+    assert_bits_equal(_spmm(W, X).cpu().numpy(), oracle.spmm(c, X_np), "Y")
+    assert_bits_equal(_sddmm(W, dY, X).cpu().numpy(), oracle.sddmm(c, dY_np, X_np), "dW")
+    WT, perm = layout.transpose_with_perm(W)
+    WT_o, perm_o = oracle.transpose_with_perm(c)
+    csr_arrays_equal(to_oracle(WT), WT_o, "WT")
+    assert_bits_equal(perm.cpu().numpy(), perm_o, "perm")
+
+
+def test_empty_shapes(dev):
+    empty = layout.PaddedCSR(8, 16, device=dev)
+    Y = _spmm(empty, torch.randn(16, 4, device=dev))
+    assert Y.shape == (8, 4) and torch.count_nonzero(Y).item() == 0
+    dW = _sddmm(empty, torch.randn(8, 4, device=dev), torch.randn(16, 4, device=dev))
+    assert dW.shape == (0,)
+    zero_rows = layout.PaddedCSR(0, 5, device=dev)
+    assert _spmm(zero_rows, torch.randn(5, 3, device=dev)).shape == (0, 3)
+    c, X_np, _ = _case(6, 9, 3, 2, seed=1)
+    W = from_oracle(c, dev)
+    assert _spmm(W, _t(X_np[:, :0], dev)).shape == (6, 0)
+    zeros = from_oracle(oracle.from_dense(np.zeros((5, 7), np.float32)), dev)
+    assert torch.count_nonzero(_spmm(zeros, torch.randn(7, 3, device=dev))).item() == 0
+    no_cols = layout.PaddedCSR(4, 0, device=dev)
+    Y = _spmm(no_cols, torch.empty(0, 6, device=dev))
+    assert Y.shape == (4, 6) and torch.count_nonzero(Y).item() == 0
+
+
+def test_shape_errors_raise_value_error(dev):
+    c, X_np, dY_np = _case(8, 16, 4, 3, seed=2)
+    W = from_oracle(c, dev)
+    with pytest.raises(ValueError, match="shape mismatch"):
+        _spmm(W, torch.randn(17, 4, device=dev))
+    with pytest.raises(ValueError, match="dY.shape"):
+        _sddmm(W, torch.randn(9, 4, device=dev), _t(X_np, dev))
+    with pytest.raises(ValueError, match="X.shape"):
+        _sddmm(W, _t(dY_np, dev), torch.randn(15, 4, device=dev))
+
+
+def test_repeated_calls_are_bit_identical(dev):
+    c, X_np, dY_np = _case(64, 128, 96, 20, seed=9)
+    W = from_oracle(c, dev)
+    X, dY = _t(X_np, dev), _t(dY_np, dev)
+    y0, g0 = _spmm(W, X), _sddmm(W, dY, X)
+    t0 = layout.transpose_with_perm(W)
+    for _ in range(3):
+        assert torch.equal(_spmm(W, X), y0)
+        assert torch.equal(_sddmm(W, dY, X), g0)
+        t = layout.transpose_with_perm(W)
+        assert torch.equal(t[1], t0[1]) and torch.equal(t[0].col_indices, t0[0].col_indices)
+
+
+# ─────────────────────────── transpose ─────────────────────────────────
+
+@pytest.mark.parametrize("M,K,sparsity,pr", [
+    (3, 4, 0.5, 0.2), (8, 8, 0.0, 0.2), (8, 8, 0.9, 0.2), (16, 32, 0.8, 0.0), (32, 16, 0.8, 1.0),
+    (1, 1, 0.0, 0.2), (1, 16, 0.5, 0.2), (16, 1, 0.5, 0.2), (64, 64, 0.99, 0.2),
+    (512, 784, 0.9, 0.2), (1536, 384, 0.9, 0.2), (300, 7, 0.3, 0.3)])
+def test_transpose_bit_exact(dev, M, K, sparsity, pr):
+    print(f"[transpose] {M}x{K} s={sparsity} pr={pr}", flush=True)
+    c = oracle.bernoulli(M, K, sparsity, seed=M + K)
+    W = from_oracle(c, dev)
+    WT, perm = layout.transpose_with_perm(W, padding_ratio=pr)
+    WT_o, perm_o = oracle.transpose_with_perm(c, pr)
+    csr_arrays_equal(to_oracle(WT), WT_o, "WT")
+    assert_bits_equal(perm.cpu().numpy(), perm_o, "perm")
+    assert WT.nnz == c.nnz and WT.shape == (K, M)
+    WT.assert_invariants()
+
+
+def test_transpose_wide_matrix_uses_column_chunks(dev):
+    """ncols > 16384 exercises the multi-pass (column-chunked) LDS counters."""
+    c = oracle.uniform_rows(40, 40000, 300, seed=4)
+    W = from_oracle(c, dev)
+    WT, perm = layout.transpose_with_perm(W)
+    WT_o, perm_o = oracle.transpose_with_perm(c)
+    csr_arrays_equal(to_oracle(WT), WT_o, "WT")
+    assert_bits_equal(perm.cpu().numpy(), perm_o, "perm")
+
+
+def test_transpose_of_empty_and_empty_ctor(dev):
+    W = layout.PaddedCSR(5, 8, device=dev)
+    WT = W.transpose()
+    assert WT.shape == (8, 5) and WT.nnz == 0
+    assert WT.row_capacity.tolist() == [1] * 8
+    WT.assert_invariants()
+    W0 = layout.PaddedCSR(0, 3, device=dev)
+    assert W0.transpose().row_capacity.tolist() == [1, 1, 1]
+
+
+def test_transpose_refresh_matches_oracle(dev):
+    c = oracle.bernoulli(64, 48, 0.8, seed=6)
+    W = from_oracle(c, dev)
+    WT, perm = layout.transpose_with_perm(W)
+    with torch.no_grad():
+        W.values.mul_(-3.0).add_(0.25)
+    before = WT.values.clone()
+    _lib.transpose_refresh(W.values, perm, WT.values)
+    expect = oracle.refresh(before.cpu().numpy(), W.values.cpu().numpy(), perm.cpu().numpy())
+    assert_bits_equal(WT.values.cpu().numpy(), expect, "refreshed values")
+
+
+def test_transpose_negative_padding_ratio(dev):
+    W = from_oracle(oracle.bernoulli(4, 4, 0.5, seed=1), dev)
+    with pytest.raises(ValueError, match="padding_ratio"):
+        W.transpose(padding_ratio=-0.1)
