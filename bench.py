@@ -1,0 +1,556 @@
+#!/usr/bin/env python3
+"""Benchmark of the padded-CSR training hot path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--workload c2] [--no-graph] [--no-cpu]
+
+Prints ONE JSON line (rank 0). Workloads (BASELINE.json `configs`):
+
+  c2  (default, configs[1]) 2-layer MLP 784->512->10, both SparseLinear at 90%
+      sparsity, fp32, ReLU, cross-entropy, batch 256 of U[0,1) inputs with
+      labels U{0..9}; one step = forward, dX/dW backward and an SGD update
+      (lr 0.01) of the live slots and biases. value = samples (tokens) / s.
+  c1  (configs[0]) one 512x784 layer, 78 live columns per row, N=256; one
+      step = forward Y, dW and dX (cached transpose refresh + SpMM on WT).
+      value = algorithmic GB/s of fwd+dX+dW.
+
+The timed region replays the step captured in a HIP graph (--no-graph: eager
+launches); inputs and weights are resident in HBM before it starts. The
+dominant kernel's average duration is then measured with HIP events around
+back-to-back launches of that kernel on the step's own tensors (queued
+behind a GPU sleep so no host gap enters the interval); `roofline.achieved`
+is its algorithmic bytes per launch divided by that duration.
+
+The CPU baseline runs the same step with the reference's own kernels
+(oracle/_ref: csrc/kernels/*.cpp compiled at the reference flags, OpenMP
+threads = OMP_NUM_THREADS) and torch CPU ops for the dense parts, timed over
+a bounded sample on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "SpMM fwd+dX+dW achieved HBM GB/s & effective GFLOP/s; train-step tokens/s"
+HBM_PEAK_GBS = 8000.0
+FP32_VALU_PEAK_TFLOPS = 157.3
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2"])
+    ap.add_argument("--no-graph", action="store_true", help="time eager launches")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="approximate CPU-baseline budget")
+    ap.add_argument("--seed", type=int, default=0)
+    return ap.parse_args()
+
+
+# ───────────────────────────── byte / flop model ─────────────────────────────
+# Algorithmic (compulsory) traffic per launch: f32/i32 = 4 B, i64 = 8 B.
+
+def bytes_fwd(nnz, M, K, N):  # values+cols, row_start+row_nnz, X read, Y written
+    return 8 * nnz + 8 * M + 4 * K * N + 4 * M * N
+
+
+def bytes_dw(nnz, cap, M, K, N):  # cols, row arrays, dY + X read, dW (all slots) written
+    return 4 * nnz + 8 * M + 4 * M * N + 4 * K * N + 4 * cap
+
+
+def bytes_refresh(nnz, capT):  # perm (i64) read, gathered values, WT values written
+    return 8 * capT + 4 * nnz + 4 * capT
+
+
+def flops(nnz, N):
+    return 2 * nnz * N
+
+
+# ───────────────────────────── timing helpers ────────────────────────────────
+
+def kernel_avg_ms(fn, reps: int = 200) -> float:
+    """Average device time of `fn` (one kernel launch) over back-to-back launches."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(int(2e7))  # keeps the GPU busy while the launches queue up
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def stage(msg: str) -> None:
+    """Progress marker on stderr, flushed, so a failing run names its stage."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def timed_loop(step, steps: int):
+    import torch
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
+
+
+def capture(step_body, warm_iters: int = 3):
+    """Capture step_body() into a HIP graph after warming it on a side stream."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(warm_iters):
+            step_body()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = step_body()
+    return g, out
+
+
+# ───────────────────────────── workload C2 ───────────────────────────────────
+
+class C2:
+    name = "c2"
+    desc = ("2-layer MLP 784->512->10, SparseLinear 90%/90%, fp32, ReLU, cross-entropy, "
+            "batch 256, SGD lr 0.01")
+    batch = 256
+
+    def __init__(self, dev, seed):
+        import torch
+        import torch.nn as nn
+
+        import sparsecore_amd as slk
+
+        torch.manual_seed(seed)
+        self.l1 = slk.SparseLinear(784, 512, sparsity=0.9)
+        self.l2 = slk.SparseLinear(512, 10, sparsity=0.9)
+        self.model = nn.Sequential(self.l1, nn.ReLU(), self.l2).to(dev)
+        g = torch.Generator().manual_seed(seed + 1)
+        self.x = torch.rand(self.batch, 784, generator=g).to(dev)
+        self.labels = torch.randint(0, 10, (self.batch,), generator=g).to(dev)
+        self.opt = torch.optim.SGD(self.model.parameters(), lr=0.01)
+        self.dev = dev
+
+    def body(self):
+        import torch.nn.functional as F
+
+        self.opt.zero_grad(set_to_none=True)
+        loss = F.cross_entropy(self.model(self.x), self.labels)
+        loss.backward()
+        self.opt.step()
+        # detached: the caller must not keep this step's autograd graph (and its
+        # AccumulateGrad nodes, bound to the stream they ran on) alive
+        return loss.detach()
+
+    def params(self):
+        return [p for p in self.model.parameters()]
+
+    def tokens_per_step(self):
+        return self.batch
+
+    def kernels(self):
+        """(name, launch fn, bytes, flops) of the HIP kernels one step runs."""
+        import torch
+
+        from sparsecore_amd import _lib, ops
+
+        out = []
+        N = self.batch
+        x_col = self.x.t().contiguous()
+        h = torch.relu(self.l1(self.x)).detach()
+        h_col = h.t().contiguous()
+        for tag, layer, X in (("l1", self.l1, x_col), ("l2", self.l2, h_col)):
+            W = layer._csr
+            M, K = W.nrows, W.ncols
+            Y = torch.empty(M, N, device=self.dev)
+            dY = torch.randn(M, N, device=self.dev)
+            dW = torch.empty(W.total_capacity, device=self.dev)
+            view = W._view()
+            out.append((f"spmm_fwd[{tag} {M}x{K}]",
+                        lambda view=view, X=X, Y=Y: _lib.spmm(view, X, Y),
+                        bytes_fwd(W.nnz, M, K, N), flops(W.nnz, N)))
+            out.append((f"sddmm_dw[{tag} {M}x{K}]",
+                        lambda view=view, dY=dY, X=X, dW=dW: _lib.sddmm(view, dY, X, dW,
+                                                                       _lib.SLK_DW_SIMD),
+                        bytes_dw(W.nnz, W.total_capacity, M, K, N), flops(W.nnz, N)))
+            if tag == "l2":  # layer 1's input needs no gradient, so no dX there
+                WT = ops._cached_transpose(W)
+                perm = ops._transpose_cache[id(W)][3]
+                dX = torch.empty(K, N, device=self.dev)
+                vT = WT._view()
+                out.append((f"spmm_dx[{tag} {K}x{M}]",
+                            lambda vT=vT, dY=dY, dX=dX: _lib.spmm(vT, dY, dX),
+                            bytes_fwd(WT.nnz, K, M, N), flops(W.nnz, N)))
+                out.append((f"transpose_refresh[{tag}]",
+                            lambda W=W, perm=perm, WT=WT: _lib.transpose_refresh(
+                                W.values, perm, WT.values),
+                            bytes_refresh(W.nnz, WT.total_capacity), 0))
+        return out
+
+    def spmm_layer(self):
+        return self.l1._csr
+
+
+# ───────────────────────────── workload C1 ───────────────────────────────────
+
+class C1:
+    name = "c1"
+    desc = "one 512x784 layer, 78 live/row (90%), values N(0,0.02), pr 0.2, N=256"
+
+    def __init__(self, dev, seed):
+        import numpy as np
+        import torch
+
+        import oracle  # noqa: F401  (synthetic topology generator only)
+        from sparsecore_amd import PaddedCSR
+
+        M, K, N = 512, 784, 256
+        rng = np.random.default_rng(seed)
+        cols = [np.sort(rng.choice(K, 78, replace=False)).astype(np.int32) for _ in range(M)]
+        vals = [rng.normal(0, 0.02, 78).astype(np.float32) for _ in range(M)]
+        crow = np.concatenate([[0], np.cumsum([78] * M)])
+        W_dense = torch.zeros(M, K)
+        for i in range(M):
+            W_dense[i, torch.from_numpy(cols[i]).long()] = torch.from_numpy(vals[i])
+        del crow
+        self.W = PaddedCSR.from_dense(W_dense, padding_ratio=0.2).to(dev)
+        self.X = torch.from_numpy(rng.standard_normal((K, N)).astype(np.float32)).to(dev)
+        self.dY = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).to(dev)
+        self.M, self.K, self.N = M, K, N
+        self.dev = dev
+        from sparsecore_amd import ops
+
+        ops._cached_transpose(self.W)  # build once (topology fixed)
+
+    def body(self):
+        from sparsecore_amd import ops
+
+        Y = ops._launch_spmm(self.W, self.X)
+        dW = ops._launch_sddmm(self.W, self.dY, self.X, "simd")
+        WT = ops._cached_transpose(self.W)
+        dX = ops._launch_spmm(WT, self.dY)
+        return Y, dW, dX
+
+    def params(self):
+        return []
+
+    def step_bytes(self):
+        W = self.W
+        WT = __import__("sparsecore_amd").ops._cached_transpose(W)
+        M, K, N = self.M, self.K, self.N
+        return (bytes_fwd(W.nnz, M, K, N) + bytes_dw(W.nnz, W.total_capacity, M, K, N)
+                + bytes_refresh(W.nnz, WT.total_capacity) + bytes_fwd(W.nnz, K, M, N))
+
+    def step_flops(self):
+        return 3 * flops(self.W.nnz, self.N)
+
+    def kernels(self):
+        import torch
+
+        from sparsecore_amd import _lib, ops
+
+        W = self.W
+        M, K, N = self.M, self.K, self.N
+        WT = ops._cached_transpose(W)
+        perm = ops._transpose_cache[id(W)][3]
+        Y = torch.empty(M, N, device=self.dev)
+        dW = torch.empty(W.total_capacity, device=self.dev)
+        dX = torch.empty(K, N, device=self.dev)
+        v, vT = W._view(), WT._view()
+        return [
+            ("spmm_fwd", lambda: _lib.spmm(v, self.X, Y), bytes_fwd(W.nnz, M, K, N),
+             flops(W.nnz, N)),
+            ("sddmm_dw", lambda: _lib.sddmm(v, self.dY, self.X, dW, _lib.SLK_DW_SIMD),
+             bytes_dw(W.nnz, W.total_capacity, M, K, N), flops(W.nnz, N)),
+            ("transpose_refresh", lambda: _lib.transpose_refresh(W.values, perm, WT.values),
+             bytes_refresh(W.nnz, WT.total_capacity), 0),
+            ("spmm_dx", lambda: _lib.spmm(vT, self.dY, dX), bytes_fwd(W.nnz, K, M, N),
+             flops(W.nnz, N)),
+        ]
+
+
+# ───────────────────────────── CPU baseline ──────────────────────────────────
+
+def cpu_baseline(work, seconds: float):
+    """The same step on this host's cores with the reference's own kernels."""
+    import numpy as np
+    import torch
+
+    import oracle
+
+    kind = "reference" if oracle.ref_available() else "port"
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+
+    class HostLayer:
+        """Reference-path layer: RefCsr values aliased with a torch Parameter."""
+
+        def __init__(self, csr):
+            self.c = oracle.Csr(csr.nrows, csr.ncols, csr.values.detach().cpu().numpy(),
+                                csr.col_indices.cpu().numpy(), csr.row_start.cpu().numpy(),
+                                csr.row_nnz.cpu().numpy(), csr.row_capacity.cpu().numpy())
+            if kind == "reference":
+                self.r = oracle.RefCsr(self.c)
+                self.values = torch.from_numpy(self.r.values_view())
+                WT, perm = oracle.transpose_with_perm(self.c)
+                self.rt = oracle.RefCsr(WT)
+                self.wt_values = self.rt.values_view()
+                self.perm = perm
+                self.live = perm >= 0
+            else:
+                self.values = torch.from_numpy(self.c.values)
+                self.WT, self.perm = oracle.transpose_with_perm(self.c)
+                self.live = self.perm >= 0
+
+        def fwd(self, X):
+            if kind == "reference":
+                Y = np.empty((self.c.nrows, X.shape[1]), np.float32)
+                self.r.spmm_into(X, Y)
+                return Y
+            return oracle.spmm(self.c, X)
+
+        def dw(self, dY, X):
+            if kind == "reference":
+                dW = np.empty(self.c.total_capacity, np.float32)
+                self.r.sddmm_into(dY, X, dW)
+                return dW
+            return oracle.sddmm(self.c, dY, X)
+
+        def dx(self, dY):
+            # cache hit: refresh WT values through perm (ops.py:83-94), then SpMM
+            if kind == "reference":
+                self.wt_values[self.live] = self.values.numpy()[self.perm[self.live]]
+                out = np.empty((self.rt.p.nrows, dY.shape[1]), np.float32)
+                self.rt.spmm_into(dY, out)
+                return out
+            self.WT.values[self.live] = self.values.numpy()[self.perm[self.live]]
+            return oracle.spmm(self.WT, dY)
+
+    class RefFn(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, values, layer, X):
+            ctx.layer = layer
+            ctx.save_for_backward(X)
+            return torch.from_numpy(layer.fwd(X.detach().contiguous().numpy()))
+
+        @staticmethod
+        def backward(ctx, dY):
+            (X,) = ctx.saved_tensors
+            dYc = dY.detach().contiguous().numpy()
+            layer = ctx.layer
+            dW = torch.from_numpy(layer.dw(dYc, X.detach().numpy()))
+            dX = torch.from_numpy(layer.dx(dYc))  # the reference always computes dX
+            return dW, None, dX
+
+    if isinstance(work, C2):
+        layers = []
+        for gl in (work.l1, work.l2):
+            hl = HostLayer(gl._csr)
+            w = torch.nn.Parameter(hl.values)
+            b = torch.nn.Parameter(gl.bias.detach().cpu().clone())
+            layers.append((hl, w, b))
+        x = work.x.cpu()
+        labels = work.labels.cpu()
+        opt = torch.optim.SGD([p for _, w, b in layers for p in (w, b)], lr=0.01)
+
+        def step():
+            opt.zero_grad(set_to_none=True)
+            h = x
+            for idx, (hl, w, b) in enumerate(layers):
+                h = RefFn.apply(w, hl, h.t().contiguous()).t() + b
+                if idx == 0:
+                    h = torch.relu(h)
+            loss = torch.nn.functional.cross_entropy(h, labels)
+            loss.backward()
+            opt.step()
+
+        unit_per_step = work.tokens_per_step()
+        unit = "tokens/s"
+        sample = "C2 train steps (MLP 784->512->10, batch 256)"
+    else:
+        hl = HostLayer(work.W)
+        X = work.X.cpu().numpy()
+        dY = work.dY.cpu().numpy()
+
+        def step():
+            hl.fwd(X)
+            hl.dw(dY, X)
+            hl.dx(dY)
+
+        unit_per_step = work.step_bytes() / 1e9
+        unit = "GB/s"
+        sample = "C1 fwd+dW+dX steps (512x784, N=256)"
+
+    for _ in range(3):
+        step()
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        step()
+        n += 1
+        if time.perf_counter() - t0 > seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": unit_per_step * n / dt, "unit": unit, "cores": threads, "kind": kind,
+            "sample": f"{n} {sample} in {dt:.1f} s, OpenMP/torch threads={threads}, "
+                      f"ms/step={1e3 * dt / n:.3f}"}
+
+
+# ───────────────────────────── main ──────────────────────────────────────────
+
+def main():
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              f"the multi-GPU sharding is a design note, not a measured path.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import sparsecore_amd
+
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs a HIP device")
+    if not sparsecore_amd.native_available():
+        sys.exit("bench.py: libsparsecore_amd.so is not built (python -m sparsecore_amd.build)")
+    dev = torch.device("cuda:0")
+    stage(f"workload {args.workload}: building")
+    work = (C2 if args.workload == "c2" else C1)(dev, args.seed)
+
+    stage("eager warmup")
+    for _ in range(max(1, args.warmup)):
+        work.body()
+    torch.cuda.synchronize()
+
+    use_graph = not args.no_graph
+    graph_ok = False
+    if use_graph:
+        params = work.params()
+        snap = [p.detach().clone() for p in params]
+        stage("eager reference steps for the graph check")
+        eager_flat = []
+        for _ in range(3):
+            o = work.body()
+            eager_flat += [t.detach().clone() for t in (o if isinstance(o, tuple) else (o,))]
+            del o
+        eager_params = [p.detach().clone() for p in params]
+        with torch.no_grad():
+            for p, s in zip(params, snap):
+                p.copy_(s)
+        torch.cuda.synchronize()
+        stage("graph capture")
+        g, gout = capture(work.body)
+        stage("graph replay check")
+        with torch.no_grad():
+            for p, s in zip(params, snap):
+                p.copy_(s)
+        graph_ok = True
+        for i in range(3):
+            g.replay()
+            torch.cuda.synchronize()
+            got = [t for t in (gout if isinstance(gout, tuple) else (gout,))]
+            per = len(got)
+            want = eager_flat[i * per:(i + 1) * per]
+            if not all(torch.equal(a, b) for a, b in zip(got, want)):
+                graph_ok = False
+        if not all(torch.equal(p, e) for p, e in zip(params, eager_params)):
+            graph_ok = False
+        if not graph_ok:
+            print("bench.py: graph replay differs from eager; timing eager launches",
+                  file=sys.stderr)
+        step = g.replay if graph_ok else work.body
+        for _ in range(args.warmup):
+            step()
+    else:
+        step = work.body
+
+    stage(f"timed region: {args.steps} steps (graph={graph_ok if use_graph else False})")
+    elapsed = timed_loop(step, args.steps)
+    ms_per_step = 1e3 * elapsed / args.steps
+
+    kern = []
+    for name, fn, nbytes, nflops in work.kernels():
+        stage(f"kernel timing: {name}")
+        ms = kernel_avg_ms(fn)
+        kern.append({"kernel": name, "avg_us": round(ms * 1e3, 3), "bytes": nbytes,
+                     "flops": nflops, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)})
+    dom = max(kern, key=lambda k: k["avg_us"])
+    achieved = dom["bytes"] / (dom["avg_us"] * 1e-6) / 1e9
+    traffic = None
+    tf = ROOT / "profiles" / f"traffic_{args.workload}.json"
+    if tf.exists():
+        traffic = json.loads(tf.read_text()).get(dom["kernel"].split("[")[0])
+
+    if isinstance(work, C2):
+        value = work.tokens_per_step() * args.steps / elapsed
+        unit = "tokens/s"
+        W = work.spmm_layer()
+        l1 = [k for k in kern if "[l1" in k["kernel"]]
+        spmm_us = sum(k["avg_us"] for k in kern)
+        path = {"spmm_kernels_us_per_step": round(spmm_us, 2),
+                "layer1_fwd_dw_GBps": round(sum(k["bytes"] for k in l1) /
+                                            (sum(k["avg_us"] for k in l1) * 1e-6) / 1e9, 1),
+                "layer1_fwd_dw_GFLOPs": round(sum(k["flops"] for k in l1) /
+                                              (sum(k["avg_us"] for k in l1) * 1e-6) / 1e9, 1),
+                "layer1_nnz": W.nnz}
+        config = {"workload": "c2: " + work.desc, "global_batch": work.batch,
+                  "graph": graph_ok}
+    else:
+        value = work.step_bytes() * args.steps / elapsed / 1e9
+        unit = "GB/s"
+        path = {"GFLOP/s": round(work.step_flops() * args.steps / elapsed / 1e9, 1),
+                "step_bytes": work.step_bytes(), "nnz": work.W.nnz}
+        config = {"workload": "c1: " + work.desc, "graph": graph_ok}
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": config,
+        "path": path,
+        "kernels": kern,
+        "roofline": {"bound": "hbm", "kernel": dom["kernel"], "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        stage("cpu baseline")
+        try:
+            line["cpu_baseline"] = cpu_baseline(work, args.cpu_seconds)
+        except Exception as e:  # the baseline is reported, never required
+            line["cpu_baseline"] = {"error": repr(e)}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -345,6 +345,8 @@ def _ref_lib():
         lib.ref_rewrite_row.argtypes = [ctypes.c_void_p, _i64, _i64, _i32p, _f32p]
         lib.ref_csr_arrays.argtypes = [ctypes.c_void_p, _f32p, _i32p, _i32p,
                                        ctypes.POINTER(ctypes.c_int64)]
+        lib.ref_csr_values_ptr.restype = _f32p
+        lib.ref_csr_values_ptr.argtypes = [ctypes.c_void_p]
         _ref = lib
     return _ref
 
@@ -398,6 +400,23 @@ class RefCsr:
         vals = np.ascontiguousarray(vals, dtype=np.float32)
         self._check(_ref_lib().ref_rewrite_row(self.h, row, cols.shape[0], _ptr(cols, _i32p),
                                                _ptr(vals, _f32p)))
+
+    def values_view(self) -> np.ndarray:
+        """Writable numpy view of the reference object's own values buffer."""
+        ptr = _ref_lib().ref_csr_values_ptr(self.h)
+        return np.ctypeslib.as_array(ptr, shape=(self.p.total_capacity,))
+
+    def spmm_into(self, X: np.ndarray, Y: np.ndarray, kernel: str = "simd") -> None:
+        K, N = X.shape
+        fn = _ref_lib().ref_spmm_simd if kernel != "scalar" else _ref_lib().ref_spmm_scalar
+        self._check(fn(self.h, _ptr(X, _f32p), K, N, _ptr(Y, _f32p)))
+
+    def sddmm_into(self, dY: np.ndarray, X: np.ndarray, dW: np.ndarray,
+                   kernel: str = "simd") -> None:
+        K, N = X.shape
+        fn = (_ref_lib().ref_spmm_grad_w_simd if kernel != "scalar"
+              else _ref_lib().ref_spmm_grad_w)
+        self._check(fn(self.h, _ptr(dY, _f32p), N, _ptr(X, _f32p), K, _ptr(dW, _f32p)))
 
     def arrays(self):
         p = self.p

@@ -106,6 +106,12 @@ REF_API int ref_rewrite_row(void* p, int64_t row, int64_t n, const int32_t* cols
     });
 }
 
+// Address of p's own values buffer (what the reference exposes as the
+// writable zero-copy `values` view, csrc/bindings.cpp:663-666).
+REF_API float* ref_csr_values_ptr(void* p) {
+    return static_cast<sparselab::PaddedCSR*>(p)->values.data();
+}
+
 // Copies the current arrays of p out (after rewrite_row).
 REF_API void ref_csr_arrays(void* p, float* values, int32_t* col, int32_t* row_nnz,
                             int64_t* topology_version) {

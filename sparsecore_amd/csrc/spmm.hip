@@ -4,16 +4,25 @@
 // Y is zeroed, then for every row i and live slot s (in slot order) the
 // write-through update  y[i,j] = fma(v_s, X[c_s, j], y[i,j])  is applied to
 // all j. Every output element is therefore an ordered fused multiply-add
-// chain starting at +0.0. This kernel evaluates exactly that chain per
+// chain starting at +0.0. Both kernels here evaluate exactly that chain per
 // element, so results are bit-identical to the reference CPU kernels.
 //
-// Work decomposition: one "item" is (row, column tile). A tile is L lanes
-// of VEC consecutive columns; a 64-wide wave holds 64/L items. Items are
-// ordered tile-major (item = tile * M + row) so that waves resident at the
-// same time gather from the same K x (L*VEC) slab of X, which stays in L2.
-// With L = 64 the item is wave-uniform, the row metadata and the (col, value)
-// stream are read through the scalar cache, and each slot costs one
-// coalesced VEC*64-float gather of an X row segment.
+// Work decomposition: one "item" is (row, column tile). Items are ordered
+// tile-major (item = tile * M + row) so that waves resident at the same time
+// gather from the same K x tile slab of X, which stays in L2.
+//
+//  * spmm_wave_kernel — one item per wave (64 lanes x VEC columns). The
+//    row's (col, value) stream is fetched 64 slots at a time with one
+//    coalesced load into lane registers and broadcast slot by slot with
+//    readlane, so the X gathers use a scalar base address. Gathers are
+//    issued U slots at a time into two register buffers that alternate
+//    (the next batch is in flight while the current one is consumed), so a
+//    wave keeps 2U gathers outstanding instead of waiting once per slot.
+//  * spmm_group_kernel — several items per wave (L < 64 lanes each) for
+//    narrow X (N < 64): each lane streams its row's metadata itself.
+//
+// VEC (floats per lane) is chosen so that small problems still launch
+// enough waves to hide gather latency; large problems use 16-byte gathers.
 #include "common.hpp"
 
 #include <cstdlib>
@@ -22,7 +31,6 @@ namespace slk {
 namespace {
 
 constexpr int kSpmmBlock = 256;  // 4 waves per workgroup
-constexpr int kUnroll = 8;       // slots whose X gathers are in flight together
 
 template <int VEC>
 struct VecIO;
@@ -41,6 +49,19 @@ struct VecIO<4> {
 };
 
 template <>
+struct VecIO<2> {
+    typedef float T __attribute__((ext_vector_type(2)));
+    static __device__ __forceinline__ T load(const float* p) {
+        return *reinterpret_cast<const T*>(p);
+    }
+    static __device__ __forceinline__ void store(float* p, const float* a) {
+        T v = {a[0], a[1]};
+        *reinterpret_cast<T*>(p) = v;
+    }
+    static __device__ __forceinline__ float get(const T& v, int k) { return v[k]; }
+};
+
+template <>
 struct VecIO<1> {
     typedef float T;
     static __device__ __forceinline__ T load(const float* p) { return *p; }
@@ -48,21 +69,123 @@ struct VecIO<1> {
     static __device__ __forceinline__ float get(const T& v, int) { return v; }
 };
 
+__device__ __forceinline__ int32_t bcast_i(int32_t v, int32_t lane) {
+    return __builtin_amdgcn_readlane(v, lane);
+}
+__device__ __forceinline__ float bcast_f(float v, int32_t lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Gathers X rows of slots [k, k + U) of the staged metadata chunk (n = slots
+// of the chunk). A full batch is unguarded; the chunk's last batch checks k.
+// The X row base is wave-uniform (scalar) and the lane offset a 32-bit
+// vector offset, so each gather is one load with no per-slot vector math.
+template <int VEC>
+__device__ __forceinline__ typename VecIO<VEC>::T gather(const float* __restrict__ X, int32_t c,
+                                                         int64_t N, uint32_t off_bytes) {
+    const char* rowp = reinterpret_cast<const char*>(X + static_cast<int64_t>(c) * N);
+    return VecIO<VEC>::load(reinterpret_cast<const float*>(rowp + off_bytes));
+}
+
+template <int VEC, int U>
+__device__ __forceinline__ void issue(typename VecIO<VEC>::T (&x)[U], int32_t mc, int32_t k,
+                                      int32_t n, const float* __restrict__ X, int64_t N,
+                                      uint32_t n0, bool active) {
+    if (!active) return;
+    if (k + U <= n) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) x[u] = gather<VEC>(X, bcast_i(mc, k + u), N, n0);
+    } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (k + u < n) x[u] = gather<VEC>(X, bcast_i(mc, k + u), N, n0);
+    }
+}
+
+template <int VEC, int U>
+__device__ __forceinline__ void consume(const typename VecIO<VEC>::T (&x)[U], float mv, int32_t k,
+                                        int32_t n, float (&acc)[VEC], bool active) {
+    if (!active) return;
+    if (k + U <= n) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const float v = bcast_f(mv, k + u);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(v, VecIO<VEC>::get(x[u], e), acc[e]);
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (k + u < n) {
+                const float v = bcast_f(mv, k + u);
+#pragma unroll
+                for (int e = 0; e < VEC; ++e)
+                    acc[e] = __builtin_fmaf(v, VecIO<VEC>::get(x[u], e), acc[e]);
+            }
+        }
+    }
+}
+
+template <int VEC, int U>
+__global__ __launch_bounds__(kSpmmBlock) void spmm_wave_kernel(
+    int64_t M, int64_t N, int64_t nitems, const int32_t* __restrict__ row_start,
+    const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ col,
+    const float* __restrict__ val, const float* __restrict__ X, float* __restrict__ Y) {
+    typedef typename VecIO<VEC>::T T;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t item = wave_id();
+    if (item >= nitems) return;  // wave-uniform; no barriers below
+    const int64_t tile = item / M;
+    const int64_t row = item - tile * M;
+    const int64_t n0 = (tile * kWave + lane) * VEC;
+    const bool active = n0 < N;  // N % VEC == 0, so n0 + VEC <= N
+    const int32_t start = row_start[row];
+    const int32_t nnz = row_nnz[row];
+    const uint32_t off = static_cast<uint32_t>(n0) * 4u;  // 4N < 2^31 (launcher check)
+
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
+
+    for (int32_t base = 0; base < nnz; base += kWave) {
+        const int32_t n = (nnz - base < kWave) ? nnz - base : kWave;
+        int32_t mc = 0;
+        float mv = 0.0f;
+        if (lane < n) {
+            mc = col[start + base + lane];
+            mv = val[start + base + lane];
+        }
+        T xa[U], xc[U];
+        issue<VEC, U>(xa, mc, 0, n, X, N, off, active);
+        for (int32_t k = 0;;) {
+            issue<VEC, U>(xc, mc, k + U, n, X, N, off, active && k + U < n);
+            consume<VEC, U>(xa, mv, k, n, acc, active);
+            k += U;
+            if (k >= n) break;
+            issue<VEC, U>(xa, mc, k + U, n, X, N, off, active && k + U < n);
+            consume<VEC, U>(xc, mv, k, n, acc, active);
+            k += U;
+            if (k >= n) break;
+        }
+    }
+    if (active) VecIO<VEC>::store(Y + row * N + n0, acc);
+}
+
 template <int L, int VEC>
-__global__ __launch_bounds__(kSpmmBlock) void spmm_kernel(
-    int64_t M, int64_t N, int64_t nitems,
-    const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
-    const int32_t* __restrict__ col, const float* __restrict__ val,
-    const float* __restrict__ X, float* __restrict__ Y) {
+__global__ __launch_bounds__(kSpmmBlock) void spmm_group_kernel(
+    int64_t M, int64_t N, int64_t nitems, const int32_t* __restrict__ row_start,
+    const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ col,
+    const float* __restrict__ val, const float* __restrict__ X, float* __restrict__ Y) {
     typedef VecIO<VEC> IO;
+    constexpr int kUnroll = 8;
     constexpr int kItemsPerWave = kWave / L;
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t item = wave_id() * kItemsPerWave + lane / L;
-    if (item >= nitems) return;  // no barriers below: early exit is safe
+    if (item >= nitems) return;
     const int64_t tile = item / M;
     const int64_t row = item - tile * M;
     const int64_t n0 = (tile * L + (lane % L)) * VEC;
-    const bool active = n0 < N;  // N % VEC == 0 when VEC > 1, so n0 + VEC <= N
+    const bool active = n0 < N;
 
     const int32_t start = row_start[row];
     const int32_t nnz = row_nnz[row];
@@ -72,7 +195,7 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_kernel(
 
     float acc[VEC];
 #pragma unroll
-    for (int k = 0; k < VEC; ++k) acc[k] = 0.0f;
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
 
     int32_t s = 0;
     for (; s + kUnroll <= nnz; s += kUnroll) {
@@ -85,15 +208,13 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_kernel(
         }
         typename IO::T x[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
+        for (int u = 0; u < kUnroll; ++u)
             if (active) x[u] = IO::load(xb + static_cast<int64_t>(c[u]) * N);
-        }
         if (active) {
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
+            for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
-                for (int k = 0; k < VEC; ++k) acc[k] = __builtin_fmaf(v[u], IO::get(x[u], k), acc[k]);
-            }
+                for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(v[u], IO::get(x[u], e), acc[e]);
         }
     }
     for (; s < nnz; ++s) {
@@ -102,51 +223,56 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_kernel(
         if (active) {
             const typename IO::T x = IO::load(xb + static_cast<int64_t>(c) * N);
 #pragma unroll
-            for (int k = 0; k < VEC; ++k) acc[k] = __builtin_fmaf(v, IO::get(x, k), acc[k]);
+            for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(v, IO::get(x, e), acc[e]);
         }
     }
     if (active) IO::store(Y + row * N + n0, acc);
 }
 
-template <int L, int VEC>
-int launch(const slk_csr* W, const float* X, int64_t N, float* Y, hipStream_t st) {
+int launch_blocks(int64_t waves, int64_t* blocks) {
+    *blocks = ceil_div(waves, kSpmmBlock / kWave);
+    if (*blocks > INT32_MAX) return fail(SLK_EINVAL, "spmm: problem too large for one launch");
+    return SLK_OK;
+}
+
+template <int VEC>
+int launch_wave(const slk_csr* W, const float* X, int64_t N, float* Y, hipStream_t st) {
+    constexpr int U = VEC == 4 ? 8 : 16;
     const int64_t M = W->nrows;
-    const int64_t tiles = ceil_div(N, static_cast<int64_t>(L) * VEC);
-    const int64_t nitems = M * tiles;
-    const int64_t waves = ceil_div(nitems, kWave / L);
-    const int64_t blocks = ceil_div(waves, kSpmmBlock / kWave);
-    if (blocks > INT32_MAX) return fail(SLK_EINVAL, "spmm: problem too large for one launch");
-    hipLaunchKernelGGL((spmm_kernel<L, VEC>), dim3(static_cast<unsigned>(blocks)),
+    const int64_t nitems = M * ceil_div(N, int64_t{kWave} * VEC);
+    int64_t blocks;
+    if (int rc = launch_blocks(nitems, &blocks)) return rc;
+    hipLaunchKernelGGL((spmm_wave_kernel<VEC, U>), dim3(static_cast<unsigned>(blocks)),
                        dim3(kSpmmBlock), 0, st, M, N, nitems, W->row_start, W->row_nnz,
                        W->col_indices, W->values, X, Y);
     return check_launch("spmm");
 }
 
-template <int VEC>
-int dispatch_L(int L, const slk_csr* W, const float* X, int64_t N, float* Y, hipStream_t st) {
+template <int L, int VEC>
+int launch_group(const slk_csr* W, const float* X, int64_t N, float* Y, hipStream_t st) {
+    const int64_t M = W->nrows;
+    const int64_t nitems = M * ceil_div(N, static_cast<int64_t>(L) * VEC);
+    int64_t blocks;
+    if (int rc = launch_blocks(ceil_div(nitems, kWave / L), &blocks)) return rc;
+    hipLaunchKernelGGL((spmm_group_kernel<L, VEC>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kSpmmBlock), 0, st, M, N, nitems, W->row_start, W->row_nnz,
+                       W->col_indices, W->values, X, Y);
+    return check_launch("spmm");
+}
+
+int launch_group_L(int L, const slk_csr* W, const float* X, int64_t N, float* Y, hipStream_t st) {
     switch (L) {
-        case 1: return launch<1, VEC>(W, X, N, Y, st);
-        case 2: return launch<2, VEC>(W, X, N, Y, st);
-        case 4: return launch<4, VEC>(W, X, N, Y, st);
-        case 8: return launch<8, VEC>(W, X, N, Y, st);
-        case 16: return launch<16, VEC>(W, X, N, Y, st);
-        case 32: return launch<32, VEC>(W, X, N, Y, st);
-        default: return launch<64, VEC>(W, X, N, Y, st);
+        case 1: return launch_group<1, 1>(W, X, N, Y, st);
+        case 2: return launch_group<2, 1>(W, X, N, Y, st);
+        case 4: return launch_group<4, 1>(W, X, N, Y, st);
+        case 8: return launch_group<8, 1>(W, X, N, Y, st);
+        case 16: return launch_group<16, 1>(W, X, N, Y, st);
+        default: return launch_group<32, 1>(W, X, N, Y, st);
     }
 }
 
-// Lanes per item: the smallest power of two whose tile covers the row
-// (capped at a full wave), unless SLK_SPMM_LANES overrides it.
-int pick_lanes(int64_t N, int vec) {
-    if (const char* e = std::getenv("SLK_SPMM_LANES")) {
-        const int v = std::atoi(e);
-        if (v == 1 || v == 2 || v == 4 || v == 8 || v == 16 || v == 32 || v == 64) return v;
-    }
-    const int64_t need = ceil_div(N, vec);
-    int L = 1;
-    while (L < kWave && L < need) L <<= 1;
-    return L;
-}
+// Waves worth launching: enough to give every CU several to switch between.
+constexpr int64_t kTargetWaves = 4096;
 
 }  // namespace
 }  // namespace slk
@@ -164,9 +290,27 @@ extern "C" int slk_spmm(const slk_csr* W, const float* X, int64_t K, int64_t N, 
     }
     if (W->nrows == 0 || N == 0) return SLK_OK;
     if (Y == nullptr || (K > 0 && X == nullptr)) return fail(SLK_EINVAL, "spmm: NULL X or Y");
-    const bool v4 = (N % 4 == 0) && (reinterpret_cast<uintptr_t>(X) % 16 == 0) &&
-                    (reinterpret_cast<uintptr_t>(Y) % 16 == 0);
+    if (N > INT32_MAX / 4) return fail(SLK_EINVAL, "spmm: N exceeds the 32-bit lane offset range");
     hipStream_t st = as_stream(stream);
-    if (v4) return dispatch_L<4>(pick_lanes(N, 4), W, X, N, Y, st);
-    return dispatch_L<1>(pick_lanes(N, 1), W, X, N, Y, st);
+    const uintptr_t align = reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(Y);
+    const int64_t M = W->nrows;
+
+    int vec = 1;
+    if (const char* e = std::getenv("SLK_SPMM_VEC")) vec = std::atoi(e);
+    else if (N % 4 == 0 && align % 16 == 0 && M * ceil_div(N, 256) >= kTargetWaves) vec = 4;
+    else if (N % 2 == 0 && align % 8 == 0 && M * ceil_div(N, 128) >= kTargetWaves) vec = 2;
+    if ((vec == 4 && (N % 4 || align % 16)) || (vec == 2 && (N % 2 || align % 8)) ||
+        (vec != 1 && vec != 2 && vec != 4)) {
+        vec = 1;
+    }
+    if (N < kWave * vec) {
+        // Narrow X: pack several rows per wave.
+        int L = 1;
+        while (L < 32 && L < N) L <<= 1;
+        if (L < kWave && L >= N) return launch_group_L(L, W, X, N, Y, st);
+        vec = 1;
+    }
+    if (vec == 4) return launch_wave<4>(W, X, N, Y, st);
+    if (vec == 2) return launch_wave<2>(W, X, N, Y, st);
+    return launch_wave<1>(W, X, N, Y, st);
 }

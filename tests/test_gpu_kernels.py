@@ -105,10 +105,14 @@ def test_unaligned_inputs_take_the_scalar_load_path(dev, N):
     assert_bits_equal(_sddmm(W, dY, X).cpu().numpy(), oracle.sddmm(c, dY_np, X_np), "dW")
 
 
-@pytest.mark.parametrize("lanes", [1, 4, 16, 64])
-def test_spmm_every_tile_width(dev, monkeypatch, lanes):
-    monkeypatch.setenv("SLK_SPMM_LANES", str(lanes))
-    c, X_np, _ = _case(40, 50, 300, 9, seed=lanes)
+@pytest.mark.parametrize("vec", [1, 2, 4])
+@pytest.mark.parametrize("N,per_row", [(300, 9), (1024, 150), (4100, 3)])
+def test_spmm_every_vector_width(dev, monkeypatch, vec, N, per_row):
+    """Each lane width of the one-row-per-wave kernel (the launcher picks it by
+    problem size; SLK_SPMM_VEC forces it), including rows longer than one
+    64-slot metadata chunk and partial last batches."""
+    monkeypatch.setenv("SLK_SPMM_VEC", str(vec))
+    c, X_np, _ = _case(40, 200, N, per_row, seed=vec * 7 + N)
     W = from_oracle(c, dev)
     assert_bits_equal(_spmm(W, _t(X_np, dev)).cpu().numpy(), oracle.spmm(c, X_np), "Y")
 
