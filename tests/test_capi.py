@@ -1,0 +1,86 @@
+"""The C-ABI library: it loads, exports every entry point include/*.h declares,
+and its host-side argument checks answer without touching a device.
+
+No kernel is launched here (no GPU is needed): every call below returns from
+argument validation before any HIP call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from sparsecore_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _declared_symbols():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        names |= set(re.findall(r"SLK_API\s+[\w\s\*]+?\b(slk_\w+)\s*\(", h.read_text()))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = _declared_symbols()
+    assert declared == set(_lib.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.slk_abi_version() == _lib.ABI_VERSION
+
+
+def test_exported_symbols_are_exactly_the_api():
+    import subprocess
+
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], check=True,
+                         capture_output=True, text=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert exported == _declared_symbols()
+
+
+def _view(M=4, K=6, cap=0):
+    return _lib.CsrView(M, K, cap, None, None, 1, 1, 1)
+
+
+def test_shape_checks_answer_on_the_host():
+    lib = _lib.load()
+    v = _view()
+    rc = lib.slk_spmm(ctypes.byref(v), None, 7, 3, None, None)
+    assert rc == _lib.SLK_EINVAL
+    msg = lib.slk_last_error().decode()
+    assert "shape mismatch" in msg and "ncols=6" in msg
+    rc = lib.slk_sddmm(ctypes.byref(v), None, 5, None, 6, 3, None, _lib.SLK_DW_SIMD, None)
+    assert rc == _lib.SLK_EINVAL and "dY.shape" in lib.slk_last_error().decode()
+    rc = lib.slk_sddmm(ctypes.byref(v), None, 4, None, 9, 3, None, _lib.SLK_DW_SIMD, None)
+    assert rc == _lib.SLK_EINVAL and "X.shape" in lib.slk_last_error().decode()
+    rc = lib.slk_sddmm(ctypes.byref(v), None, 4, None, 6, 3, None, 7, None)
+    assert rc == _lib.SLK_EINVAL and "order" in lib.slk_last_error().decode()
+    bad = _lib.CsrView(-1, 3, 0, None, None, None, None, None)
+    assert lib.slk_spmm(ctypes.byref(bad), None, 3, 1, None, None) == _lib.SLK_EINVAL
+    rc = lib.slk_transpose_count(ctypes.byref(v), -0.5, None, 0, None, None, None, None, None)
+    assert rc == _lib.SLK_EINVAL and "padding_ratio" in lib.slk_last_error().decode()
+
+
+def test_empty_problems_are_no_ops():
+    lib = _lib.load()
+    v = _lib.CsrView(0, 6, 0, None, None, None, None, None)
+    assert lib.slk_spmm(ctypes.byref(v), None, 6, 3, None, None) == _lib.SLK_OK
+    assert lib.slk_last_error().decode() == ""
+    v = _view(cap=0)
+    assert lib.slk_sddmm(ctypes.byref(v), None, 4, None, 6, 3, None, 0, None) == _lib.SLK_OK
+    assert lib.slk_transpose_refresh(None, 0, None, 0, None, None) == _lib.SLK_OK
+
+
+@pytest.mark.parametrize("M,K,expect_rows_per_block", [(512, 784, 4), (16384, 16384, 16)])
+def test_transpose_workspace_is_bounded(M, K, expect_rows_per_block):
+    lib = _lib.load()
+    v = _lib.CsrView(M, K, 0, None, None, None, None, None)
+    nbytes = lib.slk_transpose_workspace_bytes(ctypes.byref(v))
+    nblk = -(-M // expect_rows_per_block)
+    assert nbytes == nblk * K * 4
+    assert nbytes <= (1 << 24) * 4
