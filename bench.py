@@ -55,6 +55,9 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU-baseline budget")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="after the run, copy a buffer of this many MiB three times (a "
+                         "known-size reference dispatch for HBM byte counters)")
     return ap.parse_args()
 
 
@@ -543,6 +546,15 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "cpu_baseline": None,
     }
+    if args.calibrate_copy_mib > 0:
+        stage(f"copy calibration: {args.calibrate_copy_mib} MiB x 3")
+        n = args.calibrate_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, device=dev)
+        dst = torch.empty(n, device=dev)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if not args.no_cpu:
         stage("cpu baseline")
         try:

@@ -29,11 +29,26 @@ __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + 
 // Validates the parts of a CSR view every kernel relies on.
 int validate_csr(const slk_csr* W, const char* who);
 
-// Wave index of the calling thread, made wave-uniform so that values derived
-// from it live in scalar registers (and row metadata loads become scalar).
+// MI355X has 8 XCDs (each with its own L2); the dispatcher hands workgroup b
+// to XCD (b mod 8). This renumbers workgroups so that every XCD receives one
+// contiguous range of logical workgroups: consecutive work (same X column
+// tile, neighbouring rows) then shares one L2 instead of being spread over
+// all eight. A bijection on [0, nb); if the dispatch order differed only
+// cache locality would change, never the result.
+constexpr int kXcds = 8;
+
+__device__ __forceinline__ int64_t xcd_logical_block(int64_t b, int64_t nb) {
+    const int64_t x = b % kXcds, q = b / kXcds;
+    const int64_t per = nb / kXcds, extra = nb % kXcds;
+    return x * per + (x < extra ? x : extra) + q;
+}
+
+// Wave index of the calling thread over XCD-grouped workgroups, made
+// wave-uniform so that values derived from it live in scalar registers (and
+// row metadata loads become scalar).
 __device__ __forceinline__ int64_t wave_id() {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    return static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + w;
+    return xcd_logical_block(blockIdx.x, gridDim.x) * (blockDim.x >> 6) + w;
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
