@@ -49,7 +49,7 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c5-95", "c5-99"])
     ap.add_argument("--no-graph", action="store_true", help="time eager launches")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -90,6 +90,12 @@ def kernel_avg_ms(fn, reps: int = 200) -> float:
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    fn()
+    end.record()
+    torch.cuda.synchronize()
+    one = start.elapsed_time(end)
+    reps = max(5, min(reps, int(100.0 / max(one, 1e-3))))  # ~0.1 s of launches at most
     torch.cuda._sleep(int(2e7))  # keeps the GPU busy while the launches queue up
     start.record()
     for _ in range(reps):
@@ -215,36 +221,81 @@ class C2:
         return self.l1._csr
 
 
-# ───────────────────────────── workload C1 ───────────────────────────────────
+# ───────────────────────── single-layer workloads (C1, C5) ────────────────────
 
-class C1:
-    name = "c1"
-    desc = "one 512x784 layer, 78 live/row (90%), values N(0,0.02), pr 0.2, N=256"
+def zipf_row_counts(M: int, K: int, density: float, s: float, seed: int):
+    """nnz_i = min(K, c * rank^-s) with c water-filled so the total is density*M*K,
+    assigned to rows in a seeded random order."""
+    import numpy as np
 
-    def __init__(self, dev, seed):
-        import numpy as np
+    target = int(round(density * M * K))
+    ranks = np.arange(1, M + 1, dtype=np.float64) ** (-s)
+    lo, hi = 0.0, float(K) * M
+    for _ in range(200):
+        mid = 0.5 * (lo + hi)
+        if np.minimum(K, np.floor(mid * ranks)).sum() < target:
+            lo = mid
+        else:
+            hi = mid
+    counts = np.minimum(K, np.floor(hi * ranks)).astype(np.int64)
+    short = target - int(counts.sum())
+    for i in range(M):  # hand the rounding remainder to the largest non-full rows
+        if short <= 0:
+            break
+        add = min(short, K - int(counts[i]))
+        counts[i] += add
+        short -= add
+    return counts[np.random.default_rng(seed).permutation(M)]
+
+
+def device_rows_csr(counts, K: int, sigma: float, seed: int, dev, padding_ratio=0.2):
+    """Row i gets counts[i] distinct uniform columns and N(0, sigma) values, all
+    drawn on the device (13.4M entries at C5-95% would be slow on the host)."""
+    import torch
+
+    from sparsecore_amd import layout
+
+    M = len(counts)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    cnt = torch.as_tensor(counts, device=dev)
+    rows, cols = [], []
+    chunk = max(1, (1 << 25) // max(K, 1))
+    for r0 in range(0, M, chunk):
+        r1 = min(M, r0 + chunk)
+        scores = torch.rand(r1 - r0, K, generator=g, device=dev)
+        order = torch.argsort(scores, dim=1)
+        rank = torch.empty_like(order)
+        rank.scatter_(1, order, torch.arange(K, device=dev).expand(r1 - r0, K))
+        r, c = (rank < cnt[r0:r1, None]).nonzero(as_tuple=True)
+        rows.append(r + r0)
+        cols.append(c)
+        del scores, order, rank
+    rows = torch.cat(rows)
+    cols = torch.cat(cols)
+    vals = torch.randn(rows.numel(), generator=g, device=dev) * sigma
+    return layout.from_coo(rows, cols, vals, (M, K), padding_ratio=padding_ratio)
+
+
+class LayerWork:
+    """One SparseLinear-shaped layer: Y = W·X, dW = SDDMM(dY, X), dX = Wᵀ·dY via
+    the cached transpose (refresh + SpMM) — the three kernels of the path."""
+
+    def __init__(self, name, desc, W, X, dY):
         import torch
 
-        import oracle  # noqa: F401  (synthetic topology generator only)
-        from sparsecore_amd import PaddedCSR
-
-        M, K, N = 512, 784, 256
-        rng = np.random.default_rng(seed)
-        cols = [np.sort(rng.choice(K, 78, replace=False)).astype(np.int32) for _ in range(M)]
-        vals = [rng.normal(0, 0.02, 78).astype(np.float32) for _ in range(M)]
-        crow = np.concatenate([[0], np.cumsum([78] * M)])
-        W_dense = torch.zeros(M, K)
-        for i in range(M):
-            W_dense[i, torch.from_numpy(cols[i]).long()] = torch.from_numpy(vals[i])
-        del crow
-        self.W = PaddedCSR.from_dense(W_dense, padding_ratio=0.2).to(dev)
-        self.X = torch.from_numpy(rng.standard_normal((K, N)).astype(np.float32)).to(dev)
-        self.dY = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).to(dev)
-        self.M, self.K, self.N = M, K, N
-        self.dev = dev
         from sparsecore_amd import ops
 
-        ops._cached_transpose(self.W)  # build once (topology fixed)
+        self.name, self.desc = name, desc
+        self.W, self.X, self.dY = W, X, dY
+        self.M, self.K = W.nrows, W.ncols
+        self.N = X.shape[1]
+        self.dev = X.device
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ops._cached_transpose(W)  # topology fixed: build once
+        torch.cuda.synchronize()
+        self.rebuild_ms = 1e3 * (time.perf_counter() - t0)
 
     def body(self):
         from sparsecore_amd import ops
@@ -258,9 +309,13 @@ class C1:
     def params(self):
         return []
 
+    def _WT(self):
+        from sparsecore_amd import ops
+
+        return ops._cached_transpose(self.W)
+
     def step_bytes(self):
-        W = self.W
-        WT = __import__("sparsecore_amd").ops._cached_transpose(W)
+        W, WT = self.W, self._WT()
         M, K, N = self.M, self.K, self.N
         return (bytes_fwd(W.nnz, M, K, N) + bytes_dw(W.nnz, W.total_capacity, M, K, N)
                 + bytes_refresh(W.nnz, WT.total_capacity) + bytes_fwd(W.nnz, K, M, N))
@@ -275,7 +330,7 @@ class C1:
 
         W = self.W
         M, K, N = self.M, self.K, self.N
-        WT = ops._cached_transpose(W)
+        WT = self._WT()
         perm = ops._transpose_cache[id(W)][3]
         Y = torch.empty(M, N, device=self.dev)
         dW = torch.empty(W.total_capacity, device=self.dev)
@@ -291,6 +346,42 @@ class C1:
             ("spmm_dx", lambda: _lib.spmm(vT, self.dY, dX), bytes_fwd(W.nnz, K, M, N),
              flops(W.nnz, N)),
         ]
+
+
+def make_c1(dev, seed):
+    import numpy as np
+    import torch
+
+    from sparsecore_amd import PaddedCSR
+
+    M, K, N = 512, 784, 256
+    rng = np.random.default_rng(seed)
+    W_dense = torch.zeros(M, K)
+    for i in range(M):
+        cols = torch.from_numpy(np.sort(rng.choice(K, 78, replace=False)))
+        W_dense[i, cols] = torch.from_numpy(rng.normal(0, 0.02, 78).astype(np.float32))
+    W = PaddedCSR.from_dense(W_dense, padding_ratio=0.2).to(dev)
+    X = torch.from_numpy(rng.standard_normal((K, N)).astype(np.float32)).to(dev)
+    dY = torch.from_numpy(rng.standard_normal((M, N)).astype(np.float32)).to(dev)
+    return LayerWork("c1", "one 512x784 layer, 78 live/row (90%), values N(0,0.02), pr 0.2, N=256",
+                     W, X, dY)
+
+
+def make_c5(dev, seed, density):
+    import torch
+
+    M = K = 16384
+    N = 4096
+    counts = zipf_row_counts(M, K, density, 1.1, seed)
+    W = device_rows_csr(counts, K, 0.01, seed + 1, dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 2)
+    X = torch.randn(K, N, generator=g, device=dev)
+    dY = torch.randn(M, N, generator=g, device=dev)
+    pct = int(round(100 * (1 - density)))
+    return LayerWork(f"c5-{pct}",
+                     f"16384x16384 at {pct}% sparsity, Zipf(1.1) rows (max {int(counts.max())}, "
+                     f"min {int(counts.min())}), values N(0,0.01), N=4096", W, X, dY)
 
 
 # ───────────────────────────── CPU baseline ──────────────────────────────────
@@ -403,10 +494,13 @@ def cpu_baseline(work, seconds: float):
 
         unit_per_step = work.step_bytes() / 1e9
         unit = "GB/s"
-        sample = "C1 fwd+dW+dX steps (512x784, N=256)"
+        sample = f"{work.name} fwd+dW+dX steps ({work.M}x{work.K}, N={work.N})"
 
-    for _ in range(3):
-        step()
+    t0 = time.perf_counter()
+    step()
+    if time.perf_counter() - t0 < seconds / 20:
+        for _ in range(2):
+            step()
     t0 = time.perf_counter()
     n = 0
     while True:
@@ -438,7 +532,12 @@ def main():
         sys.exit("bench.py: libsparsecore_amd.so is not built (python -m sparsecore_amd.build)")
     dev = torch.device("cuda:0")
     stage(f"workload {args.workload}: building")
-    work = (C2 if args.workload == "c2" else C1)(dev, args.seed)
+    if args.workload == "c2":
+        work = C2(dev, args.seed)
+    elif args.workload == "c1":
+        work = make_c1(dev, args.seed)
+    else:
+        work = make_c5(dev, args.seed, 0.05 if args.workload == "c5-95" else 0.01)
 
     stage("eager warmup")
     for _ in range(max(1, args.warmup)):
@@ -523,7 +622,8 @@ def main():
         unit = "GB/s"
         path = {"GFLOP/s": round(work.step_flops() * args.steps / elapsed / 1e9, 1),
                 "step_bytes": work.step_bytes(), "nnz": work.W.nnz}
-        config = {"workload": "c1: " + work.desc, "graph": graph_ok}
+        config = {"workload": f"{work.name}: {work.desc}", "graph": graph_ok,
+                  "transpose_rebuild_ms": round(work.rebuild_ms, 3)}
 
     line = {
         "metric": METRIC,

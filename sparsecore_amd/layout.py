@@ -33,6 +33,7 @@ from . import _lib
 
 __all__ = [
     "PaddedCSR",
+    "from_coo",
     "from_dense",
     "from_torch_sparse_csr",
     "random",
@@ -568,6 +569,49 @@ def random(nrows: int, ncols: int, *, sparsity: float, padding_ratio: float = 0.
     return from_dense(W, threshold=0.0, padding_ratio=padding_ratio, device=device)
 
 
+def from_coo(rows: torch.Tensor, cols: torch.Tensor, values: torch.Tensor, shape,
+             *, padding_ratio: float = 0.2, device=None) -> PaddedCSR:
+    """PaddedCSR from coordinate triples, built where the inputs live (GPU or CPU).
+
+    Entries are ordered by (row, column); a repeated (row, column) raises
+    ValueError. Capacities follow the float64 rule of layout.py:46-68. The
+    arrays are validated with the same invariant checker as the constructor
+    (on the device for device inputs), so a GPU-built matrix never leaves HBM.
+    """
+    if padding_ratio < 0:
+        raise ValueError(f"padding_ratio must be >= 0, got {padding_ratio}")
+    M, K = (int(s) for s in shape)
+    dev = torch.device(device) if device is not None else values.device
+    rows = rows.to(dev, torch.int64).reshape(-1)
+    cols = cols.to(dev, torch.int64).reshape(-1)
+    values = values.detach().to(dev, _F32).reshape(-1)
+    n = rows.numel()
+    if cols.numel() != n or values.numel() != n:
+        raise ValueError("from_coo: rows, cols and values must have the same length")
+    if n and (int(rows.min()) < 0 or int(rows.max()) >= M or int(cols.min()) < 0
+              or int(cols.max()) >= K):
+        raise ValueError(f"from_coo: coordinates out of range for shape ({M}, {K})")
+    key = rows * max(K, 1) + cols
+    order = torch.argsort(key)
+    key, rows, cols, values = key[order], rows[order], cols[order], values[order]
+    if n > 1 and bool((key[1:] == key[:-1]).any()):
+        raise ValueError("from_coo: repeated (row, column) entry")
+    row_nnz = torch.bincount(rows, minlength=M) if M else torch.zeros(0, dtype=torch.int64,
+                                                                      device=dev)
+    cap = torch.clamp(torch.ceil(row_nnz.to(torch.float64) * (1.0 + padding_ratio)),
+                      min=1.0).to(torch.int64)
+    start = torch.cumsum(cap, 0) - cap
+    total = int(cap.sum()) if M else 0
+    first = torch.cumsum(row_nnz, 0) - row_nnz
+    dest = start[rows] + (torch.arange(n, device=dev) - first[rows])
+    v = torch.zeros(total, dtype=_F32, device=dev)
+    c = torch.full((total,), -1, dtype=_I32, device=dev)
+    v[dest] = values
+    c[dest] = cols.to(_I32)
+    p = PaddedCSR(M, K, v, c, start.to(_I32), row_nnz.to(_I32), cap.to(_I32))
+    return p
+
+
 def _live_slots(p: PaddedCSR):
     """(rows, slots) of every live entry, in row-major order, on p's device."""
     dev = p.device
@@ -630,6 +674,7 @@ def transpose(p: PaddedCSR, *, padding_ratio: float = 0.2) -> PaddedCSR:
     return transpose_with_perm(p, padding_ratio=padding_ratio)[0]
 
 
+PaddedCSR.from_coo = staticmethod(from_coo)
 PaddedCSR.from_dense = staticmethod(from_dense)
 PaddedCSR.from_torch_sparse_csr = staticmethod(from_torch_sparse_csr)
 PaddedCSR.random = staticmethod(random)
