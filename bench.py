@@ -49,7 +49,7 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c5-95", "c5-99"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c5-95", "c5-99"])
     ap.add_argument("--no-graph", action="store_true", help="time eager launches")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -151,6 +151,7 @@ class C2:
 
         import sparsecore_amd as slk
 
+        self.seed = seed
         torch.manual_seed(seed)
         self.l1 = slk.SparseLinear(784, 512, sparsity=0.9)
         self.l2 = slk.SparseLinear(512, 10, sparsity=0.9)
@@ -219,6 +220,137 @@ class C2:
 
     def spmm_layer(self):
         return self.l1._csr
+
+
+# ───────────────────────────── workload C3 ───────────────────────────────────
+
+class C3:
+    """10M-param char-level decoder, d_model 384, 6 layers,
+    6 heads, FFN 1536, vocab 65, context 256, batch 32 (8192 tokens), fp32.
+    Attention projections (fused QKV 384->1152 and O 384->384, as the
+    reference's demo_15_mini_gpt.py builds them) are SparseLinear at 70%; FFN
+    up/down are SparseLinear at 90%; embeddings, LayerNorms and the LM head
+    are dense. One step = forward + backward (no optimizer step, as the
+    config specifies); value = tokens / s."""
+
+    name = "c3"
+    d_model, n_layers, n_heads, d_ff, vocab, ctx, batch = 384, 6, 6, 1536, 65, 256, 32
+    desc = ("10M char GPT: d384 6L 6H FFN1536 vocab65 ctx256 batch32 (8192 tokens), fp32; "
+            "QKV/O SparseLinear 70%, FFN SparseLinear 90%; forward+backward")
+
+    def __init__(self, dev, seed):
+        import torch
+        import torch.nn as nn
+        import torch.nn.functional as F
+
+        import sparsecore_amd as slk
+
+        D, H = self.d_model, self.n_heads
+
+        class Attn(nn.Module):
+            def __init__(self):
+                super().__init__()
+                self.qkv = slk.SparseLinear(D, 3 * D, sparsity=0.7, bias=False)
+                self.o = slk.SparseLinear(D, D, sparsity=0.7, bias=False)
+
+            def forward(self, x):
+                B, T, C = x.shape
+                q, k, v = self.qkv(x).chunk(3, dim=-1)
+                q = q.reshape(B, T, H, C // H).transpose(1, 2)
+                k = k.reshape(B, T, H, C // H).transpose(1, 2)
+                v = v.reshape(B, T, H, C // H).transpose(1, 2)
+                a = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+                return self.o(a.transpose(1, 2).reshape(B, T, C))
+
+        d_ff = self.d_ff
+
+        class Block(nn.Module):
+            def __init__(self):
+                super().__init__()
+                self.ln1 = nn.LayerNorm(D)
+                self.attn = Attn()
+                self.ln2 = nn.LayerNorm(D)
+                self.up = slk.SparseLinear(D, d_ff, sparsity=0.9, bias=False)
+                self.down = slk.SparseLinear(d_ff, D, sparsity=0.9, bias=False)
+
+            def forward(self, x):
+                x = x + self.attn(self.ln1(x))
+                return x + self.down(F.gelu(self.up(self.ln2(x))))
+
+        ctx, vocab = self.ctx, self.vocab
+
+        class GPT(nn.Module):
+            def __init__(self):
+                super().__init__()
+                self.tok = nn.Embedding(vocab, D)
+                self.pos = nn.Embedding(ctx, D)
+                self.blocks = nn.ModuleList([Block() for _ in range(C3.n_layers)])
+                self.ln_f = nn.LayerNorm(D)
+                self.head = nn.Linear(D, vocab, bias=False)
+
+            def forward(self, idx):
+                x = self.tok(idx) + self.pos(torch.arange(idx.shape[1], device=idx.device))
+                for b in self.blocks:
+                    x = b(x)
+                return self.head(self.ln_f(x))
+
+        self.seed = seed
+        torch.manual_seed(seed)
+        self.model = GPT().to(dev)
+        g = torch.Generator().manual_seed(seed + 1)
+        self.idx = torch.randint(0, vocab, (self.batch, ctx), generator=g).to(dev)
+        self.tgt = torch.randint(0, vocab, (self.batch, ctx), generator=g).to(dev)
+        self.dev = dev
+
+    def body(self):
+        import torch.nn.functional as F
+
+        for p in self.model.parameters():
+            p.grad = None
+        logits = self.model(self.idx)
+        loss = F.cross_entropy(logits.reshape(-1, self.vocab), self.tgt.reshape(-1))
+        loss.backward()
+        return loss.detach()
+
+    def params(self):
+        return list(self.model.parameters())
+
+    def tokens_per_step(self):
+        return self.batch * self.ctx
+
+    def sparse_layers(self):
+        b = self.model.blocks[0]
+        return [("qkv", b.attn.qkv), ("o", b.attn.o), ("up", b.up), ("down", b.down)]
+
+    def kernels(self):
+        """The HIP kernels of block 0's four sparse layers at N = 8192 tokens."""
+        import torch
+
+        from sparsecore_amd import _lib, ops
+
+        N = self.batch * self.ctx
+        out = []
+        for tag, layer in self.sparse_layers():
+            W = layer._csr
+            M, K = W.nrows, W.ncols
+            X = torch.randn(K, N, device=self.dev)
+            Y = torch.empty(M, N, device=self.dev)
+            dY = torch.randn(M, N, device=self.dev)
+            dW = torch.empty(W.total_capacity, device=self.dev)
+            dX = torch.empty(K, N, device=self.dev)
+            WT = ops._cached_transpose(W)
+            v, vT = W._view(), WT._view()
+            out.append((f"spmm_fwd[{tag} {M}x{K}]", lambda v=v, X=X, Y=Y: _lib.spmm(v, X, Y),
+                        bytes_fwd(W.nnz, M, K, N), flops(W.nnz, N)))
+            out.append((f"sddmm_dw[{tag} {M}x{K}]",
+                        lambda v=v, dY=dY, X=X, dW=dW: _lib.sddmm(v, dY, X, dW, _lib.SLK_DW_SIMD),
+                        bytes_dw(W.nnz, W.total_capacity, M, K, N), flops(W.nnz, N)))
+            out.append((f"spmm_dx[{tag} {K}x{M}]", lambda vT=vT, dY=dY, dX=dX: _lib.spmm(vT, dY, dX),
+                        bytes_fwd(W.nnz, K, M, N), flops(W.nnz, N)))
+        return out
+
+    def spmm_layer(self):
+        return self.model.blocks[0].up._csr
 
 
 # ───────────────────────── single-layer workloads (C1, C5) ────────────────────
@@ -457,31 +589,60 @@ def cpu_baseline(work, seconds: float):
             dX = torch.from_numpy(layer.dx(dYc))  # the reference always computes dX
             return dW, None, dX
 
-    if isinstance(work, C2):
-        layers = []
-        for gl in (work.l1, work.l2):
-            hl = HostLayer(gl._csr)
-            w = torch.nn.Parameter(hl.values)
-            b = torch.nn.Parameter(gl.bias.detach().cpu().clone())
-            layers.append((hl, w, b))
-        x = work.x.cpu()
-        labels = work.labels.cpu()
-        opt = torch.optim.SGD([p for _, w, b in layers for p in (w, b)], lr=0.01)
+    class RefLinear(torch.nn.Module):
+        """SparseLinear.forward (nn.py:210-245) over the reference's kernels."""
 
-        def step():
-            opt.zero_grad(set_to_none=True)
-            h = x
-            for idx, (hl, w, b) in enumerate(layers):
-                h = RefFn.apply(w, hl, h.t().contiguous()).t() + b
-                if idx == 0:
-                    h = torch.relu(h)
-            loss = torch.nn.functional.cross_entropy(h, labels)
-            loss.backward()
-            opt.step()
+        def __init__(self, sl):
+            super().__init__()
+            self.hl = HostLayer(sl._csr)
+            self.w = torch.nn.Parameter(self.hl.values)
+            self.bias = (None if sl.bias is None
+                         else torch.nn.Parameter(sl.bias.detach().cpu().clone()))
+            self.fin, self.fout = sl.in_features, sl.out_features
 
+        def forward(self, x):
+            shp = x.shape
+            X_col = x.reshape(-1, self.fin).contiguous().t().contiguous()
+            y = RefFn.apply(self.w, self.hl, X_col).t()
+            if self.bias is not None:
+                y = y + self.bias
+            return y.reshape(shp[:-1] + (self.fout,))
+
+    def swap_sparse(module):
+        import sparsecore_amd as slk
+
+        for name, child in list(module.named_children()):
+            if isinstance(child, slk.SparseLinear):
+                setattr(module, name, RefLinear(child))
+            else:
+                swap_sparse(child)
+
+    if isinstance(work, (C2, C3)):
+        # same seed on the CPU: identical weights and inputs, then the
+        # SparseLinear layers run on the reference kernels
+        host = type(work)(torch.device("cpu"), work.seed)
+        swap_sparse(host.model)
+        if isinstance(work, C2):
+            opt = torch.optim.SGD(host.model.parameters(), lr=0.01)
+
+            def step():
+                opt.zero_grad(set_to_none=True)
+                loss = torch.nn.functional.cross_entropy(host.model(host.x), host.labels)
+                loss.backward()
+                opt.step()
+
+            sample = "C2 train steps (MLP 784->512->10, batch 256)"
+        else:
+            def step():
+                for prm in host.model.parameters():
+                    prm.grad = None
+                logits = host.model(host.idx)
+                torch.nn.functional.cross_entropy(logits.reshape(-1, host.vocab),
+                                                  host.tgt.reshape(-1)).backward()
+
+            sample = "C3 forward+backward steps (10M char GPT, 8192 tokens)"
         unit_per_step = work.tokens_per_step()
         unit = "tokens/s"
-        sample = "C2 train steps (MLP 784->512->10, batch 256)"
     else:
         hl = HostLayer(work.W)
         X = work.X.cpu().numpy()
@@ -534,6 +695,8 @@ def main():
     stage(f"workload {args.workload}: building")
     if args.workload == "c2":
         work = C2(dev, args.seed)
+    elif args.workload == "c3":
+        work = C3(dev, args.seed)
     elif args.workload == "c1":
         work = make_c1(dev, args.seed)
     else:
@@ -617,6 +780,18 @@ def main():
                 "layer1_nnz": W.nnz}
         config = {"workload": "c2: " + work.desc, "global_batch": work.batch,
                   "graph": graph_ok}
+    elif isinstance(work, C3):
+        value = work.tokens_per_step() * args.steps / elapsed
+        unit = "tokens/s"
+        per_block_us = sum(k["avg_us"] for k in kern)
+        path = {"block0_sparse_kernels_us": round(per_block_us, 1),
+                "block0_sparse_GBps": round(sum(k["bytes"] for k in kern) /
+                                            (per_block_us * 1e-6) / 1e9, 1),
+                "block0_sparse_GFLOPs": round(sum(k["flops"] for k in kern) /
+                                              (per_block_us * 1e-6) / 1e9, 1),
+                "sparse_kernel_share_of_step": round(6 * per_block_us * 1e-3 / ms_per_step, 3)}
+        config = {"workload": "c3: " + work.desc, "global_batch": work.batch,
+                  "seq_len": work.ctx, "graph": graph_ok}
     else:
         value = work.step_bytes() * args.steps / elapsed / 1e9
         unit = "GB/s"
