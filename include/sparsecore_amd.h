@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define SLK_ABI_VERSION 1
+#define SLK_ABI_VERSION 2
 
 #if defined(__GNUC__)
 #define SLK_API __attribute__((visibility("default")))
@@ -69,6 +69,11 @@ typedef struct slk_csr {
     const int32_t* row_start;
     const int32_t* row_nnz;
     const int32_t* row_capacity;
+    /* Optional (may be NULL): a permutation of [0, nrows) listing rows by
+     * descending row_nnz. slk_spmm then schedules the longest rows first (in
+     * bands of 256 rows) so skewed rows do not straggle; results are the same
+     * either way. Not part of the reference layout — a cached schedule. */
+    const int32_t* row_order;
 } slk_csr;
 
 /* Thread-local description of the last failure of this thread ("" if none). */

@@ -21,7 +21,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libsparsecore_amd.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 SLK_OK, SLK_EINVAL, SLK_EDEVICE = 0, 1, 2
 SLK_DW_SIMD, SLK_DW_SCALAR = 0, 1
@@ -53,6 +53,7 @@ class CsrView(ctypes.Structure):
         ("row_start", ctypes.c_void_p),
         ("row_nnz", ctypes.c_void_p),
         ("row_capacity", ctypes.c_void_p),
+        ("row_order", ctypes.c_void_p),
     ]
 
 

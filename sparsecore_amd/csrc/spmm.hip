@@ -8,8 +8,13 @@
 // element, so results are bit-identical to the reference CPU kernels.
 //
 // Work decomposition: one "item" is (row, column tile). Items are ordered
-// tile-major (item = tile * M + row) so that waves resident at the same time
-// gather from the same K x tile slab of X, which stays in L2.
+// tile-major (item = tile * M + r) so that waves resident at the same time
+// gather from the same K x tile slab of X, which stays in L2. Within a tile,
+// r indexes W->row_order when the caller supplies it (rows by descending
+// nnz): the longest rows of every tile start first, so a few heavy rows of a
+// skewed matrix do not run alone at the end of the grid, and the rows that
+// share a wave in spmm_group_kernel have similar lengths. The order changes
+// only which wave computes a row, never the arithmetic.
 //
 //  * spmm_wave_kernel — one item per wave (64 lanes x VEC columns). The
 //    row's (col, value) stream is fetched 64 slots at a time with one
@@ -128,15 +133,17 @@ __device__ __forceinline__ void consume(const typename VecIO<VEC>::T (&x)[U], fl
 
 template <int VEC, int U>
 __global__ __launch_bounds__(kSpmmBlock) void spmm_wave_kernel(
-    int64_t M, int64_t N, int64_t nitems, const int32_t* __restrict__ row_start,
-    const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ col,
-    const float* __restrict__ val, const float* __restrict__ X, float* __restrict__ Y) {
+    int64_t M, int64_t N, int64_t nitems, const int32_t* __restrict__ order,
+    const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
+    const int32_t* __restrict__ col, const float* __restrict__ val,
+    const float* __restrict__ X, float* __restrict__ Y) {
     typedef typename VecIO<VEC>::T T;
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t item = wave_id();
     if (item >= nitems) return;  // wave-uniform; no barriers below
     const int64_t tile = item / M;
-    const int64_t row = item - tile * M;
+    const int64_t r = item - tile * M;
+    const int64_t row = order != nullptr ? order[r] : r;
     const int64_t n0 = (tile * kWave + lane) * VEC;
     const bool active = n0 < N;  // N % VEC == 0, so n0 + VEC <= N
     const int32_t start = row_start[row];
@@ -173,9 +180,10 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_wave_kernel(
 
 template <int L, int VEC>
 __global__ __launch_bounds__(kSpmmBlock) void spmm_group_kernel(
-    int64_t M, int64_t N, int64_t nitems, const int32_t* __restrict__ row_start,
-    const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ col,
-    const float* __restrict__ val, const float* __restrict__ X, float* __restrict__ Y) {
+    int64_t M, int64_t N, int64_t nitems, const int32_t* __restrict__ order,
+    const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
+    const int32_t* __restrict__ col, const float* __restrict__ val,
+    const float* __restrict__ X, float* __restrict__ Y) {
     typedef VecIO<VEC> IO;
     constexpr int kUnroll = 8;
     constexpr int kItemsPerWave = kWave / L;
@@ -183,7 +191,8 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_group_kernel(
     const int64_t item = wave_id() * kItemsPerWave + lane / L;
     if (item >= nitems) return;
     const int64_t tile = item / M;
-    const int64_t row = item - tile * M;
+    const int64_t r = item - tile * M;
+    const int64_t row = order != nullptr ? order[r] : r;
     const int64_t n0 = (tile * L + (lane % L)) * VEC;
     const bool active = n0 < N;
 
@@ -229,10 +238,168 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_group_kernel(
     if (active) IO::store(Y + row * N + n0, acc);
 }
 
+// ───────────────────────── LDS-tiled kernel ─────────────────────────────────
+//
+// spmm_tile_kernel — for large problems. A workgroup of 8 waves owns a
+// 64-row x 128-column output tile: each wave holds 8 rows, each lane two
+// adjacent columns, accumulators in registers. X is streamed through LDS in
+// chunks of kTileK rows (the next chunk is prefetched into registers while
+// the current one is consumed). For each chunk every row consumes its slots
+// whose column falls in the chunk; columns ascend within a row, so walking
+// the chunks in order visits each row's slots in slot order and the fma chain
+// of every element is exactly the reference's. Each X element is fetched
+// from L2/HBM once per workgroup and read from LDS by every row of the tile
+// that uses it, instead of being gathered through L1 once per slot.
+//
+// A wave advances its 8 rows in lockstep (one slot of every row per step), so
+// eight independent LDS reads are in flight per step. A row's (col, value)
+// stream sits in registers 64 slots at a time and is reloaded when less than
+// half of the batch is left; a row with more slots in one chunk than its
+// batch holds (a near-dense row) finishes the chunk in a per-row loop.
+constexpr int kTileCols = 128;                     // 64 lanes x 2 columns
+constexpr int kTileK = 64;                         // X rows per LDS chunk
+constexpr int kRowsPerWave = 8;
+constexpr int kTileWaves = 8;
+constexpr int kTileRows = kRowsPerWave * kTileWaves;  // 64
+constexpr int kTileThreads = kTileWaves * kWave;      // 512
+constexpr int kTilePrefetch = kTileK * kTileCols / (2 * kTileThreads);  // float2 per thread
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void tile_reload(int32_t& base, int32_t pos, int32_t end, int lane,
+                                            const int32_t* __restrict__ col,
+                                            const float* __restrict__ val, int32_t& mc,
+                                            float& mv) {
+    base = pos;
+    const int32_t sl = pos + lane;
+    mc = sl < end ? col[sl] : INT32_MAX;
+    mv = sl < end ? val[sl] : 0.0f;
+}
+
+__global__ __launch_bounds__(kTileThreads) void spmm_tile_kernel(
+    int64_t M, int64_t K, int64_t N, int64_t nrowblk, const int32_t* __restrict__ row_start,
+    const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ col,
+    const float* __restrict__ val, const float* __restrict__ X, float* __restrict__ Y) {
+    __shared__ f32x2 xs[kTileK][kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t lb = xcd_logical_block(blockIdx.x, gridDim.x);
+    const int64_t ntile = lb / nrowblk;
+    const int64_t rb = lb - ntile * nrowblk;
+    const int64_t n = ntile * kTileCols + 2 * lane;  // N is even for this kernel
+    const bool n_ok = n < N;
+    const int64_t r0 = rb * kTileRows + static_cast<int64_t>(w) * kRowsPerWave;
+
+    int32_t pos[kRowsPerWave], end[kRowsPerWave], base[kRowsPerWave];
+    int32_t mc[kRowsPerWave];
+    float mv[kRowsPerWave];
+    f32x2 acc[kRowsPerWave];
+#pragma unroll
+    for (int r = 0; r < kRowsPerWave; ++r) {
+        const int64_t row = r0 + r;
+        const int32_t s = row < M ? row_start[row] : 0;
+        const int32_t e = row < M ? s + row_nnz[row] : 0;
+        pos[r] = s;
+        end[r] = e;
+        tile_reload(base[r], s, e, lane, col, val, mc[r], mv[r]);
+        acc[r] = f32x2{0.0f, 0.0f};
+    }
+
+    // thread t stages chunk rows (t / 64) + 8j, j < kTilePrefetch, at its two columns
+    const int krow0 = threadIdx.x >> 6;
+    f32x2 pre[kTilePrefetch];
+    auto prefetch = [&](int64_t k0) {
+#pragma unroll
+        for (int j = 0; j < kTilePrefetch; ++j) {
+            const int64_t k = k0 + krow0 + j * kTileWaves;
+            pre[j] = (k < K && n_ok) ? *reinterpret_cast<const f32x2*>(X + k * N + n)
+                                     : f32x2{0.0f, 0.0f};
+        }
+    };
+    const int64_t nchunks = ceil_div(K, kTileK);
+    prefetch(0);
+    for (int64_t ch = 0; ch < nchunks; ++ch) {
+        __syncthreads();  // every wave is done reading the previous chunk
+#pragma unroll
+        for (int j = 0; j < kTilePrefetch; ++j) xs[krow0 + j * kTileWaves][lane] = pre[j];
+        __syncthreads();
+        const int32_t k0 = static_cast<int32_t>(ch * kTileK);
+        const int32_t k1 = k0 + kTileK;
+        if (ch + 1 < nchunks) prefetch(k1);
+
+        int32_t first[kRowsPerWave], cnt[kRowsPerWave];
+        int32_t lo = kWave, hi = 0;
+#pragma unroll
+        for (int r = 0; r < kRowsPerWave; ++r) {
+            if (pos[r] < end[r] && pos[r] > base[r] + kWave / 2)
+                tile_reload(base[r], pos[r], end[r], lane, col, val, mc[r], mv[r]);
+            first[r] = pos[r] - base[r];
+            cnt[r] = __popcll(__ballot(lane >= first[r] && mc[r] < k1));
+            lo = cnt[r] < lo ? cnt[r] : lo;
+            hi = cnt[r] > hi ? cnt[r] : hi;
+        }
+        int32_t k = 0;
+        for (; k < lo; ++k) {  // every row has a slot at step k
+            f32x2 x[kRowsPerWave];
+#pragma unroll
+            for (int r = 0; r < kRowsPerWave; ++r) x[r] = xs[bcast_i(mc[r], first[r] + k) - k0][lane];
+#pragma unroll
+            for (int r = 0; r < kRowsPerWave; ++r) {
+                const float v = bcast_f(mv[r], first[r] + k);
+                acc[r][0] = __builtin_fmaf(v, x[r][0], acc[r][0]);
+                acc[r][1] = __builtin_fmaf(v, x[r][1], acc[r][1]);
+            }
+        }
+        for (; k < hi; ++k) {
+#pragma unroll
+            for (int r = 0; r < kRowsPerWave; ++r) {
+                if (k < cnt[r]) {
+                    const f32x2 x = xs[bcast_i(mc[r], first[r] + k) - k0][lane];
+                    const float v = bcast_f(mv[r], first[r] + k);
+                    acc[r][0] = __builtin_fmaf(v, x[0], acc[r][0]);
+                    acc[r][1] = __builtin_fmaf(v, x[1], acc[r][1]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kRowsPerWave; ++r) {
+            pos[r] += cnt[r];
+            // batch used up while the row may still have slots in this chunk
+            while (pos[r] < end[r] && pos[r] == base[r] + kWave) {
+                tile_reload(base[r], pos[r], end[r], lane, col, val, mc[r], mv[r]);
+                const int32_t c2 = __popcll(__ballot(mc[r] < k1));
+                for (int32_t q = 0; q < c2; ++q) {
+                    const f32x2 x = xs[bcast_i(mc[r], q) - k0][lane];
+                    const float v = bcast_f(mv[r], q);
+                    acc[r][0] = __builtin_fmaf(v, x[0], acc[r][0]);
+                    acc[r][1] = __builtin_fmaf(v, x[1], acc[r][1]);
+                }
+                pos[r] += c2;
+            }
+        }
+    }
+    if (n_ok) {
+#pragma unroll
+        for (int r = 0; r < kRowsPerWave; ++r)
+            if (r0 + r < M) *reinterpret_cast<f32x2*>(Y + (r0 + r) * N + n) = acc[r];
+    }
+}
+
 int launch_blocks(int64_t waves, int64_t* blocks) {
     *blocks = ceil_div(waves, kSpmmBlock / kWave);
     if (*blocks > INT32_MAX) return fail(SLK_EINVAL, "spmm: problem too large for one launch");
     return SLK_OK;
+}
+
+int launch_tile(const slk_csr* W, const float* X, int64_t N, float* Y, hipStream_t st) {
+    const int64_t M = W->nrows;
+    const int64_t nrowblk = ceil_div(M, kTileRows);
+    const int64_t blocks = nrowblk * ceil_div(N, kTileCols);
+    if (blocks > INT32_MAX) return fail(SLK_EINVAL, "spmm: problem too large for one launch");
+    hipLaunchKernelGGL(spmm_tile_kernel, dim3(static_cast<unsigned>(blocks)),
+                       dim3(kTileThreads), 0, st, M, W->ncols, N, nrowblk, W->row_start,
+                       W->row_nnz, W->col_indices, W->values, X, Y);
+    return check_launch("spmm");
 }
 
 template <int VEC>
@@ -243,8 +410,8 @@ int launch_wave(const slk_csr* W, const float* X, int64_t N, float* Y, hipStream
     int64_t blocks;
     if (int rc = launch_blocks(nitems, &blocks)) return rc;
     hipLaunchKernelGGL((spmm_wave_kernel<VEC, U>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(kSpmmBlock), 0, st, M, N, nitems, W->row_start, W->row_nnz,
-                       W->col_indices, W->values, X, Y);
+                       dim3(kSpmmBlock), 0, st, M, N, nitems, W->row_order, W->row_start,
+                       W->row_nnz, W->col_indices, W->values, X, Y);
     return check_launch("spmm");
 }
 
@@ -255,8 +422,8 @@ int launch_group(const slk_csr* W, const float* X, int64_t N, float* Y, hipStrea
     int64_t blocks;
     if (int rc = launch_blocks(ceil_div(nitems, kWave / L), &blocks)) return rc;
     hipLaunchKernelGGL((spmm_group_kernel<L, VEC>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(kSpmmBlock), 0, st, M, N, nitems, W->row_start, W->row_nnz,
-                       W->col_indices, W->values, X, Y);
+                       dim3(kSpmmBlock), 0, st, M, N, nitems, W->row_order, W->row_start,
+                       W->row_nnz, W->col_indices, W->values, X, Y);
     return check_launch("spmm");
 }
 
@@ -294,6 +461,16 @@ extern "C" int slk_spmm(const slk_csr* W, const float* X, int64_t K, int64_t N, 
     hipStream_t st = as_stream(stream);
     const uintptr_t align = reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(Y);
     const int64_t M = W->nrows;
+
+    // Kernel choice: the per-wave gather kernels. The LDS-tiled kernel is
+    // opt-in (SLK_SPMM_KERNEL=tile, where its layout needs — even N, 8-byte
+    // aligned X and Y — hold): on the measured workloads it does not beat the
+    // wave kernel, whose X gathers already hit L2 for the tile-major order.
+    bool tile = false;
+    if (const char* e = std::getenv("SLK_SPMM_KERNEL")) {
+        if (e[0] == 't') tile = N % 2 == 0 && align % 8 == 0;
+    }
+    if (tile) return launch_tile(W, X, N, Y, st);
 
     int vec = 1;
     if (const char* e = std::getenv("SLK_SPMM_VEC")) vec = std::atoi(e);

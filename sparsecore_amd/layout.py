@@ -250,6 +250,7 @@ class PaddedCSR:
         self._nnz = nnz
         self._topology_version = 0
         self._cview = None
+        self._order = None      # (topology_version, device row schedule) for the view
         self._host_rows = None  # cached numpy (row_start, row_nnz, row_capacity)
 
     # ─── shape and aggregates (bindings.cpp:631-660) ────────────────
@@ -331,12 +332,24 @@ class PaddedCSR:
                 f"{who}: the PaddedCSR lives on {self._values.device}; the padded-CSR kernels run "
                 f"on the HIP device only — move it with .cuda() / .to('cuda')")
 
+    # Matrices with at least this many rows get a longest-rows-first schedule
+    # (slk_csr.row_order) so that skewed rows do not straggle in slk_spmm.
+    _ORDER_MIN_ROWS = 2048
+
     def _view(self) -> _lib.CsrView:
         v = self._cview
         if v is None:
+            order = None
+            if self._nrows >= self._ORDER_MIN_ROWS and self._on_device():
+                if self._order is None or self._order[0] != self._topology_version:
+                    # stable: equal-length rows keep their natural order
+                    self._order = (self._topology_version,
+                                   torch.argsort(self._row_nnz, descending=True,
+                                                 stable=True).to(_I32))
+                order = self._order[1]
             v = _lib.CsrView(self._nrows, self._ncols, self._values.numel(),
                              _lib.ptr(self._values), _lib.ptr(self._col), _lib.ptr(self._rs),
-                             _lib.ptr(self._row_nnz), _lib.ptr(self._row_cap))
+                             _lib.ptr(self._row_nnz), _lib.ptr(self._row_cap), _lib.ptr(order))
             self._cview = v
         return v
 
@@ -451,6 +464,7 @@ class PaddedCSR:
         self._nnz += n - int(nz[row_idx])
         nz[row_idx] = n
         self._topology_version += 1
+        self._cview = None  # the row schedule depends on row_nnz
 
     # ─── device movement ───────────────────────────────────────────
     def to(self, device) -> "PaddedCSR":

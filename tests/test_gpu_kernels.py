@@ -117,6 +117,32 @@ def test_spmm_every_vector_width(dev, monkeypatch, vec, N, per_row):
     assert_bits_equal(_spmm(W, _t(X_np, dev)).cpu().numpy(), oracle.spmm(c, X_np), "Y")
 
 
+@pytest.mark.parametrize("M,K,N,per_row", [
+    (1, 1, 2, 1), (63, 127, 62, 40), (64, 128, 128, 128), (65, 129, 130, 100),
+    (200, 300, 1000, 37), (130, 1000, 200, 700), (70, 5000, 96, 3000), (33, 260, 130, 0),
+    (9, 64, 256, 64)])
+def test_spmm_tile_kernel_bit_exact(dev, monkeypatch, M, K, N, per_row):
+    """The LDS-tiled kernel (forced): partial row/column tiles, K not a multiple
+    of the chunk, rows with more than 64 slots in one chunk, dense rows, empty rows."""
+    monkeypatch.setenv("SLK_SPMM_KERNEL", "tile")
+    print(f"[tile] M={M} K={K} N={N} per_row={per_row}", flush=True)
+    c, X_np, _ = _case(M, K, N, per_row, seed=M + K + N)
+    W = from_oracle(c, dev)
+    assert_bits_equal(_spmm(W, _t(X_np, dev)).cpu().numpy(), oracle.spmm(c, X_np), "Y")
+
+
+def test_spmm_tile_kernel_skewed_rows(dev, monkeypatch):
+    monkeypatch.setenv("SLK_SPMM_KERNEL", "tile")
+    c = oracle.zipf_rows(300, 700, 0.08, 1.1, seed=5, sigma=0.5)
+    X_np = np.random.default_rng(5).standard_normal((700, 192)).astype(np.float32)
+    W = from_oracle(c, dev)
+    assert_bits_equal(_spmm(W, _t(X_np, dev)).cpu().numpy(), oracle.spmm(c, X_np), "Y")
+    WT, _ = layout.transpose_with_perm(W)
+    dY_np = np.random.default_rng(6).standard_normal((300, 192)).astype(np.float32)
+    WT_o, _ = oracle.transpose_with_perm(c)
+    assert_bits_equal(_spmm(WT, _t(dY_np, dev)).cpu().numpy(), oracle.spmm(WT_o, dY_np), "dX")
+
+
 @pytest.mark.parametrize("pr", [0.0, 0.2, 0.5, 1.0])
 def test_padding_slots_of_dW_are_exactly_zero(dev, pr):
     c, X_np, dY_np = _case(20, 30, 9, 6, seed=11, pr=pr)
@@ -140,6 +166,49 @@ def test_skewed_rows_bit_exact(dev):
     WT_o, perm_o = oracle.transpose_with_perm(c)
     csr_arrays_equal(to_oracle(WT), WT_o, "WT")
     assert_bits_equal(perm.cpu().numpy(), perm_o, "perm")
+
+
+@pytest.mark.parametrize("N", [1, 5, 40, 256, 1028])
+def test_row_order_schedule_bit_exact(dev, N):
+    """Tall skewed matrices get a longest-rows-first schedule (slk_csr.row_order).
+    The schedule moves rows between waves only: results stay bit-exact, for the
+    one-row-per-wave kernel and for the several-rows-per-wave kernel (N < 64)."""
+    print(f"[row_order] N={N}", flush=True)
+    c = oracle.zipf_rows(3000, 400, 0.03, 1.1, seed=N, sigma=0.5)
+    rng = np.random.default_rng(N)
+    X_np = rng.standard_normal((400, N)).astype(np.float32)
+    W = from_oracle(c, dev)
+    v = W._view()
+    assert v.row_order is not None
+    order = W._order[1].cpu().numpy()
+    assert sorted(order.tolist()) == list(range(3000))
+    assert np.all(np.diff(c.row_nnz[order]) <= 0)
+    want = oracle.spmm(c, X_np)
+    X = _t(X_np, dev)
+    assert_bits_equal(_spmm(W, X).cpu().numpy(), want, "Y (row_order)")
+    # any permutation is a valid schedule: a random one through the C view
+    perm = torch.from_numpy(rng.permutation(3000).astype(np.int32)).to(dev)
+    v2 = _lib.CsrView(*[getattr(v, f) for f, _ in _lib.CsrView._fields_[:-1]], perm.data_ptr())
+    Y = torch.empty(3000, N, device=dev)
+    _lib.spmm(v2, X, Y)
+    assert_bits_equal(Y.cpu().numpy(), want, "Y (random order)")
+    # and no schedule at all
+    v3 = _lib.CsrView(*[getattr(v, f) for f, _ in _lib.CsrView._fields_[:-1]], None)
+    _lib.spmm(v3, X, Y)
+    assert_bits_equal(Y.cpu().numpy(), want, "Y (natural order)")
+
+
+def test_row_order_follows_rewrite_row(dev):
+    """rewrite_row changes row_nnz, so the cached schedule is rebuilt."""
+    c = oracle.uniform_rows(2048, 64, 4, seed=2, sigma=1.0, padding_ratio=3.0)
+    W = from_oracle(c, dev)
+    W._view()
+    W.rewrite_row(1500, np.arange(16, dtype=np.int32), np.ones(16, np.float32))
+    W._view()
+    assert int(W._order[1][0]) == 1500
+    X_np = np.random.default_rng(1).standard_normal((64, 70)).astype(np.float32)
+    assert_bits_equal(_spmm(W, _t(X_np, dev)).cpu().numpy(),
+                      oracle.spmm(to_oracle(W), X_np), "Y after rewrite_row")
 
 
 def test_empty_shapes(dev):
