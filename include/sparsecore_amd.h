@@ -149,6 +149,58 @@ SLK_API int slk_transpose_refresh(const float* W_values, int64_t W_capacity,
 SLK_API int slk_check_invariants(const slk_csr* W, int64_t col_indices_len,
                          int64_t* result_dev, void* stream);
 
+/* ─── Topology mutation (SET / RigL) and the dense gradient ───────────── */
+
+/* Bytes of device workspace slk_live_abs_kth needs (independent of W). */
+#define SLK_KTH_WORKSPACE_BYTES 8448
+
+/* *thr_dev = the k-th smallest |values[s]| over W's live slots (1 <= k <=
+ * number of live slots), i.e. np.partition(np.abs(live), k-1)[k-1] — the
+ * global drop threshold of SET and RigL (sparselab/router.py:394-412 and
+ * :648-661). Exact: a radix select on the float bits, no rounding.        */
+SLK_API int slk_live_abs_kth(const slk_csr* W, int64_t k, void* workspace,
+                             int64_t workspace_bytes, float* thr_dev, void* stream);
+
+/* Grow rule of slk_drop_grow. */
+enum slk_grow_rule {
+    SLK_GROW_RANDOM = 0,   /* SET: uniform over the row's empty columns       */
+    SLK_GROW_GRADIENT = 1, /* RigL: largest |G[i, c]| over the empty columns  */
+};
+
+/* Bytes of device workspace slk_drop_grow needs for W (row staging).       */
+SLK_API int64_t slk_drop_grow_workspace_bytes(const slk_csr* W);
+
+/* One SET / RigL drop-and-grow pass over every row of W, in place
+ * (replaces the per-row loop of sparselab/router.py:414-478 for SET and
+ * :663-732 for RigL, with its PaddedCSR.rewrite_row calls,
+ * csrc/kernels/padded_csr.cpp:219-296). For each row with live slots:
+ *   keep the slots with |v| > *thr_dev (if none, the first slot of largest
+ *   |v|); n_grow = min(dropped, ncols - kept); grow n_grow columns outside
+ *   the kept set with value 0 and write the row back sorted by column.
+ * Grow choice: SLK_GROW_GRADIENT takes the n_grow largest |G[i*ldg + c]|
+ * (ties: lower column first; NaN last); SLK_GROW_RANDOM takes the n_grow
+ * smallest 32-bit keys splitmix64(seed, i*ncols + c), which is a uniform
+ * random subset (the reference draws it with numpy's Generator.choice, a
+ * stream this cannot reproduce). Row nnz, row_start and capacities never
+ * change (a row regrows exactly what it dropped), so only `values` and
+ * `col_indices` — which must be W's own arrays — are written. ncols is at
+ * most 131072.                                                              */
+SLK_API int slk_drop_grow(const slk_csr* W, float* values, int32_t* col_indices,
+                          const float* thr_dev, int rule, const float* G, int64_t ldg,
+                          uint64_t seed, void* workspace, int64_t workspace_bytes,
+                          void* stream);
+
+/* G = dY·X^T, G is M x K row-major: G[i,k] = sum_j dY[i,j]·X[k,j], each
+ * element one running sum over j in order, with the arithmetic of the
+ * reference build (products of whole 4-element groups rounded, then added;
+ * the last N mod 4 terms fused). Replaces `_core.dense_grad`
+ * (csrc/bindings.cpp:445-485, csrc/kernels/dense_grad.cpp:24-84).
+ * token_major = 0: dY is M x N and X is K x N (the reference's layout);
+ * token_major = 1: dY is N x M and X is N x K (a layer's (tokens, features)
+ * activations, as RigL captures them), read without a transpose copy.     */
+SLK_API int slk_dense_grad(const float* dY, const float* X, int64_t M, int64_t K,
+                           int64_t N, int token_major, float* G, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,6 +23,9 @@ Contents
       refresh             sparselab/ops.py:83-94
       check_invariants    csrc/kernels/padded_csr.cpp:79-196
       rewrite_row         csrc/kernels/padded_csr.cpp:219-296
+      live_abs_kth        sparselab/router.py:394-412 (global drop threshold)
+      drop_grow           sparselab/router.py:414-478 (SET), :663-732 (RigL)
+      splitmix_keys       SET's grow keys (our generator; see drop_grow)
 
 How each function is pinned (see tests/test_oracle.py):
   spmm / sddmm / dense_grad — bit-exact against the reference build where it
@@ -35,6 +38,14 @@ How each function is pinned (see tests/test_oracle.py):
       (capacities [3, 3, 2], starts [0, 3, 6]) and round trips.
   check_invariants — message-for-message against the reference checker.
   rewrite_row — array-for-array against the reference's rewrite_row.
+  live_abs_kth — np.partition is the reference's own expression; also
+      against a full sort.
+  drop_grow — survivors against a literal per-row restatement of the
+      reference's keep rule; RigL grows against the reference's argpartition
+      choice (set equality where |G| has no ties at the cut) and its known
+      answer (column 15 grown); nnz, invariants and zero-init grows;
+      splitmix_keys against the generator's published first output; SET grow
+      uniformity by a chi-square test over seeds.
 """
 
 from __future__ import annotations
@@ -287,6 +298,81 @@ def rewrite_row(p: Csr, row: int, cols, vals) -> Csr:
 
 
 # ───────────────────────────── kernels (C) ─────────────────────────────
+
+
+def live_abs_kth(p: Csr, k: int) -> np.float32:
+    """k-th smallest |v| over the live slots (router.py:394-412)."""
+    live = np.concatenate([p.values[s:s + n] for s, n in zip(p.row_start, p.row_nnz)]
+                          + [np.zeros(0, np.float32)])
+    return np.partition(np.abs(live), k - 1)[k - 1]
+
+
+_GAMMA = np.uint64(0x9E3779B97F4A7C15)
+
+
+def splitmix_keys(seed: int, row: int, ncols: int, cols: np.ndarray) -> np.ndarray:
+    """32-bit grow keys of SET: the high half of splitmix64 output number
+    row*ncols + c + 1 of the stream seeded by ``seed`` (published generator:
+    Steele, Lea & Flood 2014; first output for seed 0 is 0xE220A8397B1DCDAF)."""
+    with np.errstate(over="ignore"):
+        idx = np.uint64(row) * np.uint64(ncols) + cols.astype(np.uint64) + np.uint64(1)
+        z = np.uint64(seed & (2**64 - 1)) + idx * _GAMMA
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        z = z ^ (z >> np.uint64(31))
+    return (z >> np.uint64(32)).astype(np.uint32)
+
+
+def _grow_keys_rigl(g_row: np.ndarray) -> np.ndarray:
+    """Smaller key = preferred: ~bits(|G|), NaN last."""
+    a = np.abs(g_row.astype(np.float32))
+    keys = ~a.view(np.uint32)
+    keys[np.isnan(a)] = np.uint32(0xFFFFFFFF)
+    return keys
+
+
+def drop_grow(p: Csr, k_drop: int, rule: str, G: np.ndarray | None = None,
+              seed: int = 0) -> Csr:
+    """One SET ("random") / RigL ("gradient") update of every row, on a copy.
+
+    Follows the per-row loop of router.py:414-478 (SET) and :663-732 (RigL):
+    keep |v| > threshold (the row's first largest |v| if none survive), grow
+    n_grow = min(dropped, ncols - kept) columns outside the kept set with
+    value 0, rewrite the row sorted by column. Grow choice: the n_grow
+    smallest keys, ties to the lower column; keys are ~bits(|G[i]|) (RigL:
+    largest |G| first) or splitmix_keys(seed, i, ...) (SET).
+    """
+    q = p.copy()
+    thr = live_abs_kth(p, k_drop)
+    all_cols = np.arange(p.ncols, dtype=np.int64)
+    for i in range(p.nrows):
+        s, n = int(p.row_start[i]), int(p.row_nnz[i])
+        if n == 0:
+            continue
+        cols = p.col_indices[s:s + n]
+        vals = p.values[s:s + n]
+        keep = np.abs(vals) > thr
+        if not keep.any():
+            keep[int(np.argmax(np.abs(vals)))] = True
+        kc, kv = cols[keep], vals[keep]
+        n_drop = n - int(keep.sum())
+        empty = np.setdiff1d(all_cols, kc.astype(np.int64))
+        n_grow = min(n_drop, empty.size)
+        if n_grow > 0:
+            if rule == "gradient":
+                keys = _grow_keys_rigl(G[i, empty])
+            else:
+                keys = splitmix_keys(seed, i, p.ncols, empty)
+            order = np.lexsort((empty, keys))  # by key, then column
+            grow = np.sort(empty[order[:n_grow]]).astype(np.int32)
+        else:
+            grow = np.zeros(0, np.int32)
+        mc = np.concatenate([kc, grow])
+        mv = np.concatenate([kv, np.zeros(grow.size, np.float32)])
+        o = np.argsort(mc, kind="stable")
+        q.col_indices[s:s + n] = mc[o]
+        q.values[s:s + n] = mv[o]
+    return q
 
 
 def spmm(p: Csr, X: np.ndarray, nthreads: int = 0) -> np.ndarray:

@@ -26,6 +26,8 @@ ABI_VERSION = 2
 SLK_OK, SLK_EINVAL, SLK_EDEVICE = 0, 1, 2
 SLK_DW_SIMD, SLK_DW_SCALAR = 0, 1
 SLK_CHECK_WORDS = 5
+SLK_KTH_WORKSPACE_BYTES = 8448
+SLK_GROW_RANDOM, SLK_GROW_GRADIENT = 0, 1
 
 # Every symbol include/sparsecore_amd.h declares.
 EXPORTS = (
@@ -38,6 +40,10 @@ EXPORTS = (
     "slk_transpose_fill",
     "slk_transpose_refresh",
     "slk_check_invariants",
+    "slk_live_abs_kth",
+    "slk_drop_grow_workspace_bytes",
+    "slk_drop_grow",
+    "slk_dense_grad",
 )
 
 
@@ -78,8 +84,16 @@ def _declare(lib) -> None:
     lib.slk_transpose_fill.argtypes = [_csrp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp]
     lib.slk_transpose_refresh.argtypes = [_vp, _i64, _vp, _i64, _vp, _vp]
     lib.slk_check_invariants.argtypes = [_csrp, _i64, _vp, _vp]
+    lib.slk_live_abs_kth.argtypes = [_csrp, _i64, _vp, _i64, _vp, _vp]
+    lib.slk_drop_grow_workspace_bytes.restype = _i64
+    lib.slk_drop_grow_workspace_bytes.argtypes = [_csrp]
+    lib.slk_drop_grow.argtypes = [_csrp, _vp, _vp, _vp, ctypes.c_int, _vp, _i64, ctypes.c_uint64,
+                                  _vp, _i64, _vp]
+    lib.slk_dense_grad.argtypes = [_vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp, _vp]
+    sized = ("slk_last_error", "slk_abi_version", "slk_transpose_workspace_bytes",
+             "slk_drop_grow_workspace_bytes")
     for name in EXPORTS:
-        if name not in ("slk_last_error", "slk_abi_version", "slk_transpose_workspace_bytes"):
+        if name not in sized:
             getattr(lib, name).restype = ctypes.c_int
 
 
@@ -183,5 +197,35 @@ def check_invariants(view: CsrView, col_len: int, result: torch.Tensor) -> None:
     lib = load()
     rc = lib.slk_check_invariants(ctypes.byref(view), col_len, result.data_ptr(),
                                   stream_of(result))
+    if rc:
+        _raise(rc)
+
+
+def live_abs_kth(view: CsrView, k: int, ws: torch.Tensor, thr: torch.Tensor) -> None:
+    lib = load()
+    rc = lib.slk_live_abs_kth(ctypes.byref(view), k, ws.data_ptr(), ws.numel(), thr.data_ptr(),
+                              stream_of(thr))
+    if rc:
+        _raise(rc)
+
+
+def drop_grow_workspace_bytes(view: CsrView) -> int:
+    return int(load().slk_drop_grow_workspace_bytes(ctypes.byref(view)))
+
+
+def drop_grow(view: CsrView, thr: torch.Tensor, rule: int, G: torch.Tensor | None, seed: int,
+              ws: torch.Tensor) -> None:
+    lib = load()
+    ldg = G.stride(0) if G is not None else 0
+    rc = lib.slk_drop_grow(ctypes.byref(view), view.values, view.col_indices, thr.data_ptr(), rule,
+                           ptr(G), ldg, seed & (2**64 - 1), ptr(ws), ws.numel(), stream_of(thr))
+    if rc:
+        _raise(rc)
+
+
+def dense_grad(dY: torch.Tensor, X: torch.Tensor, M: int, K: int, N: int, token_major: bool,
+               G: torch.Tensor) -> None:
+    lib = load()
+    rc = lib.slk_dense_grad(ptr(dY), ptr(X), M, K, N, int(token_major), ptr(G), stream_of(G))
     if rc:
         _raise(rc)

@@ -1,0 +1,535 @@
+// Topology mutation on the device: the drop/grow pass of SET and RigL, the
+// global drop threshold they share, and the dense gradient RigL ranks its
+// grow candidates by.
+//
+// Reference (sparselab/router.py:378-478 SET, :598-732 RigL): per layer,
+//   threshold = k-th smallest |v| over all live slots, k = max(1, int(f*nnz));
+//   per row: keep |v| > threshold (at least the largest slot), then grow as
+//   many columns as were dropped, outside the kept set, zero-initialised, and
+//   rewrite the row sorted by column (PaddedCSR.rewrite_row).
+// A row always regrows exactly what it dropped (ncols - kept >= dropped), so
+// row_nnz, row_start and the capacities never change: only the live parts of
+// col_indices and values are rewritten.
+//
+//   kth_*        radix select (digits of 11, 10, 10 bits) over the bit
+//                patterns of |v| of the live slots: for non-negative floats
+//                the unsigned order of the bits is the numeric order, so the
+//                result is exact. Three histogram launches plus three
+//                one-workgroup pick launches; no host synchronisation.
+//   drop_grow    one workgroup per row. Survivors and grows are marked in
+//                LDS bitmaps over the row's columns; grows are the n_grow
+//                smallest 32-bit keys among the unmarked columns (a per-row
+//                radix select with 8-bit digits, ties to the lower column).
+//                RigL keys are ~bits(|G|) (largest |G| first); SET keys are
+//                splitmix64 hashes (a uniform random subset). A column's new
+//                slot is its rank in the union bitmap; the row is staged in a
+//                workspace and copied back.
+//   dense_grad   128x128 output tile per workgroup, 8x8 per thread, j staged
+//                through LDS 16 at a time. Each output element is one running
+//                sum over j in order with the reference build's arithmetic.
+#include "common.hpp"
+
+namespace slk {
+namespace {
+
+// ───────────────────────── global k-th |value| ─────────────────────────────
+
+constexpr int kSelBins = 2048;
+constexpr int kSelThreads = 256;
+
+struct SelState {
+    uint32_t prefix;
+    uint32_t found;
+    int64_t need;
+    uint32_t hist[kSelBins];
+};
+static_assert(sizeof(SelState) <= SLK_KTH_WORKSPACE_BYTES, "workspace too small");
+
+// Digit p covers bits [shift, shift + width) of the 31-bit key (bit 31 of
+// |v| is always 0).
+__host__ __device__ constexpr int sel_shift(int p) { return p == 0 ? 20 : (p == 1 ? 10 : 0); }
+__host__ __device__ constexpr int sel_width(int p) { return p == 0 ? 11 : 10; }
+
+__global__ __launch_bounds__(kSelThreads) void kth_init_kernel(SelState* st, int64_t k) {
+    for (int b = threadIdx.x; b < kSelBins; b += kSelThreads) st->hist[b] = 0;
+    if (threadIdx.x == 0) {
+        st->prefix = 0;
+        st->found = 1;
+        st->need = k;
+    }
+}
+
+__global__ __launch_bounds__(kSelThreads) void kth_hist_kernel(
+    int64_t cap, const int32_t* __restrict__ col, const float* __restrict__ val,
+    SelState* __restrict__ st, int pass) {
+    __shared__ uint32_t h[kSelBins];
+    for (int b = threadIdx.x; b < kSelBins; b += kSelThreads) h[b] = 0;
+    __syncthreads();
+    const int shift = sel_shift(pass);
+    const uint32_t mask = (1u << sel_width(pass)) - 1u;
+    const uint32_t prefix = st->prefix;
+    const int hi = shift + sel_width(pass);
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kSelThreads;
+    for (int64_t s = static_cast<int64_t>(blockIdx.x) * kSelThreads + threadIdx.x; s < cap;
+         s += stride) {
+        if (col[s] < 0) continue;  // padding
+        const uint32_t u = __float_as_uint(fabsf(val[s]));
+        if (pass == 0 || (u >> hi) == prefix) atomicAdd(&h[(u >> shift) & mask], 1u);
+    }
+    __syncthreads();
+    for (int b = threadIdx.x; b < kSelBins; b += kSelThreads)
+        if (h[b] != 0) atomicAdd(&st->hist[b], h[b]);
+}
+
+// Inclusive scan of one int64 per thread over a 256-thread workgroup.
+__device__ int64_t block_inclusive_scan(int64_t v, int64_t* tmp) {
+    const int t = threadIdx.x;
+    tmp[t] = v;
+    __syncthreads();
+    for (int off = 1; off < static_cast<int>(blockDim.x); off <<= 1) {
+        const int64_t add = t >= off ? tmp[t - off] : 0;
+        __syncthreads();
+        tmp[t] += add;
+        __syncthreads();
+    }
+    const int64_t r = tmp[t];
+    __syncthreads();
+    return r;
+}
+
+__global__ __launch_bounds__(kSelThreads) void kth_pick_kernel(SelState* __restrict__ st, int pass,
+                                                              float* __restrict__ thr_out) {
+    __shared__ int64_t tmp[kSelThreads];
+    __shared__ uint32_t digit;
+    __shared__ int64_t below;
+    __shared__ int hit;
+    constexpr int kPer = kSelBins / kSelThreads;
+    const int t = threadIdx.x;
+    const int nbins = 1 << sel_width(pass);
+    int64_t local = 0;
+    for (int q = 0; q < kPer; ++q) {
+        const int b = t * kPer + q;
+        if (b < nbins) local += st->hist[b];
+    }
+    if (t == 0) hit = 0;
+    const int64_t incl = block_inclusive_scan(local, tmp);
+    const int64_t excl = incl - local;
+    const int64_t need = st->need;
+    if (excl < need && need <= incl) {
+        int64_t c = excl;
+        for (int q = 0; q < kPer; ++q) {
+            const int b = t * kPer + q;
+            const int64_t h = b < nbins ? st->hist[b] : 0;
+            if (c + h >= need) {
+                digit = static_cast<uint32_t>(b);
+                below = c;
+                hit = 1;
+                break;
+            }
+            c += h;
+        }
+    }
+    __syncthreads();
+    for (int b = t; b < kSelBins; b += kSelThreads) st->hist[b] = 0;
+    if (t == 0) {
+        if (!hit) st->found = 0;  // k exceeded the live count: caller's contract broken
+        const uint32_t p = hit ? ((st->prefix << sel_width(pass)) | digit) : st->prefix;
+        st->prefix = p;
+        st->need = need - (hit ? below : 0);
+        if (pass == 2) thr_out[0] = st->found ? __uint_as_float(p) : __builtin_nanf("");
+    }
+}
+
+// ───────────────────────── drop / grow ─────────────────────────────────────
+
+constexpr int kDgThreads = 256;
+constexpr int64_t kDgMaxCols = 131072;
+
+__device__ __forceinline__ uint32_t set_key(uint64_t seed, int64_t row, int64_t K, int64_t c) {
+    // splitmix64: output number (row*K + c + 1) of the stream seeded by `seed`
+    uint64_t z = seed + static_cast<uint64_t>(row * K + c + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return static_cast<uint32_t>(z >> 32);
+}
+
+template <bool RIGL>
+__device__ __forceinline__ uint32_t grow_key(const float* __restrict__ g_row, uint64_t seed,
+                                             int64_t row, int64_t K, int64_t c) {
+    if (RIGL) {
+        const float a = fabsf(g_row[c]);
+        if (a != a) return 0xFFFFFFFFu;  // NaN: least preferred
+        return ~__float_as_uint(a);
+    }
+    return set_key(seed, row, K, c);
+}
+
+__device__ __forceinline__ bool bit_of(const uint32_t* bm, int64_t c) {
+    return (bm[c >> 5] >> (c & 31)) & 1u;
+}
+
+template <bool RIGL>
+__global__ __launch_bounds__(kDgThreads) void drop_grow_kernel(
+    int64_t K, int64_t Kw, const int32_t* __restrict__ row_start,
+    const int32_t* __restrict__ row_nnz, float* __restrict__ values, int32_t* __restrict__ cols,
+    const float* __restrict__ thr_ptr, const float* __restrict__ G, int64_t ldg, uint64_t seed,
+    int32_t* __restrict__ stage_col, float* __restrict__ stage_val) {
+    extern __shared__ uint32_t lds[];
+    uint32_t* keep = lds;         // survivors
+    uint32_t* grow = lds + Kw;    // grown columns
+    uint32_t* wpre = lds + 2 * Kw;  // exclusive prefix of popcounts of keep|grow
+    __shared__ int64_t tmp[kDgThreads];
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t s_digit;
+    __shared__ int64_t s_below;
+    __shared__ unsigned long long s_best;
+
+    const int64_t i = blockIdx.x;
+    const int t = threadIdx.x;
+    const int32_t n_live = row_nnz[i];
+    if (n_live <= 0) return;  // the reference skips empty rows
+    const int32_t start = row_start[i];
+    const float thr = thr_ptr[0];
+
+    for (int64_t w = t; w < Kw; w += kDgThreads) keep[w] = grow[w] = 0;
+    if (t == 0) s_best = 0;
+    __syncthreads();
+
+    // Survivors: |v| strictly above the threshold.
+    int64_t kept = 0;
+    unsigned long long best = 0;
+    for (int32_t s = t; s < n_live; s += kDgThreads) {
+        const uint32_t u = __float_as_uint(fabsf(values[start + s]));
+        if (__uint_as_float(u) > thr) {
+            ++kept;
+            const int32_t c = cols[start + s];
+            atomicOr(&keep[c >> 5], 1u << (c & 31));
+        }
+        // np.argmax: largest |v| (NaN above all), first slot among equals
+        const unsigned long long key =
+            (static_cast<unsigned long long>(u) << 32) | (0xFFFFFFFFull - static_cast<uint32_t>(s));
+        if (key > best) best = key;
+    }
+    int64_t n_keep = block_inclusive_scan(kept, tmp);
+    n_keep = tmp[kDgThreads - 1];
+    __syncthreads();
+    if (n_keep == 0) {
+        atomicMax(&s_best, best);
+        __syncthreads();
+        if (t == 0) {
+            const int32_t s = static_cast<int32_t>(0xFFFFFFFFull - (s_best & 0xFFFFFFFFull));
+            const int32_t c = cols[start + s];
+            keep[c >> 5] |= 1u << (c & 31);
+        }
+        n_keep = 1;
+        __syncthreads();
+    }
+
+    const int64_t n_drop = n_live - n_keep;
+    const int64_t n_empty = K - n_keep;
+    const int64_t n_grow = n_drop < n_empty ? n_drop : n_empty;
+    const float* g_row = RIGL ? G + i * ldg : nullptr;
+
+    if (n_grow > 0) {
+        // Radix select of the n_grow smallest keys among unmarked columns.
+        uint32_t prefix = 0;
+        int64_t need = n_grow;
+        for (int pass = 0; pass < 4; ++pass) {
+            const int shift = 24 - 8 * pass;
+            hist[t] = 0;
+            __syncthreads();
+            for (int64_t c = t; c < K; c += kDgThreads) {
+                if (bit_of(keep, c)) continue;
+                const uint32_t u = grow_key<RIGL>(g_row, seed, i, K, c);
+                if (pass == 0 || (u >> (shift + 8)) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
+            }
+            __syncthreads();
+            const int64_t h = hist[t];
+            const int64_t incl = block_inclusive_scan(h, tmp);
+            if (incl - h < need && need <= incl) {
+                s_digit = static_cast<uint32_t>(t);
+                s_below = incl - h;
+            }
+            __syncthreads();
+            prefix = (prefix << 8) | s_digit;
+            need -= s_below;
+            __syncthreads();
+        }
+        // Take every key below the selected one and the first `need` columns
+        // (ascending) whose key equals it.
+        const uint32_t T = prefix;
+        int64_t taken_eq = 0;
+        for (int64_t c0 = 0; c0 < K; c0 += kDgThreads) {
+            const int64_t c = c0 + t;
+            bool lt = false, eq = false;
+            if (c < K && !bit_of(keep, c)) {
+                const uint32_t u = grow_key<RIGL>(g_row, seed, i, K, c);
+                lt = u < T;
+                eq = u == T;
+            }
+            const int64_t e = eq ? 1 : 0;
+            const int64_t incl = block_inclusive_scan(e, tmp);
+            const int64_t chunk_eq = tmp[kDgThreads - 1];
+            if (lt || (eq && taken_eq + incl - 1 < need)) atomicOr(&grow[c >> 5], 1u << (c & 31));
+            taken_eq += chunk_eq;
+            __syncthreads();
+        }
+        __syncthreads();
+    }
+
+    // Slot of column c in the new row = number of marked columns below c.
+    const int64_t per = ceil_div(Kw, kDgThreads);
+    const int64_t w0 = t * per;
+    const int64_t w1 = w0 + per < Kw ? w0 + per : Kw;
+    int64_t cnt = 0;
+    for (int64_t w = w0; w < w1; ++w) cnt += __popc(keep[w] | grow[w]);
+    const int64_t incl = block_inclusive_scan(cnt, tmp);
+    int64_t run = incl - cnt;
+    for (int64_t w = w0; w < w1; ++w) {
+        wpre[w] = static_cast<uint32_t>(run);
+        run += __popc(keep[w] | grow[w]);
+    }
+    __syncthreads();
+
+    auto rank_of = [&](int64_t c) -> int64_t {
+        const uint32_t word = keep[c >> 5] | grow[c >> 5];
+        const uint32_t below_mask = (c & 31) ? (0xFFFFFFFFu >> (32 - (c & 31))) : 0u;
+        return static_cast<int64_t>(wpre[c >> 5]) + __popc(word & below_mask);
+    };
+    for (int32_t s = t; s < n_live; s += kDgThreads) {
+        const int32_t c = cols[start + s];
+        if (bit_of(keep, c)) {
+            const int64_t p = start + rank_of(c);
+            stage_col[p] = c;
+            stage_val[p] = values[start + s];
+        }
+    }
+    for (int64_t w = t; w < Kw; w += kDgThreads) {
+        uint32_t bits = grow[w];
+        while (bits) {
+            const int b = __builtin_ctz(bits);
+            bits &= bits - 1;
+            const int64_t c = w * 32 + b;
+            const int64_t p = start + rank_of(c);
+            stage_col[p] = static_cast<int32_t>(c);
+            stage_val[p] = 0.0f;
+        }
+    }
+    __syncthreads();
+    for (int32_t s = t; s < n_live; s += kDgThreads) {
+        cols[start + s] = stage_col[start + s];
+        values[start + s] = stage_val[start + s];
+    }
+}
+
+// ───────────────────────── dense gradient ──────────────────────────────────
+
+constexpr int kGT = 128;  // output tile edge (rows of G and columns of G)
+constexpr int kGJ = 16;   // j values staged per step
+constexpr int kGThreads = 256;
+constexpr int kGPad = 4;
+
+// Stages a kGT x kGJ slab (rows r0.., j0..) of a matrix whose element (r, j)
+// sits at p[r*N + j] (TOKEN_MAJOR = false) or p[j*R + r] (TOKEN_MAJOR = true)
+// into s[j][r]. Out-of-range entries are staged as 0 and never summed.
+template <bool TOKEN_MAJOR>
+__device__ __forceinline__ void stage_slab(float (*s)[kGT + kGPad], const float* __restrict__ p,
+                                           int64_t R, int64_t N, int64_t r0, int64_t j0) {
+    const int t = threadIdx.x;
+    if (TOKEN_MAJOR) {
+        // consecutive threads read consecutive r of one j
+        const int r = t & (kGT - 1);
+        const int jb = t >> 7;  // 0..1
+#pragma unroll
+        for (int q = 0; q < kGJ / 2; ++q) {
+            const int j = jb + 2 * q;
+            const int64_t rr = r0 + r, jj = j0 + j;
+            s[j][r] = (rr < R && jj < N) ? p[jj * R + rr] : 0.0f;
+        }
+    } else {
+        // consecutive threads read consecutive j of one row
+        const int j = t & (kGJ - 1);
+        const int rb = t >> 4;  // 0..15
+#pragma unroll
+        for (int q = 0; q < kGT / 16; ++q) {
+            const int r = rb + 16 * q;
+            const int64_t rr = r0 + r, jj = j0 + j;
+            s[j][r] = (rr < R && jj < N) ? p[rr * N + jj] : 0.0f;
+        }
+    }
+}
+
+template <bool TOKEN_MAJOR>
+__global__ __launch_bounds__(kGThreads) void dense_grad_kernel(
+    int64_t M, int64_t K, int64_t N, int64_t N4, const float* __restrict__ dY,
+    const float* __restrict__ X, float* __restrict__ G) {
+    __shared__ float As[kGJ][kGT + kGPad];
+    __shared__ float Bs[kGJ][kGT + kGPad];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const int64_t i0 = static_cast<int64_t>(blockIdx.y) * kGT;
+    const int64_t k0 = static_cast<int64_t>(blockIdx.x) * kGT;
+
+    float acc[8][8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[r][c] = 0.0f;
+
+    for (int64_t j0 = 0; j0 < N; j0 += kGJ) {
+        stage_slab<TOKEN_MAJOR>(As, dY, M, N, i0, j0);
+        stage_slab<TOKEN_MAJOR>(Bs, X, K, N, k0, j0);
+        __syncthreads();
+        const int jn = N - j0 < kGJ ? static_cast<int>(N - j0) : kGJ;
+        // j < N4: product rounded, then added; j >= N4: fused (the reference
+        // build's evaluation of `acc += a*b`).
+        int jsplit = N4 - j0 < 0 ? 0 : (N4 - j0 > jn ? jn : static_cast<int>(N4 - j0));
+        for (int jj = 0; jj < jsplit; ++jj) {
+            float a[8], b[8];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) a[r] = As[jj][ty * 8 + r];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) b[c] = Bs[jj][tx * 8 + c];
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const float p = a[r] * b[c];
+                    acc[r][c] = acc[r][c] + p;
+                }
+        }
+        for (int jj = jsplit; jj < jn; ++jj) {
+            float a[8], b[8];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) a[r] = As[jj][ty * 8 + r];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) b[c] = Bs[jj][tx * 8 + c];
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) acc[r][c] = __builtin_fmaf(a[r], b[c], acc[r][c]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        const int64_t i = i0 + ty * 8 + r;
+        if (i >= M) break;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const int64_t k = k0 + tx * 8 + c;
+            if (k < K) G[i * K + k] = acc[r][c];
+        }
+    }
+}
+
+__global__ __launch_bounds__(kGThreads) void zero_kernel(float* __restrict__ p, int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kGThreads;
+    for (int64_t q = static_cast<int64_t>(blockIdx.x) * kGThreads + threadIdx.x; q < n; q += stride)
+        p[q] = 0.0f;
+}
+
+}  // namespace
+}  // namespace slk
+
+extern "C" int slk_live_abs_kth(const slk_csr* W, int64_t k, void* workspace,
+                                int64_t workspace_bytes, float* thr_dev, void* stream) {
+    using namespace slk;
+    clear_error();
+    if (int rc = validate_csr(W, "live_abs_kth")) return rc;
+    if (workspace == nullptr || workspace_bytes < SLK_KTH_WORKSPACE_BYTES)
+        return fail(SLK_EINVAL, "live_abs_kth: workspace smaller than SLK_KTH_WORKSPACE_BYTES");
+    if (thr_dev == nullptr) return fail(SLK_EINVAL, "live_abs_kth: NULL threshold output");
+    if (k < 1 || k > W->total_capacity)
+        return fail(SLK_EINVAL, "live_abs_kth: k=" + std::to_string(k) +
+                                    " outside [1, live slots]");
+    hipStream_t st = as_stream(stream);
+    SelState* s = static_cast<SelState*>(workspace);
+    hipLaunchKernelGGL(kth_init_kernel, dim3(1), dim3(kSelThreads), 0, st, s, k);
+    const int64_t cap = W->total_capacity;
+    int64_t blocks = ceil_div(cap, int64_t{kSelThreads} * 8);
+    if (blocks > 2048) blocks = 2048;
+    if (blocks < 1) blocks = 1;
+    for (int pass = 0; pass < 3; ++pass) {
+        hipLaunchKernelGGL(kth_hist_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kSelThreads),
+                           0, st, cap, W->col_indices, W->values, s, pass);
+        hipLaunchKernelGGL(kth_pick_kernel, dim3(1), dim3(kSelThreads), 0, st, s, pass, thr_dev);
+    }
+    return check_launch("live_abs_kth");
+}
+
+extern "C" int64_t slk_drop_grow_workspace_bytes(const slk_csr* W) {
+    if (W == nullptr || W->total_capacity < 0) return 0;
+    return W->total_capacity * 8;
+}
+
+extern "C" int slk_drop_grow(const slk_csr* W, float* values, int32_t* col_indices,
+                             const float* thr_dev, int rule, const float* G, int64_t ldg,
+                             uint64_t seed, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
+    using namespace slk;
+    clear_error();
+    if (int rc = validate_csr(W, "drop_grow")) return rc;
+    if (values != W->values || col_indices != W->col_indices)
+        return fail(SLK_EINVAL, "drop_grow: values/col_indices must be W's own arrays");
+    if (rule != SLK_GROW_RANDOM && rule != SLK_GROW_GRADIENT)
+        return fail(SLK_EINVAL, "drop_grow: unknown grow rule " + std::to_string(rule));
+    if (W->ncols > kDgMaxCols)
+        return fail(SLK_EINVAL, "drop_grow: ncols=" + std::to_string(W->ncols) +
+                                    " exceeds the supported maximum " + std::to_string(kDgMaxCols));
+    if (W->nrows == 0 || W->total_capacity == 0) return SLK_OK;
+    if (thr_dev == nullptr) return fail(SLK_EINVAL, "drop_grow: NULL threshold");
+    if (rule == SLK_GROW_GRADIENT && (G == nullptr || ldg < W->ncols))
+        return fail(SLK_EINVAL, "drop_grow: the gradient rule needs G with ldg >= ncols");
+    if (workspace == nullptr || workspace_bytes < W->total_capacity * 8)
+        return fail(SLK_EINVAL, "drop_grow: workspace smaller than slk_drop_grow_workspace_bytes");
+    if (W->nrows > INT32_MAX) return fail(SLK_EINVAL, "drop_grow: too many rows for one launch");
+    hipStream_t st = as_stream(stream);
+    const int64_t K = W->ncols;
+    const int64_t Kw = ceil_div(K, 32) > 0 ? ceil_div(K, 32) : 1;
+    const size_t lds = static_cast<size_t>(3 * Kw) * sizeof(uint32_t);
+    int32_t* stage_col = static_cast<int32_t*>(workspace);
+    float* stage_val = reinterpret_cast<float*>(stage_col + W->total_capacity);
+    const dim3 grid(static_cast<unsigned>(W->nrows));
+    if (rule == SLK_GROW_GRADIENT) {
+        hipLaunchKernelGGL(drop_grow_kernel<true>, grid, dim3(kDgThreads), lds, st, K, Kw,
+                           W->row_start, W->row_nnz, values, col_indices, thr_dev, G, ldg, seed,
+                           stage_col, stage_val);
+    } else {
+        hipLaunchKernelGGL(drop_grow_kernel<false>, grid, dim3(kDgThreads), lds, st, K, Kw,
+                           W->row_start, W->row_nnz, values, col_indices, thr_dev, G, ldg, seed,
+                           stage_col, stage_val);
+    }
+    return check_launch("drop_grow");
+}
+
+extern "C" int slk_dense_grad(const float* dY, const float* X, int64_t M, int64_t K, int64_t N,
+                              int token_major, float* G, void* stream) {
+    using namespace slk;
+    clear_error();
+    if (M < 0 || K < 0 || N < 0) return fail(SLK_EINVAL, "dense_grad: shape params must be non-negative");
+    if (M == 0 || K == 0) return SLK_OK;
+    if (G == nullptr) return fail(SLK_EINVAL, "dense_grad: NULL G");
+    hipStream_t st = as_stream(stream);
+    if (N == 0) {  // empty sums: G = 0 (a kernel, not a memset, so graph capture stays safe)
+        const int64_t n = M * K;
+        int64_t blocks = ceil_div(n, kGThreads);
+        if (blocks > 65536) blocks = 65536;
+        hipLaunchKernelGGL(zero_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kGThreads), 0, st,
+                           G, n);
+        return check_launch("dense_grad");
+    }
+    if (dY == nullptr || X == nullptr) return fail(SLK_EINVAL, "dense_grad: NULL dY or X");
+    const int64_t gx = ceil_div(K, kGT), gy = ceil_div(M, kGT);
+    if (gx > INT32_MAX || gy > 65535) return fail(SLK_EINVAL, "dense_grad: problem too large for one launch");
+    const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+    const int64_t N4 = N & ~int64_t{3};
+    if (token_major) {
+        hipLaunchKernelGGL(dense_grad_kernel<true>, grid, dim3(kGThreads), 0, st, M, K, N, N4, dY,
+                           X, G);
+    } else {
+        hipLaunchKernelGGL(dense_grad_kernel<false>, grid, dim3(kGThreads), 0, st, M, K, N, N4, dY,
+                           X, G);
+    }
+    return check_launch("dense_grad");
+}

@@ -466,6 +466,31 @@ class PaddedCSR:
         self._topology_version += 1
         self._cview = None  # the row schedule depends on row_nnz
 
+    def _drop_grow(self, k_drop: int, rule: int, G: torch.Tensor | None = None,
+                   seed: int = 0) -> None:
+        """One SET / RigL drop-and-grow pass over every row, on the device.
+
+        Drops the live slots with |v| <= the k_drop-th smallest live |v| (each
+        row keeps at least its largest slot), regrows as many columns per row
+        (RigL: largest |G| first; SET: a uniform random subset keyed by
+        ``seed``), zero-initialised, rows rewritten sorted by column. Row nnz
+        and capacities do not change. Bumps ``topology_version``.
+        """
+        self._require_device("drop_grow")
+        if not 1 <= k_drop <= self._nnz:
+            raise ValueError(f"drop_grow: k_drop={k_drop} outside [1, nnz={self._nnz}]")
+        dev = self._values.device
+        view = self._view()
+        ws = torch.empty(_lib.SLK_KTH_WORKSPACE_BYTES, dtype=torch.uint8, device=dev)
+        thr = torch.empty(1, dtype=_F32, device=dev)
+        _lib.live_abs_kth(view, k_drop, ws, thr)
+        stage = torch.empty(_lib.drop_grow_workspace_bytes(view), dtype=torch.uint8, device=dev)
+        _lib.drop_grow(view, thr, rule, G, seed, stage)
+        # row_nnz is unchanged, so the cached row schedule stays valid
+        self._topology_version += 1
+        if self._order is not None:
+            self._order = (self._topology_version, self._order[1])
+
     # ─── device movement ───────────────────────────────────────────
     def to(self, device) -> "PaddedCSR":
         device = torch.device(device)

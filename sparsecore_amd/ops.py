@@ -26,7 +26,7 @@ import torch
 from . import _lib
 from .layout import PaddedCSR, transpose_with_perm
 
-__all__ = ["spmm"]
+__all__ = ["spmm", "dense_grad"]
 
 _KERNELS = ("auto", "simd", "scalar")
 
@@ -160,3 +160,42 @@ def spmm(W: PaddedCSR, X: torch.Tensor, *, kernel: str = "auto") -> torch.Tensor
     if X_f32.requires_grad or W_values_t.requires_grad:
         return _SpMMFunction.apply(W_values_t, W, X_f32, kernel)
     return _launch_spmm(W, X_f32)
+
+
+def dense_grad(dY: torch.Tensor, X: torch.Tensor) -> torch.Tensor:
+    """G = dY @ Xᵀ (M x K) for dense dY (M x N) and X (K x N) on the GPU.
+
+    Mirrors ``_core.dense_grad`` (csrc/bindings.cpp:445-485): 2-D inputs,
+    converted to contiguous float32, ValueError on a rank or inner-dimension
+    mismatch with the reference's message. Every element is the reference
+    build's running sum over N in order, so G is bit-identical to
+    csrc/kernels/dense_grad.cpp:57-83.
+    """
+    for name, t in (("dY", dY), ("X", X)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"dense_grad: {name} must be a torch.Tensor, got {type(t).__name__}")
+        if t.dim() != 2:
+            raise ValueError(f"dense_grad: {name} must be 2-D, got ndim={t.dim()}.")
+        if t.device.type != "cuda":
+            raise RuntimeError(f"dense_grad: {name} must be on a HIP (ROCm) device "
+                               f"(got device={t.device}).")
+    if dY.device != X.device:
+        raise RuntimeError(f"dense_grad: dY is on {dY.device} but X is on {X.device}")
+    M, N = dY.shape
+    K, N_x = X.shape
+    if N != N_x:
+        raise ValueError(f"dense_grad: dY.shape[1]={N} must equal X.shape[1]={N_x} "
+                         f"(shared inner dim N).")
+    G = torch.empty((M, K), dtype=torch.float32, device=dY.device)
+    _lib.dense_grad(_device_f32(dY), _device_f32(X), M, K, N, False, G)
+    return G
+
+
+def _dense_grad_token_major(dy: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """G = dyᵀ @ x for token-major dy (N x M) and x (N x K): the same G as
+    ``dense_grad(dy.t(), x.t())``, bit for bit, without the transpose copies."""
+    N, M = dy.shape
+    K = x.shape[1]
+    G = torch.empty((M, K), dtype=torch.float32, device=dy.device)
+    _lib.dense_grad(_device_f32(dy), _device_f32(x), M, K, N, True, G)
+    return G

@@ -84,3 +84,30 @@ def test_transpose_workspace_is_bounded(M, K, expect_rows_per_block):
     nblk = -(-M // expect_rows_per_block)
     assert nbytes == nblk * K * 4
     assert nbytes <= (1 << 24) * 4
+
+
+def test_topology_entry_points_check_arguments_on_the_host():
+    lib = _lib.load()
+    # fake, never dereferenced slot pointers: every call fails validation first
+    v = _lib.CsrView(4, 6, 10, 8, 8, 1, 1, 1)
+    rc = lib.slk_live_abs_kth(ctypes.byref(v), 3, None, 0, None, None)
+    assert rc == _lib.SLK_EINVAL and "workspace" in lib.slk_last_error().decode()
+    rc = lib.slk_live_abs_kth(ctypes.byref(v), 0, 1, _lib.SLK_KTH_WORKSPACE_BYTES, 1, None)
+    assert rc == _lib.SLK_EINVAL and "k=0" in lib.slk_last_error().decode()
+    rc = lib.slk_drop_grow(ctypes.byref(v), 16, 8, 1, 0, None, 0, 0, None, 0, None)
+    assert rc == _lib.SLK_EINVAL and "own arrays" in lib.slk_last_error().decode()
+    rc = lib.slk_drop_grow(ctypes.byref(v), 8, 8, 1, 5, None, 0, 0, None, 0, None)
+    assert rc == _lib.SLK_EINVAL and "rule" in lib.slk_last_error().decode()
+    wide = _lib.CsrView(4, 200000, 10, 8, 8, 1, 1, 1)
+    rc = lib.slk_drop_grow(ctypes.byref(wide), 8, 8, 1, 0, None, 0, 0, None, 0, None)
+    assert rc == _lib.SLK_EINVAL and "ncols" in lib.slk_last_error().decode()
+    rc = lib.slk_drop_grow(ctypes.byref(v), 8, 8, 1, _lib.SLK_GROW_GRADIENT, None, 0, 0,
+                           None, 0, None)
+    assert rc == _lib.SLK_EINVAL and "ldg" in lib.slk_last_error().decode()
+    rc = lib.slk_drop_grow(ctypes.byref(v), 8, 8, 1, _lib.SLK_GROW_RANDOM, None, 0, 0,
+                           None, 79, None)
+    assert rc == _lib.SLK_EINVAL and "workspace" in lib.slk_last_error().decode()
+    assert lib.slk_drop_grow_workspace_bytes(ctypes.byref(v)) == 80
+    rc = lib.slk_dense_grad(None, None, -1, 2, 2, 0, None, None)
+    assert rc == _lib.SLK_EINVAL and "non-negative" in lib.slk_last_error().decode()
+    assert lib.slk_dense_grad(None, None, 0, 5, 4, 0, None, None) == _lib.SLK_OK

@@ -49,11 +49,15 @@ def test_spmm_matches_dense_matmul(dev, M, K, N, sparsity):
     if M * K < 4 and sparsity >= 0.9:
         pytest.skip("not enough cells for >=90% sparsity")
     W, Wd = _W(M, K, sparsity, 42, dev)
-    X = torch.randn(K, N, device=dev)
+    X = torch.randn(K, N, generator=torch.Generator().manual_seed(M * K + N)).to(dev)
     Y = slk.spmm(W, X)
     assert Y.shape == (M, N) and Y.dtype == torch.float32 and Y.device == X.device
-    Y_ref = (Wd.double() @ X.double()).float()
-    assert torch.allclose(Y, Y_ref, rtol=1e-5, atol=1e-5)
+    # float64 product; the float32 chain's error is bounded relative to the
+    # sum of |terms| (a plain rtol=1e-5 is too tight where terms cancel)
+    Y64 = Wd.double() @ X.double()
+    bound = 1e-5 * (Wd.double().abs() @ X.double().abs()) + 1e-6
+    err = (Y.double() - Y64).abs()
+    assert bool((err <= bound).all()), f"max err {err.max().item():.3e}"
     # and bit-exact against the reference arithmetic
     assert_bits_equal(Y.cpu().numpy(), oracle.spmm(to_oracle(W), X.cpu().numpy()), "Y")
 
