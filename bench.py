@@ -49,7 +49,9 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c5-95", "c5-99"])
+    ap.add_argument("--workload", default="c2",
+                    choices=["c1", "c2", "c3", "c4", "c5-95", "c5-99", "c5-95-rigl",
+                             "c5-99-rigl"])
     ap.add_argument("--no-graph", action="store_true", help="time eager launches")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -222,36 +224,39 @@ class C2:
         return self.l1._csr
 
 
-# ───────────────────────────── workload C3 ───────────────────────────────────
+# ─────────────────────────── workloads C3 / C4 ───────────────────────────────
 
-class C3:
-    """BASELINE configs[2]: 10M-param char-level decoder, d_model 384, 6 layers,
-    6 heads, FFN 1536, vocab 65, context 256, batch 32 (8192 tokens), fp32.
-    Attention projections (fused QKV 384->1152 and O 384->384, as the
-    reference's demo_15_mini_gpt.py builds them) are SparseLinear at 70%; FFN
-    up/down are SparseLinear at 90%; embeddings, LayerNorms and the LM head
-    are dense. One step = forward + backward (no optimizer step, as the
-    config specifies); value = tokens / s."""
+class GPTWork:
+    """Char-level decoder-only transformer with SparseLinear projections.
 
-    name = "c3"
-    d_model, n_layers, n_heads, d_ff, vocab, ctx, batch = 384, 6, 6, 1536, 65, 256, 32
-    desc = ("10M char GPT: d384 6L 6H FFN1536 vocab65 ctx256 batch32 (8192 tokens), fp32; "
-            "QKV/O SparseLinear 70%, FFN SparseLinear 90%; forward+backward")
+    Attention projections (fused QKV D->3D and O D->D, as the reference's
+    demo_15_mini_gpt.py builds them) are SparseLinear at `attn_sparsity`; FFN
+    up/down are SparseLinear at `ffn_sparsity`; embeddings, LayerNorms and the
+    LM head are dense. Subclasses fix the configuration."""
 
-    def __init__(self, dev, seed):
+    name = desc = ""
+    d_model = n_layers = n_heads = d_ff = vocab = ctx = batch = 0
+    attn_sparsity, ffn_sparsity = 0.7, 0.9
+    train = False       # SGD step (lr 0.01) inside the step
+    set_update = False  # SET drop/regrow + device transpose rebuild inside the step
+    dynamic = False     # topology changes every step (no graph capture)
+
+    def __init__(self, dev, seed, with_set: bool = True):
         import torch
         import torch.nn as nn
         import torch.nn.functional as F
 
         import sparsecore_amd as slk
 
-        D, H = self.d_model, self.n_heads
+        cfg = type(self)
+        D, H, d_ff, ctx, vocab = cfg.d_model, cfg.n_heads, cfg.d_ff, cfg.ctx, cfg.vocab
+        sa, sf = cfg.attn_sparsity, cfg.ffn_sparsity
 
         class Attn(nn.Module):
             def __init__(self):
                 super().__init__()
-                self.qkv = slk.SparseLinear(D, 3 * D, sparsity=0.7, bias=False)
-                self.o = slk.SparseLinear(D, D, sparsity=0.7, bias=False)
+                self.qkv = slk.SparseLinear(D, 3 * D, sparsity=sa, bias=False)
+                self.o = slk.SparseLinear(D, D, sparsity=sa, bias=False)
 
             def forward(self, x):
                 B, T, C = x.shape
@@ -262,29 +267,27 @@ class C3:
                 a = F.scaled_dot_product_attention(q, k, v, is_causal=True)
                 return self.o(a.transpose(1, 2).reshape(B, T, C))
 
-        d_ff = self.d_ff
-
         class Block(nn.Module):
             def __init__(self):
                 super().__init__()
                 self.ln1 = nn.LayerNorm(D)
                 self.attn = Attn()
                 self.ln2 = nn.LayerNorm(D)
-                self.up = slk.SparseLinear(D, d_ff, sparsity=0.9, bias=False)
-                self.down = slk.SparseLinear(d_ff, D, sparsity=0.9, bias=False)
+                self.up = slk.SparseLinear(D, d_ff, sparsity=sf, bias=False)
+                self.down = slk.SparseLinear(d_ff, D, sparsity=sf, bias=False)
 
             def forward(self, x):
                 x = x + self.attn(self.ln1(x))
                 return x + self.down(F.gelu(self.up(self.ln2(x))))
 
-        ctx, vocab = self.ctx, self.vocab
+        n_layers = cfg.n_layers
 
         class GPT(nn.Module):
             def __init__(self):
                 super().__init__()
                 self.tok = nn.Embedding(vocab, D)
                 self.pos = nn.Embedding(ctx, D)
-                self.blocks = nn.ModuleList([Block() for _ in range(C3.n_layers)])
+                self.blocks = nn.ModuleList([Block() for _ in range(n_layers)])
                 self.ln_f = nn.LayerNorm(D)
                 self.head = nn.Linear(D, vocab, bias=False)
 
@@ -301,6 +304,11 @@ class C3:
         self.idx = torch.randint(0, vocab, (self.batch, ctx), generator=g).to(dev)
         self.tgt = torch.randint(0, vocab, (self.batch, ctx), generator=g).to(dev)
         self.dev = dev
+        self.opt = torch.optim.SGD(self.model.parameters(), lr=0.01) if cfg.train else None
+        self.algo = None
+        if cfg.set_update and with_set:
+            self.algo = slk.SET(sparsity=sf, drop_fraction=0.3, update_freq=1, seed=seed)
+            self.model.apply(self.algo)
 
     def body(self):
         import torch.nn.functional as F
@@ -310,7 +318,19 @@ class C3:
         logits = self.model(self.idx)
         loss = F.cross_entropy(logits.reshape(-1, self.vocab), self.tgt.reshape(-1))
         loss.backward()
+        if self.opt is not None:
+            self.opt.step()
+        if self.algo is not None:
+            self.topology_update()
         return loss.detach()
+
+    def topology_update(self):
+        """SET on every sparse layer, then each layer's transpose rebuilt on the device."""
+        from sparsecore_amd import ops
+
+        self.algo.step()
+        for layer in self.algo.layers:
+            ops._cached_transpose(layer._csr)
 
     def params(self):
         return list(self.model.parameters())
@@ -323,7 +343,7 @@ class C3:
         return [("qkv", b.attn.qkv), ("o", b.attn.o), ("up", b.up), ("down", b.down)]
 
     def kernels(self):
-        """The HIP kernels of block 0's four sparse layers at N = 8192 tokens."""
+        """The HIP kernels of block 0's four sparse layers at N = batch*ctx tokens."""
         import torch
 
         from sparsecore_amd import _lib, ops
@@ -351,6 +371,57 @@ class C3:
 
     def spmm_layer(self):
         return self.model.blocks[0].up._csr
+
+
+class C3(GPTWork):
+    """BASELINE configs[2]: 10M-param char-level decoder, d_model 384, 6 layers,
+    6 heads, FFN 1536, vocab 65, context 256, batch 32 (8192 tokens), fp32,
+    QKV/O at 70%, FFN at 90%. One step = forward + backward (no optimizer
+    step, as the config specifies); value = tokens / s."""
+
+    name = "c3"
+    d_model, n_layers, n_heads, d_ff, vocab, ctx, batch = 384, 6, 6, 1536, 65, 256, 32
+    desc = ("10M char GPT: d384 6L 6H FFN1536 vocab65 ctx256 batch32 (8192 tokens), fp32; "
+            "QKV/O SparseLinear 70%, FFN SparseLinear 90%; forward+backward")
+
+
+class C4(GPTWork):
+    """60M-param mini-GPT, d_model 768, 8 layers, 12 heads,
+    FFN 3072, vocab 65, context 512, batch 16 (8192 tokens), fp32, attention
+    projections at 70%, FFN at 90%. One step = forward, backward, SGD update
+    (lr 0.01), then one SET rewrite of every sparse layer (drop the 30%
+    smallest |w| per layer, regrow at uniform-random empty columns, zero-init)
+    and the device transpose rebuild of every layer. value = tokens / s."""
+
+    name = "c4"
+    d_model, n_layers, n_heads, d_ff, vocab, ctx, batch = 768, 8, 12, 3072, 65, 512, 16
+    train = set_update = dynamic = True
+    desc = ("60M mini-GPT: d768 8L 12H FFN3072 vocab65 ctx512 batch16 (8192 tokens), fp32; "
+            "QKV/O SparseLinear 70%, FFN SparseLinear 90%; forward+backward+SGD, then SET "
+            "(drop 30% smallest |w| per layer, uniform regrow) + device transpose rebuild "
+            "every step")
+
+    def kernels(self):
+        """Block 0's SpMM/SDDMM kernels plus one layer's topology update."""
+        from sparsecore_amd import _lib, ops
+
+        out = super().kernels()
+        W = self.model.blocks[0].up._csr
+        k = max(1, int(0.3 * W.nnz))
+        seed = [0]
+
+        def set_up():
+            seed[0] += 1
+            W._drop_grow(k, _lib.SLK_GROW_RANDOM, None, seed[0])
+
+        def rebuild():
+            ops._transpose_cache.pop(id(W), None)
+            ops._cached_transpose(W)
+
+        out.append(("set_drop_grow[up 3072x768]", set_up, 0, 0))
+        out.append(("transpose_rebuild[up 3072x768]", rebuild,
+                    8 * W.nrows + 8 * W.nnz + 16 * int(1.2 * W.nnz + W.ncols) + 12 * W.ncols, 0))
+        return out
 
 
 # ───────────────────────── single-layer workloads (C1, C5) ────────────────────
@@ -413,13 +484,14 @@ class LayerWork:
     """One SparseLinear-shaped layer: Y = W·X, dW = SDDMM(dY, X), dX = Wᵀ·dY via
     the cached transpose (refresh + SpMM) — the three kernels of the path."""
 
-    def __init__(self, name, desc, W, X, dY):
+    def __init__(self, name, desc, W, X, dY, rigl: bool = False):
         import torch
 
         from sparsecore_amd import ops
 
         self.name, self.desc = name, desc
         self.W, self.X, self.dY = W, X, dY
+        self.rigl = self.dynamic = rigl
         self.M, self.K = W.nrows, W.ncols
         self.N = X.shape[1]
         self.dev = X.device
@@ -436,7 +508,19 @@ class LayerWork:
         dW = ops._launch_sddmm(self.W, self.dY, self.X, "simd")
         WT = ops._cached_transpose(self.W)
         dX = ops._launch_spmm(WT, self.dY)
+        if self.rigl:
+            self.topology_update()
         return Y, dW, dX
+
+    def topology_update(self):
+        """RigL: G = dY·Xᵀ, drop the 30% smallest |w|, regrow at the top-|G|
+        dead positions, then rebuild the transpose on the device."""
+        from sparsecore_amd import _lib, ops
+
+        G = ops.dense_grad(self.dY, self.X)
+        self.W._drop_grow(max(1, int(0.3 * self.W.nnz)), _lib.SLK_GROW_GRADIENT, G)
+        del G
+        ops._cached_transpose(self.W)
 
     def params(self):
         return []
@@ -477,6 +561,29 @@ class LayerWork:
              bytes_refresh(W.nnz, WT.total_capacity), 0),
             ("spmm_dx", lambda: _lib.spmm(vT, self.dY, dX), bytes_fwd(W.nnz, K, M, N),
              flops(W.nnz, N)),
+        ] + (self._rigl_kernels() if self.rigl else [])
+
+    def _rigl_kernels(self):
+        import torch
+
+        from sparsecore_amd import _lib, ops
+
+        W = self.W
+        M, K, N = self.M, self.K, self.N
+        G = torch.empty(M, K, device=self.dev)
+        k = max(1, int(0.3 * W.nnz))
+        Gd = ops.dense_grad(self.dY, self.X)
+
+        def rebuild():
+            ops._transpose_cache.pop(id(W), None)
+            ops._cached_transpose(W)
+
+        return [
+            ("dense_grad", lambda: _lib.dense_grad(self.dY, self.X, M, K, N, False, G),
+             4 * (M * N + K * N + M * K), 2 * M * K * N),
+            ("rigl_drop_grow", lambda: W._drop_grow(k, _lib.SLK_GROW_GRADIENT, Gd), 0, 0),
+            ("transpose_rebuild", rebuild,
+             8 * M + 8 * W.nnz + 16 * int(1.2 * W.nnz + K) + 12 * K, 0),
         ]
 
 
@@ -499,7 +606,7 @@ def make_c1(dev, seed):
                      W, X, dY)
 
 
-def make_c5(dev, seed, density):
+def make_c5(dev, seed, density, rigl=False):
     import torch
 
     M = K = 16384
@@ -511,9 +618,12 @@ def make_c5(dev, seed, density):
     X = torch.randn(K, N, generator=g, device=dev)
     dY = torch.randn(M, N, generator=g, device=dev)
     pct = int(round(100 * (1 - density)))
-    return LayerWork(f"c5-{pct}",
+    extra = ("; step = fwd + dW + dX + RigL rewrite (G = dY.X^T, drop 30% smallest |w|, "
+             "regrow at top-|G| dead positions) + device transpose rebuild") if rigl else ""
+    return LayerWork(f"c5-{pct}" + ("-rigl" if rigl else ""),
                      f"16384x16384 at {pct}% sparsity, Zipf(1.1) rows (max {int(counts.max())}, "
-                     f"min {int(counts.min())}), values N(0,0.01), N=4096", W, X, dY)
+                     f"min {int(counts.min())}), values N(0,0.01), N=4096" + extra, W, X, dY,
+                     rigl=rigl)
 
 
 # ───────────────────────────── CPU baseline ──────────────────────────────────
@@ -562,6 +672,35 @@ def cpu_baseline(work, seconds: float):
                 self.r.sddmm_into(dY, X, dW)
                 return dW
             return oracle.sddmm(self.c, dY, X)
+
+        def set_update(self, rng):
+            self.topo_update("random", seed=int(rng.integers(0, 2**63)))
+
+        def topo_update(self, rule, seed=0, G=None):
+            """SET / RigL on this layer (router.py:378-478 / :598-732 restated in
+            oracle.drop_grow), rows written back through the reference's
+            rewrite_row, then the transpose rebuilt (layout.py:460-536 restated)."""
+            if kind == "reference":
+                vals, cols, nnz, _ = self.r.arrays()
+                c = oracle.Csr(self.c.nrows, self.c.ncols, vals, cols, self.c.row_start, nnz,
+                               self.c.row_capacity)
+            else:
+                c = self.c
+            q = oracle.drop_grow(c, max(1, int(0.3 * c.nnz)), rule, G=G, seed=seed)
+            if kind == "reference":
+                for i in range(q.nrows):
+                    s0, n = int(q.row_start[i]), int(q.row_nnz[i])
+                    if n:
+                        self.r.rewrite_row(i, q.col_indices[s0:s0 + n], q.values[s0:s0 + n])
+                self.c = q
+                WT, self.perm = oracle.transpose_with_perm(q)
+                self.rt = oracle.RefCsr(WT)
+                self.wt_values = self.rt.values_view()
+            else:
+                self.c.col_indices[:] = q.col_indices
+                self.c.values[:] = q.values
+                self.WT, self.perm = oracle.transpose_with_perm(self.c)
+            self.live = self.perm >= 0
 
         def dx(self, dY):
             # cache hit: refresh WT values through perm (ops.py:83-94), then SpMM
@@ -617,10 +756,13 @@ def cpu_baseline(work, seconds: float):
             else:
                 swap_sparse(child)
 
-    if isinstance(work, (C2, C3)):
+    if isinstance(work, (C2, GPTWork)):
         # same seed on the CPU: identical weights and inputs, then the
         # SparseLinear layers run on the reference kernels
-        host = type(work)(torch.device("cpu"), work.seed)
+        if isinstance(work, GPTWork):
+            host = type(work)(torch.device("cpu"), work.seed, with_set=False)
+        else:
+            host = type(work)(torch.device("cpu"), work.seed)
         swap_sparse(host.model)
         if isinstance(work, C2):
             opt = torch.optim.SGD(host.model.parameters(), lr=0.01)
@@ -633,16 +775,34 @@ def cpu_baseline(work, seconds: float):
 
             sample = "C2 train steps (MLP 784->512->10, batch 256)"
         else:
+            opt = torch.optim.SGD(host.model.parameters(), lr=0.01) if work.train else None
+            refs = [m for m in host.model.modules() if isinstance(m, RefLinear)]
+            set_rng = np.random.default_rng(work.seed)
+
             def step():
                 for prm in host.model.parameters():
                     prm.grad = None
                 logits = host.model(host.idx)
                 torch.nn.functional.cross_entropy(logits.reshape(-1, host.vocab),
                                                   host.tgt.reshape(-1)).backward()
+                if opt is not None:
+                    opt.step()
+                if work.set_update:
+                    for rl in refs:
+                        rl.hl.set_update(set_rng)
 
-            sample = "C3 forward+backward steps (10M char GPT, 8192 tokens)"
+            if work.set_update:
+                sample = (f"{work.name.upper()} train steps (fwd+bwd+SGD on the reference kernels; "
+                          f"SET on {len(refs)} layers: numpy restatement of router.py with the "
+                          f"reference's rewrite_row; numpy transpose rebuild), "
+                          f"{work.tokens_per_step()} tokens")
+            else:
+                sample = (f"{work.name.upper()} forward+backward steps, "
+                          f"{work.tokens_per_step()} tokens")
         unit_per_step = work.tokens_per_step()
         unit = "tokens/s"
+    elif work.rigl:
+        return _cpu_rigl_sample(work, HostLayer, kind, threads, seconds)
     else:
         hl = HostLayer(work.W)
         X = work.X.cpu().numpy()
@@ -675,6 +835,59 @@ def cpu_baseline(work, seconds: float):
                       f"ms/step={1e3 * dt / n:.3f}"}
 
 
+def _cpu_rigl_sample(work, HostLayer, kind, threads, seconds):
+    """C5 RigL step on the host, sampled on the first 1/16 of W's rows (the
+    rows are a random permutation of the Zipf ranks): fwd + dW + dX on the
+    reference kernels, the reference's dense_grad, the RigL rewrite and the
+    transpose rebuild. Each part's time is scaled to the full layer (kernel
+    and rewrite parts by the nnz ratio, dense_grad by the row ratio)."""
+    import types
+
+    import oracle
+
+    W = work.W
+    M, K, N = work.M, work.K, work.N
+    Ms = max(1, M // 16)
+    end = int(W.row_start[Ms].item()) if Ms < M else W.total_capacity
+    sl = types.SimpleNamespace(nrows=Ms, ncols=K, values=W.values[:end],
+                               col_indices=W.col_indices[:end], row_start=W.row_start[:Ms],
+                               row_nnz=W.row_nnz[:Ms], row_capacity=W.row_capacity[:Ms])
+    hl = HostLayer(sl)
+    nnz_s = hl.c.nnz
+    X = work.X.cpu().numpy()
+    dY = work.dY[:Ms].cpu().numpy()
+    dense = oracle.ref_dense_grad if kind == "reference" else oracle.dense_grad
+    t_k = t_g = t_u = 0.0
+    n = 0
+    t_all = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        hl.fwd(X)
+        hl.dw(dY, X)
+        hl.dx(dY)
+        t1 = time.perf_counter()
+        G = dense(dY, X)
+        t2 = time.perf_counter()
+        hl.topo_update("gradient", G=G)
+        t3 = time.perf_counter()
+        if n > 0:  # the first step is the warmup
+            t_k += t1 - t0
+            t_g += t2 - t1
+            t_u += t3 - t2
+        n += 1
+        if n >= 3 and time.perf_counter() - t_all > seconds:
+            break
+    steps = n - 1
+    r_nnz, r_rows = W.nnz / max(nnz_s, 1), M / Ms
+    est = (t_k * r_nnz + t_g * r_rows + t_u * r_nnz) / steps
+    return {"value": N / est, "unit": "tokens/s", "cores": threads, "kind": kind,
+            "sample": f"{steps} RigL steps on rows 0..{Ms - 1} of {M} (nnz {nnz_s} of {W.nnz}), "
+                      f"scaled to the full layer: fwd+dW+dX {1e3 * t_k / steps:.1f} ms x "
+                      f"{r_nnz:.2f}, dense_grad {1e3 * t_g / steps:.1f} ms x {r_rows:.0f}, "
+                      f"rewrite+rebuild {1e3 * t_u / steps:.1f} ms x {r_nnz:.2f} = "
+                      f"{1e3 * est:.0f} ms/step, OpenMP threads={threads}"}
+
+
 # ───────────────────────────── main ──────────────────────────────────────────
 
 def main():
@@ -697,17 +910,20 @@ def main():
         work = C2(dev, args.seed)
     elif args.workload == "c3":
         work = C3(dev, args.seed)
+    elif args.workload == "c4":
+        work = C4(dev, args.seed)
     elif args.workload == "c1":
         work = make_c1(dev, args.seed)
     else:
-        work = make_c5(dev, args.seed, 0.05 if args.workload == "c5-95" else 0.01)
+        work = make_c5(dev, args.seed, 0.05 if args.workload.startswith("c5-95") else 0.01,
+                       rigl=args.workload.endswith("rigl"))
 
     stage("eager warmup")
     for _ in range(max(1, args.warmup)):
         work.body()
     torch.cuda.synchronize()
 
-    use_graph = not args.no_graph
+    use_graph = not args.no_graph and not getattr(work, "dynamic", False)
     graph_ok = False
     if use_graph:
         params = work.params()
@@ -752,6 +968,11 @@ def main():
     stage(f"timed region: {args.steps} steps (graph={graph_ok if use_graph else False})")
     elapsed = timed_loop(step, args.steps)
     ms_per_step = 1e3 * elapsed / args.steps
+    topo_ms = 0.0
+    if getattr(work, "algo", None) is not None or getattr(work, "rigl", False):
+        stage("topology update timing (SET/RigL + transpose rebuild)")
+        reps = 5
+        topo_ms = 1e3 * timed_loop(work.topology_update, reps) / reps
 
     kern = []
     for name, fn, nbytes, nflops in work.kernels():
@@ -759,7 +980,9 @@ def main():
         ms = kernel_avg_ms(fn)
         kern.append({"kernel": name, "avg_us": round(ms * 1e3, 3), "bytes": nbytes,
                      "flops": nflops, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)})
-    dom = max(kern, key=lambda k: k["avg_us"])
+    # roofline on the path's dominant kernel (forward SpMM, dX SpMM or dW SDDMM)
+    dom = max((k for k in kern if k["kernel"].startswith(("spmm", "sddmm"))),
+              key=lambda k: k["avg_us"])
     achieved = dom["bytes"] / (dom["avg_us"] * 1e-6) / 1e9
     traffic = None
     tf = ROOT / "profiles" / f"traffic_{args.workload}.json"
@@ -780,18 +1003,28 @@ def main():
                 "layer1_nnz": W.nnz}
         config = {"workload": "c2: " + work.desc, "global_batch": work.batch,
                   "graph": graph_ok}
-    elif isinstance(work, C3):
+    elif isinstance(work, GPTWork):
         value = work.tokens_per_step() * args.steps / elapsed
         unit = "tokens/s"
-        per_block_us = sum(k["avg_us"] for k in kern)
+        per_block_us = sum(k["avg_us"] for k in kern if k["kernel"].startswith(("spmm", "sddmm")))
         path = {"block0_sparse_kernels_us": round(per_block_us, 1),
                 "block0_sparse_GBps": round(sum(k["bytes"] for k in kern) /
                                             (per_block_us * 1e-6) / 1e9, 1),
                 "block0_sparse_GFLOPs": round(sum(k["flops"] for k in kern) /
                                               (per_block_us * 1e-6) / 1e9, 1),
-                "sparse_kernel_share_of_step": round(6 * per_block_us * 1e-3 / ms_per_step, 3)}
-        config = {"workload": "c3: " + work.desc, "global_batch": work.batch,
+                "sparse_kernel_share_of_step": round(work.n_layers * per_block_us * 1e-3 /
+                                                     ms_per_step, 3)}
+        if work.algo is not None:
+            path["topology_update_ms_per_step"] = round(topo_ms, 3)
+        config = {"workload": f"{work.name}: {work.desc}", "global_batch": work.batch,
                   "seq_len": work.ctx, "graph": graph_ok}
+    elif work.rigl:
+        value = work.N * args.steps / elapsed
+        unit = "tokens/s"
+        path = {"fwd_dw_dx_us": round(sum(k["avg_us"] for k in kern[:4]), 1),
+                "step_bytes_fwd_dw_dx": work.step_bytes(), "nnz": work.W.nnz,
+                "topology_update_ms_per_step": round(topo_ms, 3)}
+        config = {"workload": f"{work.name}: {work.desc}", "graph": False}
     else:
         value = work.step_bytes() * args.steps / elapsed / 1e9
         unit = "GB/s"
