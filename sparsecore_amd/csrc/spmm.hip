@@ -18,11 +18,13 @@
 //
 //  * spmm_wave_kernel — one item per wave (64 lanes x VEC columns). The
 //    row's (col, value) stream is fetched 64 slots at a time with one
-//    coalesced load into lane registers and broadcast slot by slot with
-//    readlane, so the X gathers use a scalar base address. Gathers are
-//    issued U slots at a time into two register buffers that alternate
-//    (the next batch is in flight while the current one is consumed), so a
-//    wave keeps 2U gathers outstanding instead of waiting once per slot.
+//    coalesced load into lane registers (the next chunk is requested as soon
+//    as the current one starts) and broadcast slot by slot with readlane, so
+//    the X gathers use a scalar base address. Gathers are issued U slots at
+//    a time into two register buffers that alternate (the next batch — the
+//    next chunk's first one at a chunk's end — is in flight while the current
+//    one is consumed), so a wave keeps 2U gathers outstanding instead of
+//    waiting once per slot, and never drains at a chunk boundary.
 //  * spmm_group_kernel — several items per wave (L < 64 lanes each) for
 //    narrow X (N < 64): each lane streams its row's metadata itself.
 //
@@ -131,6 +133,18 @@ __device__ __forceinline__ void consume(const typename VecIO<VEC>::T (&x)[U], fl
     }
 }
 
+__device__ __forceinline__ void load_meta(const int32_t* __restrict__ col,
+                                          const float* __restrict__ val, int32_t start,
+                                          int32_t base, int32_t nnz, int lane, int32_t& mc,
+                                          float& mv) {
+    mc = 0;
+    mv = 0.0f;
+    if (base + lane < nnz) {
+        mc = col[start + base + lane];
+        mv = val[start + base + lane];
+    }
+}
+
 template <int VEC, int U>
 __global__ __launch_bounds__(kSpmmBlock) void spmm_wave_kernel(
     int64_t M, int64_t N, int64_t nitems, const int32_t* __restrict__ order,
@@ -154,16 +168,37 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_wave_kernel(
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
 
-    for (int32_t base = 0; base < nnz; base += kWave) {
-        const int32_t n = (nnz - base < kWave) ? nnz - base : kWave;
-        int32_t mc = 0;
-        float mv = 0.0f;
-        if (lane < n) {
-            mc = col[start + base + lane];
-            mv = val[start + base + lane];
+    static_assert(kWave % (2 * U) == 0, "a full chunk holds an even number of batches");
+    int32_t mc, nmc = 0;
+    float mv, nmv = 0.0f;
+    load_meta(col, val, start, 0, nnz, lane, mc, mv);
+    if (nnz > kWave) load_meta(col, val, start, kWave, nnz, lane, nmc, nmv);
+    T xa[U], xc[U];
+    issue<VEC, U>(xa, mc, 0, nnz < kWave ? nnz : kWave, X, N, off, active);
+    int32_t base = 0;
+    // Full 64-slot chunks: batches alternate xa, xc, xa, ... and the chunk's
+    // last step already issues the next chunk's first batch into xa, so the
+    // gathers never drain at a chunk boundary.
+    for (; base + kWave <= nnz; base += kWave) {
+#pragma unroll
+        for (int32_t k = 0; k < kWave; k += 2 * U) {
+            issue<VEC, U>(xc, mc, k + U, kWave, X, N, off, active);
+            consume<VEC, U>(xa, mv, k, kWave, acc, active);
+            if (k + 2 * U < kWave) {
+                issue<VEC, U>(xa, mc, k + 2 * U, kWave, X, N, off, active);
+            } else if (base + kWave < nnz) {
+                const int32_t nn = nnz - base - kWave;
+                issue<VEC, U>(xa, nmc, 0, nn < kWave ? nn : kWave, X, N, off, active);
+            }
+            consume<VEC, U>(xc, mv, k + U, kWave, acc, active);
         }
-        T xa[U], xc[U];
-        issue<VEC, U>(xa, mc, 0, n, X, N, off, active);
+        mc = nmc;
+        mv = nmv;
+        if (base + 2 * kWave < nnz) load_meta(col, val, start, base + 2 * kWave, nnz, lane, nmc, nmv);
+    }
+    // Last, partial chunk (xa already holds its first batch).
+    if (base < nnz) {
+        const int32_t n = nnz - base;
         for (int32_t k = 0;;) {
             issue<VEC, U>(xc, mc, k + U, n, X, N, off, active && k + U < n);
             consume<VEC, U>(xa, mv, k, n, acc, active);
