@@ -70,9 +70,10 @@ typedef struct slk_csr {
     const int32_t* row_nnz;
     const int32_t* row_capacity;
     /* Optional (may be NULL): a permutation of [0, nrows) listing rows by
-     * descending row_nnz. slk_spmm then schedules the longest rows first (in
-     * bands of 256 rows) so skewed rows do not straggle; results are the same
-     * either way. Not part of the reference layout — a cached schedule. */
+     * descending row_nnz. slk_spmm then starts the longest rows of every
+     * column tile first, so skewed rows do not straggle at the end of the
+     * grid; results are the same either way. Not part of the reference
+     * layout — a schedule the caller caches per topology. */
     const int32_t* row_order;
 } slk_csr;
 
