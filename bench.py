@@ -161,7 +161,10 @@ class C2:
         g = torch.Generator().manual_seed(seed + 1)
         self.x = torch.rand(self.batch, 784, generator=g).to(dev)
         self.labels = torch.randint(0, 10, (self.batch,), generator=g).to(dev)
-        self.opt = torch.optim.SGD(self.model.parameters(), lr=0.01)
+        # foreach=False: torch's multi-tensor SGD kernel gives each 64Ki-element
+        # chunk one workgroup, so these four small tensors run on 4 workgroups
+        # (≈20 µs); one elementwise update per tensor fills the GPU instead.
+        self.opt = torch.optim.SGD(self.model.parameters(), lr=0.01, foreach=False)
         self.dev = dev
 
     def body(self):

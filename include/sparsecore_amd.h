@@ -91,6 +91,14 @@ SLK_API int slk_abi_version(void);
 SLK_API int slk_spmm(const slk_csr* W, const float* X, int64_t K, int64_t N,
              float* Y, void* stream);
 
+/* Y[i,:] = (W·X)[i,:] + bias[i]: slk_spmm with SparseLinear's bias add
+ * (sparselab/nn.py:237-241, `y_flat + self.bias`) fused into the store. Each
+ * element is the same fma chain as slk_spmm, then one float32 add of
+ * bias[i] — the rounding of the reference's separate add. bias is a device
+ * array of W->nrows floats.                                                 */
+SLK_API int slk_spmm_bias(const slk_csr* W, const float* X, int64_t K, int64_t N,
+                  const float* bias, float* Y, void* stream);
+
 /* dW[s] = dot(dY[i,:], X[col[s],:]) for every live slot s of row i, and
  * dW[s] = 0 for every padding slot. Replaces `spmm_grad_w_simd` /
  * `spmm_grad_w` (csrc/bindings.cpp:318-431). `order` is an slk_dw_order.

@@ -34,6 +34,7 @@ EXPORTS = (
     "slk_last_error",
     "slk_abi_version",
     "slk_spmm",
+    "slk_spmm_bias",
     "slk_sddmm",
     "slk_transpose_workspace_bytes",
     "slk_transpose_count",
@@ -76,6 +77,7 @@ def _declare(lib) -> None:
     lib.slk_last_error.argtypes = []
     lib.slk_abi_version.restype = ctypes.c_int
     lib.slk_spmm.argtypes = [_csrp, _vp, _i64, _i64, _vp, _vp]
+    lib.slk_spmm_bias.argtypes = [_csrp, _vp, _i64, _i64, _vp, _vp, _vp]
     lib.slk_sddmm.argtypes = [_csrp, _vp, _i64, _vp, _i64, _i64, _vp, ctypes.c_int, _vp]
     lib.slk_transpose_workspace_bytes.restype = _i64
     lib.slk_transpose_workspace_bytes.argtypes = [_csrp]
@@ -143,9 +145,16 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None or t.numel() == 0 else t.data_ptr()
 
 
-def spmm(view: CsrView, X: torch.Tensor, Y: torch.Tensor) -> None:
+def spmm(view: CsrView, X: torch.Tensor, Y: torch.Tensor,
+         bias: torch.Tensor | None = None) -> None:
+    """Y = W·X, plus bias[i] on row i when a (float32, contiguous) bias is given."""
     lib = load()
-    rc = lib.slk_spmm(ctypes.byref(view), ptr(X), X.shape[0], X.shape[1], ptr(Y), stream_of(Y))
+    if bias is None:
+        rc = lib.slk_spmm(ctypes.byref(view), ptr(X), X.shape[0], X.shape[1], ptr(Y),
+                          stream_of(Y))
+    else:
+        rc = lib.slk_spmm_bias(ctypes.byref(view), ptr(X), X.shape[0], X.shape[1], ptr(bias),
+                               ptr(Y), stream_of(Y))
     if rc:
         _raise(rc)
 

@@ -133,6 +133,14 @@ __device__ __forceinline__ void consume(const typename VecIO<VEC>::T (&x)[U], fl
     }
 }
 
+// Bias epilogue: y = fl(chain + b), one rounding after the finished chain —
+// what the reference's separate `y + bias` (sparselab/nn.py:237-241) gives.
+template <int VEC>
+__device__ __forceinline__ void add_bias(float (&acc)[VEC], float b) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = acc[e] + b;
+}
+
 __device__ __forceinline__ void load_meta(const int32_t* __restrict__ col,
                                           const float* __restrict__ val, int32_t start,
                                           int32_t base, int32_t nnz, int lane, int32_t& mc,
@@ -150,7 +158,7 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_wave_kernel(
     int64_t M, int64_t N, int64_t nitems, const int32_t* __restrict__ order,
     const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
     const int32_t* __restrict__ col, const float* __restrict__ val,
-    const float* __restrict__ X, float* __restrict__ Y) {
+    const float* __restrict__ X, const float* __restrict__ bias, float* __restrict__ Y) {
     typedef typename VecIO<VEC>::T T;
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t item = wave_id();
@@ -210,7 +218,10 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_wave_kernel(
             if (k >= n) break;
         }
     }
-    if (active) VecIO<VEC>::store(Y + row * N + n0, acc);
+    if (active) {
+        if (bias != nullptr) add_bias<VEC>(acc, bias[row]);
+        VecIO<VEC>::store(Y + row * N + n0, acc);
+    }
 }
 
 template <int L, int VEC>
@@ -218,7 +229,7 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_group_kernel(
     int64_t M, int64_t N, int64_t nitems, const int32_t* __restrict__ order,
     const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
     const int32_t* __restrict__ col, const float* __restrict__ val,
-    const float* __restrict__ X, float* __restrict__ Y) {
+    const float* __restrict__ X, const float* __restrict__ bias, float* __restrict__ Y) {
     typedef VecIO<VEC> IO;
     constexpr int kUnroll = 8;
     constexpr int kItemsPerWave = kWave / L;
@@ -270,7 +281,10 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_group_kernel(
             for (int e = 0; e < VEC; ++e) acc[e] = __builtin_fmaf(v, IO::get(x, e), acc[e]);
         }
     }
-    if (active) IO::store(Y + row * N + n0, acc);
+    if (active) {
+        if (bias != nullptr) add_bias<VEC>(acc, bias[row]);
+        IO::store(Y + row * N + n0, acc);
+    }
 }
 
 // ───────────────────────── LDS-tiled kernel ─────────────────────────────────
@@ -314,7 +328,8 @@ __device__ __forceinline__ void tile_reload(int32_t& base, int32_t pos, int32_t 
 __global__ __launch_bounds__(kTileThreads) void spmm_tile_kernel(
     int64_t M, int64_t K, int64_t N, int64_t nrowblk, const int32_t* __restrict__ row_start,
     const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ col,
-    const float* __restrict__ val, const float* __restrict__ X, float* __restrict__ Y) {
+    const float* __restrict__ val, const float* __restrict__ X, const float* __restrict__ bias,
+    float* __restrict__ Y) {
     __shared__ f32x2 xs[kTileK][kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -416,7 +431,14 @@ __global__ __launch_bounds__(kTileThreads) void spmm_tile_kernel(
     if (n_ok) {
 #pragma unroll
         for (int r = 0; r < kRowsPerWave; ++r)
-            if (r0 + r < M) *reinterpret_cast<f32x2*>(Y + (r0 + r) * N + n) = acc[r];
+            if (r0 + r < M) {
+                if (bias != nullptr) {
+                    const float b = bias[r0 + r];
+                    acc[r][0] = acc[r][0] + b;
+                    acc[r][1] = acc[r][1] + b;
+                }
+                *reinterpret_cast<f32x2*>(Y + (r0 + r) * N + n) = acc[r];
+            }
     }
 }
 
@@ -426,19 +448,21 @@ int launch_blocks(int64_t waves, int64_t* blocks) {
     return SLK_OK;
 }
 
-int launch_tile(const slk_csr* W, const float* X, int64_t N, float* Y, hipStream_t st) {
+int launch_tile(const slk_csr* W, const float* X, int64_t N, const float* bias, float* Y,
+                hipStream_t st) {
     const int64_t M = W->nrows;
     const int64_t nrowblk = ceil_div(M, kTileRows);
     const int64_t blocks = nrowblk * ceil_div(N, kTileCols);
     if (blocks > INT32_MAX) return fail(SLK_EINVAL, "spmm: problem too large for one launch");
     hipLaunchKernelGGL(spmm_tile_kernel, dim3(static_cast<unsigned>(blocks)),
                        dim3(kTileThreads), 0, st, M, W->ncols, N, nrowblk, W->row_start,
-                       W->row_nnz, W->col_indices, W->values, X, Y);
+                       W->row_nnz, W->col_indices, W->values, X, bias, Y);
     return check_launch("spmm");
 }
 
 template <int VEC>
-int launch_wave(const slk_csr* W, const float* X, int64_t N, float* Y, hipStream_t st) {
+int launch_wave(const slk_csr* W, const float* X, int64_t N, const float* bias, float* Y,
+                hipStream_t st) {
     constexpr int U = VEC == 4 ? 8 : 16;
     const int64_t M = W->nrows;
     const int64_t nitems = M * ceil_div(N, int64_t{kWave} * VEC);
@@ -446,42 +470,41 @@ int launch_wave(const slk_csr* W, const float* X, int64_t N, float* Y, hipStream
     if (int rc = launch_blocks(nitems, &blocks)) return rc;
     hipLaunchKernelGGL((spmm_wave_kernel<VEC, U>), dim3(static_cast<unsigned>(blocks)),
                        dim3(kSpmmBlock), 0, st, M, N, nitems, W->row_order, W->row_start,
-                       W->row_nnz, W->col_indices, W->values, X, Y);
+                       W->row_nnz, W->col_indices, W->values, X, bias, Y);
     return check_launch("spmm");
 }
 
 template <int L, int VEC>
-int launch_group(const slk_csr* W, const float* X, int64_t N, float* Y, hipStream_t st) {
+int launch_group(const slk_csr* W, const float* X, int64_t N, const float* bias, float* Y,
+                 hipStream_t st) {
     const int64_t M = W->nrows;
     const int64_t nitems = M * ceil_div(N, static_cast<int64_t>(L) * VEC);
     int64_t blocks;
     if (int rc = launch_blocks(ceil_div(nitems, kWave / L), &blocks)) return rc;
     hipLaunchKernelGGL((spmm_group_kernel<L, VEC>), dim3(static_cast<unsigned>(blocks)),
                        dim3(kSpmmBlock), 0, st, M, N, nitems, W->row_order, W->row_start,
-                       W->row_nnz, W->col_indices, W->values, X, Y);
+                       W->row_nnz, W->col_indices, W->values, X, bias, Y);
     return check_launch("spmm");
 }
 
-int launch_group_L(int L, const slk_csr* W, const float* X, int64_t N, float* Y, hipStream_t st) {
+int launch_group_L(int L, const slk_csr* W, const float* X, int64_t N, const float* bias,
+                   float* Y, hipStream_t st) {
     switch (L) {
-        case 1: return launch_group<1, 1>(W, X, N, Y, st);
-        case 2: return launch_group<2, 1>(W, X, N, Y, st);
-        case 4: return launch_group<4, 1>(W, X, N, Y, st);
-        case 8: return launch_group<8, 1>(W, X, N, Y, st);
-        case 16: return launch_group<16, 1>(W, X, N, Y, st);
-        default: return launch_group<32, 1>(W, X, N, Y, st);
+        case 1: return launch_group<1, 1>(W, X, N, bias, Y, st);
+        case 2: return launch_group<2, 1>(W, X, N, bias, Y, st);
+        case 4: return launch_group<4, 1>(W, X, N, bias, Y, st);
+        case 8: return launch_group<8, 1>(W, X, N, bias, Y, st);
+        case 16: return launch_group<16, 1>(W, X, N, bias, Y, st);
+        default: return launch_group<32, 1>(W, X, N, bias, Y, st);
     }
 }
 
 // Waves worth launching: enough to give every CU several to switch between.
 constexpr int64_t kTargetWaves = 4096;
 
-}  // namespace
-}  // namespace slk
-
-extern "C" int slk_spmm(const slk_csr* W, const float* X, int64_t K, int64_t N, float* Y,
-                        void* stream) {
-    using namespace slk;
+// Y = W·X (+ bias per row): the shared body of slk_spmm and slk_spmm_bias.
+int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const float* bias,
+              float* Y, void* stream) {
     clear_error();
     if (int rc = validate_csr(W, "spmm")) return rc;
     if (N < 0 || K < 0) return fail(SLK_EINVAL, "spmm: negative X shape");
@@ -505,7 +528,7 @@ extern "C" int slk_spmm(const slk_csr* W, const float* X, int64_t K, int64_t N, 
     if (const char* e = std::getenv("SLK_SPMM_KERNEL")) {
         if (e[0] == 't') tile = N % 2 == 0 && align % 8 == 0;
     }
-    if (tile) return launch_tile(W, X, N, Y, st);
+    if (tile) return launch_tile(W, X, N, bias, Y, st);
 
     int vec = 1;
     if (const char* e = std::getenv("SLK_SPMM_VEC")) vec = std::atoi(e);
@@ -519,10 +542,27 @@ extern "C" int slk_spmm(const slk_csr* W, const float* X, int64_t K, int64_t N, 
         // Narrow X: pack several rows per wave.
         int L = 1;
         while (L < 32 && L < N) L <<= 1;
-        if (L < kWave && L >= N) return launch_group_L(L, W, X, N, Y, st);
+        if (L < kWave && L >= N) return launch_group_L(L, W, X, N, bias, Y, st);
         vec = 1;
     }
-    if (vec == 4) return launch_wave<4>(W, X, N, Y, st);
-    if (vec == 2) return launch_wave<2>(W, X, N, Y, st);
-    return launch_wave<1>(W, X, N, Y, st);
+    if (vec == 4) return launch_wave<4>(W, X, N, bias, Y, st);
+    if (vec == 2) return launch_wave<2>(W, X, N, bias, Y, st);
+    return launch_wave<1>(W, X, N, bias, Y, st);
+}
+
+}  // namespace
+}  // namespace slk
+
+extern "C" int slk_spmm(const slk_csr* W, const float* X, int64_t K, int64_t N, float* Y,
+                        void* stream) {
+    return slk::spmm_impl(W, X, K, N, nullptr, Y, stream);
+}
+
+extern "C" int slk_spmm_bias(const slk_csr* W, const float* X, int64_t K, int64_t N,
+                             const float* bias, float* Y, void* stream) {
+    if (bias == nullptr && W != nullptr && W->nrows > 0) {
+        slk::clear_error();
+        return slk::fail(SLK_EINVAL, "spmm_bias: NULL bias");
+    }
+    return slk::spmm_impl(W, X, K, N, bias, Y, stream);
 }

@@ -17,7 +17,7 @@ import torch.nn as nn
 
 from . import layout as _layout
 from .layout import PaddedCSR
-from .ops import _SpMMFunction
+from .ops import _SpMMBiasFunction, _SpMMFunction
 
 __all__ = ["SparseLinear"]
 
@@ -100,12 +100,18 @@ class SparseLinear(nn.Module):
         if orig_shape[-1] != self.in_features:
             raise ValueError(f"SparseLinear expects input last dim {self.in_features}, "
                              f"got {orig_shape[-1]}")
-        x_flat = x.reshape(-1, self.in_features).contiguous()
-        X_col = x_flat.t().contiguous()
-        Y_col = _SpMMFunction.apply(self._values, self._csr, X_col, "simd")
+        # (N, in) -> (in, N) row-major. One copy at most: none when x is the
+        # transposed view a previous SparseLinear returned.
+        X_col = x.reshape(-1, self.in_features).t().contiguous()
+        b = self.bias
+        if b is not None and b.dtype == torch.float32 and b.device == X_col.device:
+            # bias add fused into the SpMM store: same bits as the separate add
+            Y_col = _SpMMBiasFunction.apply(self._values, b, self._csr, X_col, "simd")
+        else:
+            Y_col = _SpMMFunction.apply(self._values, self._csr, X_col, "simd")
+            if b is not None:
+                Y_col = Y_col + b[:, None]
         y_flat = Y_col.t()
-        if self.bias is not None:
-            y_flat = y_flat + self.bias
         return y_flat.reshape(orig_shape[:-1] + (self.out_features,))
 
     @property

@@ -66,9 +66,9 @@ def _clear_transpose_cache() -> None:
     _transpose_cache.clear()
 
 
-def _launch_spmm(W: PaddedCSR, X: torch.Tensor) -> torch.Tensor:
+def _launch_spmm(W: PaddedCSR, X: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
     Y = torch.empty((W.nrows, X.shape[1]), dtype=torch.float32, device=X.device)
-    _lib.spmm(W._view(), X, Y)
+    _lib.spmm(W._view(), X, Y, bias)
     return Y
 
 
@@ -117,15 +117,55 @@ class _SpMMFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dY):
         W_values, X = ctx.saved_tensors
-        W = ctx.W
-        dY_f32 = _device_f32(dY)
-        dW_values = dX = None
-        if ctx.needs_input_grad[0]:
-            dW_values = _launch_sddmm(W, dY_f32, _device_f32(X), ctx.kernel)
-        if ctx.needs_input_grad[2]:
-            WT = _cached_transpose(W)
-            dX = _launch_spmm(WT, dY_f32)
+        dW_values, dX = _spmm_backward(ctx.W, X, _device_f32(dY), ctx.kernel,
+                                       ctx.needs_input_grad[0], ctx.needs_input_grad[2])
         return dW_values, None, dX, None
+
+
+def _spmm_backward(W: PaddedCSR, X: torch.Tensor, dY_f32: torch.Tensor, kernel: str,
+                   need_dw: bool, need_dx: bool):
+    """dW on the live slots (SDDMM) and dX = Wᵀ·dY through the transpose cache
+    (ops.py:167-210); a gradient that is not needed is not computed."""
+    dW_values = dX = None
+    if need_dw:
+        dW_values = _launch_sddmm(W, dY_f32, _device_f32(X), kernel)
+    if need_dx:
+        WT = _cached_transpose(W)
+        dX = _launch_spmm(WT, dY_f32)
+    return dW_values, dX
+
+
+class _SpMMBiasFunction(torch.autograd.Function):
+    """``Y = W @ X + bias[:, None]`` in one launch: SparseLinear's forward with
+    the bias add (sparselab/nn.py:237-241) fused into the SpMM's store.
+
+    Y holds the same bits as ``_SpMMFunction`` followed by a separate float32
+    add. Backward is ``_SpMMFunction``'s, plus dbias = Σ_n dY[:, n].
+    """
+
+    @staticmethod
+    def forward(ctx, W_values, bias, W, X, kernel):
+        ctx.save_for_backward(W_values, X)
+        ctx.W = W
+        ctx.kernel = kernel
+        if kernel not in _KERNELS:
+            raise ValueError(f"spmm: unknown kernel={kernel!r}. Expected one of: "
+                             f"{sorted(_KERNELS)}.")
+        _check_same_device(W, X, "spmm", "X")
+        _check_same_device(W, bias, "spmm", "bias")
+        if bias.dtype != torch.float32 or bias.shape != (W.nrows,):
+            raise ValueError(f"spmm: bias must be float32 of shape ({W.nrows},), got "
+                             f"{bias.dtype} {tuple(bias.shape)}")
+        return _launch_spmm(W, _device_f32(X), bias.contiguous())
+
+    @staticmethod
+    def backward(ctx, dY):
+        W_values, X = ctx.saved_tensors
+        dY_f32 = _device_f32(dY)
+        dW_values, dX = _spmm_backward(ctx.W, X, dY_f32, ctx.kernel, ctx.needs_input_grad[0],
+                                       ctx.needs_input_grad[3])
+        dbias = dY_f32.sum(dim=1) if ctx.needs_input_grad[1] else None
+        return dW_values, dbias, None, dX, None
 
 
 def spmm(W: PaddedCSR, X: torch.Tensor, *, kernel: str = "auto") -> torch.Tensor:

@@ -111,3 +111,10 @@ def test_topology_entry_points_check_arguments_on_the_host():
     rc = lib.slk_dense_grad(None, None, -1, 2, 2, 0, None, None)
     assert rc == _lib.SLK_EINVAL and "non-negative" in lib.slk_last_error().decode()
     assert lib.slk_dense_grad(None, None, 0, 5, 4, 0, None, None) == _lib.SLK_OK
+
+
+def test_spmm_bias_rejects_null_bias_on_the_host():
+    lib = _lib.load()
+    v = _view()
+    rc = lib.slk_spmm_bias(ctypes.byref(v), None, 6, 3, None, None, None)
+    assert rc == _lib.SLK_EINVAL and "bias" in lib.slk_last_error().decode()

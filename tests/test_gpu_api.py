@@ -233,6 +233,35 @@ def test_sparse_linear_forward_matches_dense(dev):
         layer(torch.randn(4, 12, device=dev))
 
 
+@pytest.mark.parametrize("batch", [1, 37, 256])
+def test_sparse_linear_with_bias_bit_exact_vs_oracle(dev, batch):
+    """SparseLinear's forward (bias fused into the SpMM store) gives the bits of
+    the reference's spmm followed by its separate `y + bias`; dW and dX are
+    the oracle's bit for bit and dbias is Σ over the batch. The second layer
+    takes the first one's transposed-view output directly (no input copy)."""
+    torch.manual_seed(batch)
+    l1 = SparseLinear(784, 512, sparsity=0.9).to(dev)
+    l2 = SparseLinear(512, 10, sparsity=0.9).to(dev)
+    x = torch.rand(batch, 784, device=dev)
+    h = torch.relu(l1(x)).detach().requires_grad_(True)
+    y = l2(h)
+    up = torch.randn_like(y)
+    y.backward(up)
+    c = to_oracle(l2._csr)
+    b = l2.bias.detach().cpu().numpy()
+    H_col = h.detach().t().contiguous().cpu().numpy()
+    dY_col = up.t().contiguous().cpu().numpy()
+    assert_bits_equal(y.detach().t().cpu().numpy(), oracle.spmm(c, H_col) + b[:, None], "y")
+    assert_bits_equal(l2._values.grad.cpu().numpy(), oracle.sddmm(c, dY_col, H_col), "dW")
+    WT, _ = oracle.transpose_with_perm(c)
+    assert_bits_equal(h.grad.t().cpu().numpy(), oracle.spmm(WT, dY_col), "dX")
+    torch.testing.assert_close(l2.bias.grad, up.sum(0), rtol=1e-5, atol=1e-5)
+    c1 = to_oracle(l1._csr)
+    X_col = x.t().contiguous().cpu().numpy()
+    h_ref = np.maximum(oracle.spmm(c1, X_col) + l1.bias.detach().cpu().numpy()[:, None], 0)
+    assert_bits_equal(h.detach().t().cpu().numpy(), h_ref, "relu(l1)")
+
+
 def test_sparse_linear_zero_sparsity_matches_nn_linear(dev):
     torch.manual_seed(7)
     layer = SparseLinear(16, 8, sparsity=0.0).to(dev)

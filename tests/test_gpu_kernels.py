@@ -131,6 +131,29 @@ def test_spmm_tile_kernel_bit_exact(dev, monkeypatch, M, K, N, per_row):
     assert_bits_equal(_spmm(W, _t(X_np, dev)).cpu().numpy(), oracle.spmm(c, X_np), "Y")
 
 
+@pytest.mark.parametrize("env,N", [
+    ({"SLK_SPMM_VEC": "1"}, 300), ({"SLK_SPMM_VEC": "2"}, 300), ({"SLK_SPMM_VEC": "4"}, 1024),
+    ({}, 5), ({}, 40), ({"SLK_SPMM_KERNEL": "tile"}, 130)])
+def test_spmm_bias_epilogue_bit_exact(dev, monkeypatch, env, N):
+    """slk_spmm_bias = slk_spmm followed by one float32 add of bias[i] per row,
+    in every kernel (wave kernel at each lane width, packed narrow-N kernel,
+    LDS-tiled kernel), including rows with no live slot (Y = 0 + bias)."""
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    print(f"[bias] env={env} N={N}", flush=True)
+    c, X_np, _ = _case(45, 150, N, 20, seed=N + len(env))
+    c.row_nnz[3] = 0
+    c.col_indices[c.row_start[3]:c.row_start[3] + c.row_capacity[3]] = -1
+    c.values[c.row_start[3]:c.row_start[3] + c.row_capacity[3]] = 0.0
+    b_np = np.random.default_rng(N).standard_normal(45).astype(np.float32)
+    W = from_oracle(c, dev)
+    Y = torch.empty(45, N, device=dev)
+    _lib.spmm(W._view(), _t(X_np, dev), Y, _t(b_np, dev))
+    ref = oracle.spmm(c, X_np) + b_np[:, None]
+    assert ref.dtype == np.float32
+    assert_bits_equal(Y.cpu().numpy(), ref, "Y+bias")
+
+
 def test_spmm_tile_kernel_skewed_rows(dev, monkeypatch):
     monkeypatch.setenv("SLK_SPMM_KERNEL", "tile")
     c = oracle.zipf_rows(300, 700, 0.08, 1.1, seed=5, sigma=0.5)
