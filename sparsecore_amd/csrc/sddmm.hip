@@ -29,11 +29,15 @@
 // dW needs no separate memset.
 #include "common.hpp"
 
+#include <cstdlib>
+
 namespace slk {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kSlotsPerWave = 16;  // SIMD order: 4 lanes per slot
+constexpr int kSlotsPerWave = 16;  // SIMD order: 4 lanes per slot group
+constexpr int64_t kWinMinN = 1024;
+constexpr int64_t kWinMinSlots = 2048 * kSlotsPerWave;  // 2048 waves
 
 // Largest r in [0, M) with row_start[r] <= slot (rows tile [0, cap)).
 __device__ __forceinline__ int64_t row_of_slot(const int32_t* __restrict__ row_start, int64_t M,
@@ -146,6 +150,192 @@ __global__ __launch_bounds__(kBlock) void sddmm_simd_kernel(
     }
 }
 
+// SIMD order, N swept window by window, dY staged in LDS (16-byte path).
+//
+// Same arithmetic as sddmm_simd_kernel, slot by slot. Two things bound that
+// kernel at large N, and this one removes both (measured with rocprofv3 on
+// a 2304x768 layer at N=8192):
+//  * Locality. Streaming each slot's whole X and dY rows makes the resident
+//    waves touch every X row at scattered offsets: L2 hit rate 26%. Here a
+//    wave owns G groups of 16 slots and advances all of them through N one
+//    256-float window at a time; waves start together and do the same work
+//    per window, so at any moment they read one narrow band of X and dY
+//    columns, which stays in L2 (87% hits) — the locality tile-major order
+//    gives the forward.
+//  * Load issue. With locality fixed, the kernel runs at the rate of 16-byte
+//    wave loads, and loading dY per lane doubles their count although all 16
+//    slots of a group usually share one dY row. Each group instead stages the
+//    dY windows of the first and the last row of its slots in LDS, one 1 KB
+//    load per row per window, prefetched a window ahead in registers; lanes
+//    read their pieces from LDS, so X is the only per-lane stream. A lane
+//    whose slot lies in a third row of its group (rows shorter than 16 slots)
+//    loads its dY pieces directly.
+// The 16 partial sums of every slot stay in registers across windows. The LDS
+// region is private to the wave: wave-level fences order its stores and loads.
+constexpr int64_t kWin = 256;  // floats per window: 16 steps of 16
+
+__device__ __forceinline__ void fma4x(f32x4 d, f32x4 x, float& a0, float& a1, float& a2,
+                                      float& a3) {
+    a0 = __builtin_fmaf(d[0], x[0], a0);
+    a1 = __builtin_fmaf(d[1], x[1], a1);
+    a2 = __builtin_fmaf(d[2], x[2], a2);
+    a3 = __builtin_fmaf(d[3], x[3], a3);
+}
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int G>
+__global__ __launch_bounds__(kBlock) void sddmm_simd_win_kernel(
+    int64_t M, int64_t N, int64_t cap_total,
+    const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
+    const int32_t* __restrict__ col, const float* __restrict__ dY,
+    const float* __restrict__ X, float* __restrict__ dW) {
+    constexpr int kWavesPerBlock = kBlock / kWave;
+    __shared__ f32x4 dys[kWavesPerBlock][G][2][kWave];  // 2 KiB per group
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wv = threadIdx.x >> 6;
+    const int g = lane >> 2;
+    const int q = lane & 3;
+    const int64_t base = wave_id() * (kSlotsPerWave * G);
+    if (base >= cap_total) return;  // wave-uniform
+
+    bool in[G], live[G], direct[G];
+    int sel[G];
+    int32_t rA[G], rB[G];
+    const float* dyr[G];
+    const float* xr[G];
+    int64_t r = row_of_slot(row_start, M, min(base + g, cap_total - 1));
+    bool any_direct = false;
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+        const int64_t gbase = base + kSlotsPerWave * k;
+        const int64_t slot = gbase + g;
+        in[k] = slot < cap_total;
+        live[k] = false;
+        if (in[k]) {
+            while (r + 1 < M && row_start[r + 1] <= slot) ++r;
+            live[k] = (slot - row_start[r]) < row_nnz[r];
+        }
+        // first and last row of group k (lane 0 holds its first slot)
+        const int last = gbase < cap_total
+                             ? 4 * static_cast<int>(min<int64_t>(kSlotsPerWave - 1, cap_total - 1 - gbase))
+                             : 0;
+        rA[k] = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(r));
+        rB[k] = __builtin_amdgcn_readlane(static_cast<int32_t>(r), last);
+        sel[k] = r == rA[k] ? 0 : 1;
+        direct[k] = live[k] && r != rA[k] && r != rB[k];
+        any_direct |= __ballot(direct[k]) != 0;
+        dyr[k] = dY + (live[k] ? r * N : 0);
+        xr[k] = X + (live[k] ? static_cast<int64_t>(col[slot]) * N : 0);
+    }
+    const int64_t n16 = (N / 16) * 16;
+    const int64_t nwin = ceil_div(n16, kWin);
+    float acc[G][4];
+    f32x4 pa[G], pb[G];
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+        acc[k][0] = acc[k][1] = acc[k][2] = acc[k][3] = 0.f;
+        pa[k] = pb[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    auto fetch = [&](int64_t w) {
+        const int64_t j = w * kWin + 4 * lane;
+        if (j < n16) {
+#pragma unroll
+            for (int k = 0; k < G; ++k) {
+                pa[k] = *reinterpret_cast<const f32x4*>(dY + static_cast<int64_t>(rA[k]) * N + j);
+                if (rB[k] != rA[k])
+                    pb[k] = *reinterpret_cast<const f32x4*>(dY + static_cast<int64_t>(rB[k]) * N + j);
+            }
+        }
+    };
+    if (nwin > 0) fetch(0);
+    for (int64_t w = 0; w < nwin; ++w) {
+#pragma unroll
+        for (int k = 0; k < G; ++k) {
+            dys[wv][k][0][lane] = pa[k];
+            if (rB[k] != rA[k]) dys[wv][k][1][lane] = pb[k];
+        }
+        wave_sync();
+        if (w + 1 < nwin) fetch(w + 1);
+        const int64_t j0 = w * kWin;
+        const int tn = static_cast<int>(min<int64_t>(16, n16 / 16 - w * 16));
+#pragma unroll
+        for (int k = 0; k < G; ++k) {
+            if (!live[k]) continue;
+            const int sk = sel[k];
+            const float* xw = xr[k] + j0 + 4 * q;
+            if (!any_direct) {
+                int t = 0;
+                for (; t + 4 <= tn; t += 4) {
+                    const f32x4 x0 = *reinterpret_cast<const f32x4*>(xw + 16 * t);
+                    const f32x4 x1 = *reinterpret_cast<const f32x4*>(xw + 16 * t + 16);
+                    const f32x4 x2 = *reinterpret_cast<const f32x4*>(xw + 16 * t + 32);
+                    const f32x4 x3 = *reinterpret_cast<const f32x4*>(xw + 16 * t + 48);
+                    fma4x(dys[wv][k][sk][q + 4 * t], x0, acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+                    fma4x(dys[wv][k][sk][q + 4 * t + 4], x1, acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+                    fma4x(dys[wv][k][sk][q + 4 * t + 8], x2, acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+                    fma4x(dys[wv][k][sk][q + 4 * t + 12], x3, acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+                }
+                for (; t < tn; ++t)
+                    fma4x(dys[wv][k][sk][q + 4 * t], *reinterpret_cast<const f32x4*>(xw + 16 * t),
+                          acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+            } else {
+                const float* dw = dyr[k] + j0 + 4 * q;
+                for (int t = 0; t < tn; ++t) {
+                    // the LDS piece is read unconditionally: a branch between an LDS and
+                    // a global load gets merged into a load through a select of the two
+                    // addresses, which this compiler cannot lower
+                    f32x4 d = dys[wv][k][sk][q + 4 * t];
+                    if (direct[k]) d = *reinterpret_cast<const f32x4*>(dw + 16 * t);
+                    fma4x(d, *reinterpret_cast<const f32x4*>(xw + 16 * t),
+                          acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+                }
+            }
+        }
+        wave_sync();  // every lane has read this window before it is overwritten
+    }
+    // a[l] = v[l] + v[l+8]: lanes q=0,1 take the partner q^2 (v[8..15]).
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[k][e] = acc[k][e] + __shfl_xor(acc[k][e], 2);
+    }
+    int64_t jt = n16;
+    if (N - n16 >= 8) {
+        if (q < 2) {
+            const int64_t j = n16 + 4 * q;
+#pragma unroll
+            for (int k = 0; k < G; ++k) {
+                if (live[k]) {
+                    fma4x(*reinterpret_cast<const f32x4*>(dyr[k] + j),
+                          *reinterpret_cast<const f32x4*>(xr[k] + j),
+                          acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+                }
+            }
+        }
+        jt += 8;
+    }
+    // s4[k] = a[k] + a[k+4]: lane q=0 holds a[0..3], lane q=1 holds a[4..7].
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[k][e] = acc[k][e] + __shfl_xor(acc[k][e], 1);
+    }
+    if (q == 0) {
+#pragma unroll
+        for (int k = 0; k < G; ++k) {
+            if (!in[k]) continue;
+            const float rsum = (acc[k][0] + acc[k][2]) + (acc[k][1] + acc[k][3]);
+            dW[base + kSlotsPerWave * k + g] =
+                live[k] ? running_sum(dyr[k] + jt, xr[k] + jt, N - jt, rsum) : 0.0f;
+        }
+    }
+}
+
 __global__ __launch_bounds__(kBlock) void sddmm_scalar_kernel(
     int64_t M, int64_t N, int64_t cap_total,
     const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
@@ -197,18 +387,30 @@ extern "C" int slk_sddmm(const slk_csr* W, const float* dY, int64_t dY_rows, con
                            X, dW);
         return check_launch(who);
     }
-    const int64_t waves = ceil_div(cap, kSlotsPerWave);
-    const int64_t blocks = ceil_div(waves, kBlock / kWave);
     const bool v4 = (N % 4 == 0) && (reinterpret_cast<uintptr_t>(X) % 16 == 0) &&
                     (reinterpret_cast<uintptr_t>(dY) % 16 == 0);
-    if (v4) {
-        hipLaunchKernelGGL(sddmm_simd_kernel<true>, dim3(static_cast<unsigned>(blocks)),
-                           dim3(kBlock), 0, st, W->nrows, N, cap, W->row_start, W->row_nnz,
-                           W->col_indices, dY, X, dW);
+    // Windowed sweep (G groups per wave) for the 16-byte path at large N, with
+    // the most groups per wave that still leaves ~8 waves per CU (measured on
+    // the C3/C4 layer shapes); SLK_SDDMM_G=1|2|4 overrides G (1 = one group
+    // per wave, whole rows).
+    int G = 1;
+    if (v4 && N >= kWinMinN) G = cap >= 4 * kWinMinSlots ? 4 : cap >= 2 * kWinMinSlots ? 2 : 1;
+    if (const char* e = std::getenv("SLK_SDDMM_G")) G = std::atoi(e);
+    if (!v4 || (G != 2 && G != 4)) G = 1;
+    const int64_t waves = ceil_div(cap, kSlotsPerWave * G);
+    const int64_t blocks = ceil_div(waves, kBlock / kWave);
+    if (blocks > INT32_MAX) return fail(SLK_EINVAL, std::string(who) + ": problem too large");
+    const dim3 grid(static_cast<unsigned>(blocks));
+#define SLK_SDDMM_ARGS W->nrows, N, cap, W->row_start, W->row_nnz, W->col_indices, dY, X, dW
+    if (G == 2) {
+        hipLaunchKernelGGL(sddmm_simd_win_kernel<2>, grid, dim3(kBlock), 0, st, SLK_SDDMM_ARGS);
+    } else if (G == 4) {
+        hipLaunchKernelGGL(sddmm_simd_win_kernel<4>, grid, dim3(kBlock), 0, st, SLK_SDDMM_ARGS);
+    } else if (v4) {
+        hipLaunchKernelGGL(sddmm_simd_kernel<true>, grid, dim3(kBlock), 0, st, SLK_SDDMM_ARGS);
     } else {
-        hipLaunchKernelGGL(sddmm_simd_kernel<false>, dim3(static_cast<unsigned>(blocks)),
-                           dim3(kBlock), 0, st, W->nrows, N, cap, W->row_start, W->row_nnz,
-                           W->col_indices, dY, X, dW);
+        hipLaunchKernelGGL(sddmm_simd_kernel<false>, grid, dim3(kBlock), 0, st, SLK_SDDMM_ARGS);
     }
+#undef SLK_SDDMM_ARGS
     return check_launch(who);
 }

@@ -287,158 +287,153 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_group_kernel(
     }
 }
 
-// ───────────────────────── LDS-tiled kernel ─────────────────────────────────
+// ───────────────────────── LDS-staged kernel ────────────────────────────────
 //
-// spmm_tile_kernel — for large problems. A workgroup of 8 waves owns a
-// 64-row x 128-column output tile: each wave holds 8 rows, each lane two
-// adjacent columns, accumulators in registers. X is streamed through LDS in
-// chunks of kTileK rows (the next chunk is prefetched into registers while
-// the current one is consumed). For each chunk every row consumes its slots
+// spmm_lds_kernel — for large problems, where every X element is used by
+// several rows of a workgroup. A workgroup of 16 waves owns R = 16·RW rows x
+// 256 columns of Y: each lane holds 4 adjacent columns of RW rows in
+// registers. X is streamed through LDS in chunks of kLdsK rows x 256 columns
+// (1 KB per X row), double-buffered: chunk c+1 is loaded into registers while
+// chunk c is read from LDS and is then written to the other buffer, so one
+// barrier per chunk orders both. For each chunk every row consumes its slots
 // whose column falls in the chunk; columns ascend within a row, so walking
-// the chunks in order visits each row's slots in slot order and the fma chain
-// of every element is exactly the reference's. Each X element is fetched
-// from L2/HBM once per workgroup and read from LDS by every row of the tile
-// that uses it, instead of being gathered through L1 once per slot.
+// the chunks in order visits each row's slots in slot order and every
+// element's fma chain is exactly the reference's. Each X element is fetched
+// from L2/HBM once per workgroup and then read from LDS — about eight times
+// the bandwidth of global gathers on gfx950 — by every row that uses it.
 //
-// A wave advances its 8 rows in lockstep (one slot of every row per step), so
-// eight independent LDS reads are in flight per step. A row's (col, value)
-// stream sits in registers 64 slots at a time and is reloaded when less than
-// half of the batch is left; a row with more slots in one chunk than its
-// batch holds (a near-dense row) finishes the chunk in a per-row loop.
-constexpr int kTileCols = 128;                     // 64 lanes x 2 columns
-constexpr int kTileK = 64;                         // X rows per LDS chunk
-constexpr int kRowsPerWave = 8;
-constexpr int kTileWaves = 8;
-constexpr int kTileRows = kRowsPerWave * kTileWaves;  // 64
-constexpr int kTileThreads = kTileWaves * kWave;      // 512
-constexpr int kTilePrefetch = kTileK * kTileCols / (2 * kTileThreads);  // float2 per thread
+// Row metadata: each row keeps two 64-slot windows of (column, value) in lane
+// registers, the current one and the next, which is requested as soon as the
+// current one is entered, so a row never waits on its stream inside a chunk.
+// The row's slots that fall in a chunk are a run of the window: a ballot gives
+// its length and readlane broadcasts each slot's column and value. Rows are
+// dealt to waves round-robin (row r0 + w + 16j), which spreads the few heavy
+// rows of a skewed matrix over different waves.
+constexpr int kLdsWaves = 16;
+constexpr int kLdsThreads = kLdsWaves * kWave;          // 1024
+constexpr int kLdsK = 64;                               // X rows per chunk
+constexpr int kLdsCols = 4 * kWave;                     // 256 columns per workgroup
+constexpr int kLdsStage = kLdsK * kWave / kLdsThreads;  // 16-byte loads per thread per chunk
 
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ void tile_reload(int32_t& base, int32_t pos, int32_t end, int lane,
-                                            const int32_t* __restrict__ col,
-                                            const float* __restrict__ val, int32_t& mc,
-                                            float& mv) {
-    base = pos;
-    const int32_t sl = pos + lane;
-    mc = sl < end ? col[sl] : INT32_MAX;
-    mv = sl < end ? val[sl] : 0.0f;
+__device__ __forceinline__ void lds_window(const int32_t* __restrict__ col,
+                                           const float* __restrict__ val, int32_t at,
+                                           int32_t end, int lane, int32_t& c, float& v) {
+    const int32_t s = at + lane;
+    c = s < end ? col[s] : INT32_MAX;  // past the row: never below a chunk end
+    v = s < end ? val[s] : 0.0f;
 }
 
-__global__ __launch_bounds__(kTileThreads) void spmm_tile_kernel(
+__device__ __forceinline__ void fma4(float v, const f32x4& x, f32x4& acc) {
+    acc[0] = __builtin_fmaf(v, x[0], acc[0]);
+    acc[1] = __builtin_fmaf(v, x[1], acc[1]);
+    acc[2] = __builtin_fmaf(v, x[2], acc[2]);
+    acc[3] = __builtin_fmaf(v, x[3], acc[3]);
+}
+
+template <int RW>
+__global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
     int64_t M, int64_t K, int64_t N, int64_t nrowblk, const int32_t* __restrict__ row_start,
     const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ col,
     const float* __restrict__ val, const float* __restrict__ X, const float* __restrict__ bias,
     float* __restrict__ Y) {
-    __shared__ f32x2 xs[kTileK][kWave];
+    __shared__ f32x4 xs[2][kLdsK][kWave];  // 128 KiB
     const int lane = threadIdx.x & (kWave - 1);
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t lb = xcd_logical_block(blockIdx.x, gridDim.x);
-    const int64_t ntile = lb / nrowblk;
-    const int64_t rb = lb - ntile * nrowblk;
-    const int64_t n = ntile * kTileCols + 2 * lane;  // N is even for this kernel
-    const bool n_ok = n < N;
-    const int64_t r0 = rb * kTileRows + static_cast<int64_t>(w) * kRowsPerWave;
+    const int64_t tile = lb / nrowblk;  // tile-major: a tile's row blocks share X chunks in L2
+    const int64_t rb = lb - tile * nrowblk;
+    const int64_t n = tile * kLdsCols + 4 * lane;
+    const bool n_ok = n < N;  // N % 4 == 0 for this kernel
+    const int64_t r0 = rb * (kLdsWaves * RW) + w;
 
-    int32_t pos[kRowsPerWave], end[kRowsPerWave], base[kRowsPerWave];
-    int32_t mc[kRowsPerWave];
-    float mv[kRowsPerWave];
-    f32x2 acc[kRowsPerWave];
+    int32_t pos[RW], end[RW], base[RW], mc[RW], nmc[RW];
+    float mv[RW], nmv[RW];
+    f32x4 acc[RW];
 #pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r) {
-        const int64_t row = r0 + r;
+    for (int j = 0; j < RW; ++j) {
+        const int64_t row = r0 + static_cast<int64_t>(kLdsWaves) * j;
         const int32_t s = row < M ? row_start[row] : 0;
         const int32_t e = row < M ? s + row_nnz[row] : 0;
-        pos[r] = s;
-        end[r] = e;
-        tile_reload(base[r], s, e, lane, col, val, mc[r], mv[r]);
-        acc[r] = f32x2{0.0f, 0.0f};
+        pos[j] = base[j] = s;
+        end[j] = e;
+        lds_window(col, val, s, e, lane, mc[j], mv[j]);
+        lds_window(col, val, s + kWave, e, lane, nmc[j], nmv[j]);
+        acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    // thread t stages chunk rows (t / 64) + 8j, j < kTilePrefetch, at its two columns
-    const int krow0 = threadIdx.x >> 6;
-    f32x2 pre[kTilePrefetch];
+    // thread t stages chunk rows (t / 64) + 16i, i < kLdsStage, at its 4 columns
+    const int krow = threadIdx.x >> 6;
+    f32x4 pre[kLdsStage];
     auto prefetch = [&](int64_t k0) {
 #pragma unroll
-        for (int j = 0; j < kTilePrefetch; ++j) {
-            const int64_t k = k0 + krow0 + j * kTileWaves;
-            pre[j] = (k < K && n_ok) ? *reinterpret_cast<const f32x2*>(X + k * N + n)
-                                     : f32x2{0.0f, 0.0f};
+        for (int i = 0; i < kLdsStage; ++i) {
+            const int64_t k = k0 + krow + i * kLdsWaves;
+            pre[i] = (k < K && n_ok) ? *reinterpret_cast<const f32x4*>(X + k * N + n)
+                                     : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
     };
-    const int64_t nchunks = ceil_div(K, kTileK);
+    auto stage = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < kLdsStage; ++i) xs[b][krow + i * kLdsWaves][lane] = pre[i];
+    };
+    const int64_t nchunks = ceil_div(K, kLdsK);
     prefetch(0);
+    stage(0);
+    __syncthreads();
     for (int64_t ch = 0; ch < nchunks; ++ch) {
-        __syncthreads();  // every wave is done reading the previous chunk
+        const int b = static_cast<int>(ch & 1);
+        const bool more = ch + 1 < nchunks;
+        if (more) prefetch((ch + 1) * kLdsK);
+        const int32_t k0 = static_cast<int32_t>(ch * kLdsK);
+        const int32_t k1 = k0 + kLdsK;
 #pragma unroll
-        for (int j = 0; j < kTilePrefetch; ++j) xs[krow0 + j * kTileWaves][lane] = pre[j];
+        for (int j = 0; j < RW; ++j) {
+            int32_t first = pos[j] - base[j];
+            while (true) {
+                const int32_t cnt = __popcll(__ballot(lane >= first && mc[j] < k1));
+                int32_t k = 0;
+                for (; k + 2 <= cnt; k += 2) {
+                    const int32_t c0 = bcast_i(mc[j], first + k);
+                    const int32_t c1 = bcast_i(mc[j], first + k + 1);
+                    const float v0 = bcast_f(mv[j], first + k);
+                    const float v1 = bcast_f(mv[j], first + k + 1);
+                    const f32x4 x0 = xs[b][c0 - k0][lane];
+                    const f32x4 x1 = xs[b][c1 - k0][lane];
+                    fma4(v0, x0, acc[j]);
+                    fma4(v1, x1, acc[j]);
+                }
+                if (k < cnt) {
+                    const int32_t c0 = bcast_i(mc[j], first + k);
+                    fma4(bcast_f(mv[j], first + k), xs[b][c0 - k0][lane], acc[j]);
+                }
+                pos[j] += cnt;
+                if (first + cnt < kWave) break;  // the run ended inside this window
+                // window used up: shift the next one in and request the one after
+                base[j] += kWave;
+                mc[j] = nmc[j];
+                mv[j] = nmv[j];
+                lds_window(col, val, base[j] + kWave, end[j], lane, nmc[j], nmv[j]);
+                first = 0;
+            }
+        }
+        if (more) stage(b ^ 1);
         __syncthreads();
-        const int32_t k0 = static_cast<int32_t>(ch * kTileK);
-        const int32_t k1 = k0 + kTileK;
-        if (ch + 1 < nchunks) prefetch(k1);
-
-        int32_t first[kRowsPerWave], cnt[kRowsPerWave];
-        int32_t lo = kWave, hi = 0;
-#pragma unroll
-        for (int r = 0; r < kRowsPerWave; ++r) {
-            if (pos[r] < end[r] && pos[r] > base[r] + kWave / 2)
-                tile_reload(base[r], pos[r], end[r], lane, col, val, mc[r], mv[r]);
-            first[r] = pos[r] - base[r];
-            cnt[r] = __popcll(__ballot(lane >= first[r] && mc[r] < k1));
-            lo = cnt[r] < lo ? cnt[r] : lo;
-            hi = cnt[r] > hi ? cnt[r] : hi;
-        }
-        int32_t k = 0;
-        for (; k < lo; ++k) {  // every row has a slot at step k
-            f32x2 x[kRowsPerWave];
-#pragma unroll
-            for (int r = 0; r < kRowsPerWave; ++r) x[r] = xs[bcast_i(mc[r], first[r] + k) - k0][lane];
-#pragma unroll
-            for (int r = 0; r < kRowsPerWave; ++r) {
-                const float v = bcast_f(mv[r], first[r] + k);
-                acc[r][0] = __builtin_fmaf(v, x[r][0], acc[r][0]);
-                acc[r][1] = __builtin_fmaf(v, x[r][1], acc[r][1]);
-            }
-        }
-        for (; k < hi; ++k) {
-#pragma unroll
-            for (int r = 0; r < kRowsPerWave; ++r) {
-                if (k < cnt[r]) {
-                    const f32x2 x = xs[bcast_i(mc[r], first[r] + k) - k0][lane];
-                    const float v = bcast_f(mv[r], first[r] + k);
-                    acc[r][0] = __builtin_fmaf(v, x[0], acc[r][0]);
-                    acc[r][1] = __builtin_fmaf(v, x[1], acc[r][1]);
-                }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < kRowsPerWave; ++r) {
-            pos[r] += cnt[r];
-            // batch used up while the row may still have slots in this chunk
-            while (pos[r] < end[r] && pos[r] == base[r] + kWave) {
-                tile_reload(base[r], pos[r], end[r], lane, col, val, mc[r], mv[r]);
-                const int32_t c2 = __popcll(__ballot(mc[r] < k1));
-                for (int32_t q = 0; q < c2; ++q) {
-                    const f32x2 x = xs[bcast_i(mc[r], q) - k0][lane];
-                    const float v = bcast_f(mv[r], q);
-                    acc[r][0] = __builtin_fmaf(v, x[0], acc[r][0]);
-                    acc[r][1] = __builtin_fmaf(v, x[1], acc[r][1]);
-                }
-                pos[r] += c2;
-            }
-        }
     }
     if (n_ok) {
 #pragma unroll
-        for (int r = 0; r < kRowsPerWave; ++r)
-            if (r0 + r < M) {
+        for (int j = 0; j < RW; ++j) {
+            const int64_t row = r0 + static_cast<int64_t>(kLdsWaves) * j;
+            if (row < M) {
                 if (bias != nullptr) {
-                    const float b = bias[r0 + r];
-                    acc[r][0] = acc[r][0] + b;
-                    acc[r][1] = acc[r][1] + b;
+                    const float bb = bias[row];
+                    acc[j][0] = acc[j][0] + bb;
+                    acc[j][1] = acc[j][1] + bb;
+                    acc[j][2] = acc[j][2] + bb;
+                    acc[j][3] = acc[j][3] + bb;
                 }
-                *reinterpret_cast<f32x2*>(Y + (r0 + r) * N + n) = acc[r];
+                *reinterpret_cast<f32x4*>(Y + row * N + n) = acc[j];
             }
+        }
     }
 }
 
@@ -448,16 +443,26 @@ int launch_blocks(int64_t waves, int64_t* blocks) {
     return SLK_OK;
 }
 
-int launch_tile(const slk_csr* W, const float* X, int64_t N, const float* bias, float* Y,
-                hipStream_t st) {
+template <int RW>
+int launch_lds_rw(const slk_csr* W, const float* X, int64_t N, const float* bias, float* Y,
+                  hipStream_t st) {
     const int64_t M = W->nrows;
-    const int64_t nrowblk = ceil_div(M, kTileRows);
-    const int64_t blocks = nrowblk * ceil_div(N, kTileCols);
+    const int64_t nrowblk = ceil_div(M, int64_t{kLdsWaves} * RW);
+    const int64_t blocks = nrowblk * ceil_div(N, kLdsCols);
     if (blocks > INT32_MAX) return fail(SLK_EINVAL, "spmm: problem too large for one launch");
-    hipLaunchKernelGGL(spmm_tile_kernel, dim3(static_cast<unsigned>(blocks)),
-                       dim3(kTileThreads), 0, st, M, W->ncols, N, nrowblk, W->row_start,
+    hipLaunchKernelGGL((spmm_lds_kernel<RW>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kLdsThreads), 0, st, M, W->ncols, N, nrowblk, W->row_start,
                        W->row_nnz, W->col_indices, W->values, X, bias, Y);
     return check_launch("spmm");
+}
+
+int launch_lds(int rw, const slk_csr* W, const float* X, int64_t N, const float* bias, float* Y,
+               hipStream_t st) {
+    switch (rw) {
+        case 2: return launch_lds_rw<2>(W, X, N, bias, Y, st);
+        case 4: return launch_lds_rw<4>(W, X, N, bias, Y, st);
+        default: return launch_lds_rw<8>(W, X, N, bias, Y, st);
+    }
 }
 
 template <int VEC>
@@ -501,6 +506,13 @@ int launch_group_L(int L, const slk_csr* W, const float* X, int64_t N, const flo
 
 // Waves worth launching: enough to give every CU several to switch between.
 constexpr int64_t kTargetWaves = 4096;
+// LDS kernel thresholds (measured on the C3/C4/C5 layer shapes): N from which
+// it is considered, workgroups needed to keep the chip evenly busy (one per
+// CU at a time: 128 KiB of LDS each), and expected uses of each staged X
+// element below which direct gathers are as fast.
+constexpr int64_t kLdsMinN = 1024;
+constexpr int64_t kLdsMinBlocks = 512;
+constexpr double kLdsMinReuse = 4.0;
 
 // Y = W·X (+ bias per row): the shared body of slk_spmm and slk_spmm_bias.
 int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const float* bias,
@@ -520,15 +532,33 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
     const uintptr_t align = reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(Y);
     const int64_t M = W->nrows;
 
-    // Kernel choice: the per-wave gather kernels. The LDS-tiled kernel is
-    // opt-in (SLK_SPMM_KERNEL=tile, where its layout needs — even N, 8-byte
-    // aligned X and Y — hold): on the measured workloads it does not beat the
-    // wave kernel, whose X gathers already hit L2 for the tile-major order.
-    bool tile = false;
-    if (const char* e = std::getenv("SLK_SPMM_KERNEL")) {
-        if (e[0] == 't') tile = N % 2 == 0 && align % 8 == 0;
+    // Kernel choice. The LDS-staged kernel needs 16-byte lanes (N % 4 == 0,
+    // aligned X and Y) and pays off when each staged X element feeds several
+    // rows of a workgroup: expected uses = density x rows per workgroup. The
+    // per-wave gather kernels cover everything else (small N is latency-bound).
+    // SLK_SPMM_KERNEL=lds|wave and SLK_SPMM_RW=2|4|8 override the choice.
+    const bool lds_ok = N % 4 == 0 && align % 16 == 0;
+    int rw = 0;
+    if (lds_ok && N >= kLdsMinN) {
+        const double density =
+            K > 0 ? static_cast<double>(W->total_capacity) / (1.2 * M * K) : 0.0;
+        const int64_t tiles = ceil_div(N, kLdsCols);
+        for (int cand : {8, 4, 2}) {
+            const int64_t blocks = ceil_div(M, int64_t{kLdsWaves} * cand) * tiles;
+            if (blocks >= kLdsMinBlocks && density * kLdsWaves * cand >= kLdsMinReuse) {
+                rw = cand;
+                break;
+            }
+        }
     }
-    if (tile) return launch_tile(W, X, N, bias, Y, st);
+    if (const char* e = std::getenv("SLK_SPMM_KERNEL")) {
+        if (e[0] == 'w') rw = 0;
+        if (e[0] == 'l' && lds_ok && rw == 0) rw = 8;
+    }
+    if (const char* e = std::getenv("SLK_SPMM_RW")) {
+        if (rw != 0) rw = std::atoi(e);
+    }
+    if (rw != 0) return launch_lds(rw, W, X, N, bias, Y, st);
 
     int vec = 1;
     if (const char* e = std::getenv("SLK_SPMM_VEC")) vec = std::atoi(e);

@@ -117,15 +117,18 @@ def test_spmm_every_vector_width(dev, monkeypatch, vec, N, per_row):
     assert_bits_equal(_spmm(W, _t(X_np, dev)).cpu().numpy(), oracle.spmm(c, X_np), "Y")
 
 
+@pytest.mark.parametrize("rw", [2, 4, 8])
 @pytest.mark.parametrize("M,K,N,per_row", [
-    (1, 1, 2, 1), (63, 127, 62, 40), (64, 128, 128, 128), (65, 129, 130, 100),
-    (200, 300, 1000, 37), (130, 1000, 200, 700), (70, 5000, 96, 3000), (33, 260, 130, 0),
-    (9, 64, 256, 64)])
-def test_spmm_tile_kernel_bit_exact(dev, monkeypatch, M, K, N, per_row):
-    """The LDS-tiled kernel (forced): partial row/column tiles, K not a multiple
-    of the chunk, rows with more than 64 slots in one chunk, dense rows, empty rows."""
-    monkeypatch.setenv("SLK_SPMM_KERNEL", "tile")
-    print(f"[tile] M={M} K={K} N={N} per_row={per_row}", flush=True)
+    (1, 1, 4, 1), (63, 127, 64, 40), (64, 128, 256, 128), (65, 129, 260, 100),
+    (200, 300, 1000, 37), (130, 1000, 200, 700), (70, 5000, 96, 3000), (33, 260, 132, 0),
+    (9, 64, 256, 64), (300, 64, 512, 64)])
+def test_spmm_lds_kernel_bit_exact(dev, monkeypatch, rw, M, K, N, per_row):
+    """The LDS-staged kernel (forced, each rows-per-wave variant): partial row
+    blocks and column tiles, K not a multiple of the chunk, rows with more than
+    64 slots in one chunk (fully dense rows), empty rows."""
+    monkeypatch.setenv("SLK_SPMM_KERNEL", "lds")
+    monkeypatch.setenv("SLK_SPMM_RW", str(rw))
+    print(f"[lds rw={rw}] M={M} K={K} N={N} per_row={per_row}", flush=True)
     c, X_np, _ = _case(M, K, N, per_row, seed=M + K + N)
     W = from_oracle(c, dev)
     assert_bits_equal(_spmm(W, _t(X_np, dev)).cpu().numpy(), oracle.spmm(c, X_np), "Y")
@@ -133,11 +136,12 @@ def test_spmm_tile_kernel_bit_exact(dev, monkeypatch, M, K, N, per_row):
 
 @pytest.mark.parametrize("env,N", [
     ({"SLK_SPMM_VEC": "1"}, 300), ({"SLK_SPMM_VEC": "2"}, 300), ({"SLK_SPMM_VEC": "4"}, 1024),
-    ({}, 5), ({}, 40), ({"SLK_SPMM_KERNEL": "tile"}, 130)])
+    ({}, 5), ({}, 40), ({"SLK_SPMM_KERNEL": "lds"}, 132),
+    ({"SLK_SPMM_KERNEL": "lds", "SLK_SPMM_RW": "2"}, 1024)])
 def test_spmm_bias_epilogue_bit_exact(dev, monkeypatch, env, N):
     """slk_spmm_bias = slk_spmm followed by one float32 add of bias[i] per row,
     in every kernel (wave kernel at each lane width, packed narrow-N kernel,
-    LDS-tiled kernel), including rows with no live slot (Y = 0 + bias)."""
+    LDS-staged kernel), including rows with no live slot (Y = 0 + bias)."""
     for k, v in env.items():
         monkeypatch.setenv(k, v)
     print(f"[bias] env={env} N={N}", flush=True)
@@ -154,8 +158,8 @@ def test_spmm_bias_epilogue_bit_exact(dev, monkeypatch, env, N):
     assert_bits_equal(Y.cpu().numpy(), ref, "Y+bias")
 
 
-def test_spmm_tile_kernel_skewed_rows(dev, monkeypatch):
-    monkeypatch.setenv("SLK_SPMM_KERNEL", "tile")
+def test_spmm_lds_kernel_skewed_rows(dev, monkeypatch):
+    monkeypatch.setenv("SLK_SPMM_KERNEL", "lds")
     c = oracle.zipf_rows(300, 700, 0.08, 1.1, seed=5, sigma=0.5)
     X_np = np.random.default_rng(5).standard_normal((700, 192)).astype(np.float32)
     W = from_oracle(c, dev)
@@ -189,6 +193,36 @@ def test_skewed_rows_bit_exact(dev):
     WT_o, perm_o = oracle.transpose_with_perm(c)
     csr_arrays_equal(to_oracle(WT), WT_o, "WT")
     assert_bits_equal(perm.cpu().numpy(), perm_o, "perm")
+
+
+@pytest.mark.parametrize("G", [1, 2, 4])
+@pytest.mark.parametrize("N", [16, 24, 256, 260, 264, 271, 512, 1000, 1031, 2048])
+def test_sddmm_windowed_groups_bit_exact(dev, monkeypatch, G, N):
+    """dW with G groups of 16 slots per wave swept through N one window at a
+    time (the launcher's choice for 16-byte-aligned large N; SLK_SDDMM_G forces
+    G, 1 = the one-group kernel). Cases: groups inside one row, across rows,
+    rows of 1..3 live slots, empty rows, a fully dense row, padding ratios 0
+    and 1, an 8-wide tail step, a scalar tail, partial windows, and a capacity
+    that is not a multiple of the wave."""
+    monkeypatch.setenv("SLK_SDDMM_G", str(G))
+    kernel = f"G={G}"
+    print(f"[sddmm {kernel}] N={N}", flush=True)
+    rng = np.random.default_rng(N + G)
+    cases = [oracle.uniform_rows(97, 50, 3, seed=N, sigma=1.0, padding_ratio=0.2),
+             oracle.uniform_rows(64, 40, 1, seed=N + 1, sigma=1.0, padding_ratio=0.0),
+             oracle.zipf_rows(120, 300, 0.05, 1.1, seed=N + 2, sigma=0.5),
+             oracle.uniform_rows(33, 64, 20, seed=N + 3, sigma=1.0, padding_ratio=1.0),
+             oracle.uniform_rows(7, 500, 300, seed=N + 4, sigma=1.0, padding_ratio=0.2)]
+    c = cases[3]
+    c.row_nnz[5] = 0
+    c.col_indices[c.row_start[5]:c.row_start[5] + c.row_capacity[5]] = -1
+    c.values[c.row_start[5]:c.row_start[5] + c.row_capacity[5]] = 0.0
+    for i, c in enumerate(cases):
+        X_np = rng.standard_normal((c.ncols, N)).astype(np.float32)
+        dY_np = rng.standard_normal((c.nrows, N)).astype(np.float32)
+        W = from_oracle(c, dev)
+        got = _sddmm(W, _t(dY_np, dev), _t(X_np, dev)).cpu().numpy()
+        assert_bits_equal(got, oracle.sddmm(c, dY_np, X_np), f"dW case {i}")
 
 
 @pytest.mark.parametrize("N", [1, 5, 40, 256, 1028])
