@@ -392,17 +392,18 @@ __global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
             while (true) {
                 const int32_t cnt = __popcll(__ballot(lane >= first && mc[j] < k1));
                 int32_t k = 0;
-                for (; k + 2 <= cnt; k += 2) {
-                    const int32_t c0 = bcast_i(mc[j], first + k);
-                    const int32_t c1 = bcast_i(mc[j], first + k + 1);
-                    const float v0 = bcast_f(mv[j], first + k);
-                    const float v1 = bcast_f(mv[j], first + k + 1);
-                    const f32x4 x0 = xs[b][c0 - k0][lane];
-                    const f32x4 x1 = xs[b][c1 - k0][lane];
-                    fma4(v0, x0, acc[j]);
-                    fma4(v1, x1, acc[j]);
+                for (; k + 4 <= cnt; k += 4) {  // four LDS reads in flight
+                    const int32_t s0 = first + k;
+                    const f32x4 x0 = xs[b][bcast_i(mc[j], s0) - k0][lane];
+                    const f32x4 x1 = xs[b][bcast_i(mc[j], s0 + 1) - k0][lane];
+                    const f32x4 x2 = xs[b][bcast_i(mc[j], s0 + 2) - k0][lane];
+                    const f32x4 x3 = xs[b][bcast_i(mc[j], s0 + 3) - k0][lane];
+                    fma4(bcast_f(mv[j], s0), x0, acc[j]);
+                    fma4(bcast_f(mv[j], s0 + 1), x1, acc[j]);
+                    fma4(bcast_f(mv[j], s0 + 2), x2, acc[j]);
+                    fma4(bcast_f(mv[j], s0 + 3), x3, acc[j]);
                 }
-                if (k < cnt) {
+                for (; k < cnt; ++k) {
                     const int32_t c0 = bcast_i(mc[j], first + k);
                     fma4(bcast_f(mv[j], first + k), xs[b][c0 - k0][lane], acc[j]);
                 }
@@ -468,7 +469,7 @@ int launch_lds(int rw, const slk_csr* W, const float* X, int64_t N, const float*
 template <int VEC>
 int launch_wave(const slk_csr* W, const float* X, int64_t N, const float* bias, float* Y,
                 hipStream_t st) {
-    constexpr int U = VEC == 4 ? 8 : 16;
+    constexpr int U = VEC == 4 ? 8 : VEC == 2 ? 16 : 32;  // 2U gathers in flight per wave
     const int64_t M = W->nrows;
     const int64_t nitems = M * ceil_div(N, int64_t{kWave} * VEC);
     int64_t blocks;
