@@ -10,12 +10,13 @@
 //
 //   T1 hist    one workgroup per block of B consecutive W rows counts the
 //              block's columns in LDS and writes bh[b][c].
-//   T2 colscan one thread per column turns bh[.][c] into the exclusive
-//              prefix over blocks (the block's starting rank inside WT row c)
-//              and writes WT row_nnz / row_capacity.
+//   T2 colscan turns bh[.][c] into the exclusive prefix over blocks (the
+//              block's starting rank inside WT row c), 16 waves per 64
+//              columns, and writes WT row_nnz / row_capacity.
 //   T3 scan    exclusive scan of the WT capacities -> WT row_start, capT.
 //   (host)     reads capT, allocates the WT slot arrays.
-//   T4 pad     writes padding slots (col -1, value 0, perm -1).
+//   T4 pad     writes padding slots (col -1, value 0, perm -1), one wave
+//              per WT row.
 //   T5 scatter one wave per block walks its rows in ascending order and
 //              places every live slot at WT row_start[c] + rank, with the
 //              running rank kept per column in LDS. A row's columns are
@@ -77,32 +78,44 @@ __global__ __launch_bounds__(256) void tr_hist_kernel(
     }
 }
 
-__global__ __launch_bounds__(256) void tr_colscan_kernel(int64_t K, int64_t nblk,
-                                                         double one_plus_pr,
-                                                         int32_t* __restrict__ bh,
-                                                         int32_t* __restrict__ nnz_t,
-                                                         int32_t* __restrict__ cap_t) {
-    const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (c >= K) return;
+// T2: 16 waves per workgroup, one lane per column: wave w sums its share of
+// the blocks for the workgroup's 64 columns (coalesced rows of bh), the
+// partial sums are combined in LDS, and each wave rewrites its share as the
+// exclusive prefix.
+constexpr int kColScanWaves = 16;
+
+__global__ __launch_bounds__(kColScanWaves * kWave) void tr_colscan_kernel(
+    int64_t K, int64_t nblk, double one_plus_pr, int32_t* __restrict__ bh,
+    int32_t* __restrict__ nnz_t, int32_t* __restrict__ cap_t) {
+    __shared__ int32_t part[kColScanWaves][kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int w = threadIdx.x >> 6;
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * kWave + lane;
+    const bool ok = c < K;
+    const int64_t per = ceil_div(nblk, kColScanWaves);
+    const int64_t b0 = min(nblk, w * per);
+    const int64_t b1 = min(nblk, b0 + per);
+    int32_t sum = 0;
+    if (ok) {
+        for (int64_t b = b0; b < b1; ++b) sum += bh[b * K + c];
+    }
+    part[w][lane] = sum;
+    __syncthreads();
     int32_t run = 0;
-    int64_t b = 0;
-    for (; b + 4 <= nblk; b += 4) {
-        const int32_t t0 = bh[(b + 0) * K + c], t1 = bh[(b + 1) * K + c];
-        const int32_t t2 = bh[(b + 2) * K + c], t3 = bh[(b + 3) * K + c];
-        bh[(b + 0) * K + c] = run; run += t0;
-        bh[(b + 1) * K + c] = run; run += t1;
-        bh[(b + 2) * K + c] = run; run += t2;
-        bh[(b + 3) * K + c] = run; run += t3;
+    for (int v = 0; v < w; ++v) run += part[v][lane];
+    if (ok) {
+        for (int64_t b = b0; b < b1; ++b) {
+            const int32_t t = bh[b * K + c];
+            bh[b * K + c] = run;
+            run += t;
+        }
     }
-    for (; b < nblk; ++b) {
-        const int32_t t = bh[b * K + c];
-        bh[b * K + c] = run;
-        run += t;
+    if (ok && w == kColScanWaves - 1) {  // the last share ends at the column total
+        nnz_t[c] = run;
+        // layout.py:66-67: np.maximum(1, np.ceil(nnz.astype(float64) * (1 + pr))).astype(int32)
+        const double scaled = ceil(static_cast<double>(run) * one_plus_pr);
+        cap_t[c] = scaled < 1.0 ? 1 : static_cast<int32_t>(scaled);
     }
-    nnz_t[c] = run;
-    // layout.py:66-67: np.maximum(1, np.ceil(nnz.astype(float64) * (1 + pr))).astype(int32)
-    const double scaled = ceil(static_cast<double>(run) * one_plus_pr);
-    cap_t[c] = scaled < 1.0 ? 1 : static_cast<int32_t>(scaled);
 }
 
 constexpr int kScanThreads = 1024;
@@ -135,16 +148,19 @@ __global__ __launch_bounds__(kScanThreads) void tr_scan_kernel(int64_t K,
     if (t == kScanThreads - 1) *cap_total = part[t];
 }
 
+// T4: one wave per WT row; lanes write consecutive padding slots.
 __global__ __launch_bounds__(256) void tr_pad_kernel(int64_t K, const int32_t* __restrict__ start_t,
                                                      const int32_t* __restrict__ nnz_t,
                                                      const int32_t* __restrict__ cap_t,
                                                      float* __restrict__ val_t,
                                                      int32_t* __restrict__ col_t,
                                                      int64_t* __restrict__ perm) {
-    const int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t c = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
     if (c >= K) return;
+    const int lane = threadIdx.x & (kWave - 1);
     const int64_t rs = start_t[c];
-    for (int64_t p = rs + nnz_t[c]; p < rs + cap_t[c]; ++p) {
+    const int64_t end = rs + cap_t[c];
+    for (int64_t p = rs + nnz_t[c] + lane; p < end; p += kWave) {
         col_t[p] = -1;
         val_t[p] = 0.0f;
         perm[p] = -1;
@@ -250,8 +266,9 @@ extern "C" int slk_transpose_count(const slk_csr* W, double padding_ratio, void*
                            bh);
         if (int rc = check_launch("transpose_count/hist")) return rc;
     }
-    hipLaunchKernelGGL(tr_colscan_kernel, dim3(static_cast<unsigned>(ceil_div(K, 256))), dim3(256),
-                       0, st, K, p.nblk, 1.0 + padding_ratio, bh, WT_row_nnz, WT_row_capacity);
+    hipLaunchKernelGGL(tr_colscan_kernel, dim3(static_cast<unsigned>(ceil_div(K, kWave))),
+                       dim3(kColScanWaves * kWave), 0, st, K, p.nblk, 1.0 + padding_ratio, bh,
+                       WT_row_nnz, WT_row_capacity);
     if (int rc = check_launch("transpose_count/colscan")) return rc;
     hipLaunchKernelGGL(tr_scan_kernel, dim3(1), dim3(kScanThreads), 0, st, K, WT_row_capacity,
                        WT_row_start, capT_dev);
@@ -280,9 +297,9 @@ extern "C" int slk_transpose_fill(const slk_csr* W, const void* workspace, int64
         return fail(SLK_EINVAL, "transpose: workspace too small");
     }
     hipStream_t st = as_stream(stream);
-    hipLaunchKernelGGL(tr_pad_kernel, dim3(static_cast<unsigned>(ceil_div(K, 256))), dim3(256), 0,
-                       st, K, WT_row_start, WT_row_nnz, WT_row_capacity, WT_values, WT_col_indices,
-                       perm);
+    hipLaunchKernelGGL(tr_pad_kernel, dim3(static_cast<unsigned>(ceil_div(K, 256 / kWave))),
+                       dim3(256), 0, st, K, WT_row_start, WT_row_nnz, WT_row_capacity, WT_values,
+                       WT_col_indices, perm);
     if (int rc = check_launch("transpose_fill/pad")) return rc;
     if (p.nblk == 0) return SLK_OK;
     const size_t lds = static_cast<size_t>(K < kColChunk ? K : kColChunk) * sizeof(int32_t);
