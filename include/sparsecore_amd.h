@@ -107,6 +107,15 @@ SLK_API int slk_sddmm(const slk_csr* W, const float* dY, int64_t dY_rows,
               const float* X, int64_t X_rows, int64_t N, float* dW,
               int order, void* stream);
 
+/* slk_sddmm plus dbias[i] = sum_j dY[i,j] (W->nrows floats) in the same
+ * launch: the gradient of SparseLinear's bias add (sparselab/nn.py:237-241),
+ * which the reference gets from torch autograd as a separate reduction. dW
+ * is bit-identical to slk_sddmm's; each dbias element is a fixed-order sum
+ * (lane-strided partials, then a butterfly), repeatable run to run.         */
+SLK_API int slk_sddmm_bias(const slk_csr* W, const float* dY, int64_t dY_rows,
+                   const float* X, int64_t X_rows, int64_t N, float* dW,
+                   float* dbias, int order, void* stream);
+
 /* Transpose build, part 1 of 2 (replaces the index work of
  * `transpose_with_perm`, sparselab/layout.py:460-536).
  * Bytes of device workspace slk_transpose_count needs for W.                */
@@ -209,6 +218,16 @@ SLK_API int slk_drop_grow(const slk_csr* W, float* values, int32_t* col_indices,
  * activations, as RigL captures them), read without a transpose copy.     */
 SLK_API int slk_dense_grad(const float* dY, const float* X, int64_t M, int64_t K,
                            int64_t N, int token_major, float* G, void* stream);
+
+/* ─── Dense layout ─────────────────────────────────────────────────────── */
+
+/* dst = src^T for a float32 matrix: src is rows x cols with row stride
+ * ld_src (>= cols), dst is cols x rows row-major; a bitwise copy. Replaces
+ * the layout copies around the kernels: SparseLinear's `x.t().contiguous()`
+ * (sparselab/nn.py:235) and the backward's `dY.contiguous()` of a transposed
+ * gradient (sparselab/ops.py:174).                                          */
+SLK_API int slk_transpose_dense(const float* src, int64_t rows, int64_t cols,
+                                int64_t ld_src, float* dst, void* stream);
 
 #ifdef __cplusplus
 }

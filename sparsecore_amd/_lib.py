@@ -36,6 +36,7 @@ EXPORTS = (
     "slk_spmm",
     "slk_spmm_bias",
     "slk_sddmm",
+    "slk_sddmm_bias",
     "slk_transpose_workspace_bytes",
     "slk_transpose_count",
     "slk_transpose_fill",
@@ -45,6 +46,7 @@ EXPORTS = (
     "slk_drop_grow_workspace_bytes",
     "slk_drop_grow",
     "slk_dense_grad",
+    "slk_transpose_dense",
 )
 
 
@@ -79,6 +81,7 @@ def _declare(lib) -> None:
     lib.slk_spmm.argtypes = [_csrp, _vp, _i64, _i64, _vp, _vp]
     lib.slk_spmm_bias.argtypes = [_csrp, _vp, _i64, _i64, _vp, _vp, _vp]
     lib.slk_sddmm.argtypes = [_csrp, _vp, _i64, _vp, _i64, _i64, _vp, ctypes.c_int, _vp]
+    lib.slk_sddmm_bias.argtypes = [_csrp, _vp, _i64, _vp, _i64, _i64, _vp, _vp, ctypes.c_int, _vp]
     lib.slk_transpose_workspace_bytes.restype = _i64
     lib.slk_transpose_workspace_bytes.argtypes = [_csrp]
     lib.slk_transpose_count.argtypes = [_csrp, ctypes.c_double, _vp, _i64, _vp, _vp, _vp, _vp,
@@ -92,6 +95,7 @@ def _declare(lib) -> None:
     lib.slk_drop_grow.argtypes = [_csrp, _vp, _vp, _vp, ctypes.c_int, _vp, _i64, ctypes.c_uint64,
                                   _vp, _i64, _vp]
     lib.slk_dense_grad.argtypes = [_vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp, _vp]
+    lib.slk_transpose_dense.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp]
     sized = ("slk_last_error", "slk_abi_version", "slk_transpose_workspace_bytes",
              "slk_drop_grow_workspace_bytes")
     for name in EXPORTS:
@@ -160,10 +164,15 @@ def spmm(view: CsrView, X: torch.Tensor, Y: torch.Tensor,
 
 
 def sddmm(view: CsrView, dY: torch.Tensor, X: torch.Tensor, dW: torch.Tensor,
-          order: int) -> None:
+          order: int, dbias: torch.Tensor | None = None) -> None:
+    """dW on the live slots; with ``dbias`` also its row sums of dY (same launch)."""
     lib = load()
-    rc = lib.slk_sddmm(ctypes.byref(view), ptr(dY), dY.shape[0], ptr(X), X.shape[0],
-                       X.shape[1], ptr(dW), order, stream_of(dW))
+    if dbias is None:
+        rc = lib.slk_sddmm(ctypes.byref(view), ptr(dY), dY.shape[0], ptr(X), X.shape[0],
+                           X.shape[1], ptr(dW), order, stream_of(dW))
+    else:
+        rc = lib.slk_sddmm_bias(ctypes.byref(view), ptr(dY), dY.shape[0], ptr(X), X.shape[0],
+                                X.shape[1], ptr(dW), ptr(dbias), order, stream_of(dbias))
     if rc:
         _raise(rc)
 
@@ -236,5 +245,16 @@ def dense_grad(dY: torch.Tensor, X: torch.Tensor, M: int, K: int, N: int, token_
                G: torch.Tensor) -> None:
     lib = load()
     rc = lib.slk_dense_grad(ptr(dY), ptr(X), M, K, N, int(token_major), ptr(G), stream_of(G))
+    if rc:
+        _raise(rc)
+
+
+def transpose_dense(src: torch.Tensor, dst: torch.Tensor) -> None:
+    """dst (cols x rows, contiguous) = srcᵀ for a float32 src (rows x cols) whose
+    rows are contiguous (stride(1) == 1)."""
+    lib = load()
+    rows, cols = src.shape
+    rc = lib.slk_transpose_dense(ptr(src), rows, cols, src.stride(0) if rows > 1 else cols,
+                                 ptr(dst), stream_of(dst))
     if rc:
         _raise(rc)

@@ -98,6 +98,23 @@ __device__ __forceinline__ float running_sum(const float* __restrict__ a,
     return acc;
 }
 
+// dbias[row] = sum_j dY[row, j], one wave per row: lane-strided partial sums
+// combined by a butterfly, so the order is fixed and the result repeatable.
+// This is the gradient of SparseLinear's bias add (sparselab/nn.py:237-241),
+// which torch's autograd forms as a separate reduction; here it rides in the
+// weight-gradient launch as extra waves.
+__device__ __forceinline__ void bias_row_sum(const float* __restrict__ dY, int64_t M, int64_t N,
+                                             int64_t row, float* __restrict__ dbias) {
+    if (row >= M) return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const float* p = dY + row * N;
+    float acc = 0.0f;
+    for (int64_t j = lane; j < N; j += kWave) acc = acc + p[j];
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off);
+    if (lane == 0) dbias[row] = acc;
+}
+
 template <bool V4>
 __device__ __forceinline__ void load4(const float* p, float& a, float& b, float& c, float& d) {
     if constexpr (V4) {
@@ -113,12 +130,17 @@ __global__ __launch_bounds__(kBlock) void sddmm_simd_kernel(
     int64_t M, int64_t N, int64_t cap_total,
     const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
     const int32_t* __restrict__ col, const float* __restrict__ dY,
-    const float* __restrict__ X, float* __restrict__ dW) {
+    const float* __restrict__ X, float* __restrict__ dW, float* __restrict__ dbias,
+    int64_t slot_waves) {
     const int lane = threadIdx.x & (kWave - 1);
     const int g = lane >> 2;  // slot within the wave
     const int q = lane & 3;   // owns virtual lanes 4q..4q+3
-    const int64_t wslot = wave_id() * kSlotsPerWave;
-    if (wslot >= cap_total) return;  // wave-uniform
+    const int64_t wid = wave_id();
+    if (wid >= slot_waves) {  // wave-uniform: a bias-gradient wave
+        if (dbias != nullptr) bias_row_sum(dY, M, N, wid - slot_waves, dbias);
+        return;
+    }
+    const int64_t wslot = wid * kSlotsPerWave;
     const int64_t slot = wslot + g;
     const bool in_range = slot < cap_total;
     const WaveRows rows(row_start, M, wslot, min(wslot + kSlotsPerWave - 1, cap_total - 1));
@@ -230,15 +252,20 @@ __global__ __launch_bounds__(kBlock) void sddmm_simd_win_kernel(
     int64_t M, int64_t N, int64_t cap_total,
     const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
     const int32_t* __restrict__ col, const float* __restrict__ dY,
-    const float* __restrict__ X, float* __restrict__ dW) {
+    const float* __restrict__ X, float* __restrict__ dW, float* __restrict__ dbias,
+    int64_t slot_waves) {
     constexpr int kWavesPerBlock = kBlock / kWave;
     __shared__ f32x4 dys[kWavesPerBlock][G][2][kWave];  // 2 KiB per group
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = threadIdx.x >> 6;
     const int g = lane >> 2;
     const int q = lane & 3;
-    const int64_t base = wave_id() * (kSlotsPerWave * G);
-    if (base >= cap_total) return;  // wave-uniform
+    const int64_t wid = wave_id();
+    if (wid >= slot_waves) {  // wave-uniform: a bias-gradient wave
+        if (dbias != nullptr) bias_row_sum(dY, M, N, wid - slot_waves, dbias);
+        return;
+    }
+    const int64_t base = wid * (kSlotsPerWave * G);
 
     bool in[G], live[G], direct[G];
     int sel[G];
@@ -379,9 +406,14 @@ __global__ __launch_bounds__(kBlock) void sddmm_scalar_kernel(
     int64_t M, int64_t N, int64_t cap_total,
     const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
     const int32_t* __restrict__ col, const float* __restrict__ dY,
-    const float* __restrict__ X, float* __restrict__ dW) {
-    const int64_t wslot = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) & ~int64_t{kWave - 1};
-    if (wslot >= cap_total) return;  // wave-uniform
+    const float* __restrict__ X, float* __restrict__ dW, float* __restrict__ dbias,
+    int64_t slot_waves) {
+    const int64_t wid = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+    if (wid >= slot_waves) {  // wave-uniform: a bias-gradient wave
+        if (dbias != nullptr) bias_row_sum(dY, M, N, wid - slot_waves, dbias);
+        return;
+    }
+    const int64_t wslot = wid * kWave;
     const WaveRows rows(row_start, M, wslot, min(wslot + kWave - 1, cap_total - 1));
     const int64_t slot = wslot + (threadIdx.x & (kWave - 1));
     if (slot >= cap_total) return;
@@ -395,12 +427,9 @@ __global__ __launch_bounds__(kBlock) void sddmm_scalar_kernel(
     dW[slot] = running_sum(dyr, xr, N, 0.0f);
 }
 
-}  // namespace
-}  // namespace slk
 
-extern "C" int slk_sddmm(const slk_csr* W, const float* dY, int64_t dY_rows, const float* X,
-                         int64_t X_rows, int64_t N, float* dW, int order, void* stream) {
-    using namespace slk;
+int sddmm_impl(const slk_csr* W, const float* dY, int64_t dY_rows, const float* X,
+               int64_t X_rows, int64_t N, float* dW, float* dbias, int order, void* stream) {
     clear_error();
     const char* who = order == SLK_DW_SCALAR ? "spmm_grad_w" : "spmm_grad_w_simd";
     if (int rc = validate_csr(W, who)) return rc;
@@ -419,14 +448,17 @@ extern "C" int slk_sddmm(const slk_csr* W, const float* dY, int64_t dY_rows, con
     }
     if (N < 0) return fail(SLK_EINVAL, std::string(who) + ": negative N");
     const int64_t cap = W->total_capacity;
-    if (cap == 0) return SLK_OK;
-    if (dW == nullptr) return fail(SLK_EINVAL, std::string(who) + ": NULL dW");
+    const int64_t bias_waves = dbias != nullptr ? W->nrows : 0;
+    if (cap == 0 && bias_waves == 0) return SLK_OK;
+    if (dW == nullptr && cap > 0) return fail(SLK_EINVAL, std::string(who) + ": NULL dW");
     hipStream_t st = as_stream(stream);
     if (order == SLK_DW_SCALAR) {
-        const int64_t blocks = ceil_div(cap, kBlock);
+        const int64_t slot_waves = ceil_div(cap, kWave);
+        const int64_t blocks = ceil_div(slot_waves + bias_waves, kBlock / kWave);
+        if (blocks > INT32_MAX) return fail(SLK_EINVAL, std::string(who) + ": problem too large");
         hipLaunchKernelGGL(sddmm_scalar_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kBlock),
                            0, st, W->nrows, N, cap, W->row_start, W->row_nnz, W->col_indices, dY,
-                           X, dW);
+                           X, dW, dbias, slot_waves);
         return check_launch(who);
     }
     const bool v4 = (N % 4 == 0) && (reinterpret_cast<uintptr_t>(X) % 16 == 0) &&
@@ -439,11 +471,12 @@ extern "C" int slk_sddmm(const slk_csr* W, const float* dY, int64_t dY_rows, con
     if (v4 && N >= kWinMinN) G = cap >= 4 * kWinMinSlots ? 4 : cap >= 2 * kWinMinSlots ? 2 : 1;
     if (const char* e = std::getenv("SLK_SDDMM_G")) G = std::atoi(e);
     if (!v4 || (G != 2 && G != 4)) G = 1;
-    const int64_t waves = ceil_div(cap, kSlotsPerWave * G);
-    const int64_t blocks = ceil_div(waves, kBlock / kWave);
+    const int64_t slot_waves = ceil_div(cap, kSlotsPerWave * G);
+    const int64_t blocks = ceil_div(slot_waves + bias_waves, kBlock / kWave);
     if (blocks > INT32_MAX) return fail(SLK_EINVAL, std::string(who) + ": problem too large");
     const dim3 grid(static_cast<unsigned>(blocks));
-#define SLK_SDDMM_ARGS W->nrows, N, cap, W->row_start, W->row_nnz, W->col_indices, dY, X, dW
+#define SLK_SDDMM_ARGS \
+    W->nrows, N, cap, W->row_start, W->row_nnz, W->col_indices, dY, X, dW, dbias, slot_waves
     if (G == 2) {
         hipLaunchKernelGGL(sddmm_simd_win_kernel<2>, grid, dim3(kBlock), 0, st, SLK_SDDMM_ARGS);
     } else if (G == 4) {
@@ -455,4 +488,22 @@ extern "C" int slk_sddmm(const slk_csr* W, const float* dY, int64_t dY_rows, con
     }
 #undef SLK_SDDMM_ARGS
     return check_launch(who);
+}
+
+}  // namespace
+}  // namespace slk
+
+extern "C" int slk_sddmm(const slk_csr* W, const float* dY, int64_t dY_rows, const float* X,
+                         int64_t X_rows, int64_t N, float* dW, int order, void* stream) {
+    return slk::sddmm_impl(W, dY, dY_rows, X, X_rows, N, dW, nullptr, order, stream);
+}
+
+extern "C" int slk_sddmm_bias(const slk_csr* W, const float* dY, int64_t dY_rows, const float* X,
+                              int64_t X_rows, int64_t N, float* dW, float* dbias, int order,
+                              void* stream) {
+    if (dbias == nullptr && W != nullptr && W->nrows > 0) {
+        slk::clear_error();
+        return slk::fail(SLK_EINVAL, "spmm_grad_w: NULL dbias");
+    }
+    return slk::sddmm_impl(W, dY, dY_rows, X, X_rows, N, dW, dbias, order, stream);
 }

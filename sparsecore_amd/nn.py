@@ -17,7 +17,7 @@ import torch.nn as nn
 
 from . import layout as _layout
 from .layout import PaddedCSR
-from .ops import _SpMMBiasFunction, _SpMMFunction
+from .ops import _SparseLinearFunction
 
 __all__ = ["SparseLinear"]
 
@@ -100,17 +100,18 @@ class SparseLinear(nn.Module):
         if orig_shape[-1] != self.in_features:
             raise ValueError(f"SparseLinear expects input last dim {self.in_features}, "
                              f"got {orig_shape[-1]}")
-        # (N, in) -> (in, N) row-major. One copy at most: none when x is the
-        # transposed view a previous SparseLinear returned.
-        X_col = x.reshape(-1, self.in_features).t().contiguous()
+        # One autograd node: the (N, in) -> (in, N) layout change (none when x
+        # is the transposed view a previous SparseLinear returned), the SpMM
+        # with the bias add fused into its store, and the matching backward.
+        x_flat = x.reshape(-1, self.in_features)
+        if x_flat.dtype != torch.float32:
+            x_flat = x_flat.to(torch.float32)
         b = self.bias
-        if b is not None and b.dtype == torch.float32 and b.device == X_col.device:
-            # bias add fused into the SpMM store: same bits as the separate add
-            Y_col = _SpMMBiasFunction.apply(self._values, b, self._csr, X_col, "simd")
+        if b is not None and b.dtype != torch.float32:
+            Y_col = _SparseLinearFunction.apply(self._values, None, self._csr, x_flat, "simd")
+            Y_col = Y_col + b.to(torch.float32)[:, None]
         else:
-            Y_col = _SpMMFunction.apply(self._values, self._csr, X_col, "simd")
-            if b is not None:
-                Y_col = Y_col + b[:, None]
+            Y_col = _SparseLinearFunction.apply(self._values, b, self._csr, x_flat, "simd")
         y_flat = Y_col.t()
         return y_flat.reshape(orig_shape[:-1] + (self.out_features,))
 

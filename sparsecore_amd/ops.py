@@ -72,10 +72,11 @@ def _launch_spmm(W: PaddedCSR, X: torch.Tensor, bias: torch.Tensor | None = None
     return Y
 
 
-def _launch_sddmm(W: PaddedCSR, dY: torch.Tensor, X: torch.Tensor, kernel: str) -> torch.Tensor:
+def _launch_sddmm(W: PaddedCSR, dY: torch.Tensor, X: torch.Tensor, kernel: str,
+                  dbias: torch.Tensor | None = None) -> torch.Tensor:
     dW = torch.empty(W.total_capacity, dtype=torch.float32, device=X.device)
     order = _lib.SLK_DW_SCALAR if kernel == "scalar" else _lib.SLK_DW_SIMD
-    _lib.sddmm(W._view(), dY, X, dW, order)
+    _lib.sddmm(W._view(), dY, X, dW, order, dbias)
     return dW
 
 
@@ -117,55 +118,85 @@ class _SpMMFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dY):
         W_values, X = ctx.saved_tensors
-        dW_values, dX = _spmm_backward(ctx.W, X, _device_f32(dY), ctx.kernel,
+        dW_values, dX = _spmm_backward(ctx.W, X, _as_row_major(dY), ctx.kernel,
                                        ctx.needs_input_grad[0], ctx.needs_input_grad[2])
         return dW_values, None, dX, None
 
 
 def _spmm_backward(W: PaddedCSR, X: torch.Tensor, dY_f32: torch.Tensor, kernel: str,
-                   need_dw: bool, need_dx: bool):
+                   need_dw: bool, need_dx: bool, dbias: torch.Tensor | None = None):
     """dW on the live slots (SDDMM) and dX = Wᵀ·dY through the transpose cache
-    (ops.py:167-210); a gradient that is not needed is not computed."""
+    (ops.py:167-210); a gradient that is not needed is not computed. With
+    ``dbias`` (and dW needed) the dW launch also writes dY's row sums there."""
     dW_values = dX = None
     if need_dw:
-        dW_values = _launch_sddmm(W, dY_f32, _device_f32(X), kernel)
+        dW_values = _launch_sddmm(W, dY_f32, _device_f32(X), kernel, dbias)
     if need_dx:
         WT = _cached_transpose(W)
         dX = _launch_spmm(WT, dY_f32)
     return dW_values, dX
 
 
-class _SpMMBiasFunction(torch.autograd.Function):
-    """``Y = W @ X + bias[:, None]`` in one launch: SparseLinear's forward with
-    the bias add (sparselab/nn.py:237-241) fused into the SpMM's store.
+def _as_row_major(t: torch.Tensor) -> torch.Tensor:
+    """``t.to(float32).contiguous()`` where a transposed view is copied by the
+    library's tiled transpose (slk_transpose_dense) instead of torch's
+    strided copy: the `dY.contiguous()` of ops.py:174, bit for bit."""
+    t = t.to(dtype=torch.float32)
+    if t.is_contiguous():
+        return t
+    if t.dim() == 2 and t.t().is_contiguous() and t.device.type == "cuda":
+        out = torch.empty(t.shape, dtype=torch.float32, device=t.device)
+        _lib.transpose_dense(t.t(), out)
+        return out
+    return t.contiguous()
 
-    Y holds the same bits as ``_SpMMFunction`` followed by a separate float32
-    add. Backward is ``_SpMMFunction``'s, plus dbias = Σ_n dY[:, n].
+
+class _SparseLinearFunction(torch.autograd.Function):
+    """SparseLinear's ``Y = W @ x_flatᵀ (+ bias[:, None])`` as one autograd node
+    (sparselab/nn.py:229-241 with ops.py:127-210 inside).
+
+    Takes the token-major input x_flat (N x K) and returns Y feature-major
+    (M x N), whose ``.t()`` is the layer output. The layout changes of the
+    reference (``x_flat.t().contiguous()``, the bias add, ``dY.contiguous()``)
+    are done by the library: the transpose by slk_transpose_dense — free when
+    x_flat is the transposed view a previous SparseLinear returned — and the
+    bias add inside the SpMM store (slk_spmm_bias: the bits of the separate
+    float32 add). Backward is ``_SpMMFunction``'s, plus dbias = Σ_n dY[:, n]
+    computed in the dW launch (slk_sddmm_bias); dx is returned as the
+    transposed view of dX (K x N).
     """
 
     @staticmethod
-    def forward(ctx, W_values, bias, W, X, kernel):
-        ctx.save_for_backward(W_values, X)
-        ctx.W = W
-        ctx.kernel = kernel
+    def forward(ctx, W_values, bias, W, x_flat, kernel):
         if kernel not in _KERNELS:
             raise ValueError(f"spmm: unknown kernel={kernel!r}. Expected one of: "
                              f"{sorted(_KERNELS)}.")
-        _check_same_device(W, X, "spmm", "X")
-        _check_same_device(W, bias, "spmm", "bias")
-        if bias.dtype != torch.float32 or bias.shape != (W.nrows,):
-            raise ValueError(f"spmm: bias must be float32 of shape ({W.nrows},), got "
-                             f"{bias.dtype} {tuple(bias.shape)}")
-        return _launch_spmm(W, _device_f32(X), bias.contiguous())
+        _check_same_device(W, x_flat, "spmm", "X")
+        X = _as_row_major(x_flat.t())
+        if bias is not None:
+            _check_same_device(W, bias, "spmm", "bias")
+            if bias.dtype != torch.float32 or bias.shape != (W.nrows,):
+                raise ValueError(f"spmm: bias must be float32 of shape ({W.nrows},), got "
+                                 f"{bias.dtype} {tuple(bias.shape)}")
+            bias = bias.contiguous()
+        ctx.save_for_backward(W_values, X)
+        ctx.W = W
+        ctx.kernel = kernel
+        return _launch_spmm(W, X, bias)
 
     @staticmethod
     def backward(ctx, dY):
         W_values, X = ctx.saved_tensors
-        dY_f32 = _device_f32(dY)
-        dW_values, dX = _spmm_backward(ctx.W, X, dY_f32, ctx.kernel, ctx.needs_input_grad[0],
-                                       ctx.needs_input_grad[3])
-        dbias = dY_f32.sum(dim=1) if ctx.needs_input_grad[1] else None
-        return dW_values, dbias, None, dX, None
+        dY_f32 = _as_row_major(dY)
+        need_dw, need_db = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        dbias = None
+        if need_db:  # fused into the dW launch when dW is computed too
+            dbias = torch.empty(dY_f32.shape[0], dtype=torch.float32, device=dY_f32.device)
+            if not need_dw:
+                torch.sum(dY_f32, dim=1, out=dbias)
+        dW_values, dX = _spmm_backward(ctx.W, X, dY_f32, ctx.kernel, need_dw,
+                                       ctx.needs_input_grad[3], dbias if need_dw else None)
+        return dW_values, dbias, None, (dX.t() if dX is not None else None), None
 
 
 def spmm(W: PaddedCSR, X: torch.Tensor, *, kernel: str = "auto") -> torch.Tensor:

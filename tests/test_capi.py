@@ -118,3 +118,17 @@ def test_spmm_bias_rejects_null_bias_on_the_host():
     v = _view()
     rc = lib.slk_spmm_bias(ctypes.byref(v), None, 6, 3, None, None, None)
     assert rc == _lib.SLK_EINVAL and "bias" in lib.slk_last_error().decode()
+
+
+def test_transpose_dense_rejects_bad_stride_on_the_host():
+    lib = _lib.load()
+    rc = lib.slk_transpose_dense(None, 4, 8, 5, None, None)
+    assert rc == _lib.SLK_EINVAL and "ld_src" in lib.slk_last_error().decode()
+
+
+def test_sddmm_bias_rejects_null_dbias_on_the_host():
+    lib = _lib.load()
+    v = _view()
+    rc = lib.slk_sddmm_bias(ctypes.byref(v), None, 4, None, 6, 3, None, None, _lib.SLK_DW_SIMD,
+                            None)
+    assert rc == _lib.SLK_EINVAL and "dbias" in lib.slk_last_error().decode()

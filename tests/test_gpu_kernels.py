@@ -364,3 +364,46 @@ def test_transpose_negative_padding_ratio(dev):
     W = from_oracle(oracle.bernoulli(4, 4, 0.5, seed=1), dev)
     with pytest.raises(ValueError, match="padding_ratio"):
         W.transpose(padding_ratio=-0.1)
+
+
+@pytest.mark.parametrize("rows,cols,ld", [(1, 1, 1), (1, 7, 9), (31, 33, 33), (256, 784, 784),
+                                          (100, 40, 64), (2048, 96, 96), (65, 1, 3)])
+def test_transpose_dense_is_a_bitwise_copy(dev, rows, cols, ld):
+    """slk_transpose_dense: dst = srcᵀ for row-strided sources, partial tiles."""
+    buf = torch.randn(rows * ld + 3, device=dev)
+    src = buf[:rows * ld].view(rows, ld)[:, :cols]
+    dst = torch.empty(cols, rows, device=dev)
+    _lib.transpose_dense(src, dst)
+    assert torch.equal(dst.view(torch.int32), src.t().contiguous().view(torch.int32))
+
+
+
+@pytest.mark.parametrize("env,N,order", [
+    ({}, 256, "simd"), ({}, 255, "simd"), ({"SLK_SDDMM_G": "2"}, 1040, "simd"),
+    ({"SLK_SDDMM_G": "4"}, 1024, "simd"), ({}, 37, "scalar"), ({}, 0, "simd")])
+def test_sddmm_bias_fuses_the_bias_gradient(dev, monkeypatch, env, N, order):
+    """slk_sddmm_bias: dW bit-identical to slk_sddmm, dbias = Σ_j dY[i, j] within
+    float32 rounding of the float64 sum, repeatable, for every dW kernel
+    (including rows with no live slot and the scalar order)."""
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    c, X_np, dY_np = _case(70, 90, N, 12, seed=N + 3)
+    c.row_nnz[4] = 0
+    c.col_indices[c.row_start[4]:c.row_start[4] + c.row_capacity[4]] = -1
+    c.values[c.row_start[4]:c.row_start[4] + c.row_capacity[4]] = 0.0
+    W = from_oracle(c, dev)
+    X, dY = _t(X_np, dev), _t(dY_np, dev)
+    ordv = _lib.SLK_DW_SCALAR if order == "scalar" else _lib.SLK_DW_SIMD
+    dW0 = torch.empty(W.total_capacity, device=dev)
+    _lib.sddmm(W._view(), dY, X, dW0, ordv)
+    runs = []
+    for _ in range(2):
+        dW = torch.empty(W.total_capacity, device=dev)
+        db = torch.full((70,), float("nan"), device=dev)
+        _lib.sddmm(W._view(), dY, X, dW, ordv, db)
+        runs.append((dW.cpu().numpy(), db.cpu().numpy()))
+    assert_bits_equal(runs[0][0], dW0.cpu().numpy(), "dW")
+    assert_bits_equal(runs[1][1], runs[0][1], "dbias repeat")
+    ref = dY_np.astype(np.float64).sum(axis=1)
+    bound = 1e-6 * np.abs(dY_np).astype(np.float64).sum(axis=1) + 1e-30
+    assert np.all(np.abs(runs[0][1] - ref) <= bound), "dbias"
