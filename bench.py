@@ -987,10 +987,13 @@ def main():
     dom = max((k for k in kern if k["kernel"].startswith(("spmm", "sddmm"))),
               key=lambda k: k["avg_us"])
     achieved = dom["bytes"] / (dom["avg_us"] * 1e-6) / 1e9
+    # HBM bytes per launch of the dominant kernel, from the committed
+    # rocprofv3 FETCH_SIZE/WRITE_SIZE summary of this workload (if any)
     traffic = None
     tf = ROOT / "profiles" / f"traffic_{args.workload}.json"
     if tf.exists():
-        traffic = json.loads(tf.read_text()).get(dom["kernel"].split("[")[0])
+        tj = json.loads(tf.read_text())
+        traffic = tj.get(dom["kernel"], tj.get(dom["kernel"].split("[")[0]))
 
     if isinstance(work, C2):
         value = work.tokens_per_step() * args.steps / elapsed
