@@ -548,11 +548,35 @@ def _build_from_rows(nrows, ncols, crow, col, vals, padding_ratio, device) -> Pa
     return p.to(device) if device is not None else p
 
 
+def _build_from_rows_device(nrows, ncols, crow, col, vals, padding_ratio, dev) -> PaddedCSR:
+    """_build_from_rows with torch ops on the HIP device: the padded arrays are
+    laid out where the input lives and validated by the device checker, so a
+    matrix built from GPU tensors never passes through host memory."""
+    crow = crow.to(dev, torch.int64)
+    n = int(crow[-1]) if nrows else 0
+    row_nnz = crow[1:] - crow[:-1]
+    cap = torch.clamp(torch.ceil(row_nnz.to(torch.float64) * (1.0 + padding_ratio)),
+                      min=1.0).to(torch.int64)
+    start = torch.cumsum(cap, 0) - cap
+    total = int(cap.sum()) if nrows else 0
+    v = torch.zeros(total, dtype=_F32, device=dev)
+    c = torch.full((total,), -1, dtype=_I32, device=dev)
+    if n:
+        rows = torch.repeat_interleave(torch.arange(nrows, device=dev), row_nnz, output_size=n)
+        dest = start[rows] + (torch.arange(n, device=dev) - crow[:-1][rows])
+        v[dest] = vals[:n].to(dev, _F32)
+        c[dest] = col[:n].to(dev, _I32)
+    return PaddedCSR(nrows, ncols, v, c, start.to(_I32), row_nnz.to(_I32), cap.to(_I32))
+
+
 def from_torch_sparse_csr(csr: torch.Tensor, *, padding_ratio: float = 0.2,
                           device=None) -> PaddedCSR:
     """PaddedCSR from a ``torch.sparse_csr`` tensor (layout.py:75-165).
 
-    The result lives on ``device`` (default: the input's device).
+    Each row's entries are copied in the order given and the constructor's
+    invariant check rejects unsorted or repeated columns, as the reference
+    does. The result lives on ``device`` (default: the input's device); a
+    HIP-resident input is converted on the device.
     """
     if csr.layout != torch.sparse_csr:
         raise ValueError(f"from_torch_sparse_csr expected layout=torch.sparse_csr, "
@@ -562,21 +586,39 @@ def from_torch_sparse_csr(csr: torch.Tensor, *, padding_ratio: float = 0.2,
     if padding_ratio < 0:
         raise ValueError(f"padding_ratio must be >= 0, got {padding_ratio}")
     nrows, ncols = csr.size()
+    target = torch.device(device) if device is not None else csr.device
+    if csr.device.type == "cuda" and target.type == "cuda":
+        return _build_from_rows_device(int(nrows), int(ncols), csr.crow_indices(),
+                                       csr.col_indices(), csr.values().detach(), padding_ratio,
+                                       target)
     crow = csr.crow_indices().contiguous().cpu().numpy().astype(np.int64)
     col = csr.col_indices().contiguous().cpu().numpy().astype(np.int32)
     vals = csr.values().detach().contiguous().cpu().numpy().astype(np.float32)
-    target = device if device is not None else csr.device
     return _build_from_rows(int(nrows), int(ncols), crow, col, vals, padding_ratio, target)
 
 
 def from_dense(W: torch.Tensor, *, threshold: float = 0.0, padding_ratio: float = 0.2,
                device=None) -> PaddedCSR:
-    """PaddedCSR holding the entries of ``W`` with |W| > threshold (layout.py:172-208)."""
+    """PaddedCSR holding the entries of ``W`` with |W| > threshold (layout.py:172-208).
+
+    Built on the device when ``W`` and the target device are HIP devices."""
     if W.dim() != 2:
         raise ValueError(f"from_dense expected 2-D tensor, got {W.dim()}-D")
     if padding_ratio < 0:
         raise ValueError(f"padding_ratio must be >= 0, got {padding_ratio}")
-    target = device if device is not None else W.device
+    target = torch.device(device) if device is not None else W.device
+    if W.device.type == "cuda" and target.type == "cuda":
+        # on the device: row-major nonzeros, the entries W.to_sparse_csr() keeps
+        Wf = W.detach().to(device=target, dtype=_F32)
+        if threshold > 0:
+            Wf = torch.where(Wf.abs() > threshold, Wf, torch.zeros_like(Wf))
+        nrows, ncols = Wf.shape
+        rows, cols = torch.nonzero(Wf != 0, as_tuple=True)
+        crow = torch.zeros(nrows + 1, dtype=torch.int64, device=target)
+        if nrows:
+            crow[1:] = torch.cumsum(torch.bincount(rows, minlength=nrows), 0)
+        return _build_from_rows_device(nrows, ncols, crow, cols, Wf[rows, cols], padding_ratio,
+                                       target)
     W_np = W.detach().to(dtype=_F32).cpu().contiguous().numpy()
     if threshold > 0:
         W_np = np.where(np.abs(W_np) > threshold, W_np, np.float32(0.0))

@@ -94,6 +94,56 @@ class SparseLinear(nn.Module):
             self._csr._bind_values(v)
         return out
 
+    # ─── topology serialization ────────────────────────────────────────
+    # The reference's state_dict holds only the values and the bias, so a
+    # receiver has to rebuild the same mask from the same seed
+    # (tests/test_sparse_linear.py:312-335). Here the topology travels too:
+    # the four structure arrays and the topology version are saved next to
+    # ``_values``, and loading them installs that topology (validated by the
+    # invariant checker) before the values are copied. A state dict without
+    # them — a reference-style checkpoint — loads values only, as before.
+    _TOPOLOGY_KEYS = ("csr_col_indices", "csr_row_start", "csr_row_nnz", "csr_row_capacity",
+                      "csr_topology_version")
+
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        super()._save_to_state_dict(destination, prefix, keep_vars)
+        csr = self._csr
+        destination[prefix + "csr_col_indices"] = csr.col_indices.detach()
+        destination[prefix + "csr_row_start"] = csr.row_start.detach()
+        destination[prefix + "csr_row_nnz"] = csr.row_nnz.detach()
+        destination[prefix + "csr_row_capacity"] = csr.row_capacity.detach()
+        destination[prefix + "csr_topology_version"] = torch.tensor(csr.topology_version,
+                                                                    dtype=torch.int64)
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                              unexpected_keys, error_msgs):
+        keys = [prefix + k for k in self._TOPOLOGY_KEYS]
+        present = [k in state_dict for k in keys]
+        if any(present) and not all(present):
+            error_msgs.append(f"SparseLinear: partial topology in state_dict (need all of "
+                              f"{', '.join(keys)})")
+        elif all(present) and prefix + "_values" in state_dict:
+            vals = state_dict[prefix + "_values"]
+            dev = self._values.device
+            try:
+                csr = PaddedCSR(self.out_features, self.in_features,
+                                vals.detach().to(dev, torch.float32),
+                                *(state_dict[k].to(dev, torch.int32) for k in keys[:4]),
+                                device=dev)
+            except ValueError as e:
+                error_msgs.append(f"SparseLinear: invalid topology in state_dict: {e}")
+            else:
+                csr._topology_version = int(state_dict[keys[4]])
+                with torch.no_grad():
+                    self._values.data = csr.values
+                csr._bind_values(self._values.data)
+                self._csr = csr
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
+                                      unexpected_keys, error_msgs)
+        for k in keys:
+            if k in unexpected_keys:
+                unexpected_keys.remove(k)
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """y = x @ Wᵀ + b with W stored as PaddedCSR (nn.py:210-245)."""
         orig_shape = x.shape

@@ -501,3 +501,54 @@ def test_rewrite_row_on_device_matches_reference(dev):
         W.rewrite_row(0, list(range(20)), [1.0] * 20)
     with pytest.raises(ValueError, match="must equal"):
         W.rewrite_row(0, [1, 2], [1.0])
+
+
+# ───────────── device construction and topology serialization ──────────
+
+@pytest.mark.parametrize("padding_ratio,threshold", [(0.2, 0.0), (0.0, 0.0), (1.0, 0.5)])
+def test_device_factories_match_host_build(dev, padding_ratio, threshold):
+    """from_dense / from_torch_sparse_csr of HIP tensors build on the device and
+    give the same arrays as the host build (empty rows included)."""
+    g = torch.Generator().manual_seed(11)
+    W = torch.randn(37, 53, generator=g) * (torch.rand(37, 53, generator=g) < 0.2)
+    W[5] = 0.0
+    host = PaddedCSR.from_dense(W, padding_ratio=padding_ratio, threshold=threshold)
+    devb = PaddedCSR.from_dense(W.to(dev), padding_ratio=padding_ratio, threshold=threshold)
+    assert devb.device.type == "cuda"
+    for name in ("values", "col_indices", "row_start", "row_nnz", "row_capacity"):
+        assert torch.equal(getattr(devb, name).cpu(), getattr(host, name)), name
+    sp = W.to_sparse_csr().to(dev)
+    devc = PaddedCSR.from_torch_sparse_csr(sp, padding_ratio=padding_ratio)
+    hostc = PaddedCSR.from_torch_sparse_csr(W.to_sparse_csr(), padding_ratio=padding_ratio)
+    for name in ("values", "col_indices", "row_start", "row_nnz", "row_capacity"):
+        assert torch.equal(getattr(devc, name).cpu(), getattr(hostc, name)), name
+
+
+def test_device_sparse_csr_with_unsorted_row_is_rejected(dev):
+    crow = torch.tensor([0, 2, 3], device=dev)
+    col = torch.tensor([3, 1, 0], device=dev)
+    val = torch.tensor([1.0, 2.0, 3.0], device=dev)
+    sp = torch.sparse_csr_tensor(crow, col, val, (2, 4))
+    with pytest.raises(ValueError, match="Invariant 6"):
+        PaddedCSR.from_torch_sparse_csr(sp)
+
+
+def test_state_dict_topology_roundtrip_on_device(dev):
+    """A receiver with another mask adopts the saved topology, including one
+    rewritten on the device by SET, and then computes the same bits."""
+    torch.manual_seed(0)
+    a = SparseLinear(64, 32, sparsity=0.8).to(dev)
+    torch.manual_seed(9)
+    b = SparseLinear(64, 32, sparsity=0.8).to(dev)
+    a._csr._drop_grow(max(1, int(0.3 * a.nnz)), slk._lib.SLK_GROW_RANDOM, None, 123)
+    b.load_state_dict(a.state_dict())
+    for name in ("values", "col_indices", "row_start", "row_nnz", "row_capacity"):
+        assert torch.equal(getattr(a._csr, name), getattr(b._csr, name)), name
+    assert b._csr.topology_version == a._csr.topology_version
+    x = torch.randn(24, 64, device=dev)
+    ya, yb = a(x), b(x)
+    assert torch.equal(ya, yb)
+    up = torch.randn_like(ya)
+    ya.backward(up)
+    yb.backward(up)
+    assert torch.equal(a._values.grad, b._values.grad) and torch.equal(a.bias.grad, b.bias.grad)

@@ -246,7 +246,76 @@ def test_sparse_linear_values_alias_csr_buffer():
     with torch.no_grad():
         layer._values.fill_(0.25)
     assert torch.all(layer._csr.values == 0.25)
-    sd = layer.state_dict()
-    assert set(sd) == {"_values", "bias"}
+    assert {n for n, _ in layer.named_parameters()} == {"_values", "bias"}
+    assert {"_values", "bias"} <= set(layer.state_dict())  # plus the topology keys
     layer.double()  # the CSR keeps its float32 buffer, as the reference does
     assert layer._values.dtype == torch.float64 and layer._csr.values.dtype == torch.float32
+
+
+# ───────────── SparseLinear topology serialization (CPU, no kernels) ─────────
+
+def _layers(seed_a=0, seed_b=5):
+    torch.manual_seed(seed_a)
+    a = SparseLinear(16, 8, sparsity=0.5)
+    torch.manual_seed(seed_b)
+    b = SparseLinear(16, 8, sparsity=0.5)
+    return a, b
+
+
+def _same_topology(a, b):
+    for name in ("values", "col_indices", "row_start", "row_nnz", "row_capacity"):
+        assert torch.equal(getattr(a._csr, name), getattr(b._csr, name)), name
+    assert a._csr.topology_version == b._csr.topology_version
+
+
+def test_state_dict_carries_the_topology():
+    a, b = _layers()
+    assert not torch.equal(a._csr.col_indices, b._csr.col_indices) or \
+        a._csr.total_capacity != b._csr.total_capacity
+    sd = a.state_dict()
+    assert {"_values", "bias", "csr_col_indices", "csr_row_start", "csr_row_nnz",
+            "csr_row_capacity", "csr_topology_version"} == set(sd)
+    b.load_state_dict(sd)  # strict: every key is consumed
+    _same_topology(a, b)
+    assert b._csr.values.data_ptr() == b._values.data_ptr()  # aliasing kept
+
+
+def test_state_dict_after_rewrite_row_and_torch_save_roundtrip(tmp_path):
+    a, b = _layers(1, 2)
+    a._csr.rewrite_row(3, [0, 5, 9], [0.5, -1.0, 2.0])
+    assert a._csr.topology_version == 1
+    path = tmp_path / "layer.pt"
+    torch.save(a.state_dict(), path)
+    b.load_state_dict(torch.load(path, weights_only=True))
+    _same_topology(a, b)
+    assert b._csr.row_nnz[3] == 3 and b._csr.topology_version == 1
+
+
+def test_values_only_state_dict_still_loads():
+    """A reference-style checkpoint (no topology keys) loads the values into a
+    layer built from the same seed, strictly (tests/test_sparse_linear.py:312-335)."""
+    a, b = _layers(0, 0)
+    with torch.no_grad():
+        a._values.mul_(2.0)
+    sd = {k: v for k, v in a.state_dict().items() if not k.startswith("csr_")}
+    b.load_state_dict(sd)
+    assert torch.equal(a._values, b._values) and b._csr.values.data_ptr() == b._values.data_ptr()
+
+
+def test_partial_or_invalid_topology_is_rejected():
+    a, b = _layers()
+    sd = a.state_dict()
+    partial = dict(sd)
+    del partial["csr_row_nnz"]
+    with pytest.raises(RuntimeError, match="partial topology"):
+        b.load_state_dict(partial)
+    bad = dict(sd)
+    cols = bad["csr_col_indices"].clone()
+    s0 = int(bad["csr_row_start"][0])
+    if int(bad["csr_row_nnz"][0]) >= 2:
+        cols[s0], cols[s0 + 1] = cols[s0 + 1].clone(), cols[s0].clone()  # unsorted row 0
+    else:
+        cols[s0] = 999  # out of range
+    bad["csr_col_indices"] = cols
+    with pytest.raises(RuntimeError, match="invalid topology"):
+        b.load_state_dict(bad)
