@@ -25,9 +25,14 @@
 // [0, total_capacity), which the padded rows tile contiguously, so every
 // wave owns the same number of slots no matter how skewed row lengths are.
 // A wave finds the rows of its slots with a 64-way search over row_start;
-// padding slots
-// (slot-in-row >= row_nnz) are written as 0 by the lane that owns them, so
-// dW needs no separate memset.
+// padding slots (slot-in-row >= row_nnz) are written as 0 by the lane that
+// owns them, so dW needs no separate memset.
+//
+// Kernels: sddmm_simd_kernel (one 16-slot group per wave, whole rows at a
+// time; small or unaligned N), sddmm_simd_win_kernel<G> (G groups per wave
+// swept through N window by window with dY staged in LDS; large N) and
+// sddmm_scalar_kernel. slk_sddmm_bias appends one wave per row that sums the
+// row of dY (the bias gradient) to the same launch.
 #include "common.hpp"
 
 #include <cstdlib>
