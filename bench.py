@@ -366,7 +366,8 @@ class GPTWork:
             out.append((f"spmm_fwd[{tag} {M}x{K}]", lambda v=v, X=X, Y=Y: _lib.spmm(v, X, Y),
                         bytes_fwd(W.nnz, M, K, N), flops(W.nnz, N)))
             out.append((f"sddmm_dw[{tag} {M}x{K}]",
-                        lambda v=v, dY=dY, X=X, dW=dW: _lib.sddmm(v, dY, X, dW, _lib.SLK_DW_SIMD),
+                        lambda W=W, dY=dY, X=X, dW=dW: _lib.sddmm(ops._sddmm_view(W, X), dY, X, dW,
+                                                                  _lib.SLK_DW_SIMD),
                         bytes_dw(W.nnz, W.total_capacity, M, K, N), flops(W.nnz, N)))
             out.append((f"spmm_dx[{tag} {K}x{M}]", lambda vT=vT, dY=dY, dX=dX: _lib.spmm(vT, dY, dX),
                         bytes_fwd(W.nnz, K, M, N), flops(W.nnz, N)))
@@ -558,7 +559,8 @@ class LayerWork:
         return [
             ("spmm_fwd", lambda: _lib.spmm(v, self.X, Y), bytes_fwd(W.nnz, M, K, N),
              flops(W.nnz, N)),
-            ("sddmm_dw", lambda: _lib.sddmm(v, self.dY, self.X, dW, _lib.SLK_DW_SIMD),
+            ("sddmm_dw", lambda: _lib.sddmm(ops._sddmm_view(W, self.X), self.dY, self.X, dW,
+                                            _lib.SLK_DW_SIMD),
              bytes_dw(W.nnz, W.total_capacity, M, K, N), flops(W.nnz, N)),
             ("transpose_refresh", lambda: _lib.transpose_refresh(W.values, perm, WT.values),
              bytes_refresh(W.nnz, WT.total_capacity), 0),

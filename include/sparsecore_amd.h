@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define SLK_ABI_VERSION 2
+#define SLK_ABI_VERSION 3
 
 #if defined(__GNUC__)
 #define SLK_API __attribute__((visibility("default")))
@@ -75,6 +75,15 @@ typedef struct slk_csr {
      * grid; results are the same either way. Not part of the reference
      * layout — a schedule the caller caches per topology. */
     const int32_t* row_order;
+    /* Optional (may be NULL): the live slots listed column block by column
+     * block (then by row, then by column), with each entry's row, and the
+     * number of entries. slk_sddmm's windowed kernel then visits the slots in
+     * that order, so the waves resident at one moment gather from one band of
+     * X rows; results are the same either way. A schedule the caller caches
+     * per topology. */
+    const int32_t* slot_list;
+    const int32_t* slot_list_row;
+    int64_t n_slot_list;
 } slk_csr;
 
 /* Thread-local description of the last failure of this thread ("" if none). */
@@ -228,6 +237,20 @@ SLK_API int slk_dense_grad(const float* dY, const float* X, int64_t M, int64_t K
  * gradient (sparselab/ops.py:174).                                          */
 SLK_API int slk_transpose_dense(const float* src, int64_t rows, int64_t cols,
                                 int64_t ld_src, float* dst, void* stream);
+
+/* Bytes of device workspace slk_slot_list_build needs for W and block_cols. */
+SLK_API int64_t slk_slot_list_workspace_bytes(const slk_csr* W, int64_t block_cols);
+
+/* Builds the optional slk_csr.slot_list schedule on the device: W's live
+ * slots ordered by column block (block b = columns [b*block_cols,
+ * (b+1)*block_cols)), then by row, then by column, into slot_list, with each
+ * entry's row in slot_list_row (both nnz entries). Deterministic, no atomics.
+ * No counterpart in the reference: its dW loop (csrc/kernels/spmm_grad.cpp,
+ * csrc/kernels/spmm_grad_avx2.cpp) walks slots in capacity order; this is
+ * a visiting order for slk_sddmm that leaves every output bit unchanged.   */
+SLK_API int slk_slot_list_build(const slk_csr* W, int64_t block_cols, void* workspace,
+                                int64_t workspace_bytes, int32_t* slot_list,
+                                int32_t* slot_list_row, void* stream);
 
 #ifdef __cplusplus
 }

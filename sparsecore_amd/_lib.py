@@ -21,7 +21,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libsparsecore_amd.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 SLK_OK, SLK_EINVAL, SLK_EDEVICE = 0, 1, 2
 SLK_DW_SIMD, SLK_DW_SCALAR = 0, 1
@@ -47,6 +47,8 @@ EXPORTS = (
     "slk_drop_grow",
     "slk_dense_grad",
     "slk_transpose_dense",
+    "slk_slot_list_workspace_bytes",
+    "slk_slot_list_build",
 )
 
 
@@ -63,6 +65,9 @@ class CsrView(ctypes.Structure):
         ("row_nnz", ctypes.c_void_p),
         ("row_capacity", ctypes.c_void_p),
         ("row_order", ctypes.c_void_p),
+        ("slot_list", ctypes.c_void_p),
+        ("slot_list_row", ctypes.c_void_p),
+        ("n_slot_list", ctypes.c_int64),
     ]
 
 
@@ -96,8 +101,11 @@ def _declare(lib) -> None:
                                   _vp, _i64, _vp]
     lib.slk_dense_grad.argtypes = [_vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp, _vp]
     lib.slk_transpose_dense.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp]
+    lib.slk_slot_list_workspace_bytes.restype = _i64
+    lib.slk_slot_list_workspace_bytes.argtypes = [_csrp, _i64]
+    lib.slk_slot_list_build.argtypes = [_csrp, _i64, _vp, _i64, _vp, _vp, _vp]
     sized = ("slk_last_error", "slk_abi_version", "slk_transpose_workspace_bytes",
-             "slk_drop_grow_workspace_bytes")
+             "slk_drop_grow_workspace_bytes", "slk_slot_list_workspace_bytes")
     for name in EXPORTS:
         if name not in sized:
             getattr(lib, name).restype = ctypes.c_int
@@ -247,6 +255,21 @@ def dense_grad(dY: torch.Tensor, X: torch.Tensor, M: int, K: int, N: int, token_
     rc = lib.slk_dense_grad(ptr(dY), ptr(X), M, K, N, int(token_major), ptr(G), stream_of(G))
     if rc:
         _raise(rc)
+
+
+def slot_list_build(view: CsrView, block_cols: int, nnz: int, device):
+    """(slot_list, slot_list_row) int32 tensors of nnz entries: W's live slots
+    by column block, row and column (slk_slot_list_build)."""
+    lib = load()
+    lst = torch.empty(nnz, dtype=torch.int32, device=device)
+    lrow = torch.empty(nnz, dtype=torch.int32, device=device)
+    nbytes = int(lib.slk_slot_list_workspace_bytes(ctypes.byref(view), int(block_cols)))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+    rc = lib.slk_slot_list_build(ctypes.byref(view), int(block_cols), ptr(ws), nbytes, ptr(lst),
+                                 ptr(lrow), stream_of(lst))
+    if rc:
+        _raise(rc)
+    return lst, lrow
 
 
 def transpose_dense(src: torch.Tensor, dst: torch.Tensor) -> None:

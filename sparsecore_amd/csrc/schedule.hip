@@ -1,0 +1,182 @@
+// Slot-list schedule for the weight gradient on large layers.
+//
+// slk_sddmm's windowed kernel can visit W's live slots in an order other than
+// the flat capacity order; the order built here takes them column block by
+// column block (block b = columns [b·C, (b+1)·C)), row by row inside a block,
+// by column inside a row. Waves resident at one moment then gather from one
+// band of X rows. The list is a permutation of the live slots, so it changes
+// which wave computes a slot, never the slot's arithmetic.
+//
+// Within a row the live columns ascend, so the row's slots in block b are one
+// run [lo(r, b), lo(r, b+1)), lo(r, b) = first live slot of row r with column
+// >= b·C. The build is a counting sort on (block, row) without atomics:
+//
+//   S1 bounds   one thread per (row, block boundary): lo(r, b) by binary
+//               search over the row's columns.
+//   S2 rowscan  one workgroup per block: exclusive scan over rows of the run
+//               lengths -> each run's offset inside its block, and the block
+//               total.
+//   S3 blkscan  one workgroup: exclusive scan of the block totals.
+//   S4 scatter  one thread per (row, block): copies its run to
+//               list[block start + run offset + i] with the row alongside.
+#include "common.hpp"
+
+namespace slk {
+namespace {
+
+constexpr int kSchedThreads = 256;
+constexpr int kScanBlock = 1024;
+
+__global__ __launch_bounds__(kSchedThreads) void sl_bounds_kernel(
+    int64_t M, int64_t nb, int64_t C, const int32_t* __restrict__ row_start,
+    const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ col,
+    int32_t* __restrict__ lo) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kSchedThreads + threadIdx.x;
+    if (t >= M * (nb + 1)) return;
+    const int64_t r = t / (nb + 1);
+    const int64_t b = t - r * (nb + 1);
+    const int64_t s0 = row_start[r];
+    int64_t a = 0, e = row_nnz[r];  // first live slot of row r with col >= b*C
+    const int64_t key = b * C;
+    while (a < e) {
+        const int64_t mid = (a + e) >> 1;
+        if (col[s0 + mid] < key) a = mid + 1; else e = mid;
+    }
+    lo[t] = static_cast<int32_t>(s0 + a);
+}
+
+// One workgroup per block b: off[r*nb + b] = sum of run lengths of rows < r,
+// total[b] = the block's entry count.
+__global__ __launch_bounds__(kScanBlock) void sl_rowscan_kernel(
+    int64_t M, int64_t nb, const int32_t* __restrict__ lo, int32_t* __restrict__ off,
+    int32_t* __restrict__ total) {
+    __shared__ int32_t part[kScanBlock];
+    const int64_t b = blockIdx.x;
+    const int t = threadIdx.x;
+    const int64_t per = ceil_div(M, kScanBlock);
+    const int64_t r0 = min(M, t * per), r1 = min(M, r0 + per);
+    auto len = [&](int64_t r) { return lo[r * (nb + 1) + b + 1] - lo[r * (nb + 1) + b]; };
+    int32_t sum = 0;
+    for (int64_t r = r0; r < r1; ++r) sum += len(r);
+    part[t] = sum;
+    __syncthreads();
+    for (int d = 1; d < kScanBlock; d <<= 1) {  // inclusive Hillis-Steele scan
+        const int32_t add = t >= d ? part[t - d] : 0;
+        __syncthreads();
+        part[t] += add;
+        __syncthreads();
+    }
+    int32_t run = part[t] - sum;
+    for (int64_t r = r0; r < r1; ++r) {
+        off[r * nb + b] = run;
+        run += len(r);
+    }
+    if (t == kScanBlock - 1) total[b] = part[t];
+}
+
+__global__ __launch_bounds__(kScanBlock) void sl_blkscan_kernel(int64_t nb,
+                                                               const int32_t* __restrict__ total,
+                                                               int32_t* __restrict__ start) {
+    __shared__ int32_t part[kScanBlock];
+    const int t = threadIdx.x;
+    const int64_t per = ceil_div(nb, kScanBlock);
+    const int64_t a = min(nb, t * per), e = min(nb, a + per);
+    int32_t sum = 0;
+    for (int64_t b = a; b < e; ++b) sum += total[b];
+    part[t] = sum;
+    __syncthreads();
+    for (int d = 1; d < kScanBlock; d <<= 1) {
+        const int32_t add = t >= d ? part[t - d] : 0;
+        __syncthreads();
+        part[t] += add;
+        __syncthreads();
+    }
+    int32_t run = part[t] - sum;
+    for (int64_t b = a; b < e; ++b) {
+        start[b] = run;
+        run += total[b];
+    }
+}
+
+__global__ __launch_bounds__(kSchedThreads) void sl_scatter_kernel(
+    int64_t M, int64_t nb, const int32_t* __restrict__ lo, const int32_t* __restrict__ off,
+    const int32_t* __restrict__ start, int32_t* __restrict__ list, int32_t* __restrict__ list_row) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kSchedThreads + threadIdx.x;
+    if (t >= M * nb) return;
+    const int64_t r = t / nb;
+    const int64_t b = t - r * nb;
+    const int32_t a = lo[r * (nb + 1) + b];
+    const int32_t e = lo[r * (nb + 1) + b + 1];
+    const int64_t dst = static_cast<int64_t>(start[b]) + off[t];
+    for (int32_t s = a; s < e; ++s) {
+        list[dst + (s - a)] = s;
+        list_row[dst + (s - a)] = static_cast<int32_t>(r);
+    }
+}
+
+struct ListPlan {
+    int64_t nb;        // column blocks
+    int64_t lo_ints;   // M * (nb + 1)
+    int64_t off_ints;  // M * nb
+    int64_t bytes;     // lo + off + total + start
+};
+
+ListPlan plan_list(int64_t M, int64_t K, int64_t C) {
+    ListPlan p{};
+    p.nb = ceil_div(K, C);
+    p.lo_ints = M * (p.nb + 1);
+    p.off_ints = M * p.nb;
+    p.bytes = static_cast<int64_t>(sizeof(int32_t)) * (p.lo_ints + p.off_ints + 2 * p.nb);
+    return p;
+}
+
+}  // namespace
+}  // namespace slk
+
+extern "C" int64_t slk_slot_list_workspace_bytes(const slk_csr* W, int64_t block_cols) {
+    if (W == nullptr || W->nrows <= 0 || W->ncols <= 0 || block_cols <= 0) return 0;
+    return slk::plan_list(W->nrows, W->ncols, block_cols).bytes;
+}
+
+extern "C" int slk_slot_list_build(const slk_csr* W, int64_t block_cols, void* workspace,
+                                   int64_t workspace_bytes, int32_t* slot_list,
+                                   int32_t* slot_list_row, void* stream) {
+    using namespace slk;
+    clear_error();
+    if (int rc = validate_csr(W, "slot_list")) return rc;
+    if (block_cols <= 0) {
+        return fail(SLK_EINVAL, "slot_list: block_cols must be positive, got " +
+                                    std::to_string(block_cols));
+    }
+    const int64_t M = W->nrows, K = W->ncols;
+    if (M == 0 || K == 0) return SLK_OK;
+    const ListPlan p = plan_list(M, K, block_cols);
+    if (workspace == nullptr || workspace_bytes < p.bytes) {
+        return fail(SLK_EINVAL, "slot_list: workspace of " + std::to_string(workspace_bytes) +
+                                    " bytes is smaller than the required " +
+                                    std::to_string(p.bytes));
+    }
+    if (slot_list == nullptr || slot_list_row == nullptr) {
+        return fail(SLK_EINVAL, "slot_list: NULL output");
+    }
+    if (p.nb > INT32_MAX || ceil_div(p.lo_ints, kSchedThreads) > INT32_MAX) {
+        return fail(SLK_EINVAL, "slot_list: matrix too large");
+    }
+    int32_t* lo = static_cast<int32_t*>(workspace);
+    int32_t* off = lo + p.lo_ints;
+    int32_t* total = off + p.off_ints;
+    int32_t* start = total + p.nb;
+    hipStream_t st = as_stream(stream);
+    hipLaunchKernelGGL(sl_bounds_kernel, dim3(static_cast<unsigned>(ceil_div(p.lo_ints, kSchedThreads))),
+                       dim3(kSchedThreads), 0, st, M, p.nb, block_cols, W->row_start, W->row_nnz,
+                       W->col_indices, lo);
+    if (int rc = check_launch("slot_list/bounds")) return rc;
+    hipLaunchKernelGGL(sl_rowscan_kernel, dim3(static_cast<unsigned>(p.nb)), dim3(kScanBlock), 0, st,
+                       M, p.nb, lo, off, total);
+    if (int rc = check_launch("slot_list/rowscan")) return rc;
+    hipLaunchKernelGGL(sl_blkscan_kernel, dim3(1), dim3(kScanBlock), 0, st, p.nb, total, start);
+    if (int rc = check_launch("slot_list/blkscan")) return rc;
+    hipLaunchKernelGGL(sl_scatter_kernel, dim3(static_cast<unsigned>(ceil_div(p.off_ints, kSchedThreads))),
+                       dim3(kSchedThreads), 0, st, M, p.nb, lo, off, start, slot_list, slot_list_row);
+    return check_launch("slot_list/scatter");
+}

@@ -44,6 +44,7 @@ constexpr int kBlock = 256;
 constexpr int kSlotsPerWave = 16;  // SIMD order: 4 lanes per slot group
 constexpr int64_t kWinMinN = 1024;
 constexpr int64_t kWinMinSlots = 2048 * kSlotsPerWave;  // 2048 waves
+constexpr int64_t kListG4Slots = 1536 * 1024;             // ~8 generations of G=4 waves
 
 // Largest r in [lo, hi) with row_start[r] <= slot, given row_start[lo] <= slot
 // (rows tile [0, cap) in order, so this is the row holding the slot).
@@ -78,7 +79,8 @@ __device__ __forceinline__ int64_t wave_row_of_slot(const int32_t* __restrict__ 
 // calls it): the two ends by wave search, then each lane narrows its own slot
 // inside that range (usually zero or one step).
 struct WaveRows {
-    int64_t first_row, last_row;
+    int64_t first_row = 0, last_row = 0;
+    WaveRows() = default;
     __device__ __forceinline__ WaveRows(const int32_t* __restrict__ row_start, int64_t M,
                                         int64_t first, int64_t last)
         : first_row(wave_row_of_slot(row_start, M, first)),
@@ -252,74 +254,125 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int G>
+// Zeroes the padding slots of one row of dW (one wave): used when the slots are
+// walked through a slot list, which holds live slots only.
+__device__ __forceinline__ void zero_row_padding(const int32_t* __restrict__ row_start,
+                                                 const int32_t* __restrict__ row_nnz,
+                                                 const int32_t* __restrict__ row_cap, int64_t M,
+                                                 int64_t row, float* __restrict__ dW) {
+    if (row >= M) return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t s0 = row_start[row];
+    const int64_t e = s0 + row_cap[row];
+    for (int64_t s = s0 + row_nnz[row] + lane; s < e; s += kWave) dW[s] = 0.0f;
+}
+
+template <int G, int NS>
 __global__ __launch_bounds__(kBlock) void sddmm_simd_win_kernel(
     int64_t M, int64_t N, int64_t cap_total,
     const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
     const int32_t* __restrict__ col, const float* __restrict__ dY,
     const float* __restrict__ X, float* __restrict__ dW, float* __restrict__ dbias,
-    int64_t slot_waves) {
+    int64_t slot_waves, const int32_t* __restrict__ row_cap,
+    const int32_t* __restrict__ slot_list, const int32_t* __restrict__ slot_row,
+    int64_t n_list) {
     constexpr int kWavesPerBlock = kBlock / kWave;
-    __shared__ f32x4 dys[kWavesPerBlock][G][2][kWave];  // 2 KiB per group
+    static_assert(NS == 2 || NS == 4, "staged rows per group");
+    __shared__ f32x4 dys[kWavesPerBlock][G][NS][kWave];  // NS KiB per group
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = threadIdx.x >> 6;
     const int g = lane >> 2;
     const int q = lane & 3;
     const int64_t wid = wave_id();
-    if (wid >= slot_waves) {  // wave-uniform: a bias-gradient wave
+    const bool listed = slot_list != nullptr;
+    if (wid >= slot_waves) {  // wave-uniform: a per-row wave
+        if (listed) zero_row_padding(row_start, row_nnz, row_cap, M, wid - slot_waves, dW);
         if (dbias != nullptr) bias_row_sum(dY, M, N, wid - slot_waves, dbias);
         return;
     }
+    // The wave's 16·G entries: slots of the flat capacity space, or (listed)
+    // entries of the slot list, whose rows come with it.
+    const int64_t space = listed ? n_list : cap_total;
     const int64_t base = wid * (kSlotsPerWave * G);
 
     bool in[G], live[G], direct[G];
     int sel[G];
-    int32_t rA[G], rB[G];
+    int32_t rs[G][NS];  // rows whose dY windows group k stages
+    int64_t slot_of[G];
     const float* dyr[G];
     const float* xr[G];
-    const int64_t last_slot = min(base + kSlotsPerWave * G - 1, cap_total - 1);
-    const WaveRows rows(row_start, M, base, last_slot);
-    int64_t r = rows.first_row;
+    int64_t r = 0;
+    WaveRows rows;
+    if (!listed) {
+        rows = WaveRows(row_start, M, base, min(base + kSlotsPerWave * G - 1, cap_total - 1));
+        r = rows.first_row;
+    }
     bool any_direct = false;
 #pragma unroll
     for (int k = 0; k < G; ++k) {
         const int64_t gbase = base + kSlotsPerWave * k;
-        const int64_t slot = gbase + g;
-        in[k] = slot < cap_total;
+        const int64_t e = gbase + g;
+        in[k] = e < space;
         live[k] = false;
+        slot_of[k] = e;
         if (in[k]) {
-            r = rows.of(row_start, r, slot);
-            live[k] = (slot - row_start[r]) < row_nnz[r];
+            if (listed) {
+                slot_of[k] = slot_list[e];
+                r = slot_row[e];
+                live[k] = true;
+            } else {
+                r = rows.of(row_start, r, e);
+                live[k] = (e - row_start[r]) < row_nnz[r];
+            }
         }
-        // first and last row of group k (lane 0 holds its first slot)
-        const int last = gbase < cap_total
-                             ? 4 * static_cast<int>(min<int64_t>(kSlotsPerWave - 1, cap_total - 1 - gbase))
+        // first and last row of group k (lane 0 holds its first entry)
+        const int last = gbase < space
+                             ? 4 * static_cast<int>(min<int64_t>(kSlotsPerWave - 1, space - 1 - gbase))
                              : 0;
-        rA[k] = __builtin_amdgcn_readfirstlane(static_cast<int32_t>(r));
-        rB[k] = __builtin_amdgcn_readlane(static_cast<int32_t>(r), last);
-        sel[k] = r == rA[k] ? 0 : 1;
-        direct[k] = live[k] && r != rA[k] && r != rB[k];
+        // staged rows: those of the group's entries 0 and last (NS = 2), or
+        // 0, 5, 10 and last (NS = 4: short row runs, as in a slot list)
+        const int32_t ri = static_cast<int32_t>(r);
+        rs[k][0] = __builtin_amdgcn_readfirstlane(ri);
+        if constexpr (NS == 4) {
+            rs[k][1] = __builtin_amdgcn_readlane(ri, min(20, last));
+            rs[k][2] = __builtin_amdgcn_readlane(ri, min(40, last));
+        }
+        rs[k][NS - 1] = __builtin_amdgcn_readlane(ri, last);
+        sel[k] = NS - 1;
+        direct[k] = live[k];
+#pragma unroll
+        for (int b = NS - 1; b >= 0; --b) {  // the first staged copy of this row
+            if (ri == rs[k][b]) {
+                sel[k] = b;
+                direct[k] = false;
+            }
+        }
         any_direct |= __ballot(direct[k]) != 0;
         dyr[k] = dY + (live[k] ? r * N : 0);
-        xr[k] = X + (live[k] ? static_cast<int64_t>(col[slot]) * N : 0);
+        xr[k] = X + (live[k] ? static_cast<int64_t>(col[slot_of[k]]) * N : 0);
     }
     const int64_t n16 = (N / 16) * 16;
     const int64_t nwin = ceil_div(n16, kWin);
     float acc[G][4];
-    f32x4 pa[G], pb[G];
+    f32x4 pst[G][NS];
 #pragma unroll
     for (int k = 0; k < G; ++k) {
         acc[k][0] = acc[k][1] = acc[k][2] = acc[k][3] = 0.f;
-        pa[k] = pb[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int b = 0; b < NS; ++b) pst[k][b] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    // buffer b is staged only when its row differs from buffer b-1's
     auto fetch = [&](int64_t w) {
         const int64_t j = w * kWin + 4 * lane;
         if (j < n16) {
 #pragma unroll
             for (int k = 0; k < G; ++k) {
-                pa[k] = *reinterpret_cast<const f32x4*>(dY + static_cast<int64_t>(rA[k]) * N + j);
-                if (rB[k] != rA[k])
-                    pb[k] = *reinterpret_cast<const f32x4*>(dY + static_cast<int64_t>(rB[k]) * N + j);
+#pragma unroll
+                for (int b = 0; b < NS; ++b) {
+                    if (b == 0 || rs[k][b] != rs[k][b - 1])
+                        pst[k][b] = *reinterpret_cast<const f32x4*>(
+                            dY + static_cast<int64_t>(rs[k][b]) * N + j);
+                }
             }
         }
     };
@@ -327,8 +380,9 @@ __global__ __launch_bounds__(kBlock) void sddmm_simd_win_kernel(
     for (int64_t w = 0; w < nwin; ++w) {
 #pragma unroll
         for (int k = 0; k < G; ++k) {
-            dys[wv][k][0][lane] = pa[k];
-            if (rB[k] != rA[k]) dys[wv][k][1][lane] = pb[k];
+#pragma unroll
+            for (int b = 0; b < NS; ++b)
+                if (b == 0 || rs[k][b] != rs[k][b - 1]) dys[wv][k][b][lane] = pst[k][b];
         }
         wave_sync();
         if (w + 1 < nwin) fetch(w + 1);
@@ -401,8 +455,7 @@ __global__ __launch_bounds__(kBlock) void sddmm_simd_win_kernel(
         for (int k = 0; k < G; ++k) {
             if (!in[k]) continue;
             const float rsum = (acc[k][0] + acc[k][2]) + (acc[k][1] + acc[k][3]);
-            dW[base + kSlotsPerWave * k + g] =
-                live[k] ? running_sum(dyr[k] + jt, xr[k] + jt, N - jt, rsum) : 0.0f;
+            dW[slot_of[k]] = live[k] ? running_sum(dyr[k] + jt, xr[k] + jt, N - jt, rsum) : 0.0f;
         }
     }
 }
@@ -476,21 +529,38 @@ int sddmm_impl(const slk_csr* W, const float* dY, int64_t dY_rows, const float* 
     if (v4 && N >= kWinMinN) G = cap >= 4 * kWinMinSlots ? 4 : cap >= 2 * kWinMinSlots ? 2 : 1;
     if (const char* e = std::getenv("SLK_SDDMM_G")) G = std::atoi(e);
     if (!v4 || (G != 2 && G != 4)) G = 1;
-    const int64_t slot_waves = ceil_div(cap, kSlotsPerWave * G);
-    const int64_t blocks = ceil_div(slot_waves + bias_waves, kBlock / kWave);
+    // The windowed kernel walks W's slot list when the caller supplies one
+    // (live slots only; one wave per row then also zeroes the row's padding).
+    const bool listed = G > 1 && W->slot_list != nullptr && W->slot_list_row != nullptr;
+    // list order: G = 4 only with many generations of waves (a short last
+    // generation costs more than the extra dY staging of G = 2)
+    if (listed && std::getenv("SLK_SDDMM_G") == nullptr) G = W->n_slot_list >= kListG4Slots ? 4 : 2;
+    const int64_t space = listed ? W->n_slot_list : cap;
+    const int64_t row_waves = listed ? W->nrows : bias_waves;
+    const int64_t slot_waves = ceil_div(space, kSlotsPerWave * G);
+    const int64_t blocks = ceil_div(slot_waves + row_waves, kBlock / kWave);
     if (blocks > INT32_MAX) return fail(SLK_EINVAL, std::string(who) + ": problem too large");
     const dim3 grid(static_cast<unsigned>(blocks));
 #define SLK_SDDMM_ARGS \
     W->nrows, N, cap, W->row_start, W->row_nnz, W->col_indices, dY, X, dW, dbias, slot_waves
-    if (G == 2) {
-        hipLaunchKernelGGL(sddmm_simd_win_kernel<2>, grid, dim3(kBlock), 0, st, SLK_SDDMM_ARGS);
+#define SLK_SDDMM_WIN_ARGS                                                                   \
+    SLK_SDDMM_ARGS, W->row_capacity, listed ? W->slot_list : nullptr,                         \
+        listed ? W->slot_list_row : nullptr, space
+    // A slot list has short row runs per column block: stage four rows per group.
+    if (G == 2 && !listed) {
+        hipLaunchKernelGGL((sddmm_simd_win_kernel<2, 2>), grid, dim3(kBlock), 0, st, SLK_SDDMM_WIN_ARGS);
+    } else if (G == 2) {
+        hipLaunchKernelGGL((sddmm_simd_win_kernel<2, 4>), grid, dim3(kBlock), 0, st, SLK_SDDMM_WIN_ARGS);
+    } else if (G == 4 && !listed) {
+        hipLaunchKernelGGL((sddmm_simd_win_kernel<4, 2>), grid, dim3(kBlock), 0, st, SLK_SDDMM_WIN_ARGS);
     } else if (G == 4) {
-        hipLaunchKernelGGL(sddmm_simd_win_kernel<4>, grid, dim3(kBlock), 0, st, SLK_SDDMM_ARGS);
+        hipLaunchKernelGGL((sddmm_simd_win_kernel<4, 4>), grid, dim3(kBlock), 0, st, SLK_SDDMM_WIN_ARGS);
     } else if (v4) {
         hipLaunchKernelGGL(sddmm_simd_kernel<true>, grid, dim3(kBlock), 0, st, SLK_SDDMM_ARGS);
     } else {
         hipLaunchKernelGGL(sddmm_simd_kernel<false>, grid, dim3(kBlock), 0, st, SLK_SDDMM_ARGS);
     }
+#undef SLK_SDDMM_WIN_ARGS
 #undef SLK_SDDMM_ARGS
     return check_launch(who);
 }

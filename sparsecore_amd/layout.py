@@ -251,6 +251,7 @@ class PaddedCSR:
         self._topology_version = 0
         self._cview = None
         self._order = None      # (topology_version, device row schedule) for the view
+        self._slist = None      # ((topology_version, block_cols), view with a slot list)
         self._host_rows = None  # cached numpy (row_start, row_nnz, row_capacity)
 
     # ─── shape and aggregates (bindings.cpp:631-660) ────────────────
@@ -352,6 +353,21 @@ class PaddedCSR:
                              _lib.ptr(self._row_nnz), _lib.ptr(self._row_cap), _lib.ptr(order))
             self._cview = v
         return v
+
+    def _view_listed(self, block_cols: int) -> _lib.CsrView:
+        """The view plus W's live slots listed column block by column block (then
+        by row and column), with their rows: a slot order for slk_sddmm on large
+        layers (slk_csr.slot_list). Built on the device (slk_slot_list_build,
+        four launches) once per topology."""
+        base = self._view()
+        key = (self._topology_version, int(block_cols), id(base))
+        if self._slist is None or self._slist[0] != key:
+            lst, lrow = _lib.slot_list_build(base, int(block_cols), self._nnz, self.device)
+            fields = {f: getattr(base, f) for f, _ in _lib.CsrView._fields_}
+            fields.update(slot_list=_lib.ptr(lst), slot_list_row=_lib.ptr(lrow),
+                          n_slot_list=int(lst.numel()))
+            self._slist = (key, _lib.CsrView(**fields), lst, lrow)
+        return self._slist[1]
 
     def _rows_host(self):
         h = self._host_rows

@@ -7,6 +7,8 @@ whose layout the PaddedCSR invariants fix uniquely.
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -31,6 +33,13 @@ def _spmm(W, X):
 
 def _sddmm(W, dY, X, kernel="simd"):
     return ops._launch_sddmm(W, dY, X, kernel)
+
+
+def _with_fields(v, **changes):
+    """A copy of a CsrView with some fields replaced."""
+    fields = {f: getattr(v, f) for f, _ in _lib.CsrView._fields_}
+    fields.update(changes)
+    return _lib.CsrView(**fields)
 
 
 # ───────────────────────── golden fixtures ─────────────────────────────
@@ -245,12 +254,12 @@ def test_row_order_schedule_bit_exact(dev, N):
     assert_bits_equal(_spmm(W, X).cpu().numpy(), want, "Y (row_order)")
     # any permutation is a valid schedule: a random one through the C view
     perm = torch.from_numpy(rng.permutation(3000).astype(np.int32)).to(dev)
-    v2 = _lib.CsrView(*[getattr(v, f) for f, _ in _lib.CsrView._fields_[:-1]], perm.data_ptr())
+    v2 = _with_fields(v, row_order=perm.data_ptr())
     Y = torch.empty(3000, N, device=dev)
     _lib.spmm(v2, X, Y)
     assert_bits_equal(Y.cpu().numpy(), want, "Y (random order)")
     # and no schedule at all
-    v3 = _lib.CsrView(*[getattr(v, f) for f, _ in _lib.CsrView._fields_[:-1]], None)
+    v3 = _with_fields(v, row_order=None)
     _lib.spmm(v3, X, Y)
     assert_bits_equal(Y.cpu().numpy(), want, "Y (natural order)")
 
@@ -407,3 +416,81 @@ def test_sddmm_bias_fuses_the_bias_gradient(dev, monkeypatch, env, N, order):
     ref = dY_np.astype(np.float64).sum(axis=1)
     bound = 1e-6 * np.abs(dY_np).astype(np.float64).sum(axis=1) + 1e-30
     assert np.all(np.abs(runs[0][1] - ref) <= bound), "dbias"
+
+
+def _expected_slot_list(c, block):
+    """Live slots sorted by (column // block, row, column) with their rows."""
+    slots, rows, cols = oracle.live_slots(c)
+    order = np.lexsort((cols, rows, cols // block))
+    return slots[order], rows[order]
+
+
+@pytest.mark.parametrize("shape,density,block", [
+    ((150, 300), 0.06, 1),        # one block per column
+    ((150, 300), 0.06, 7),
+    ((150, 300), 0.06, 300),      # a single block
+    ((150, 300), 0.06, 5000),     # block wider than the matrix
+    ((3000, 257), 0.02, 64),      # more rows than the scan's 1024 threads
+    ((5, 4100), 0.3, 3),          # more blocks than the block scan's threads
+    ((64, 64), 1.0, 16),          # fully dense
+])
+def test_slot_list_build_order(dev, shape, density, block):
+    """slk_slot_list_build lists every live slot exactly once, ordered by
+    column block, row, column, with the right rows (empty rows included)."""
+    M, K = shape
+    c = oracle.zipf_rows(M, K, density, 1.1, seed=M + K + block, sigma=0.5)
+    c.row_nnz[M // 2] = 0
+    c.col_indices[c.row_start[M // 2]:c.row_start[M // 2] + c.row_capacity[M // 2]] = -1
+    W = from_oracle(c, dev)
+    lst, lrow = _lib.slot_list_build(W._view(), block, W.nnz, dev)
+    want_s, want_r = _expected_slot_list(c, block)
+    assert np.array_equal(lst.cpu().numpy(), want_s.astype(np.int32))
+    assert np.array_equal(lrow.cpu().numpy(), want_r.astype(np.int32))
+
+
+def test_slot_list_build_rejects_bad_arguments(dev):
+    c = oracle.zipf_rows(16, 32, 0.2, 1.1, seed=3)
+    W = from_oracle(c, dev)
+    with pytest.raises(ValueError, match="block_cols"):
+        _lib.slot_list_build(W._view(), 0, W.nnz, dev)
+    lib = _lib.load()
+    view = W._view()
+    out = torch.empty(W.nnz, dtype=torch.int32, device=dev)
+    rc = lib.slk_slot_list_build(ctypes.byref(view), 4, _lib.ptr(out), 4, _lib.ptr(out),
+                                 _lib.ptr(out), None)
+    assert rc != 0 and b"workspace" in lib.slk_last_error()
+
+
+@pytest.mark.parametrize("G", [2, 4])
+@pytest.mark.parametrize("block", [1, 7, 64, 1000])
+def test_sddmm_slot_list_order_bit_exact(dev, monkeypatch, G, block):
+    """The windowed dW kernel walking the slot list (live slots by column block,
+    row, column; padding zeroed by the per-row waves) gives the same bits as
+    the flat order, with and without the fused bias gradient, including empty
+    rows and a dense row."""
+    monkeypatch.setenv("SLK_SDDMM_G", str(G))
+    c = oracle.zipf_rows(150, 300, 0.06, 1.1, seed=block, sigma=0.5)
+    c.row_nnz[7] = 0
+    c.col_indices[c.row_start[7]:c.row_start[7] + c.row_capacity[7]] = -1
+    c.values[c.row_start[7]:c.row_start[7] + c.row_capacity[7]] = 0.0
+    rng = np.random.default_rng(block)
+    N = 1032
+    X_np = rng.standard_normal((300, N)).astype(np.float32)
+    dY_np = rng.standard_normal((150, N)).astype(np.float32)
+    W = from_oracle(c, dev)
+    X, dY = _t(X_np, dev), _t(dY_np, dev)
+    view = W._view_listed(block)
+    assert view.n_slot_list == W.nnz
+    lst = W._slist[2].cpu().numpy()
+    assert sorted(lst.tolist()) == sorted(oracle.live_slots(c)[0].tolist())
+    ref = oracle.sddmm(c, dY_np, X_np)
+    dW = torch.full((W.total_capacity,), float("nan"), device=dev)
+    _lib.sddmm(view, dY, X, dW, _lib.SLK_DW_SIMD)
+    assert_bits_equal(dW.cpu().numpy(), ref, "dW listed")
+    dW2 = torch.full((W.total_capacity,), float("nan"), device=dev)
+    db = torch.empty(150, device=dev)
+    _lib.sddmm(view, dY, X, dW2, _lib.SLK_DW_SIMD, db)
+    assert_bits_equal(dW2.cpu().numpy(), ref, "dW listed + bias")
+    db_flat = torch.empty(150, device=dev)
+    _lib.sddmm(W._view(), dY, X, torch.empty_like(dW), _lib.SLK_DW_SIMD, db_flat)
+    assert torch.equal(db, db_flat)
