@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the padded-CSR training hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--workload c2] [--no-graph] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--workload c2] [--graph-steps S] [--no-graph] [--no-cpu]
 
 Prints ONE JSON line (rank 0). Workloads (BASELINE.json `configs`):
 
@@ -13,8 +13,11 @@ Prints ONE JSON line (rank 0). Workloads (BASELINE.json `configs`):
       step = forward Y, dW and dX (cached transpose refresh + SpMM on WT).
       value = algorithmic GB/s of fwd+dX+dW.
 
-The timed region replays the step captured in a HIP graph (--no-graph: eager
-launches); inputs and weights are resident in HBM before it starts. The
+The timed region replays the step captured in HIP graphs, --graph-steps
+consecutive steps per graph (default 20; the remainder by a one-step graph;
+--no-graph: eager launches), so a replay's fixed launch latency is paid once
+per graph; every step runs all of its kernels. Inputs and weights are
+resident in HBM before it starts. The
 dominant kernel's average duration is then measured with HIP events around
 back-to-back launches of that kernel on the step's own tensors (queued
 behind a GPU sleep so no host gap enters the interval); `roofline.achieved`
@@ -53,6 +56,8 @@ def parse_args():
                     choices=["c1", "c2", "c3", "c4", "c5-95", "c5-99", "c5-95-rigl",
                              "c5-99-rigl"])
     ap.add_argument("--no-graph", action="store_true", help="time eager launches")
+    ap.add_argument("--graph-steps", type=int, default=20,
+                    help="training steps captured per HIP graph (graph-captured workloads)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU-baseline budget")
@@ -123,8 +128,20 @@ def timed_loop(step, steps: int):
     return time.perf_counter() - t0
 
 
-def capture(step_body, warm_iters: int = 3):
-    """Capture step_body() into a HIP graph after warming it on a side stream."""
+def timed_run(run_steps, steps: int):
+    """Wall time of run_steps(steps), synchronized on both sides."""
+    import torch
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run_steps(steps)
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
+
+
+def capture(step_body, warm_iters: int = 3, steps: int = 1):
+    """Capture `steps` consecutive step_body() calls into one HIP graph after
+    warming it on a side stream; returns the graph and each step's output."""
     import torch
 
     s = torch.cuda.Stream()
@@ -135,8 +152,24 @@ def capture(step_body, warm_iters: int = 3):
     torch.cuda.current_stream().wait_stream(s)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        out = step_body()
-    return g, out
+        outs = [step_body() for _ in range(steps)]
+    return g, outs
+
+
+class GraphSteps:
+    """Runs n training steps as replays of an S-step graph plus, for n mod S,
+    a one-step graph. A replay costs a fixed few microseconds of launch
+    latency on top of its kernels, which a sub-100 us step feels; a graph of
+    S steps pays it once per S steps. Every step is still executed in full."""
+
+    def __init__(self, big, S, one):
+        self.big, self.S, self.one = big, S, one
+
+    def run(self, n):
+        for _ in range(n // self.S):
+            self.big.replay()
+        for _ in range(n % self.S):
+            self.one.replay()
 
 
 # ───────────────────────────── workload C2 ───────────────────────────────────
@@ -924,18 +957,23 @@ def main():
                        rigl=args.workload.endswith("rigl"))
 
     stage("eager warmup")
-    for _ in range(max(1, args.warmup)):
-        work.body()
-    torch.cuda.synchronize()
+    work.body()
+    eager_s = timed_loop(work.body, max(1, args.warmup)) / max(1, args.warmup)
 
     use_graph = not args.no_graph and not getattr(work, "dynamic", False)
     graph_ok = False
+    # Several steps per graph only where a replay's launch latency is a visible
+    # share of the step (sub-millisecond steps: C1, C2). Longer steps keep one
+    # step per graph: C3's step holds library scans (the embedding backward's
+    # rocprim select), and a 20-step graph of it faulted inside such a scan on
+    # replay, where one-step graphs of the same step replay cleanly.
+    S = max(1, min(args.graph_steps, args.steps)) if eager_s < 1e-3 else 1
     if use_graph:
         params = work.params()
         snap = [p.detach().clone() for p in params]
-        stage("eager reference steps for the graph check")
+        stage(f"eager reference steps for the graph check (2 x {S} steps)")
         eager_flat = []
-        for _ in range(3):
+        for _ in range(2 * S):
             o = work.body()
             eager_flat += [t.detach().clone() for t in (o if isinstance(o, tuple) else (o,))]
             del o
@@ -944,34 +982,41 @@ def main():
             for p, s in zip(params, snap):
                 p.copy_(s)
         torch.cuda.synchronize()
-        stage("graph capture")
-        g, gout = capture(work.body)
-        stage("graph replay check")
+        stage(f"graph capture ({S} steps per graph)")
+        g, gouts = capture(work.body, steps=S)
+        g1 = capture(work.body)[0] if args.steps % S or args.warmup % S else None
+        stage("graph replay check (two replays, every step against eager)")
         with torch.no_grad():
             for p, s in zip(params, snap):
                 p.copy_(s)
         graph_ok = True
-        for i in range(3):
+        for r in range(2):
             g.replay()
             torch.cuda.synchronize()
-            got = [t for t in (gout if isinstance(gout, tuple) else (gout,))]
-            per = len(got)
-            want = eager_flat[i * per:(i + 1) * per]
-            if not all(torch.equal(a, b) for a, b in zip(got, want)):
-                graph_ok = False
+            got = [t for o in gouts for t in (o if isinstance(o, tuple) else (o,))]
+            want = eager_flat[r * len(got):(r + 1) * len(got)]
+            graph_ok = graph_ok and len(want) == len(got) and all(
+                torch.equal(a, b) for a, b in zip(got, want))
         if not all(torch.equal(p, e) for p, e in zip(params, eager_params)):
             graph_ok = False
         if not graph_ok:
             print("bench.py: graph replay differs from eager; timing eager launches",
                   file=sys.stderr)
-        step = g.replay if graph_ok else work.body
-        for _ in range(args.warmup):
-            step()
+        if graph_ok:
+            runner = GraphSteps(g, S, g1)
+            run_steps = runner.run
+        else:
+            def run_steps(n):
+                for _ in range(n):
+                    work.body()
+        run_steps(args.warmup)
     else:
-        step = work.body
+        def run_steps(n):
+            for _ in range(n):
+                work.body()
 
     stage(f"timed region: {args.steps} steps (graph={graph_ok if use_graph else False})")
-    elapsed = timed_loop(step, args.steps)
+    elapsed = timed_run(run_steps, args.steps)
     ms_per_step = 1e3 * elapsed / args.steps
     topo_ms = 0.0
     if getattr(work, "algo", None) is not None or getattr(work, "rigl", False):
@@ -1010,7 +1055,7 @@ def main():
                                               (sum(k["avg_us"] for k in l1) * 1e-6) / 1e9, 1),
                 "layer1_nnz": W.nnz}
         config = {"workload": "c2: " + work.desc, "global_batch": work.batch,
-                  "graph": graph_ok}
+                  "graph": graph_ok, "graph_steps": S if graph_ok else 0}
     elif isinstance(work, GPTWork):
         value = work.tokens_per_step() * args.steps / elapsed
         unit = "tokens/s"
@@ -1025,7 +1070,8 @@ def main():
         if work.algo is not None:
             path["topology_update_ms_per_step"] = round(topo_ms, 3)
         config = {"workload": f"{work.name}: {work.desc}", "global_batch": work.batch,
-                  "seq_len": work.ctx, "graph": graph_ok}
+                  "seq_len": work.ctx, "graph": graph_ok,
+                  "graph_steps": S if graph_ok else 0}
     elif work.rigl:
         value = work.N * args.steps / elapsed
         unit = "tokens/s"
@@ -1039,6 +1085,7 @@ def main():
         path = {"GFLOP/s": round(work.step_flops() * args.steps / elapsed / 1e9, 1),
                 "step_bytes": work.step_bytes(), "nnz": work.W.nnz}
         config = {"workload": f"{work.name}: {work.desc}", "graph": graph_ok,
+                  "graph_steps": S if graph_ok else 0,
                   "transpose_rebuild_ms": round(work.rebuild_ms, 3)}
 
     line = {

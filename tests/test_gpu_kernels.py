@@ -418,6 +418,46 @@ def test_sddmm_bias_fuses_the_bias_gradient(dev, monkeypatch, env, N, order):
     assert np.all(np.abs(runs[0][1] - ref) <= bound), "dbias"
 
 
+def _zero_capacity_rows(M, K, per_row, empty, seed):
+    """A padded CSR whose rows in `empty` have capacity 0 (no slots at all)."""
+    rng = np.random.default_rng(seed)
+    cols, vals = [], []
+    for i in range(M):
+        n = 0 if i in empty else int(rng.integers(0, per_row + 1))
+        cols.append(np.sort(rng.choice(K, size=n, replace=False)).astype(np.int32))
+        vals.append(rng.standard_normal(n).astype(np.float32))
+    cap = np.array([0 if i in empty else max(1, int(np.ceil(len(cols[i]) * 1.2)))
+                    for i in range(M)], dtype=np.int32)
+    rs = np.zeros(M, dtype=np.int32)
+    rs[1:] = np.cumsum(cap)[:-1]
+    col = np.full(int(cap.sum()), -1, dtype=np.int32)
+    val = np.zeros(int(cap.sum()), dtype=np.float32)
+    for i in range(M):
+        col[rs[i]:rs[i] + len(cols[i])] = cols[i]
+        val[rs[i]:rs[i] + len(cols[i])] = vals[i]
+    return oracle.Csr(M, K, val, col, rs, np.array([len(x) for x in cols], np.int32), cap)
+
+
+@pytest.mark.parametrize("N", [16, 20, 64, 100, 128, 200, 256, 264, 268])
+@pytest.mark.parametrize("layout", ["dense-rows", "zero-capacity-runs"])
+def test_sddmm_rows_without_slots_bit_exact(dev, N, layout):
+    """dW at every N shape of the one-group kernel (full 16-wide steps, the
+    8-wide step, the scalar tail), including long runs of rows with capacity 0
+    between the slots of one wave (the row search must skip them)."""
+    print(f"[dW rows] N={N} {layout}", flush=True)
+    if layout == "dense-rows":
+        c = oracle.uniform_rows(300, 90, 30, seed=N, sigma=1.0)
+    else:
+        empty = set(range(5, 150)) | set(range(151, 240))
+        c = _zero_capacity_rows(400, 90, 12, empty, seed=N)
+    rng = np.random.default_rng(N)
+    X_np = rng.standard_normal((90, N)).astype(np.float32)
+    dY_np = rng.standard_normal((c.nrows, N)).astype(np.float32)
+    W = from_oracle(c, dev)
+    got = _sddmm(W, _t(dY_np, dev), _t(X_np, dev)).cpu().numpy()
+    assert_bits_equal(got, oracle.sddmm(c, dY_np, X_np), "dW")
+
+
 def _expected_slot_list(c, block):
     """Live slots sorted by (column // block, row, column) with their rows."""
     slots, rows, cols = oracle.live_slots(c)
