@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define SLK_ABI_VERSION 3
+#define SLK_ABI_VERSION 4
 
 #if defined(__GNUC__)
 #define SLK_API __attribute__((visibility("default")))
@@ -237,6 +237,35 @@ SLK_API int slk_dense_grad(const float* dY, const float* X, int64_t M, int64_t K
  * gradient (sparselab/ops.py:174).                                          */
 SLK_API int slk_transpose_dense(const float* src, int64_t rows, int64_t cols,
                                 int64_t ld_src, float* dst, void* stream);
+
+/* Yt = (W·X)^T (+ bias[i] on row i): slk_spmm / slk_spmm_bias with the
+ * result stored token-major, Yt[n*M + i] = Y[i, n] (N x M row-major) — the
+ * layout of SparseLinear's output y = (W·xᵀ)ᵀ (sparselab/nn.py:229-241),
+ * written directly for a consumer that needs it contiguous (a loss on a
+ * narrow classifier layer). The same fma chain and bias rounding as
+ * slk_spmm_bias; bias may be NULL.                                           */
+SLK_API int slk_spmm_t(const slk_csr* W, const float* X, int64_t K, int64_t N,
+                       const float* bias, float* Yt, void* stream);
+
+/* Largest W slk_backward_narrow takes (rows; slots, staged in LDS).          */
+#define SLK_NARROW_MAX_ROWS 64
+#define SLK_NARROW_MAX_CAPACITY 8192
+
+/* Backward of a narrow layer (W->nrows <= SLK_NARROW_MAX_ROWS and
+ * W->total_capacity <= SLK_NARROW_MAX_CAPACITY) in one launch, from the
+ * token-major output gradient dYt (N x M, dY[i, n] = dYt[n*M + i]):
+ *   dW    — as slk_sddmm in `order` (live slots; padding 0), if not NULL;
+ *   dbias — as slk_sddmm_bias's dbias (M floats), if not NULL;
+ *   dX    — W^T·dY, K x N row-major, bit-identical to slk_spmm on the
+ *           transpose slk_transpose_fill builds (each element the fma chain
+ *           over column c's rows in ascending order from +0.0), if not NULL.
+ * X is the layer input, X_rows x N row-major with X_rows == W->ncols (read
+ * only for dW). Replaces, for such layers, the dY.contiguous(), the dW call,
+ * the transpose-cache refresh and spmm(WT, dY) of the reference backward
+ * (sparselab/ops.py:160-210).                                               */
+SLK_API int slk_backward_narrow(const slk_csr* W, const float* dYt, int64_t N, const float* X,
+                                int64_t X_rows, float* dW, float* dbias, float* dX, int order,
+                                void* stream);
 
 /* Bytes of device workspace slk_slot_list_build needs for W and block_cols. */
 SLK_API int64_t slk_slot_list_workspace_bytes(const slk_csr* W, int64_t block_cols);

@@ -21,7 +21,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libsparsecore_amd.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 SLK_OK, SLK_EINVAL, SLK_EDEVICE = 0, 1, 2
 SLK_DW_SIMD, SLK_DW_SCALAR = 0, 1
@@ -49,7 +49,12 @@ EXPORTS = (
     "slk_transpose_dense",
     "slk_slot_list_workspace_bytes",
     "slk_slot_list_build",
+    "slk_spmm_t",
+    "slk_backward_narrow",
 )
+
+NARROW_MAX_ROWS = 64        # SLK_NARROW_MAX_ROWS
+NARROW_MAX_CAPACITY = 8192  # SLK_NARROW_MAX_CAPACITY
 
 
 class CsrView(ctypes.Structure):
@@ -104,6 +109,9 @@ def _declare(lib) -> None:
     lib.slk_slot_list_workspace_bytes.restype = _i64
     lib.slk_slot_list_workspace_bytes.argtypes = [_csrp, _i64]
     lib.slk_slot_list_build.argtypes = [_csrp, _i64, _vp, _i64, _vp, _vp, _vp]
+    lib.slk_spmm_t.argtypes = [_csrp, _vp, _i64, _i64, _vp, _vp, _vp]
+    lib.slk_backward_narrow.argtypes = [_csrp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, ctypes.c_int,
+                                        _vp]
     sized = ("slk_last_error", "slk_abi_version", "slk_transpose_workspace_bytes",
              "slk_drop_grow_workspace_bytes", "slk_slot_list_workspace_bytes")
     for name in EXPORTS:
@@ -253,6 +261,28 @@ def dense_grad(dY: torch.Tensor, X: torch.Tensor, M: int, K: int, N: int, token_
                G: torch.Tensor) -> None:
     lib = load()
     rc = lib.slk_dense_grad(ptr(dY), ptr(X), M, K, N, int(token_major), ptr(G), stream_of(G))
+    if rc:
+        _raise(rc)
+
+
+def spmm_t(view: CsrView, X: torch.Tensor, Yt: torch.Tensor,
+           bias: torch.Tensor | None = None) -> None:
+    """Yt (N x M, contiguous) = (W·X)ᵀ (+ bias per row of W) (slk_spmm_t)."""
+    lib = load()
+    rc = lib.slk_spmm_t(ctypes.byref(view), ptr(X), X.shape[0], X.shape[1], ptr(bias), ptr(Yt),
+                        stream_of(Yt))
+    if rc:
+        _raise(rc)
+
+
+def backward_narrow(view: CsrView, dYt: torch.Tensor, X: torch.Tensor,
+                    dW: torch.Tensor | None, dbias: torch.Tensor | None,
+                    dX: torch.Tensor | None, order: int) -> None:
+    """dW / dbias / dX of a narrow layer from the token-major gradient dYt
+    (N x M, contiguous); X is the K x N layer input (slk_backward_narrow)."""
+    lib = load()
+    rc = lib.slk_backward_narrow(ctypes.byref(view), ptr(dYt), dYt.shape[0], ptr(X), X.shape[0],
+                                 ptr(dW), ptr(dbias), ptr(dX), int(order), stream_of(dYt))
     if rc:
         _raise(rc)
 

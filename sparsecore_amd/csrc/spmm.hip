@@ -153,7 +153,8 @@ __device__ __forceinline__ void load_meta(const int32_t* __restrict__ col,
     }
 }
 
-template <int VEC, int U>
+// TOUT: Y is stored token-major, Y[i, n] at Y[n·M + i] (slk_spmm_t).
+template <int VEC, int U, bool TOUT = false>
 __global__ __launch_bounds__(kSpmmBlock) void spmm_wave_kernel(
     int64_t M, int64_t N, int64_t nitems, const int32_t* __restrict__ order,
     const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
@@ -220,7 +221,12 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_wave_kernel(
     }
     if (active) {
         if (bias != nullptr) add_bias<VEC>(acc, bias[row]);
-        VecIO<VEC>::store(Y + row * N + n0, acc);
+        if constexpr (TOUT) {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) Y[(n0 + e) * M + row] = acc[e];
+        } else {
+            VecIO<VEC>::store(Y + row * N + n0, acc);
+        }
     }
 }
 
@@ -516,8 +522,23 @@ constexpr int64_t kLdsMinBlocks = 512;
 constexpr double kLdsMinReuse = 4.0;
 
 // Y = W·X (+ bias per row): the shared body of slk_spmm and slk_spmm_bias.
+// Y^T for slk_spmm_t: one-row-per-wave kernel, one float per lane, each
+// lane writing its token's row of Yt (narrow layers; the stores of a wave are
+// M floats apart).
+int launch_wave_t(const slk_csr* W, const float* X, int64_t N, const float* bias, float* Yt,
+                  hipStream_t st) {
+    const int64_t M = W->nrows;
+    const int64_t nitems = M * ceil_div(N, int64_t{kWave});
+    int64_t blocks;
+    if (int rc = launch_blocks(nitems, &blocks)) return rc;
+    hipLaunchKernelGGL((spmm_wave_kernel<1, 32, true>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(kSpmmBlock), 0, st, M, N, nitems, W->row_order, W->row_start,
+                       W->row_nnz, W->col_indices, W->values, X, bias, Yt);
+    return check_launch("spmm_t");
+}
+
 int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const float* bias,
-              float* Y, void* stream) {
+              float* Y, void* stream, bool transposed_out = false) {
     clear_error();
     if (int rc = validate_csr(W, "spmm")) return rc;
     if (N < 0 || K < 0) return fail(SLK_EINVAL, "spmm: negative X shape");
@@ -530,6 +551,7 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
     if (Y == nullptr || (K > 0 && X == nullptr)) return fail(SLK_EINVAL, "spmm: NULL X or Y");
     if (N > INT32_MAX / 4) return fail(SLK_EINVAL, "spmm: N exceeds the 32-bit lane offset range");
     hipStream_t st = as_stream(stream);
+    if (transposed_out) return launch_wave_t(W, X, N, bias, Y, st);
     const uintptr_t align = reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(Y);
     const int64_t M = W->nrows;
 
@@ -596,4 +618,9 @@ extern "C" int slk_spmm_bias(const slk_csr* W, const float* X, int64_t K, int64_
         return slk::fail(SLK_EINVAL, "spmm_bias: NULL bias");
     }
     return slk::spmm_impl(W, X, K, N, bias, Y, stream);
+}
+
+extern "C" int slk_spmm_t(const slk_csr* W, const float* X, int64_t K, int64_t N,
+                          const float* bias, float* Yt, void* stream) {
+    return slk::spmm_impl(W, X, K, N, bias, Yt, stream, true);
 }

@@ -17,6 +17,7 @@ import torch.nn as nn
 
 from . import layout as _layout
 from .layout import PaddedCSR
+from . import ops as _ops
 from .ops import _SparseLinearFunction
 
 __all__ = ["SparseLinear"]
@@ -153,16 +154,20 @@ class SparseLinear(nn.Module):
         # One autograd node: the (N, in) -> (in, N) layout change (none when x
         # is the transposed view a previous SparseLinear returned), the SpMM
         # with the bias add fused into its store, and the matching backward.
+        # A narrow layer (few outputs) gets its output token-major and
+        # contiguous straight from the store; otherwise the output is the
+        # transposed view of the feature-major result.
         x_flat = x.reshape(-1, self.in_features)
         if x_flat.dtype != torch.float32:
             x_flat = x_flat.to(torch.float32)
+        narrow = _ops._narrow_layer(self._csr)
         b = self.bias
         if b is not None and b.dtype != torch.float32:
-            Y_col = _SparseLinearFunction.apply(self._values, None, self._csr, x_flat, "simd")
-            Y_col = Y_col + b.to(torch.float32)[:, None]
+            out = _SparseLinearFunction.apply(self._values, None, self._csr, x_flat, "simd")
+            y_flat = (out if narrow else out.t()) + b.to(torch.float32)
         else:
-            Y_col = _SparseLinearFunction.apply(self._values, b, self._csr, x_flat, "simd")
-        y_flat = Y_col.t()
+            out = _SparseLinearFunction.apply(self._values, b, self._csr, x_flat, "simd")
+            y_flat = out if narrow else out.t()
         return y_flat.reshape(orig_shape[:-1] + (self.out_features,))
 
     @property

@@ -173,19 +173,28 @@ def _as_row_major(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous()
 
 
+def _narrow_layer(W: PaddedCSR) -> bool:
+    """A layer small enough for the narrow path (slk_spmm_t forward,
+    slk_backward_narrow backward): at most 64 output rows and 8192 slots."""
+    return W.nrows <= _lib.NARROW_MAX_ROWS and W.total_capacity <= _lib.NARROW_MAX_CAPACITY
+
+
 class _SparseLinearFunction(torch.autograd.Function):
     """SparseLinear's ``Y = W @ x_flatᵀ (+ bias[:, None])`` as one autograd node
     (sparselab/nn.py:229-241 with ops.py:127-210 inside).
 
-    Takes the token-major input x_flat (N x K) and returns Y feature-major
-    (M x N), whose ``.t()`` is the layer output. The layout changes of the
-    reference (``x_flat.t().contiguous()``, the bias add, ``dY.contiguous()``)
-    are done by the library: the transpose by slk_transpose_dense — free when
-    x_flat is the transposed view a previous SparseLinear returned — and the
-    bias add inside the SpMM store (slk_spmm_bias: the bits of the separate
-    float32 add). Backward is ``_SpMMFunction``'s, plus dbias = Σ_n dY[:, n]
-    computed in the dW launch (slk_sddmm_bias); dx is returned as the
-    transposed view of dX (K x N).
+    Takes the token-major input x_flat (N x K). Returns Y feature-major
+    (M x N), whose ``.t()`` is the layer output, or — for a narrow layer
+    (``_narrow_layer``) — the layer output itself, token-major (N x M)
+    contiguous. The layout changes of the reference (``x_flat.t().contiguous()``,
+    the bias add, ``dY.contiguous()``) are done by the library: the transpose
+    by slk_transpose_dense — free when x_flat is the transposed view a
+    previous SparseLinear returned — and the bias add inside the SpMM store
+    (slk_spmm_bias / slk_spmm_t: the bits of the separate float32 add).
+    Backward is ``_SpMMFunction``'s, plus dbias = Σ_n dY[:, n] computed in the
+    dW launch (slk_sddmm_bias); a narrow layer does all three gradients in one
+    launch from the token-major gradient (slk_backward_narrow), with no
+    transpose cache. dx is returned as the transposed view of dX (K x N).
     """
 
     @staticmethod
@@ -204,11 +213,18 @@ class _SparseLinearFunction(torch.autograd.Function):
         ctx.save_for_backward(W_values, X)
         ctx.W = W
         ctx.kernel = kernel
+        ctx.narrow = _narrow_layer(W)
+        if ctx.narrow:
+            Yt = torch.empty(X.shape[1], W.nrows, dtype=torch.float32, device=X.device)
+            _lib.spmm_t(W._view(), X, Yt, bias)
+            return Yt
         return _launch_spmm(W, X, bias)
 
     @staticmethod
     def backward(ctx, dY):
         W_values, X = ctx.saved_tensors
+        if ctx.narrow:
+            return _narrow_backward(ctx, X, dY)
         dY_f32 = _as_row_major(dY)
         need_dw, need_db = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         dbias = None
@@ -219,6 +235,21 @@ class _SparseLinearFunction(torch.autograd.Function):
         dW_values, dX = _spmm_backward(ctx.W, X, dY_f32, ctx.kernel, need_dw,
                                        ctx.needs_input_grad[3], dbias if need_dw else None)
         return dW_values, dbias, None, (dX.t() if dX is not None else None), None
+
+
+def _narrow_backward(ctx, X: torch.Tensor, dYt: torch.Tensor):
+    """Gradients of a narrow layer from the token-major output gradient."""
+    W = ctx.W
+    dev = X.device
+    dYt = dYt.to(torch.float32).contiguous()
+    need_dw, need_db, need_dx = (ctx.needs_input_grad[0], ctx.needs_input_grad[1],
+                                 ctx.needs_input_grad[3])
+    dW = torch.empty(W.total_capacity, dtype=torch.float32, device=dev) if need_dw else None
+    dbias = torch.empty(W.nrows, dtype=torch.float32, device=dev) if need_db else None
+    dX = torch.empty(X.shape, dtype=torch.float32, device=dev) if need_dx else None
+    order = _lib.SLK_DW_SCALAR if ctx.kernel == "scalar" else _lib.SLK_DW_SIMD
+    _lib.backward_narrow(W._view(), dYt, X, dW, dbias, dX, order)
+    return dW, dbias, None, (dX.t() if dX is not None else None), None
 
 
 def spmm(W: PaddedCSR, X: torch.Tensor, *, kernel: str = "auto") -> torch.Tensor:

@@ -262,6 +262,42 @@ def test_sparse_linear_with_bias_bit_exact_vs_oracle(dev, batch):
     assert_bits_equal(h.detach().t().cpu().numpy(), h_ref, "relu(l1)")
 
 
+@pytest.mark.parametrize("out_features,batch", [(10, 256), (1, 37), (64, 5), (33, 130)])
+def test_narrow_layer_matches_general_path_bits(dev, monkeypatch, out_features, batch):
+    """A layer with at most 64 outputs runs the narrow path (token-major store,
+    one backward launch, no transpose cache); its output and all three
+    gradients are the general path's bit for bit, and the output comes back
+    contiguous."""
+    from sparsecore_amd import ops
+
+    torch.manual_seed(out_features)
+    layer = SparseLinear(300, out_features, sparsity=0.9).to(dev)
+    assert ops._narrow_layer(layer._csr)
+    x = torch.rand(batch, 300, device=dev)
+    up = torch.randn(batch, out_features, device=dev)
+    runs = []
+    for narrow in (True, False):
+        if not narrow:
+            monkeypatch.setattr(ops, "_narrow_layer", lambda W: False)
+        layer.zero_grad(set_to_none=True)
+        xi = x.clone().requires_grad_(True)
+        y = layer(xi)
+        assert y.is_contiguous() or not narrow
+        y.backward(up)
+        runs.append((y.detach().clone(), layer._values.grad.clone(), layer.bias.grad.clone(),
+                     xi.grad.clone()))
+    for a, b, what in zip(runs[0], runs[1], ("y", "dW", "dbias", "dx")):
+        assert_bits_equal(a.cpu().numpy(), b.cpu().numpy(), what)
+
+
+def test_narrow_layer_gradcheck(dev):
+    torch.manual_seed(0)
+    layer = SparseLinear(8, 4, sparsity=0.5).to(dev).double()
+    x = torch.randn(3, 8, dtype=torch.double, device=dev, requires_grad=True)
+    assert torch.autograd.gradcheck(lambda x: layer(x).sum(), (x,), eps=1e-3, atol=1e-3,
+                                    rtol=1e-3)
+
+
 def test_sparse_linear_zero_sparsity_matches_nn_linear(dev):
     torch.manual_seed(7)
     layer = SparseLinear(16, 8, sparsity=0.0).to(dev)
@@ -360,6 +396,17 @@ def test_matches_reference_init_stream(dev):
 
 # ───────────────── transpose cache (test_transpose_cache.py) ───────────
 
+@pytest.fixture
+def general_path(monkeypatch):
+    """Layers with at most 64 outputs take the narrow path, which has no
+    transpose cache (slk_backward_narrow). The cache tests below restate the
+    reference's own (tests/test_transpose_cache.py) on its shapes, so they
+    pin the general path."""
+    from sparsecore_amd import ops
+
+    monkeypatch.setattr(ops, "_narrow_layer", lambda W: False)
+
+
 def test_cache_hit_miss_refresh(dev):
     W = PaddedCSR.random(8, 16, sparsity=0.5, seed=0).to(dev)
     WT1 = _cached_transpose(W)
@@ -390,7 +437,7 @@ def test_cache_entry_dropped_with_matrix(dev):
     assert len(_transpose_cache) == 0
 
 
-def test_cached_and_fresh_gradients_match(dev):
+def test_cached_and_fresh_gradients_match(dev, general_path):
     torch.manual_seed(0)
     la = SparseLinear(16, 8, sparsity=0.5, bias=False).to(dev)
     torch.manual_seed(0)
@@ -417,7 +464,7 @@ def test_cached_and_fresh_gradients_match(dev):
     assert shape == (8, 16) and perm.dtype == torch.int64
 
 
-def test_rewrite_invalidates_cache_in_training(dev):
+def test_rewrite_invalidates_cache_in_training(dev, general_path):
     torch.manual_seed(0)
     layer = SparseLinear(16, 8, sparsity=0.5, bias=False).to(dev)
     layer(torch.randn(4, 16, device=dev, requires_grad=True)).sum().backward()
@@ -432,7 +479,7 @@ def test_rewrite_invalidates_cache_in_training(dev):
                                atol=1e-5)
 
 
-def test_gradcheck_with_cache_enabled(dev):
+def test_gradcheck_with_cache_enabled(dev, general_path):
     torch.manual_seed(0)
     layer = SparseLinear(8, 4, sparsity=0.5, bias=False).to(dev)
     x = torch.randn(3, 8, dtype=torch.double, device=dev, requires_grad=True)

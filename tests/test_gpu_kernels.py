@@ -458,6 +458,87 @@ def test_sddmm_rows_without_slots_bit_exact(dev, N, layout):
     assert_bits_equal(got, oracle.sddmm(c, dY_np, X_np), "dW")
 
 
+# ───────────────────────── narrow layers ───────────────────────────────
+
+def _narrow_case(M, K, N, per_row, seed, empty=()):
+    c = oracle.uniform_rows(M, K, per_row, seed=seed, sigma=1.0)
+    for i in empty:
+        c.row_nnz[i] = 0
+        c.col_indices[c.row_start[i]:c.row_start[i] + c.row_capacity[i]] = -1
+        c.values[c.row_start[i]:c.row_start[i] + c.row_capacity[i]] = 0.0
+    rng = np.random.default_rng(seed + 7)
+    X = rng.standard_normal((K, N)).astype(np.float32)
+    dY = rng.standard_normal((M, N)).astype(np.float32)
+    b = rng.standard_normal(M).astype(np.float32)
+    return c, X, dY, b
+
+
+@pytest.mark.parametrize("M,K,N,per_row", [
+    (10, 512, 256, 51), (1, 40, 7, 13), (64, 100, 1, 20), (33, 70, 130, 70), (5, 3000, 64, 5)])
+def test_spmm_t_token_major_bit_exact(dev, M, K, N, per_row):
+    """slk_spmm_t stores (W·X)ᵀ token-major with the same fma chain and bias
+    rounding as slk_spmm_bias, with and without bias, empty rows included."""
+    print(f"[spmm_t] M={M} K={K} N={N}", flush=True)
+    c, X_np, _, b_np = _narrow_case(M, K, N, per_row, seed=M + N, empty=(0,))
+    W = from_oracle(c, dev)
+    X = _t(X_np, dev)
+    for bias in (None, _t(b_np, dev)):
+        Yt = torch.full((N, M), float("nan"), device=dev)
+        _lib.spmm_t(W._view(), X, Yt, bias)
+        ref = oracle.spmm(c, X_np) + (b_np[:, None] if bias is not None else np.float32(0))
+        assert_bits_equal(Yt.cpu().numpy(), np.ascontiguousarray(ref.T), "Yt")
+
+
+@pytest.mark.parametrize("M,K,N,per_row", [
+    (10, 512, 256, 51), (1, 40, 7, 13), (64, 100, 3, 20), (33, 70, 130, 70), (7, 2000, 24, 9),
+    (64, 300, 64, 106)])
+@pytest.mark.parametrize("order", ["simd", "scalar"])
+def test_backward_narrow_bit_exact(dev, M, K, N, per_row, order):
+    """slk_backward_narrow from the token-major gradient: dW is the oracle's
+    in each summation order, dbias the same bits as slk_sddmm_bias's, and dX
+    the reference's spmm(WT, dY) bit for bit (rows without slots, columns no
+    row holds, N not a multiple of 4, a W of 8000 slots)."""
+    print(f"[narrow bwd] M={M} K={K} N={N} {order}", flush=True)
+    c, X_np, dY_np, _ = _narrow_case(M, K, N, per_row, seed=M * K + N, empty=(M // 2,))
+    W = from_oracle(c, dev)
+    assert W.total_capacity <= _lib.NARROW_MAX_CAPACITY
+    X, dYt = _t(X_np, dev), _t(np.ascontiguousarray(dY_np.T), dev)
+    ordv = _lib.SLK_DW_SCALAR if order == "scalar" else _lib.SLK_DW_SIMD
+    dW = torch.full((W.total_capacity,), float("nan"), device=dev)
+    db = torch.full((M,), float("nan"), device=dev)
+    dX = torch.full((K, N), float("nan"), device=dev)
+    _lib.backward_narrow(W._view(), dYt, X, dW, db, dX, ordv)
+    assert_bits_equal(dW.cpu().numpy(), oracle.sddmm(c, dY_np, X_np, order), "dW")
+    WT, _ = oracle.transpose_with_perm(c)
+    assert_bits_equal(dX.cpu().numpy(), oracle.spmm(WT, dY_np), "dX")
+    db_ref = torch.empty(M, device=dev)
+    _lib.sddmm(W._view(), _t(dY_np, dev), X, torch.empty_like(dW), ordv, db_ref)
+    assert torch.equal(db, db_ref)
+    # each output alone
+    for want in ("dW", "dbias", "dX"):
+        outs = {"dW": None, "dbias": None, "dX": None}
+        outs[want] = {"dW": torch.empty_like(dW), "dbias": torch.empty_like(db),
+                      "dX": torch.empty_like(dX)}[want]
+        _lib.backward_narrow(W._view(), dYt, X, outs["dW"], outs["dbias"], outs["dX"], ordv)
+        assert torch.equal(outs[want], {"dW": dW, "dbias": db, "dX": dX}[want]), want
+
+
+def test_backward_narrow_rejects_wide_layers(dev):
+    c, X_np, dY_np, _ = _narrow_case(65, 20, 8, 3, seed=1)
+    W = from_oracle(c, dev)
+    dYt = _t(np.ascontiguousarray(dY_np.T), dev)
+    with pytest.raises(ValueError, match="at most 64 rows"):
+        _lib.backward_narrow(W._view(), dYt, _t(X_np, dev), None, None,
+                             torch.empty(20, 8, device=dev), _lib.SLK_DW_SIMD)
+    c2, X2, dY2, _ = _narrow_case(8, 3000, 4, 1100, seed=2)
+    W2 = from_oracle(c2, dev)
+    assert W2.total_capacity > _lib.NARROW_MAX_CAPACITY
+    with pytest.raises(ValueError, match="slots"):
+        _lib.backward_narrow(W2._view(), _t(np.ascontiguousarray(dY2.T), dev), _t(X2, dev),
+                             torch.empty(W2.total_capacity, device=dev), None, None,
+                             _lib.SLK_DW_SIMD)
+
+
 def _expected_slot_list(c, block):
     """Live slots sorted by (column // block, row, column) with their rows."""
     slots, rows, cols = oracle.live_slots(c)
