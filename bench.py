@@ -231,10 +231,26 @@ class C2:
         for tag, layer, X in (("l1", self.l1, x_col), ("l2", self.l2, h_col)):
             W = layer._csr
             M, K = W.nrows, W.ncols
-            Y = torch.empty(M, N, device=self.dev)
-            dY = torch.randn(M, N, device=self.dev)
             dW = torch.empty(W.total_capacity, device=self.dev)
             view = W._view()
+            if ops._narrow_layer(W):
+                # the narrow path: token-major store, and dW + dbias + dX in one
+                # launch from the token-major gradient (no transpose cache)
+                Yt = torch.empty(N, M, device=self.dev)
+                dYt = torch.randn(N, M, device=self.dev)
+                db = torch.empty(M, device=self.dev)
+                dX = torch.empty(K, N, device=self.dev)
+                out.append((f"spmm_fwd_t[{tag} {M}x{K}]",
+                            lambda view=view, X=X, Yt=Yt: _lib.spmm_t(view, X, Yt),
+                            bytes_fwd(W.nnz, M, K, N), flops(W.nnz, N)))
+                out.append((f"backward_narrow[{tag} {M}x{K}]",
+                            lambda view=view, dYt=dYt, X=X, dW=dW, db=db, dX=dX:
+                                _lib.backward_narrow(view, dYt, X, dW, db, dX, _lib.SLK_DW_SIMD),
+                            bytes_dw(W.nnz, W.total_capacity, M, K, N) +
+                            bytes_fwd(W.nnz, K, M, N), 2 * flops(W.nnz, N)))
+                continue
+            Y = torch.empty(M, N, device=self.dev)
+            dY = torch.randn(M, N, device=self.dev)
             out.append((f"spmm_fwd[{tag} {M}x{K}]",
                         lambda view=view, X=X, Y=Y: _lib.spmm(view, X, Y),
                         bytes_fwd(W.nnz, M, K, N), flops(W.nnz, N)))
@@ -1031,7 +1047,7 @@ def main():
         kern.append({"kernel": name, "avg_us": round(ms * 1e3, 3), "bytes": nbytes,
                      "flops": nflops, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)})
     # roofline on the path's dominant kernel (forward SpMM, dX SpMM or dW SDDMM)
-    dom = max((k for k in kern if k["kernel"].startswith(("spmm", "sddmm"))),
+    dom = max((k for k in kern if k["kernel"].startswith(("spmm", "sddmm", "backward_narrow"))),
               key=lambda k: k["avg_us"])
     achieved = dom["bytes"] / (dom["avg_us"] * 1e-6) / 1e9
     # HBM bytes per launch of the dominant kernel, from the committed
