@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define SLK_ABI_VERSION 4
+#define SLK_ABI_VERSION 5
 
 #if defined(__GNUC__)
 #define SLK_API __attribute__((visibility("default")))
@@ -76,14 +76,17 @@ typedef struct slk_csr {
      * layout — a schedule the caller caches per topology. */
     const int32_t* row_order;
     /* Optional (may be NULL): the live slots listed column block by column
-     * block (then by row, then by column), with each entry's row, and the
-     * number of entries. slk_sddmm's windowed kernel then visits the slots in
-     * that order, so the waves resident at one moment gather from one band of
-     * X rows; results are the same either way. A schedule the caller caches
-     * per topology. */
+     * block (then by row, then by column), with each entry's row, the number
+     * of entries and the block width in columns (slk_slot_list_build's
+     * block_cols; 0 if unknown). slk_sddmm then visits the slots in that
+     * order, so the waves resident at one moment gather from one band of X
+     * rows, and with a block of at most 128 columns it stages each
+     * workgroup's X and dY rows in LDS; results are the same either way. A
+     * schedule the caller caches per topology. */
     const int32_t* slot_list;
     const int32_t* slot_list_row;
     int64_t n_slot_list;
+    int64_t slot_list_block;
 } slk_csr;
 
 /* Thread-local description of the last failure of this thread ("" if none). */

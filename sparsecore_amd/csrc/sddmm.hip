@@ -384,6 +384,214 @@ __global__ __launch_bounds__(kBlock) void sddmm_simd_win_kernel(
     }
 }
 
+// SIMD order over a slot list, both operands from LDS (16-byte path).
+//
+// The windowed kernel above runs at the rate its per-lane X gathers issue
+// (about one 1 KB wave load per 20 cycles per CU from L2). A slot list built
+// with a narrow column block (C = 64 or 128 columns) allows more: a workgroup takes
+// 256 consecutive list entries, which lie in one column block and a short run
+// of rows, and for every 64-float window it stages the block's C rows of X and
+// the run's dY rows (at most 64) in LDS, once per workgroup; every lane then
+// reads both of its slot's pieces from LDS, whose read rate is several times
+// the gather rate. Each staged row is padded by four 16-byte pieces (a row
+// then starts 16 banks after the previous one, the width of one slot's four
+// lanes), which measured 2-7% faster than a one-piece pad. Staging goes through
+// registers a window ahead (loads of window w+1 in flight while window w is
+// computed), with a barrier before and after each store. An entry whose column
+// lies outside the block or whose row lies outside the staged run (a
+// workgroup that straddles two blocks) reads that operand from global memory.
+// Per slot, the arithmetic is sddmm_simd_kernel's: the 16 running sums advance
+// in step order across the windows, then the same combine and scalar tail.
+// Where it pays (measured): layers whose X is far larger than the L2s, where
+// the windowed kernel streams from HBM (16384x16384 at N=4096: 16.2 -> 11.9 ms
+// at 95% sparsity with 128-column blocks, 5.0 -> 3.9 ms at 99% with 64). With
+// an L2-resident X (the 60M-GPT layers) the windowed kernel, which splits the
+// operands between the gather path and LDS, stays 10-60% faster. The caller
+// picks by the block width it builds the list with.
+constexpr int kTileWaves = 4;
+constexpr int kTileThreads = kTileWaves * kWave;
+constexpr int kTileG = 4;                                     // groups of 16 slots per wave
+constexpr int kTileEntries = kTileWaves * kTileG * kSlotsPerWave;  // 256 list entries
+constexpr int kTileWin = 64;                                  // floats per window (4 steps)
+constexpr int kTilePieces = kTileWin / 4;                     // 16-byte pieces per row
+constexpr int kTileStride = kTilePieces + 4;                  // pieces per LDS row (padded)
+constexpr int kTileRows = 64;                                 // staged dY rows at most
+constexpr int kTileRowsPerPass = kTileThreads / kTilePieces;  // 16 staged rows per pass
+constexpr int kTileMaxC = 128;                                // column block width at most
+
+template <int C>
+__global__ __launch_bounds__(kTileThreads) void sddmm_tile_kernel(
+    int64_t M, int64_t K, int64_t N, const int32_t* __restrict__ row_start,
+    const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ row_cap,
+    const int32_t* __restrict__ col, const float* __restrict__ dY, const float* __restrict__ X,
+    float* __restrict__ dW, float* __restrict__ dbias, const int32_t* __restrict__ slot_list,
+    const int32_t* __restrict__ slot_row, int64_t n_list, int64_t tile_blocks) {
+    constexpr int kLoads = (C + kTileRows) / kTileRowsPerPass;  // staged pieces per thread
+    __shared__ f32x4 xs[C * kTileStride];          // X rows c_lo .. c_lo + C - 1
+    __shared__ f32x4 ds[kTileRows * kTileStride];  // dY rows r_lo .. r_lo + 63
+    __shared__ int32_t s_rhi[kTileWaves];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wv = threadIdx.x >> 6;
+    const int g = lane >> 2;
+    const int q = lane & 3;
+    if (static_cast<int64_t>(blockIdx.x) >= tile_blocks) {  // block-uniform: per-row waves
+        const int64_t row = (static_cast<int64_t>(blockIdx.x) - tile_blocks) * kTileWaves + wv;
+        zero_row_padding(row_start, row_nnz, row_cap, M, row, dW);
+        if (dbias != nullptr) bias_row_sum(dY, M, N, row, dbias, N, 1);
+        return;
+    }
+    const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kTileEntries;  // < n_list
+    const int32_t c_lo = col[slot_list[e0]] / C * C;
+    const int32_t r_lo = slot_row[e0];
+
+    int32_t slot[kTileG], row[kTileG], cv[kTileG];
+    bool in[kTileG];
+    int32_t rmax = -1;
+#pragma unroll
+    for (int k = 0; k < kTileG; ++k) {
+        const int64_t e = e0 + (wv * kTileG + k) * kSlotsPerWave + g;
+        in[k] = e < n_list;
+        slot[k] = in[k] ? slot_list[e] : 0;
+        row[k] = in[k] ? slot_row[e] : 0;
+        cv[k] = in[k] ? col[slot[k]] : -1;
+        // rows ascend within a column block: the run ends at c_lo's block's last entry
+        if (in[k] && cv[k] >= c_lo && cv[k] < c_lo + C) rmax = max(rmax, row[k]);
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) rmax = max(rmax, __shfl_xor(rmax, off));
+    if (lane == 0) s_rhi[wv] = rmax;
+    __syncthreads();
+    int32_t rhi = s_rhi[0];
+#pragma unroll
+    for (int w = 1; w < kTileWaves; ++w) rhi = max(rhi, s_rhi[w]);
+    const int32_t nR = min(kTileRows, max(0, rhi - r_lo + 1));
+    const int32_t nC = static_cast<int32_t>(min<int64_t>(C, K - c_lo));
+
+    // LDS piece offsets of each entry's operands; outsiders read global memory
+    int32_t xo[kTileG], dO[kTileG];
+    bool xdir[kTileG], ddir[kTileG];
+    bool any_direct = false;
+#pragma unroll
+    for (int k = 0; k < kTileG; ++k) {
+        const int32_t xr = cv[k] - c_lo, dr = row[k] - r_lo;
+        xdir[k] = in[k] && !(xr >= 0 && xr < nC);
+        ddir[k] = in[k] && !(dr >= 0 && dr < nR);
+        xo[k] = (xdir[k] || !in[k] ? 0 : xr) * kTileStride + q;
+        dO[k] = (ddir[k] || !in[k] ? 0 : dr) * kTileStride + q;
+        any_direct |= __ballot(xdir[k] || ddir[k]) != 0;
+    }
+
+    // staging: thread t copies piece (t mod 16) of staged rows t/16 + 16i;
+    // rows 0..C-1 of the stage are X rows c_lo.., rows C..C+63 dY rows r_lo..
+    // (i < C/16 picks X), each 16·N floats after the previous one
+    const int pc = threadIdx.x % kTilePieces;
+    const int rr0 = threadIdx.x / kTilePieces;
+    const float* xsrc = X + static_cast<int64_t>(c_lo + rr0) * N + 4 * pc;
+    const float* dsrc = dY + static_cast<int64_t>(r_lo + rr0) * N + 4 * pc;
+    const int64_t rstep = static_cast<int64_t>(kTileRowsPerPass) * N;
+    uint32_t smask = 0;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+        const int rr = rr0 + i * kTileRowsPerPass;
+        if (rr < C ? rr < nC : rr - C < nR) smask |= 1u << i;
+    }
+    const int64_t n16 = (N / 16) * 16;
+    const int64_t nwin = ceil_div(n16, kTileWin);
+    float acc[kTileG][4];
+#pragma unroll
+    for (int k = 0; k < kTileG; ++k) acc[k][0] = acc[k][1] = acc[k][2] = acc[k][3] = 0.f;
+    f32x4 pre[kLoads];
+    auto fetch = [&](int64_t w) {
+        const int64_t j = w * kTileWin;
+        if (j + 4 * pc < n16) {
+#pragma unroll
+            for (int i = 0; i < kLoads; ++i) {
+                const float* p = i < C / kTileRowsPerPass
+                                     ? xsrc + i * rstep
+                                     : dsrc + (i - C / kTileRowsPerPass) * rstep;
+                if (smask & (1u << i)) pre[i] = *reinterpret_cast<const f32x4*>(p + j);
+            }
+        }
+    };
+    if (nwin > 0) fetch(0);
+    for (int64_t w = 0; w < nwin; ++w) {
+        if (w > 0) __syncthreads();  // every lane has read window w-1
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+            const int rr = rr0 + i * kTileRowsPerPass;
+            if (smask & (1u << i)) {
+                if (rr < C) xs[rr * kTileStride + pc] = pre[i];
+                else ds[(rr - C) * kTileStride + pc] = pre[i];
+            }
+        }
+        __syncthreads();
+        if (w + 1 < nwin) fetch(w + 1);
+        const int tn = static_cast<int>(min<int64_t>(kTileWin / 16, n16 / 16 - w * (kTileWin / 16)));
+#pragma unroll
+        for (int k = 0; k < kTileG; ++k) {
+            if (!in[k]) continue;
+            if (!any_direct && tn == kTileWin / 16) {
+#pragma unroll
+                for (int t = 0; t < kTileWin / 16; ++t)
+                    fma4x(ds[dO[k] + 4 * t], xs[xo[k] + 4 * t], acc[k][0], acc[k][1], acc[k][2],
+                          acc[k][3]);
+                // one group's 8 reads in flight at a time: hoisting all groups'
+                // reads ahead of their fmas would take 128 registers
+                __builtin_amdgcn_sched_barrier(0);
+            } else {
+                const int64_t j = w * kTileWin + 4 * q;
+                const float* xg = X + static_cast<int64_t>(cv[k]) * N + j;
+                const float* dg = dY + static_cast<int64_t>(row[k]) * N + j;
+                for (int t = 0; t < tn; ++t) {
+                    // LDS pieces read unconditionally, then replaced (see the
+                    // windowed kernel on mixing LDS and global loads)
+                    f32x4 d = ds[dO[k] + 4 * t];
+                    f32x4 x = xs[xo[k] + 4 * t];
+                    if (ddir[k]) d = *reinterpret_cast<const f32x4*>(dg + 16 * t);
+                    if (xdir[k]) x = *reinterpret_cast<const f32x4*>(xg + 16 * t);
+                    fma4x(d, x, acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+                }
+            }
+        }
+    }
+    // a[l] = v[l] + v[l+8]: lanes q=0,1 take the partner q^2 (v[8..15]).
+#pragma unroll
+    for (int k = 0; k < kTileG; ++k) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[k][e] = acc[k][e] + __shfl_xor(acc[k][e], 2);
+    }
+    int64_t jt = n16;
+    if (N - n16 >= 8) {
+        if (q < 2) {
+            const int64_t j = n16 + 4 * q;
+#pragma unroll
+            for (int k = 0; k < kTileG; ++k) {
+                if (in[k]) {
+                    fma4x(*reinterpret_cast<const f32x4*>(dY + static_cast<int64_t>(row[k]) * N + j),
+                          *reinterpret_cast<const f32x4*>(X + static_cast<int64_t>(cv[k]) * N + j),
+                          acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+                }
+            }
+        }
+        jt += 8;
+    }
+    // s4[k] = a[k] + a[k+4]: lane q=0 holds a[0..3], lane q=1 holds a[4..7].
+#pragma unroll
+    for (int k = 0; k < kTileG; ++k) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[k][e] = acc[k][e] + __shfl_xor(acc[k][e], 1);
+    }
+    if (q == 0) {
+#pragma unroll
+        for (int k = 0; k < kTileG; ++k) {
+            if (!in[k]) continue;
+            const float rsum = (acc[k][0] + acc[k][2]) + (acc[k][1] + acc[k][3]);
+            dW[slot[k]] = running_sum(dY + static_cast<int64_t>(row[k]) * N + jt,
+                                      X + static_cast<int64_t>(cv[k]) * N + jt, N - jt, rsum);
+        }
+    }
+}
+
 __global__ __launch_bounds__(kBlock) void sddmm_scalar_kernel(
     int64_t M, int64_t N, int64_t cap_total,
     const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
@@ -470,6 +678,26 @@ int sddmm_impl(const slk_csr* W, const float* dY, int64_t dY_rows, const float* 
 #define SLK_SDDMM_WIN_ARGS                                                                   \
     SLK_SDDMM_ARGS, W->row_capacity, listed ? W->slot_list : nullptr,                         \
         listed ? W->slot_list_row : nullptr, space
+    // A slot list in blocks of 64 or 128 columns: both operands through LDS.
+    const char* tile_env = std::getenv("SLK_SDDMM_TILE");  // "0": the windowed kernel
+    const int64_t cb = W->slot_list_block;
+    if (listed && v4 && (cb == 64 || cb == kTileMaxC) && (tile_env == nullptr || tile_env[0] != '0')) {
+        const int64_t tile_blocks = ceil_div(W->n_slot_list, int64_t{kTileEntries});
+        const int64_t tblocks = tile_blocks + ceil_div(W->nrows, int64_t{kTileWaves});
+        if (tblocks > INT32_MAX) return fail(SLK_EINVAL, std::string(who) + ": problem too large");
+#define SLK_TILE_ARGS                                                                        \
+    W->nrows, W->ncols, N, W->row_start, W->row_nnz, W->row_capacity, W->col_indices, dY, X, \
+        dW, dbias, W->slot_list, W->slot_list_row, W->n_slot_list, tile_blocks
+        if (cb == 64) {
+            hipLaunchKernelGGL(sddmm_tile_kernel<64>, dim3(static_cast<unsigned>(tblocks)),
+                               dim3(kTileThreads), 0, st, SLK_TILE_ARGS);
+        } else {
+            hipLaunchKernelGGL(sddmm_tile_kernel<128>, dim3(static_cast<unsigned>(tblocks)),
+                               dim3(kTileThreads), 0, st, SLK_TILE_ARGS);
+        }
+#undef SLK_TILE_ARGS
+        return check_launch(who);
+    }
     // A slot list has short row runs per column block: stage four rows per group.
     if (G == 2 && !listed) {
         hipLaunchKernelGGL((sddmm_simd_win_kernel<2, 2>), grid, dim3(kBlock), 0, st, SLK_SDDMM_WIN_ARGS);

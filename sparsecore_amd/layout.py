@@ -365,7 +365,7 @@ class PaddedCSR:
             lst, lrow = _lib.slot_list_build(base, int(block_cols), self._nnz, self.device)
             fields = {f: getattr(base, f) for f, _ in _lib.CsrView._fields_}
             fields.update(slot_list=_lib.ptr(lst), slot_list_row=_lib.ptr(lrow),
-                          n_slot_list=int(lst.numel()))
+                          n_slot_list=int(lst.numel()), slot_list_block=int(block_cols))
             self._slist = (key, _lib.CsrView(**fields), lst, lrow)
         return self._slist[1]
 

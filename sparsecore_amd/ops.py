@@ -81,6 +81,21 @@ _SLOT_LIST_MIN_NNZ = 150_000
 _SLOT_LIST_MIN_X_BYTES = 16 << 20
 
 
+_TILE_MIN_X_BYTES = 128 << 20
+
+
+def _slot_block(W: PaddedCSR, K: int, N: int) -> int:
+    """Column-block width of the slot list. Where X (K x N) is far larger than
+    the L2s, 128 or 64 columns: slk_sddmm then stages each workgroup's X and
+    dY rows in LDS (measured 23-27% faster on the 16384x16384 layers; 128
+    where a block row holds >= 4 slots, else 64). Otherwise a wider block for
+    the windowed kernel, which only needs the X band to stay in L2."""
+    if 4 * K * N >= _TILE_MIN_X_BYTES:
+        density = W.nnz / max(1, W.nrows * W.ncols)
+        return 128 if density * 128 >= 4 else 64
+    return min(1024, max(256, N // 32))
+
+
 def _sddmm_view(W: PaddedCSR, X: torch.Tensor):
     """W's view for slk_sddmm: with a slot list where it pays (see above);
     SLK_SLOT_BLOCK=<cols> forces a list with that block width, 0 none."""
@@ -89,7 +104,7 @@ def _sddmm_view(W: PaddedCSR, X: torch.Tensor):
     if forced is not None:
         return W._view_listed(int(forced)) if int(forced) > 0 else W._view()
     if W.nnz >= _SLOT_LIST_MIN_NNZ and 4 * K * N >= _SLOT_LIST_MIN_X_BYTES and N >= 1024:
-        return W._view_listed(min(1024, max(64, N // 32)))
+        return W._view_listed(_slot_block(W, K, N))
     return W._view()
 
 

@@ -582,6 +582,38 @@ def test_slot_list_build_rejects_bad_arguments(dev):
     assert rc != 0 and b"workspace" in lib.slk_last_error()
 
 
+@pytest.mark.parametrize("block", [64, 128])
+@pytest.mark.parametrize("M,K,density,N", [
+    (200, 256, 0.5, 1024),    # dense rows: a workgroup's entries span a few rows
+    (3000, 300, 0.02, 1100),  # sparse rows: runs longer than the 64 staged dY rows
+    (700, 200, 0.1, 1032),    # partial last window, 8-wide step
+    (500, 130, 0.2, 1045),    # scalar tail, a last block narrower than the block width
+])
+def test_sddmm_tile_kernel_bit_exact(dev, block, M, K, density, N):
+    """slk_sddmm on a slot list with 64- or 128-column blocks stages X and dY
+    rows in LDS per workgroup: the bits are the oracle's, including workgroups
+    that straddle two column blocks (X from global memory), rows outside the
+    staged run (dY from global memory), empty rows and the fused bias gradient."""
+    print(f"[dW tile] block={block} M={M} K={K} d={density} N={N}", flush=True)
+    c = oracle.zipf_rows(M, K, density, 0.6, seed=M + N, sigma=0.5)
+    c.row_nnz[M // 3] = 0
+    c.col_indices[c.row_start[M // 3]:c.row_start[M // 3] + c.row_capacity[M // 3]] = -1
+    rng = np.random.default_rng(N)
+    X_np = rng.standard_normal((K, N)).astype(np.float32)
+    dY_np = rng.standard_normal((M, N)).astype(np.float32)
+    W = from_oracle(c, dev)
+    X, dY = _t(X_np, dev), _t(dY_np, dev)
+    view = W._view_listed(block)
+    assert view.slot_list_block == block
+    dW = torch.full((W.total_capacity,), float("nan"), device=dev)
+    db = torch.full((M,), float("nan"), device=dev)
+    _lib.sddmm(view, dY, X, dW, _lib.SLK_DW_SIMD, db)
+    assert_bits_equal(dW.cpu().numpy(), oracle.sddmm(c, dY_np, X_np), "dW tile")
+    db_ref = torch.empty(M, device=dev)
+    _lib.sddmm(W._view(), dY, X, torch.empty_like(dW), _lib.SLK_DW_SIMD, db_ref)
+    assert torch.equal(db, db_ref)
+
+
 @pytest.mark.parametrize("G", [2, 4])
 @pytest.mark.parametrize("block", [1, 7, 64, 1000])
 def test_sddmm_slot_list_order_bit_exact(dev, monkeypatch, G, block):
