@@ -297,9 +297,11 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_group_kernel(
 //
 // spmm_lds_kernel — for large problems, where every X element is used by
 // several rows of a workgroup. A workgroup of 16 waves owns R = 16·RW rows x
-// 256 columns of Y: each lane holds 4 adjacent columns of RW rows in
-// registers. X is streamed through LDS in chunks of kLdsK rows x 256 columns
-// (1 KB per X row), double-buffered: chunk c+1 is loaded into registers while
+// 256·H columns of Y: each lane holds 4 adjacent columns of each of H
+// 256-column halves for RW rows in registers (H = 2 halves the readlane,
+// address and loop work per fma; measured 5-17% faster on the denser GPT
+// layers). X is streamed through LDS in chunks of 64/H rows x 256·H columns
+// (1 KB per X row and half), double-buffered: chunk c+1 is loaded into registers while
 // chunk c is read from LDS and is then written to the other buffer, so one
 // barrier per chunk orders both. For each chunk every row consumes its slots
 // whose column falls in the chunk; columns ascend within a row, so walking
@@ -336,25 +338,33 @@ __device__ __forceinline__ void fma4(float v, const f32x4& x, f32x4& acc) {
     acc[3] = __builtin_fmaf(v, x[3], acc[3]);
 }
 
-template <int RW>
+template <int RW, int H>
 __global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
     int64_t M, int64_t K, int64_t N, int64_t nrowblk, const int32_t* __restrict__ row_start,
     const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ col,
     const float* __restrict__ val, const float* __restrict__ X, const float* __restrict__ bias,
     float* __restrict__ Y) {
-    __shared__ f32x4 xs[2][kLdsK][kWave];  // 128 KiB
+    // H halves of 256 columns per workgroup, each lane 4 columns of each half;
+    // chunks of KC X rows keep the double buffer at 128 KiB
+    constexpr int KC = kLdsK / H;
+    __shared__ f32x4 xs[2][KC][H][kWave];  // 128 KiB
     const int lane = threadIdx.x & (kWave - 1);
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t lb = xcd_logical_block(blockIdx.x, gridDim.x);
     const int64_t tile = lb / nrowblk;  // tile-major: a tile's row blocks share X chunks in L2
     const int64_t rb = lb - tile * nrowblk;
-    const int64_t n = tile * kLdsCols + 4 * lane;
-    const bool n_ok = n < N;  // N % 4 == 0 for this kernel
+    int64_t n[H];
+    bool n_ok[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+        n[h] = tile * (H * kLdsCols) + h * kLdsCols + 4 * lane;
+        n_ok[h] = n[h] < N;  // N % 4 == 0 for this kernel
+    }
     const int64_t r0 = rb * (kLdsWaves * RW) + w;
 
     int32_t pos[RW], end[RW], base[RW], mc[RW], nmc[RW];
     float mv[RW], nmv[RW];
-    f32x4 acc[RW];
+    f32x4 acc[RW][H];
 #pragma unroll
     for (int j = 0; j < RW; ++j) {
         const int64_t row = r0 + static_cast<int64_t>(kLdsWaves) * j;
@@ -364,54 +374,69 @@ __global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
         end[j] = e;
         lds_window(col, val, s, e, lane, mc[j], mv[j]);
         lds_window(col, val, s + kWave, e, lane, nmc[j], nmv[j]);
-        acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int h = 0; h < H; ++h) acc[j][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    // thread t stages chunk rows (t / 64) + 16i, i < kLdsStage, at its 4 columns
-    const int krow = threadIdx.x >> 6;
+    // thread t stages piece t + 1024i (i < kLdsStage) of the chunk: X row
+    // p / (64H), half (p / 64) mod H, lane p mod 64
     f32x4 pre[kLdsStage];
     auto prefetch = [&](int64_t k0) {
 #pragma unroll
         for (int i = 0; i < kLdsStage; ++i) {
-            const int64_t k = k0 + krow + i * kLdsWaves;
-            pre[i] = (k < K && n_ok) ? *reinterpret_cast<const f32x4*>(X + k * N + n)
-                                     : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            const int p = threadIdx.x + i * kLdsThreads;
+            const int kr = p / (H * kWave);
+            const int h = (p / kWave) % H;
+            const int64_t k = k0 + kr;
+            const int64_t nn = tile * (H * kLdsCols) + h * kLdsCols + 4 * (p % kWave);
+            pre[i] = (k < K && nn < N) ? *reinterpret_cast<const f32x4*>(X + k * N + nn)
+                                       : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
     };
     auto stage = [&](int b) {
 #pragma unroll
-        for (int i = 0; i < kLdsStage; ++i) xs[b][krow + i * kLdsWaves][lane] = pre[i];
+        for (int i = 0; i < kLdsStage; ++i) {
+            const int p = threadIdx.x + i * kLdsThreads;
+            xs[b][p / (H * kWave)][(p / kWave) % H][p % kWave] = pre[i];
+        }
     };
-    const int64_t nchunks = ceil_div(K, kLdsK);
+    const int64_t nchunks = ceil_div(K, KC);
     prefetch(0);
     stage(0);
     __syncthreads();
     for (int64_t ch = 0; ch < nchunks; ++ch) {
         const int b = static_cast<int>(ch & 1);
         const bool more = ch + 1 < nchunks;
-        if (more) prefetch((ch + 1) * kLdsK);
-        const int32_t k0 = static_cast<int32_t>(ch * kLdsK);
-        const int32_t k1 = k0 + kLdsK;
+        if (more) prefetch((ch + 1) * KC);
+        const int32_t k0 = static_cast<int32_t>(ch * KC);
+        const int32_t k1 = k0 + KC;
 #pragma unroll
         for (int j = 0; j < RW; ++j) {
             int32_t first = pos[j] - base[j];
             while (true) {
                 const int32_t cnt = __popcll(__ballot(lane >= first && mc[j] < k1));
                 int32_t k = 0;
-                for (; k + 4 <= cnt; k += 4) {  // four LDS reads in flight
+                for (; k + 4 <= cnt; k += 4) {  // four slots' LDS reads in flight
                     const int32_t s0 = first + k;
-                    const f32x4 x0 = xs[b][bcast_i(mc[j], s0) - k0][lane];
-                    const f32x4 x1 = xs[b][bcast_i(mc[j], s0 + 1) - k0][lane];
-                    const f32x4 x2 = xs[b][bcast_i(mc[j], s0 + 2) - k0][lane];
-                    const f32x4 x3 = xs[b][bcast_i(mc[j], s0 + 3) - k0][lane];
-                    fma4(bcast_f(mv[j], s0), x0, acc[j]);
-                    fma4(bcast_f(mv[j], s0 + 1), x1, acc[j]);
-                    fma4(bcast_f(mv[j], s0 + 2), x2, acc[j]);
-                    fma4(bcast_f(mv[j], s0 + 3), x3, acc[j]);
+                    const int32_t c0 = bcast_i(mc[j], s0) - k0, c1 = bcast_i(mc[j], s0 + 1) - k0;
+                    const int32_t c2 = bcast_i(mc[j], s0 + 2) - k0, c3 = bcast_i(mc[j], s0 + 3) - k0;
+#pragma unroll
+                    for (int h = 0; h < H; ++h) {
+                        const f32x4 x0 = xs[b][c0][h][lane];
+                        const f32x4 x1 = xs[b][c1][h][lane];
+                        const f32x4 x2 = xs[b][c2][h][lane];
+                        const f32x4 x3 = xs[b][c3][h][lane];
+                        fma4(bcast_f(mv[j], s0), x0, acc[j][h]);
+                        fma4(bcast_f(mv[j], s0 + 1), x1, acc[j][h]);
+                        fma4(bcast_f(mv[j], s0 + 2), x2, acc[j][h]);
+                        fma4(bcast_f(mv[j], s0 + 3), x3, acc[j][h]);
+                    }
                 }
                 for (; k < cnt; ++k) {
-                    const int32_t c0 = bcast_i(mc[j], first + k);
-                    fma4(bcast_f(mv[j], first + k), xs[b][c0 - k0][lane], acc[j]);
+                    const int32_t c0 = bcast_i(mc[j], first + k) - k0;
+                    const float v = bcast_f(mv[j], first + k);
+#pragma unroll
+                    for (int h = 0; h < H; ++h) fma4(v, xs[b][c0][h][lane], acc[j][h]);
                 }
                 pos[j] += cnt;
                 if (first + cnt < kWave) break;  // the run ended inside this window
@@ -426,20 +451,22 @@ __global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
         if (more) stage(b ^ 1);
         __syncthreads();
     }
-    if (n_ok) {
 #pragma unroll
-        for (int j = 0; j < RW; ++j) {
-            const int64_t row = r0 + static_cast<int64_t>(kLdsWaves) * j;
-            if (row < M) {
-                if (bias != nullptr) {
-                    const float bb = bias[row];
-                    acc[j][0] = acc[j][0] + bb;
-                    acc[j][1] = acc[j][1] + bb;
-                    acc[j][2] = acc[j][2] + bb;
-                    acc[j][3] = acc[j][3] + bb;
-                }
-                *reinterpret_cast<f32x4*>(Y + row * N + n) = acc[j];
+    for (int j = 0; j < RW; ++j) {
+        const int64_t row = r0 + static_cast<int64_t>(kLdsWaves) * j;
+        if (row >= M) continue;
+        const float bb = bias != nullptr ? bias[row] : 0.0f;
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+            if (!n_ok[h]) continue;
+            f32x4 a = acc[j][h];
+            if (bias != nullptr) {
+                a[0] = a[0] + bb;
+                a[1] = a[1] + bb;
+                a[2] = a[2] + bb;
+                a[3] = a[3] + bb;
             }
+            *reinterpret_cast<f32x4*>(Y + row * N + n[h]) = a;
         }
     }
 }
@@ -450,21 +477,23 @@ int launch_blocks(int64_t waves, int64_t* blocks) {
     return SLK_OK;
 }
 
-template <int RW>
+template <int RW, int H = 1>
 int launch_lds_rw(const slk_csr* W, const float* X, int64_t N, const float* bias, float* Y,
                   hipStream_t st) {
     const int64_t M = W->nrows;
     const int64_t nrowblk = ceil_div(M, int64_t{kLdsWaves} * RW);
-    const int64_t blocks = nrowblk * ceil_div(N, kLdsCols);
+    const int64_t blocks = nrowblk * ceil_div(N, int64_t{kLdsCols} * H);
     if (blocks > INT32_MAX) return fail(SLK_EINVAL, "spmm: problem too large for one launch");
-    hipLaunchKernelGGL((spmm_lds_kernel<RW>), dim3(static_cast<unsigned>(blocks)),
+    hipLaunchKernelGGL((spmm_lds_kernel<RW, H>), dim3(static_cast<unsigned>(blocks)),
                        dim3(kLdsThreads), 0, st, M, W->ncols, N, nrowblk, W->row_start,
                        W->row_nnz, W->col_indices, W->values, X, bias, Y);
     return check_launch("spmm");
 }
 
-int launch_lds(int rw, const slk_csr* W, const float* X, int64_t N, const float* bias, float* Y,
-               hipStream_t st) {
+int launch_lds(int h, int rw, const slk_csr* W, const float* X, int64_t N, const float* bias,
+               float* Y, hipStream_t st) {
+    if (h == 2) return rw == 2 ? launch_lds_rw<2, 2>(W, X, N, bias, Y, st)
+                               : launch_lds_rw<4, 2>(W, X, N, bias, Y, st);
     switch (rw) {
         case 2: return launch_lds_rw<2>(W, X, N, bias, Y, st);
         case 4: return launch_lds_rw<4>(W, X, N, bias, Y, st);
@@ -513,13 +542,26 @@ int launch_group_L(int L, const slk_csr* W, const float* X, int64_t N, const flo
 
 // Waves worth launching: enough to give every CU several to switch between.
 constexpr int64_t kTargetWaves = 4096;
-// LDS kernel thresholds (measured on the C3/C4/C5 layer shapes): N from which
-// it is considered, workgroups needed to keep the chip evenly busy (one per
-// CU at a time: 128 KiB of LDS each), and expected uses of each staged X
-// element below which direct gathers are as fast.
+// LDS kernel: N from which it is considered, and expected uses of each staged
+// X element (density x rows per workgroup) below which direct gathers are as
+// fast (both measured on the C3/C4/C5 layer shapes).
 constexpr int64_t kLdsMinN = 1024;
-constexpr int64_t kLdsMinBlocks = 512;
 constexpr double kLdsMinReuse = 4.0;
+constexpr int64_t kCUs = 256;  // MI355X; one LDS-kernel workgroup per CU at a time
+
+// Estimated time of the LDS kernel with H halves of 256 columns per lane and
+// RW rows per wave: rounds of workgroups x X chunks x (barrier + rows x (row
+// overhead + expected slots per row and chunk x per-slot cost)). The constants
+// (40, 2, 4 and 6 per slot) were fitted to the measured times of all five
+// configurations on the 10M- and 60M-GPT and 16384^2 layer shapes, forward and
+// transpose, where the choice they give is the fastest measured in every case.
+double lds_cost(int64_t M, int64_t K, int64_t N, double density, int h, int rw) {
+    const int64_t kc = kLdsK / h;
+    const int64_t blocks = ceil_div(M, int64_t{kLdsWaves} * rw) * ceil_div(N, int64_t{kLdsCols} * h);
+    const double rounds = static_cast<double>(ceil_div(blocks, kCUs));
+    const double chunks = static_cast<double>(ceil_div(K, kc));
+    return rounds * chunks * (40.0 + rw * (2.0 + density * kc * (h == 1 ? 4.0 : 6.0)));
+}
 
 // Y = W·X (+ bias per row): the shared body of slk_spmm and slk_spmm_bias.
 // Y^T for slk_spmm_t: one-row-per-wave kernel, one float per lane, each
@@ -557,20 +599,24 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
 
     // Kernel choice. The LDS-staged kernel needs 16-byte lanes (N % 4 == 0,
     // aligned X and Y) and pays off when each staged X element feeds several
-    // rows of a workgroup: expected uses = density x rows per workgroup. The
-    // per-wave gather kernels cover everything else (small N is latency-bound).
-    // SLK_SPMM_KERNEL=lds|wave and SLK_SPMM_RW=2|4|8 override the choice.
+    // rows of a workgroup: expected uses = density x rows per workgroup. Among
+    // the configurations that pass that bar, lds_cost picks one. The per-wave
+    // gather kernels cover everything else (small N is latency-bound).
+    // SLK_SPMM_KERNEL=lds|wave, SLK_SPMM_H=1|2 and SLK_SPMM_RW=2|4|8 override.
     const bool lds_ok = N % 4 == 0 && align % 16 == 0;
-    int rw = 0;
+    int rw = 0, h = 1;
     if (lds_ok && N >= kLdsMinN) {
         const double density =
             K > 0 ? static_cast<double>(W->total_capacity) / (1.2 * M * K) : 0.0;
-        const int64_t tiles = ceil_div(N, kLdsCols);
-        for (int cand : {8, 4, 2}) {
-            const int64_t blocks = ceil_div(M, int64_t{kLdsWaves} * cand) * tiles;
-            if (blocks >= kLdsMinBlocks && density * kLdsWaves * cand >= kLdsMinReuse) {
-                rw = cand;
-                break;
+        double best = 0.0;
+        for (const int cfg : {18, 14, 12, 24, 22}) {  // h * 10 + rw
+            const int ch = cfg / 10, crw = cfg % 10;
+            if (density * kLdsWaves * crw < kLdsMinReuse) continue;
+            const double c = lds_cost(M, K, N, density, ch, crw);
+            if (rw == 0 || c < best) {
+                best = c;
+                rw = crw;
+                h = ch;
             }
         }
     }
@@ -578,10 +624,12 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
         if (e[0] == 'w') rw = 0;
         if (e[0] == 'l' && lds_ok && rw == 0) rw = 8;
     }
-    if (const char* e = std::getenv("SLK_SPMM_RW")) {
-        if (rw != 0) rw = std::atoi(e);
+    if (rw != 0) {
+        if (const char* e = std::getenv("SLK_SPMM_H")) h = e[0] == '2' ? 2 : 1;
+        if (const char* e = std::getenv("SLK_SPMM_RW")) rw = std::atoi(e);
+        if (h == 2 && rw == 8) rw = 4;  // no 8-row variant with 8 columns per lane
+        return launch_lds(h, rw, W, X, N, bias, Y, st);
     }
-    if (rw != 0) return launch_lds(rw, W, X, N, bias, Y, st);
 
     int vec = 1;
     if (const char* e = std::getenv("SLK_SPMM_VEC")) vec = std::atoi(e);

@@ -126,18 +126,20 @@ def test_spmm_every_vector_width(dev, monkeypatch, vec, N, per_row):
     assert_bits_equal(_spmm(W, _t(X_np, dev)).cpu().numpy(), oracle.spmm(c, X_np), "Y")
 
 
-@pytest.mark.parametrize("rw", [2, 4, 8])
+@pytest.mark.parametrize("h,rw", [(1, 2), (1, 4), (1, 8), (2, 2), (2, 4)])
 @pytest.mark.parametrize("M,K,N,per_row", [
     (1, 1, 4, 1), (63, 127, 64, 40), (64, 128, 256, 128), (65, 129, 260, 100),
     (200, 300, 1000, 37), (130, 1000, 200, 700), (70, 5000, 96, 3000), (33, 260, 132, 0),
-    (9, 64, 256, 64), (300, 64, 512, 64)])
-def test_spmm_lds_kernel_bit_exact(dev, monkeypatch, rw, M, K, N, per_row):
-    """The LDS-staged kernel (forced, each rows-per-wave variant): partial row
-    blocks and column tiles, K not a multiple of the chunk, rows with more than
-    64 slots in one chunk (fully dense rows), empty rows."""
+    (9, 64, 256, 64), (300, 64, 512, 64), (40, 100, 520, 50)])
+def test_spmm_lds_kernel_bit_exact(dev, monkeypatch, h, rw, M, K, N, per_row):
+    """The LDS-staged kernel (forced, each columns-per-lane and rows-per-wave
+    variant): partial row blocks and column tiles (one half of a two-half tile
+    past N), K not a multiple of the chunk, rows with more slots in one chunk
+    than the chunk's rows (fully dense rows), empty rows."""
     monkeypatch.setenv("SLK_SPMM_KERNEL", "lds")
+    monkeypatch.setenv("SLK_SPMM_H", str(h))
     monkeypatch.setenv("SLK_SPMM_RW", str(rw))
-    print(f"[lds rw={rw}] M={M} K={K} N={N} per_row={per_row}", flush=True)
+    print(f"[lds h={h} rw={rw}] M={M} K={K} N={N} per_row={per_row}", flush=True)
     c, X_np, _ = _case(M, K, N, per_row, seed=M + K + N)
     W = from_oracle(c, dev)
     assert_bits_equal(_spmm(W, _t(X_np, dev)).cpu().numpy(), oracle.spmm(c, X_np), "Y")
@@ -146,7 +148,8 @@ def test_spmm_lds_kernel_bit_exact(dev, monkeypatch, rw, M, K, N, per_row):
 @pytest.mark.parametrize("env,N", [
     ({"SLK_SPMM_VEC": "1"}, 300), ({"SLK_SPMM_VEC": "2"}, 300), ({"SLK_SPMM_VEC": "4"}, 1024),
     ({}, 5), ({}, 40), ({"SLK_SPMM_KERNEL": "lds"}, 132),
-    ({"SLK_SPMM_KERNEL": "lds", "SLK_SPMM_RW": "2"}, 1024)])
+    ({"SLK_SPMM_KERNEL": "lds", "SLK_SPMM_RW": "2"}, 1024),
+    ({"SLK_SPMM_KERNEL": "lds", "SLK_SPMM_H": "2", "SLK_SPMM_RW": "4"}, 1032)])
 def test_spmm_bias_epilogue_bit_exact(dev, monkeypatch, env, N):
     """slk_spmm_bias = slk_spmm followed by one float32 add of bias[i] per row,
     in every kernel (wave kernel at each lane width, packed narrow-N kernel,
