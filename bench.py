@@ -377,12 +377,9 @@ class GPTWork:
         return loss.detach()
 
     def topology_update(self):
-        """SET on every sparse layer, then each layer's transpose rebuilt on the device."""
-        from sparsecore_amd import ops
-
+        """SET on every sparse layer; SET then rebuilds the layers' transposes on
+        the device in one batch."""
         self.algo.step()
-        for layer in self.algo.layers:
-            ops._cached_transpose(layer._csr)
 
     def params(self):
         return list(self.model.parameters())

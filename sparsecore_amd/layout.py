@@ -40,6 +40,7 @@ __all__ = [
     "to_dense",
     "transpose",
     "transpose_with_perm",
+    "transposes_with_perm",
 ]
 
 _I32 = torch.int32
@@ -764,6 +765,45 @@ def transpose_with_perm(p: PaddedCSR, *, padding_ratio: float = 0.2):
     _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, capT, val_t, col_t, perm)
     WT = PaddedCSR._from_parts(K, M, val_t, col_t, rs_t, nnz_t, cap_t, p.nnz)
     return WT, perm
+
+
+def transposes_with_perm(ps, *, padding_ratio: float = 0.2):
+    """[(WT, perm)] for several matrices, as transpose_with_perm gives them one
+    by one, with a single device->host read: every counting pass is queued
+    first, then the WT capacities are read together, then every fill."""
+    if padding_ratio < 0:
+        raise ValueError(f"padding_ratio must be >= 0, got {padding_ratio}")
+    ps = list(ps)
+    if not ps:
+        return []
+    for p in ps:
+        p._require_device("transpose")
+    dev = ps[0].device
+    if any(p.device != dev for p in ps):
+        raise ValueError("transposes_with_perm: all matrices must be on one device")
+    caps = torch.empty(len(ps), dtype=torch.int64, device=dev)
+    staged = []
+    for i, p in enumerate(ps):
+        view = p._view()
+        K = p.ncols
+        ws = torch.empty(_lib.transpose_workspace_bytes(view), dtype=torch.uint8, device=dev)
+        rs_t = torch.empty(K, dtype=_I32, device=dev)
+        nnz_t = torch.empty(K, dtype=_I32, device=dev)
+        cap_t = torch.empty(K, dtype=_I32, device=dev)
+        _lib.transpose_count(view, padding_ratio, ws, rs_t, nnz_t, cap_t, caps[i:i + 1])
+        staged.append((view, ws, rs_t, nnz_t, cap_t))
+    capTs = caps.tolist()
+    out = []
+    for p, capT, (view, ws, rs_t, nnz_t, cap_t) in zip(ps, capTs, staged):
+        if capT > np.iinfo(np.int32).max:
+            raise ValueError(f"transpose: capacity {capT} exceeds the int32 slot range")
+        val_t = torch.empty(capT, dtype=_F32, device=dev)
+        col_t = torch.empty(capT, dtype=_I32, device=dev)
+        perm = torch.empty(capT, dtype=torch.int64, device=dev)
+        _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, capT, val_t, col_t, perm)
+        out.append((PaddedCSR._from_parts(p.ncols, p.nrows, val_t, col_t, rs_t, nnz_t, cap_t,
+                                          p.nnz), perm))
+    return out
 
 
 def transpose(p: PaddedCSR, *, padding_ratio: float = 0.2) -> PaddedCSR:

@@ -25,7 +25,7 @@ import weakref
 import torch
 
 from . import _lib
-from .layout import PaddedCSR, transpose_with_perm
+from .layout import PaddedCSR, transpose_with_perm, transposes_with_perm
 
 __all__ = ["spmm", "dense_grad"]
 
@@ -60,6 +60,21 @@ def _cached_transpose(W: PaddedCSR) -> PaddedCSR:
         weakref.finalize(W, _drop_entry, key)
     _transpose_cache[key] = (cur_version, cur_shape, WT, perm)
     return WT
+
+
+def _rebuild_stale_transposes(Ws) -> None:
+    """Rebuilds, in one batch (one device->host read for all), the cached
+    transposes of those matrices whose entry exists but whose topology has
+    changed — what the next backward of each would otherwise rebuild one by
+    one, each with its own host read. Called by SET / RigL after a rewrite."""
+    stale = []
+    for W in Ws:
+        cached = _transpose_cache.get(id(W))
+        if cached is not None and (cached[0] != W.topology_version or
+                                   cached[1] != (int(W.nrows), int(W.ncols))):
+            stale.append(W)
+    for W, (WT, perm) in zip(stale, transposes_with_perm(stale)):
+        _transpose_cache[id(W)] = (W.topology_version, (int(W.nrows), int(W.ncols)), WT, perm)
 
 
 def _clear_transpose_cache() -> None:

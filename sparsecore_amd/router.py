@@ -105,6 +105,14 @@ class DynamicSparsityAlgorithm(SparsityAlgorithm):
         if self._step_idx % self.update_freq == 0:
             self.update()
 
+    def _rebuild_transposes(self) -> None:
+        """After a rewrite, rebuild the cached transposes of the rewritten
+        layers in one batch, so the next backward finds them current instead
+        of rebuilding each with its own device->host read."""
+        from .ops import _rebuild_stale_transposes
+
+        _rebuild_stale_transposes([layer._csr for layer in self.layers])
+
     def _k_drop(self, total_nnz: int) -> int:
         # Python float product then int(), as router.py:409
         return max(1, int(self.drop_fraction * total_nnz))
@@ -134,6 +142,7 @@ class SET(DynamicSparsityAlgorithm):
     def update(self) -> None:
         for layer in self.layers:
             self._update_layer(layer, self._rng)
+        self._rebuild_transposes()
 
     def _update_layer(self, layer, rng) -> None:
         csr = layer._csr
@@ -178,6 +187,7 @@ class RigL(DynamicSparsityAlgorithm):
     def update(self) -> None:
         for layer in self.layers:
             self._update_layer(layer, self._rng)
+        self._rebuild_transposes()
 
     def _update_layer(self, layer, rng) -> None:
         from .ops import _dense_grad_token_major

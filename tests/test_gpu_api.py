@@ -479,6 +479,47 @@ def test_rewrite_invalidates_cache_in_training(dev, general_path):
                                atol=1e-5)
 
 
+def test_batched_transpose_build_matches_single_builds(dev):
+    """transposes_with_perm over several matrices gives each one's
+    transpose_with_perm arrays exactly (one capacity read for all)."""
+    from sparsecore_amd import layout
+
+    Ws = [PaddedCSR.random(m, k, sparsity=s, seed=i).to(dev)
+          for i, (m, k, s) in enumerate([(40, 70, 0.7), (5, 300, 0.9), (128, 16, 0.2), (1, 1, 0.0)])]
+    for W, (WT, perm) in zip(Ws, layout.transposes_with_perm(Ws)):
+        WT1, perm1 = layout.transpose_with_perm(W)
+        for a in ("values", "col_indices", "row_start", "row_nnz", "row_capacity"):
+            assert torch.equal(getattr(WT, a), getattr(WT1, a)), a
+        assert torch.equal(perm, perm1)
+    assert layout.transposes_with_perm([]) == []
+
+
+def test_set_step_rebuilds_stale_transposes_in_one_batch(dev, general_path):
+    """After SET rewrites the layers, their cached transposes are current (the
+    next backward hits the cache) and equal fresh transposes."""
+    torch.manual_seed(0)
+    model = nn.Sequential(SparseLinear(64, 96, sparsity=0.8), nn.ReLU(),
+                          SparseLinear(96, 80, sparsity=0.8)).to(dev)
+    algo = slk.SET(sparsity=0.8, drop_fraction=0.3, update_freq=1, seed=3)
+    model.apply(algo)
+    x = torch.randn(32, 64, device=dev, requires_grad=True)
+    model(x).sum().backward()
+    layers = [model[0], model[2]]
+    versions = [l._csr.topology_version for l in layers]
+    with torch.no_grad():
+        for l in layers:
+            l._values.add_(torch.randn_like(l._values) * 0.01)
+    algo.step()
+    for l, v0 in zip(layers, versions):
+        W = l._csr
+        assert W.topology_version != v0
+        ver, shape, WT, perm = _transpose_cache[id(W)]
+        assert ver == W.topology_version and shape == (W.nrows, W.ncols)
+        fresh = W.transpose()
+        assert torch.equal(WT.col_indices, fresh.col_indices)
+        assert torch.equal(WT.values, fresh.values)
+
+
 def test_gradcheck_with_cache_enabled(dev, general_path):
     torch.manual_seed(0)
     layer = SparseLinear(8, 4, sparsity=0.5, bias=False).to(dev)
