@@ -653,12 +653,13 @@ int sddmm_impl(const slk_csr* W, const float* dY, int64_t dY_rows, const float* 
     }
     const bool v4 = (N % 4 == 0) && (reinterpret_cast<uintptr_t>(X) % 16 == 0) &&
                     (reinterpret_cast<uintptr_t>(dY) % 16 == 0);
-    // Windowed sweep (G groups per wave) for the 16-byte path at large N, with
-    // the most groups per wave that still leaves ~8 waves per CU (measured on
-    // the C3/C4 layer shapes); SLK_SDDMM_G=1|2|4 overrides G (1 = one group
-    // per wave, whole rows).
+    // Windowed sweep (G groups per wave) for the 16-byte path at large N:
+    // G = 4 from 2048 waves of 4 groups, G = 2 from 1024 waves of 2 (measured
+    // on the C3/C4 layer shapes: the 10M-GPT attention-out layer, 53 k slots,
+    // runs 133 -> 105 us with G = 2); SLK_SDDMM_G=1|2|4 overrides G (1 = one
+    // group per wave, whole rows).
     int G = 1;
-    if (v4 && N >= kWinMinN) G = cap >= 4 * kWinMinSlots ? 4 : cap >= 2 * kWinMinSlots ? 2 : 1;
+    if (v4 && N >= kWinMinN) G = cap >= 4 * kWinMinSlots ? 4 : cap >= kWinMinSlots ? 2 : 1;
     if (const char* e = std::getenv("SLK_SDDMM_G")) G = std::atoi(e);
     if (!v4 || (G != 2 && G != 4)) G = 1;
     // The windowed kernel walks W's slot list when the caller supplies one
