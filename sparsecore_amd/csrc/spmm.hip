@@ -549,6 +549,18 @@ constexpr int64_t kLdsMinN = 1024;
 constexpr double kLdsMinReuse = 4.0;
 constexpr int64_t kCUs = 256;  // MI355X; one LDS-kernel workgroup per CU at a time
 
+// Workgroups of the LDS kernel (one per CU at a time: 128 KiB of LDS each).
+int64_t lds_blocks(int64_t M, int64_t N, int h, int rw) {
+    return ceil_div(M, int64_t{kLdsWaves} * rw) * ceil_div(N, int64_t{kLdsCols} * h);
+}
+// With fewer workgroups than this, CUs idle while each workgroup streams all
+// of K, and the wave kernels, which spread the same work over every CU, are
+// faster. Measured on 10%-dense layers with 64-2048 rows and 512-784 columns:
+// 32 workgroups 44 us against 15 us for the wave kernel, 128 workgroups 46
+// against 29 us, 208 even (33 us), 256 51 against 54 us; the 10M-GPT layers
+// that the LDS kernel wins have 192.
+constexpr int64_t kLdsMinBlocks = 3 * kCUs / 4;
+
 // Estimated time of the LDS kernel with H halves of 256 columns per lane and
 // RW rows per wave: rounds of workgroups x X chunks x (barrier + rows x (row
 // overhead + expected slots per row and chunk x per-slot cost)). The constants
@@ -557,7 +569,7 @@ constexpr int64_t kCUs = 256;  // MI355X; one LDS-kernel workgroup per CU at a t
 // transpose, where the choice they give is the fastest measured in every case.
 double lds_cost(int64_t M, int64_t K, int64_t N, double density, int h, int rw) {
     const int64_t kc = kLdsK / h;
-    const int64_t blocks = ceil_div(M, int64_t{kLdsWaves} * rw) * ceil_div(N, int64_t{kLdsCols} * h);
+    const int64_t blocks = lds_blocks(M, N, h, rw);
     const double rounds = static_cast<double>(ceil_div(blocks, kCUs));
     const double chunks = static_cast<double>(ceil_div(K, kc));
     return rounds * chunks * (40.0 + rw * (2.0 + density * kc * (h == 1 ? 4.0 : 6.0)));
@@ -599,8 +611,9 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
 
     // Kernel choice. The LDS-staged kernel needs 16-byte lanes (N % 4 == 0,
     // aligned X and Y) and pays off when each staged X element feeds several
-    // rows of a workgroup: expected uses = density x rows per workgroup. Among
-    // the configurations that pass that bar, lds_cost picks one. The per-wave
+    // rows of a workgroup: expected uses = density x rows per workgroup, and
+    // when it has enough workgroups to occupy the chip. Among the
+    // configurations that pass both bars, lds_cost picks one. The per-wave
     // gather kernels cover everything else (small N is latency-bound).
     // SLK_SPMM_KERNEL=lds|wave, SLK_SPMM_H=1|2 and SLK_SPMM_RW=2|4|8 override.
     const bool lds_ok = N % 4 == 0 && align % 16 == 0;
@@ -612,6 +625,7 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
         for (const int cfg : {18, 14, 12, 24, 22}) {  // h * 10 + rw
             const int ch = cfg / 10, crw = cfg % 10;
             if (density * kLdsWaves * crw < kLdsMinReuse) continue;
+            if (lds_blocks(M, N, ch, crw) < kLdsMinBlocks) continue;
             const double c = lds_cost(M, K, N, density, ch, crw);
             if (rw == 0 || c < best) {
                 best = c;

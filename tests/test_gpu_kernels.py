@@ -267,6 +267,36 @@ def test_row_order_schedule_bit_exact(dev, N):
     assert_bits_equal(Y.cpu().numpy(), want, "Y (natural order)")
 
 
+@pytest.mark.parametrize("h,rw", [(1, 2), (1, 4), (1, 8), (2, 2), (2, 4)])
+def test_row_order_lds_kernel_bit_exact(dev, monkeypatch, h, rw):
+    """Every LDS-staged kernel variant gives the natural order's bits whatever
+    row schedule the view carries (the longest-first one, a random
+    permutation, none): a tall skewed matrix with a partial last row block
+    (3000 rows) and a partial column tile, with and without bias."""
+    monkeypatch.setenv("SLK_SPMM_KERNEL", "lds")
+    monkeypatch.setenv("SLK_SPMM_H", str(h))
+    monkeypatch.setenv("SLK_SPMM_RW", str(rw))
+    print(f"[row_order lds h={h} rw={rw}]", flush=True)
+    c = oracle.zipf_rows(3000, 400, 0.03, 1.1, seed=rw + h, sigma=0.5)
+    rng = np.random.default_rng(rw * h)
+    N = 260
+    X_np = rng.standard_normal((400, N)).astype(np.float32)
+    b_np = rng.standard_normal(3000).astype(np.float32)
+    W = from_oracle(c, dev)
+    v = W._view()
+    assert v.row_order is not None
+    X, b = _t(X_np, dev), _t(b_np, dev)
+    want = oracle.spmm(c, X_np)
+    perm = torch.from_numpy(rng.permutation(3000).astype(np.int32)).to(dev)
+    for name, view in (("sorted", v), ("random", _with_fields(v, row_order=perm.data_ptr())),
+                       ("natural", _with_fields(v, row_order=None))):
+        Y = torch.full((3000, N), float("nan"), device=dev)
+        _lib.spmm(view, X, Y)
+        assert_bits_equal(Y.cpu().numpy(), want, f"Y ({name} order)")
+        _lib.spmm(view, X, Y, b)
+        assert_bits_equal(Y.cpu().numpy(), want + b_np[:, None], f"Y+bias ({name} order)")
+
+
 def test_row_order_follows_rewrite_row(dev):
     """rewrite_row changes row_nnz, so the cached schedule is rebuilt."""
     c = oracle.uniform_rows(2048, 64, 4, seed=2, sigma=1.0, padding_ratio=3.0)
@@ -441,18 +471,26 @@ def _zero_capacity_rows(M, K, per_row, empty, seed):
     return oracle.Csr(M, K, val, col, rs, np.array([len(x) for x in cols], np.int32), cap)
 
 
-@pytest.mark.parametrize("N", [16, 20, 64, 100, 128, 200, 256, 264, 268])
-@pytest.mark.parametrize("layout", ["dense-rows", "zero-capacity-runs"])
+@pytest.mark.parametrize("N", [16, 20, 64, 100, 128, 200, 256, 264, 268, 384, 520])
+@pytest.mark.parametrize("layout", ["dense-rows", "zero-capacity-runs", "short-zero-runs"])
 def test_sddmm_rows_without_slots_bit_exact(dev, N, layout):
-    """dW at every N shape of the one-group kernel (full 16-wide steps, the
-    8-wide step, the scalar tail), including long runs of rows with capacity 0
-    between the slots of one wave (the row search must skip them)."""
+    """dW at every N shape of the one-group kernel (pairs of 128-float blocks,
+    a lone block, 16-wide steps, the 8-wide step, the scalar tail), including
+    runs of rows with capacity 0 between the slots of one wave: long ones
+    (more than 63 rows: the fallback search) and runs of 1, 2, 30, 61, 62, 63
+    and 64 rows (the ballot over the next 64 rows' starts, at its edge)."""
     print(f"[dW rows] N={N} {layout}", flush=True)
     if layout == "dense-rows":
         c = oracle.uniform_rows(300, 90, 30, seed=N, sigma=1.0)
-    else:
+    elif layout == "zero-capacity-runs":
         empty = set(range(5, 150)) | set(range(151, 240))
         c = _zero_capacity_rows(400, 90, 12, empty, seed=N)
+    else:
+        empty, r = set(), 3
+        for run in (1, 2, 30, 61, 62, 63, 64, 1, 63):
+            empty |= set(range(r, r + run))
+            r += run + 2
+        c = _zero_capacity_rows(r + 20, 90, 12, empty, seed=N)
     rng = np.random.default_rng(N)
     X_np = rng.standard_normal((90, N)).astype(np.float32)
     dY_np = rng.standard_normal((c.nrows, N)).astype(np.float32)
