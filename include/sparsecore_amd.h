@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define SLK_ABI_VERSION 5
+#define SLK_ABI_VERSION 6
 
 #if defined(__GNUC__)
 #define SLK_API __attribute__((visibility("default")))
@@ -87,6 +87,13 @@ typedef struct slk_csr {
     const int32_t* slot_list_row;
     int64_t n_slot_list;
     int64_t slot_list_block;
+    /* Rows at the head of row_order that are long against the rest (0 = none;
+     * needs row_order; at most nrows). When slk_spmm runs its LDS-staged
+     * kernel it runs them as a launch of their own, with fewer rows per
+     * wave, and then the rest: a workgroup's waves wait on each other at
+     * every staged chunk, so rows much longer than their workgroup's others
+     * stall it. Results are the same either way. */
+    int64_t n_heavy_rows;
 } slk_csr;
 
 /* Thread-local description of the last failure of this thread ("" if none). */

@@ -21,7 +21,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libsparsecore_amd.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 SLK_OK, SLK_EINVAL, SLK_EDEVICE = 0, 1, 2
 SLK_DW_SIMD, SLK_DW_SCALAR = 0, 1
@@ -74,6 +74,7 @@ class CsrView(ctypes.Structure):
         ("slot_list_row", ctypes.c_void_p),
         ("n_slot_list", ctypes.c_int64),
         ("slot_list_block", ctypes.c_int64),
+        ("n_heavy_rows", ctypes.c_int64),
     ]
 
 

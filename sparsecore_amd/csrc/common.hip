@@ -41,6 +41,12 @@ int validate_csr(const slk_csr* W, const char* who) {
     if (W->total_capacity > 0 && (W->values == nullptr || W->col_indices == nullptr)) {
         return fail(SLK_EINVAL, std::string(who) + ": NULL slot array");
     }
+    if (W->n_heavy_rows < 0 || W->n_heavy_rows > W->nrows ||
+        (W->n_heavy_rows > 0 && W->row_order == nullptr)) {
+        return fail(SLK_EINVAL, std::string(who) + ": n_heavy_rows=" +
+                                    std::to_string(W->n_heavy_rows) +
+                                    " needs row_order and must lie in [0, nrows]");
+    }
     return SLK_OK;
 }
 

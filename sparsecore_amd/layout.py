@@ -185,6 +185,23 @@ def _check_host(nrows, ncols, values, col, rs, nnz, cap) -> str:
 #  PaddedCSR
 # ─────────────────────────────────────────────────────────────────────
 
+# A row is "heavy" for slk_spmm's LDS-staged kernel when it holds more than
+# this many times the mean row's slots (slk_csr.n_heavy_rows). Measured on the
+# 16384^2 Zipf(1.1) layer at 95% sparsity: splitting at 2x, 4x and 8x the mean
+# gave 9.4, 9.1 and 9.8 ms against 12.6 ms unsplit; uniform layers have none.
+HEAVY_ROW_FACTOR = 4.0
+
+
+def heavy_row_count(row_nnz: np.ndarray) -> int:
+    """Rows with more than HEAVY_ROW_FACTOR x the mean row_nnz: the head of the
+    longest-rows-first order that slk_spmm runs as a launch of its own."""
+    n = len(row_nnz)
+    if n == 0:
+        return 0
+    mean = float(np.asarray(row_nnz, dtype=np.float64).sum()) / n
+    return int(np.count_nonzero(np.asarray(row_nnz) > HEAVY_ROW_FACTOR * mean))
+
+
 class PaddedCSR:
     """Sparse matrix with padded-row CSR storage (reference padded_csr.hpp:47-143).
 
@@ -251,9 +268,10 @@ class PaddedCSR:
         self._nnz = nnz
         self._topology_version = 0
         self._cview = None
-        self._order = None      # (topology_version, device row schedule) for the view
+        self._order = None      # (topology_version, device row schedule, heavy rows)
         self._slist = None      # ((topology_version, block_cols), view with a slot list)
         self._host_rows = None  # cached numpy (row_start, row_nnz, row_capacity)
+        self._heavy_hint = None  # heavy_row_count(row_nnz) when a builder counted it
 
     # ─── shape and aggregates (bindings.cpp:631-660) ────────────────
     @property
@@ -341,17 +359,21 @@ class PaddedCSR:
     def _view(self) -> _lib.CsrView:
         v = self._cview
         if v is None:
-            order = None
+            order, n_heavy = None, 0
             if self._nrows >= self._ORDER_MIN_ROWS and self._on_device():
                 if self._order is None or self._order[0] != self._topology_version:
                     # stable: equal-length rows keep their natural order
+                    heavy = self._heavy_hint
+                    if heavy is None:
+                        heavy = heavy_row_count(self._rows_host()[1])
                     self._order = (self._topology_version,
                                    torch.argsort(self._row_nnz, descending=True,
-                                                 stable=True).to(_I32))
-                order = self._order[1]
+                                                 stable=True).to(_I32), heavy)
+                order, n_heavy = self._order[1], self._order[2]
             v = _lib.CsrView(self._nrows, self._ncols, self._values.numel(),
                              _lib.ptr(self._values), _lib.ptr(self._col), _lib.ptr(self._rs),
-                             _lib.ptr(self._row_nnz), _lib.ptr(self._row_cap), _lib.ptr(order))
+                             _lib.ptr(self._row_nnz), _lib.ptr(self._row_cap), _lib.ptr(order),
+                             n_heavy_rows=n_heavy)
             self._cview = v
         return v
 
@@ -482,6 +504,7 @@ class PaddedCSR:
         nz[row_idx] = n
         self._topology_version += 1
         self._cview = None  # the row schedule depends on row_nnz
+        self._heavy_hint = None
 
     def _drop_grow(self, k_drop: int, rule: int, G: torch.Tensor | None = None,
                    seed: int = 0) -> None:
@@ -506,7 +529,7 @@ class PaddedCSR:
         # row_nnz is unchanged, so the cached row schedule stays valid
         self._topology_version += 1
         if self._order is not None:
-            self._order = (self._topology_version, self._order[1])
+            self._order = (self._topology_version,) + self._order[1:]
 
     # ─── device movement ───────────────────────────────────────────
     def to(self, device) -> "PaddedCSR":
@@ -756,7 +779,10 @@ def transpose_with_perm(p: PaddedCSR, *, padding_ratio: float = 0.2):
     cap_t = torch.empty(K, dtype=_I32, device=dev)
     capT_dev = torch.empty(1, dtype=torch.int64, device=dev)
     _lib.transpose_count(view, padding_ratio, ws, rs_t, nnz_t, cap_t, capT_dev)
-    capT = int(capT_dev.item())
+    counts = torch.empty(2, dtype=torch.int64, device=dev)
+    counts[0:1].copy_(capT_dev)
+    _count_heavy(nnz_t, p.nnz, counts[1:2])
+    capT, heavy = counts.tolist()
     if capT > np.iinfo(np.int32).max:
         raise ValueError(f"transpose: capacity {capT} exceeds the int32 slot range")
     val_t = torch.empty(capT, dtype=_F32, device=dev)
@@ -764,7 +790,19 @@ def transpose_with_perm(p: PaddedCSR, *, padding_ratio: float = 0.2):
     perm = torch.empty(capT, dtype=torch.int64, device=dev)
     _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, capT, val_t, col_t, perm)
     WT = PaddedCSR._from_parts(K, M, val_t, col_t, rs_t, nnz_t, cap_t, p.nnz)
+    WT._heavy_hint = heavy
     return WT, perm
+
+
+def _count_heavy(nnz_t: torch.Tensor, nnz: int, out: torch.Tensor) -> None:
+    """out[0] = heavy_row_count of a WT whose row_nnz is nnz_t and total nnz,
+    counted on the device (read with the capacity, no extra host sync)."""
+    n = nnz_t.numel()
+    if n == 0:
+        out.zero_()
+        return
+    bar = HEAVY_ROW_FACTOR * (float(nnz) / n)  # the float64 bar of heavy_row_count
+    out.copy_((nnz_t.to(torch.float64) > bar).sum().view(1))
 
 
 def transposes_with_perm(ps, *, padding_ratio: float = 0.2):
@@ -781,7 +819,8 @@ def transposes_with_perm(ps, *, padding_ratio: float = 0.2):
     dev = ps[0].device
     if any(p.device != dev for p in ps):
         raise ValueError("transposes_with_perm: all matrices must be on one device")
-    caps = torch.empty(len(ps), dtype=torch.int64, device=dev)
+    n = len(ps)
+    caps = torch.empty(2 * n, dtype=torch.int64, device=dev)  # capacities, heavy-row counts
     staged = []
     for i, p in enumerate(ps):
         view = p._view()
@@ -791,18 +830,23 @@ def transposes_with_perm(ps, *, padding_ratio: float = 0.2):
         nnz_t = torch.empty(K, dtype=_I32, device=dev)
         cap_t = torch.empty(K, dtype=_I32, device=dev)
         _lib.transpose_count(view, padding_ratio, ws, rs_t, nnz_t, cap_t, caps[i:i + 1])
+        if K >= PaddedCSR._ORDER_MIN_ROWS:  # only scheduled views use the count
+            _count_heavy(nnz_t, p.nnz, caps[n + i:n + i + 1])
+        else:
+            caps[n + i:n + i + 1].zero_()
         staged.append((view, ws, rs_t, nnz_t, cap_t))
-    capTs = caps.tolist()
+    host = caps.tolist()
     out = []
-    for p, capT, (view, ws, rs_t, nnz_t, cap_t) in zip(ps, capTs, staged):
+    for p, capT, heavy, (view, ws, rs_t, nnz_t, cap_t) in zip(ps, host[:n], host[n:], staged):
         if capT > np.iinfo(np.int32).max:
             raise ValueError(f"transpose: capacity {capT} exceeds the int32 slot range")
         val_t = torch.empty(capT, dtype=_F32, device=dev)
         col_t = torch.empty(capT, dtype=_I32, device=dev)
         perm = torch.empty(capT, dtype=torch.int64, device=dev)
         _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, capT, val_t, col_t, perm)
-        out.append((PaddedCSR._from_parts(p.ncols, p.nrows, val_t, col_t, rs_t, nnz_t, cap_t,
-                                          p.nnz), perm))
+        WT = PaddedCSR._from_parts(p.ncols, p.nrows, val_t, col_t, rs_t, nnz_t, cap_t, p.nnz)
+        WT._heavy_hint = heavy
+        out.append((WT, perm))
     return out
 
 

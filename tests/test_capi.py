@@ -11,6 +11,7 @@ import ctypes
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 from sparsecore_amd import _lib
@@ -64,6 +65,55 @@ def test_shape_checks_answer_on_the_host():
     assert lib.slk_spmm(ctypes.byref(bad), None, 3, 1, None, None) == _lib.SLK_EINVAL
     rc = lib.slk_transpose_count(ctypes.byref(v), -0.5, None, 0, None, None, None, None, None)
     assert rc == _lib.SLK_EINVAL and "padding_ratio" in lib.slk_last_error().decode()
+
+
+def test_heavy_row_count_needs_an_order_and_a_valid_range():
+    """slk_csr.n_heavy_rows is checked before any device work: it must lie in
+    [0, nrows] and needs row_order."""
+    lib = _lib.load()
+    for n_heavy, order in ((1, None), (-1, 8), (5, 8)):
+        v = _lib.CsrView(4, 6, 0, None, None, 1, 1, 1, order, n_heavy_rows=n_heavy)
+        assert lib.slk_spmm(ctypes.byref(v), None, 6, 3, None, None) == _lib.SLK_EINVAL
+        assert "n_heavy_rows" in lib.slk_last_error().decode()
+
+
+def test_heavy_rows_are_those_far_above_the_mean():
+    from sparsecore_amd.layout import HEAVY_ROW_FACTOR, heavy_row_count
+
+    assert HEAVY_ROW_FACTOR == 4.0
+    assert heavy_row_count(np.zeros(0, np.int32)) == 0
+    assert heavy_row_count(np.full(100, 7, np.int32)) == 0  # uniform: none
+    nnz = np.full(100, 10, np.int32)
+    nnz[[3, 50]] = 200  # mean 13.8: heavy above 55.2
+    assert heavy_row_count(nnz) == 2
+    nnz[7] = 55  # mean 14.25, bar 57: still two
+    assert heavy_row_count(nnz) == 2
+    nnz[7] = 58
+    assert heavy_row_count(nnz) == 3
+    import bench
+
+    counts = bench.zipf_row_counts(16384, 16384, 0.05, 1.1, 0)
+    assert heavy_row_count(counts) == int((counts > 4 * counts.mean()).sum()) > 0
+
+
+@pytest.mark.parametrize("case", ["zipf", "ties", "uniform", "empty-rows", "none"])
+def test_transpose_builders_count_heavy_rows_like_the_host_rule(case):
+    """The transpose builders count a WT's heavy rows on the device (read with
+    its capacity); the count equals heavy_row_count on the host arrays."""
+    import torch
+
+    from sparsecore_amd import layout
+
+    rng = np.random.default_rng(3)
+    nnz = {"zipf": np.minimum(4000, (3000 * np.arange(1, 2501) ** -1.1).astype(np.int32)),
+           "ties": np.array([10] * 99 + [4 * 10 + 30], np.int32),
+           "uniform": np.full(3000, 17, np.int32),
+           "empty-rows": np.concatenate([np.zeros(500, np.int32), rng.integers(0, 50, 2000)]),
+           "none": np.zeros(0, np.int32)}[case].astype(np.int32)
+    rng.shuffle(nnz)
+    out = torch.full((1,), -1, dtype=torch.int64)
+    layout._count_heavy(torch.from_numpy(nnz), int(nnz.sum()), out)
+    assert int(out) == layout.heavy_row_count(nnz)
 
 
 def test_empty_problems_are_no_ops():

@@ -262,7 +262,7 @@ def test_row_order_schedule_bit_exact(dev, N):
     _lib.spmm(v2, X, Y)
     assert_bits_equal(Y.cpu().numpy(), want, "Y (random order)")
     # and no schedule at all
-    v3 = _with_fields(v, row_order=None)
+    v3 = _with_fields(v, row_order=None, n_heavy_rows=0)
     _lib.spmm(v3, X, Y)
     assert_bits_equal(Y.cpu().numpy(), want, "Y (natural order)")
 
@@ -289,12 +289,65 @@ def test_row_order_lds_kernel_bit_exact(dev, monkeypatch, h, rw):
     want = oracle.spmm(c, X_np)
     perm = torch.from_numpy(rng.permutation(3000).astype(np.int32)).to(dev)
     for name, view in (("sorted", v), ("random", _with_fields(v, row_order=perm.data_ptr())),
-                       ("natural", _with_fields(v, row_order=None))):
+                       ("natural", _with_fields(v, row_order=None, n_heavy_rows=0))):
         Y = torch.full((3000, N), float("nan"), device=dev)
         _lib.spmm(view, X, Y)
         assert_bits_equal(Y.cpu().numpy(), want, f"Y ({name} order)")
         _lib.spmm(view, X, Y, b)
         assert_bits_equal(Y.cpu().numpy(), want + b_np[:, None], f"Y+bias ({name} order)")
+
+
+@pytest.mark.parametrize("h,rw", [(1, 2), (1, 4), (1, 8), (2, 2), (2, 4)])
+def test_lds_heavy_row_split_bit_exact(dev, monkeypatch, h, rw):
+    """A skewed matrix's heavy rows (the head of the longest-first order) run
+    as their own LDS launch and the rest as a second one: the bits are the
+    oracle's for every split point (none, one row, a partial row block, the
+    view's own count, all but one row, all rows), every variant of the second
+    launch, with and without bias."""
+    monkeypatch.setenv("SLK_SPMM_KERNEL", "lds")
+    monkeypatch.setenv("SLK_SPMM_H", str(h))
+    monkeypatch.setenv("SLK_SPMM_RW", str(rw))
+    print(f"[heavy split h={h} rw={rw}]", flush=True)
+    c = oracle.zipf_rows(3000, 700, 0.03, 1.1, seed=h * 10 + rw, sigma=0.5)
+    rng = np.random.default_rng(rw + h)
+    N = 520
+    X_np = rng.standard_normal((700, N)).astype(np.float32)
+    b_np = rng.standard_normal(3000).astype(np.float32)
+    W = from_oracle(c, dev)
+    v = W._view()
+    assert v.row_order is not None and 0 < v.n_heavy_rows < 300
+    assert v.n_heavy_rows == layout.heavy_row_count(c.row_nnz)
+    X, b = _t(X_np, dev), _t(b_np, dev)
+    want = oracle.spmm(c, X_np)
+    for T in (0, 1, 45, v.n_heavy_rows, 2999, 3000):
+        view = _with_fields(v, n_heavy_rows=T)
+        Y = torch.full((3000, N), float("nan"), device=dev)
+        _lib.spmm(view, X, Y)
+        assert_bits_equal(Y.cpu().numpy(), want, f"Y (T={T})")
+        _lib.spmm(view, X, Y, b)
+        assert_bits_equal(Y.cpu().numpy(), want + b_np[:, None], f"Y+bias (T={T})")
+
+
+def test_transpose_builders_hint_the_heavy_row_count(dev):
+    """A transpose's heavy-row count is counted on the device with its capacity
+    (no host read of its rows), by both builders; it equals the host rule on
+    the built WT, and rewrite_row drops the hint."""
+    print("[heavy hint]", flush=True)
+    cT = oracle.zipf_rows(3000, 400, 0.03, 1.1, seed=9, sigma=0.5)
+    c, _ = oracle.transpose_with_perm(cT)  # 400 x 3000, skewed columns
+    W = from_oracle(c, dev)
+    WT1, _ = layout.transpose_with_perm(W)
+    (WT2, _), = layout.transposes_with_perm([W])
+    want = layout.heavy_row_count(cT.row_nnz)
+    assert want > 0
+    for WT in (WT1, WT2):
+        assert WT._heavy_hint == want
+        assert WT._view().n_heavy_rows == want
+        assert WT._host_rows is None  # nothing was read back for it
+    r = int(np.argmax(to_oracle(WT1).row_capacity))
+    WT1.rewrite_row(r, np.arange(3), np.ones(3, np.float32))
+    assert WT1._heavy_hint is None
+    assert WT1._view().n_heavy_rows == layout.heavy_row_count(to_oracle(WT1).row_nnz)
 
 
 def test_row_order_follows_rewrite_row(dev):
