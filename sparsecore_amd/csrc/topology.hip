@@ -25,8 +25,10 @@
 //                slot is its rank in the union bitmap; the row is staged in a
 //                workspace and copied back.
 //   dense_grad   128x128 output tile per workgroup, 8x8 per thread, j staged
-//                through LDS 16 at a time. Each output element is one running
-//                sum over j in order with the reference build's arithmetic.
+//                through LDS 16 at a time (the next 16 loaded into registers
+//                while the current 16 are summed). Each output element is one
+//                running sum over j in order with the reference build's
+//                arithmetic.
 #include "common.hpp"
 
 namespace slk {
@@ -330,33 +332,41 @@ constexpr int kGJ = 16;   // j values staged per step
 constexpr int kGThreads = 256;
 constexpr int kGPad = 4;
 
-// Stages a kGT x kGJ slab (rows r0.., j0..) of a matrix whose element (r, j)
-// sits at p[r*N + j] (TOKEN_MAJOR = false) or p[j*R + r] (TOKEN_MAJOR = true)
-// into s[j][r]. Out-of-range entries are staged as 0 and never summed.
+// Slab staging: a kGT x kGJ slab (rows r0.., j0..) of a matrix whose element
+// (r, j) sits at p[r*N + j] (TOKEN_MAJOR = false) or p[j*R + r] (TOKEN_MAJOR =
+// true) goes to s[j][r] in two halves: fetch_slab loads a thread's kGSlab
+// elements into registers (every load unconditional at a clamped, in-bounds
+// index, so all are in flight together; out-of-range entries become 0 and are
+// never summed), store_slab writes them to LDS. The kernel fetches slab s+1
+// while it computes slab s.
+constexpr int kGSlab = kGT * kGJ / kGThreads;  // elements per thread per slab (8)
+
 template <bool TOKEN_MAJOR>
-__device__ __forceinline__ void stage_slab(float (*s)[kGT + kGPad], const float* __restrict__ p,
+__device__ __forceinline__ void fetch_slab(float (&v)[kGSlab], const float* __restrict__ p,
                                            int64_t R, int64_t N, int64_t r0, int64_t j0) {
     const int t = threadIdx.x;
-    if (TOKEN_MAJOR) {
-        // consecutive threads read consecutive r of one j
-        const int r = t & (kGT - 1);
-        const int jb = t >> 7;  // 0..1
 #pragma unroll
-        for (int q = 0; q < kGJ / 2; ++q) {
-            const int j = jb + 2 * q;
-            const int64_t rr = r0 + r, jj = j0 + j;
-            s[j][r] = (rr < R && jj < N) ? p[jj * R + rr] : 0.0f;
-        }
-    } else {
-        // consecutive threads read consecutive j of one row
-        const int j = t & (kGJ - 1);
-        const int rb = t >> 4;  // 0..15
+    for (int q = 0; q < kGSlab; ++q) {
+        // TOKEN_MAJOR: consecutive threads read consecutive r of one j;
+        // otherwise consecutive j of one row
+        const int r = TOKEN_MAJOR ? (t & (kGT - 1)) : (t >> 4) + 16 * q;
+        const int j = TOKEN_MAJOR ? (t >> 7) + 2 * q : (t & (kGJ - 1));
+        const int64_t rr = r0 + r, jj = j0 + j;
+        const bool ok = rr < R && jj < N;
+        const int64_t rc = rr < R ? rr : R - 1, jc = jj < N ? jj : N - 1;
+        const float x = TOKEN_MAJOR ? p[jc * R + rc] : p[rc * N + jc];
+        v[q] = ok ? x : 0.0f;
+    }
+}
+
+template <bool TOKEN_MAJOR>
+__device__ __forceinline__ void store_slab(float (*s)[kGT + kGPad], const float (&v)[kGSlab]) {
+    const int t = threadIdx.x;
 #pragma unroll
-        for (int q = 0; q < kGT / 16; ++q) {
-            const int r = rb + 16 * q;
-            const int64_t rr = r0 + r, jj = j0 + j;
-            s[j][r] = (rr < R && jj < N) ? p[rr * N + jj] : 0.0f;
-        }
+    for (int q = 0; q < kGSlab; ++q) {
+        const int r = TOKEN_MAJOR ? (t & (kGT - 1)) : (t >> 4) + 16 * q;
+        const int j = TOKEN_MAJOR ? (t >> 7) + 2 * q : (t & (kGJ - 1));
+        s[j][r] = v[q];
     }
 }
 
@@ -376,10 +386,19 @@ __global__ __launch_bounds__(kGThreads) void dense_grad_kernel(
 #pragma unroll
         for (int c = 0; c < 8; ++c) acc[r][c] = 0.0f;
 
+    float va[kGSlab], vb[kGSlab];
+    if (N > 0) {
+        fetch_slab<TOKEN_MAJOR>(va, dY, M, N, i0, 0);
+        fetch_slab<TOKEN_MAJOR>(vb, X, K, N, k0, 0);
+    }
     for (int64_t j0 = 0; j0 < N; j0 += kGJ) {
-        stage_slab<TOKEN_MAJOR>(As, dY, M, N, i0, j0);
-        stage_slab<TOKEN_MAJOR>(Bs, X, K, N, k0, j0);
+        store_slab<TOKEN_MAJOR>(As, va);
+        store_slab<TOKEN_MAJOR>(Bs, vb);
         __syncthreads();
+        if (j0 + kGJ < N) {  // the next slab's loads fly while this one is summed
+            fetch_slab<TOKEN_MAJOR>(va, dY, M, N, i0, j0 + kGJ);
+            fetch_slab<TOKEN_MAJOR>(vb, X, K, N, k0, j0 + kGJ);
+        }
         const int jn = N - j0 < kGJ ? static_cast<int>(N - j0) : kGJ;
         // j < N4: product rounded, then added; j >= N4: fused (the reference
         // build's evaluation of `acc += a*b`).
