@@ -23,10 +23,19 @@ __global__ __launch_bounds__(kTile * kTileRowsPerPass) void transpose_f32_kernel
     const int64_t c0 = (bt % col_tiles) * kTile;
     const int tx = threadIdx.x & (kTile - 1);
     const int ty = threadIdx.x / kTile;
+    // all loads unconditional at clamped (in-bounds) indices so they are in
+    // flight together; guarded loads were each waited on before the next
+    float v[kTile / kTileRowsPerPass];
 #pragma unroll
     for (int i = 0; i < kTile; i += kTileRowsPerPass) {
         const int64_t r = r0 + ty + i, c = c0 + tx;
-        if (r < rows && c < cols) tile[ty + i][tx] = src[r * ld_src + c];
+        const int64_t rc = r < rows ? r : rows - 1, cc = c < cols ? c : cols - 1;
+        v[i / kTileRowsPerPass] = src[rc * ld_src + cc];
+    }
+#pragma unroll
+    for (int i = 0; i < kTile; i += kTileRowsPerPass) {
+        const int64_t r = r0 + ty + i, c = c0 + tx;
+        if (r < rows && c < cols) tile[ty + i][tx] = v[i / kTileRowsPerPass];
     }
     __syncthreads();
 #pragma unroll
