@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define SLK_ABI_VERSION 6
+#define SLK_ABI_VERSION 7
 
 #if defined(__GNUC__)
 #define SLK_API __attribute__((visibility("default")))
@@ -94,7 +94,29 @@ typedef struct slk_csr {
      * every staged chunk, so rows much longer than their workgroup's others
      * stall it. Results are the same either way. */
     int64_t n_heavy_rows;
+    /* Optional (may be NULL): the live slots of every (row, column block) run
+     * cut into segments of at most seg_slots consecutive slots (block b =
+     * columns [b*seg_block, (b+1)*seg_block)), as built by
+     * slk_seg_list_build: segment e covers slots seg_start[e] ..
+     * seg_start[e] + seg_count[e] - 1 of row seg_row[e]. Segments go block by
+     * block, then by row; each block's list is padded with empty segments
+     * (count 0) to a multiple of SLK_SEG_GROUP, and *seg_groups (a device
+     * int32) holds the number of such groups in use; n_seg is the arrays'
+     * length. slk_sddmm then gives each group of segments one workgroup that
+     * stages the block's X rows in LDS and keeps each segment's dY row in
+     * registers; results are the same either way. A schedule the caller
+     * caches per topology. */
+    const int32_t* seg_start;
+    const int32_t* seg_row;
+    const int32_t* seg_count;
+    const int32_t* seg_groups;
+    int64_t n_seg;
+    int64_t seg_block;
+    int64_t seg_slots;
 } slk_csr;
+
+/* Segments per group of a segment list (one slk_sddmm workgroup each). */
+#define SLK_SEG_GROUP 64
 
 /* Thread-local description of the last failure of this thread ("" if none). */
 SLK_API const char* slk_last_error(void);
@@ -290,6 +312,27 @@ SLK_API int64_t slk_slot_list_workspace_bytes(const slk_csr* W, int64_t block_co
 SLK_API int slk_slot_list_build(const slk_csr* W, int64_t block_cols, void* workspace,
                                 int64_t workspace_bytes, int32_t* slot_list,
                                 int32_t* slot_list_row, void* stream);
+
+/* Length of the segment arrays slk_seg_list_build needs for W, block_cols
+ * and seg_slots (an upper bound on the padded segment count, so the list can
+ * be built without reading anything back to the host); 0 on bad arguments. */
+SLK_API int64_t slk_seg_list_capacity(const slk_csr* W, int64_t block_cols, int64_t seg_slots);
+
+/* Bytes of device workspace slk_seg_list_build needs for W and block_cols. */
+SLK_API int64_t slk_seg_list_workspace_bytes(const slk_csr* W, int64_t block_cols);
+
+/* Builds the optional segment schedule of slk_csr on the device (see
+ * seg_start there): block_cols is 64 or 128 columns, seg_slots 4 or 8; the
+ * three arrays hold n_seg >= slk_seg_list_capacity entries, and *seg_groups
+ * receives the number of SLK_SEG_GROUP-segment groups in use. Entries past
+ * the padded list are left as empty segments. Deterministic, no atomics.
+ * No counterpart in the reference (csrc/kernels/spmm_grad_avx2.cpp walks
+ * slots in capacity order): a visiting order for slk_sddmm that leaves
+ * every output bit unchanged.                                               */
+SLK_API int slk_seg_list_build(const slk_csr* W, int64_t block_cols, int64_t seg_slots,
+                               void* workspace, int64_t workspace_bytes, int32_t* seg_start,
+                               int32_t* seg_row, int32_t* seg_count, int64_t n_seg,
+                               int32_t* seg_groups, void* stream);
 
 #ifdef __cplusplus
 }

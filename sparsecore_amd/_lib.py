@@ -21,7 +21,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libsparsecore_amd.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 SLK_OK, SLK_EINVAL, SLK_EDEVICE = 0, 1, 2
 SLK_DW_SIMD, SLK_DW_SCALAR = 0, 1
@@ -51,7 +51,12 @@ EXPORTS = (
     "slk_slot_list_build",
     "slk_spmm_t",
     "slk_backward_narrow",
+    "slk_seg_list_capacity",
+    "slk_seg_list_workspace_bytes",
+    "slk_seg_list_build",
 )
+
+SEG_GROUP = 64  # SLK_SEG_GROUP
 
 NARROW_MAX_ROWS = 64        # SLK_NARROW_MAX_ROWS
 NARROW_MAX_CAPACITY = 8192  # SLK_NARROW_MAX_CAPACITY
@@ -75,6 +80,13 @@ class CsrView(ctypes.Structure):
         ("n_slot_list", ctypes.c_int64),
         ("slot_list_block", ctypes.c_int64),
         ("n_heavy_rows", ctypes.c_int64),
+        ("seg_start", ctypes.c_void_p),
+        ("seg_row", ctypes.c_void_p),
+        ("seg_count", ctypes.c_void_p),
+        ("seg_groups", ctypes.c_void_p),
+        ("n_seg", ctypes.c_int64),
+        ("seg_block", ctypes.c_int64),
+        ("seg_slots", ctypes.c_int64),
     ]
 
 
@@ -114,8 +126,15 @@ def _declare(lib) -> None:
     lib.slk_spmm_t.argtypes = [_csrp, _vp, _i64, _i64, _vp, _vp, _vp]
     lib.slk_backward_narrow.argtypes = [_csrp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, ctypes.c_int,
                                         _vp]
+    lib.slk_seg_list_capacity.restype = _i64
+    lib.slk_seg_list_capacity.argtypes = [_csrp, _i64, _i64]
+    lib.slk_seg_list_workspace_bytes.restype = _i64
+    lib.slk_seg_list_workspace_bytes.argtypes = [_csrp, _i64]
+    lib.slk_seg_list_build.argtypes = [_csrp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp,
+                                       _vp]
     sized = ("slk_last_error", "slk_abi_version", "slk_transpose_workspace_bytes",
-             "slk_drop_grow_workspace_bytes", "slk_slot_list_workspace_bytes")
+             "slk_drop_grow_workspace_bytes", "slk_slot_list_workspace_bytes",
+             "slk_seg_list_capacity", "slk_seg_list_workspace_bytes")
     for name in EXPORTS:
         if name not in sized:
             getattr(lib, name).restype = ctypes.c_int
@@ -302,6 +321,29 @@ def slot_list_build(view: CsrView, block_cols: int, nnz: int, device):
     if rc:
         _raise(rc)
     return lst, lrow
+
+
+def seg_list_build(view: CsrView, block_cols: int, seg_slots: int, device):
+    """(seg_start, seg_row, seg_count, seg_groups) int32 tensors: W's live slots
+    cut into segments of at most seg_slots slots of one row inside one column
+    block, block by block and row by row, each block padded with empty
+    segments to whole groups of SEG_GROUP; seg_groups[0] = groups in use
+    (slk_seg_list_build). The arrays have slk_seg_list_capacity entries."""
+    lib = load()
+    n = int(lib.slk_seg_list_capacity(ctypes.byref(view), int(block_cols), int(seg_slots)))
+    n = max(n, SEG_GROUP)
+    start = torch.empty(n, dtype=torch.int32, device=device)
+    row = torch.empty(n, dtype=torch.int32, device=device)
+    count = torch.empty(n, dtype=torch.int32, device=device)
+    groups = torch.empty(1, dtype=torch.int32, device=device)
+    nbytes = int(lib.slk_seg_list_workspace_bytes(ctypes.byref(view), int(block_cols)))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+    rc = lib.slk_seg_list_build(ctypes.byref(view), int(block_cols), int(seg_slots), ptr(ws),
+                                nbytes, ptr(start), ptr(row), ptr(count), n, ptr(groups),
+                                stream_of(start))
+    if rc:
+        _raise(rc)
+    return start, row, count, groups
 
 
 def transpose_dense(src: torch.Tensor, dst: torch.Tensor) -> None:

@@ -47,6 +47,14 @@ int validate_csr(const slk_csr* W, const char* who) {
                                     std::to_string(W->n_heavy_rows) +
                                     " needs row_order and must lie in [0, nrows]");
     }
+    if (W->seg_start != nullptr &&
+        (W->seg_row == nullptr || W->seg_count == nullptr || W->seg_groups == nullptr ||
+         W->n_seg < 0 || (W->seg_block != 64 && W->seg_block != 128) ||
+         (W->seg_slots != 4 && W->seg_slots != 8))) {
+        return fail(SLK_EINVAL, std::string(who) +
+                                    ": a segment list needs seg_row, seg_count, seg_groups, "
+                                    "n_seg >= 0, seg_block 64 or 128 and seg_slots 4 or 8");
+    }
     return SLK_OK;
 }
 

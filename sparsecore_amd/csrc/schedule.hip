@@ -19,7 +19,17 @@
 //   S3 blkscan  one workgroup: exclusive scan of the block totals.
 //   S4 scatter  one thread per (row, block): copies its run to
 //               list[block start + run offset + i] with the row alongside.
+//
+// The segment list (slk_seg_list_build) is the same counting sort over
+// segments instead of slots: run (r, b) of length n becomes ceil(n / S)
+// segments of at most S consecutive slots, each block's segment count is
+// padded to a multiple of SLK_SEG_GROUP (so a group never straddles two
+// blocks), and the padding is left as empty segments by a fill pass that
+// runs first. The list's length is an upper bound the host can compute;
+// the number of groups in use is written to device memory.
 #include "common.hpp"
+
+#include <algorithm>
 
 namespace slk {
 namespace {
@@ -46,7 +56,9 @@ __global__ __launch_bounds__(kSchedThreads) void sl_bounds_kernel(
 }
 
 // One workgroup per block b: off[r*nb + b] = sum of run lengths of rows < r,
-// total[b] = the block's entry count.
+// total[b] = the block's entry count. With S > 1 a run counts as its
+// ceil(length / S) segments.
+template <int S>
 __global__ __launch_bounds__(kScanBlock) void sl_rowscan_kernel(
     int64_t M, int64_t nb, const int32_t* __restrict__ lo, int32_t* __restrict__ off,
     int32_t* __restrict__ total) {
@@ -55,7 +67,10 @@ __global__ __launch_bounds__(kScanBlock) void sl_rowscan_kernel(
     const int t = threadIdx.x;
     const int64_t per = ceil_div(M, kScanBlock);
     const int64_t r0 = min(M, t * per), r1 = min(M, r0 + per);
-    auto len = [&](int64_t r) { return lo[r * (nb + 1) + b + 1] - lo[r * (nb + 1) + b]; };
+    auto len = [&](int64_t r) {
+        const int32_t n = lo[r * (nb + 1) + b + 1] - lo[r * (nb + 1) + b];
+        return S == 1 ? n : (n + S - 1) / S;
+    };
     int32_t sum = 0;
     for (int64_t r = r0; r < r1; ++r) sum += len(r);
     part[t] = sum;
@@ -74,15 +89,20 @@ __global__ __launch_bounds__(kScanBlock) void sl_rowscan_kernel(
     if (t == kScanBlock - 1) total[b] = part[t];
 }
 
+// start[b] = exclusive scan of the block totals, each rounded up to a
+// multiple of PAD; with PAD > 1 *groups = the padded sum / PAD.
+template <int PAD>
 __global__ __launch_bounds__(kScanBlock) void sl_blkscan_kernel(int64_t nb,
                                                                const int32_t* __restrict__ total,
-                                                               int32_t* __restrict__ start) {
+                                                               int32_t* __restrict__ start,
+                                                               int32_t* __restrict__ groups) {
     __shared__ int32_t part[kScanBlock];
     const int t = threadIdx.x;
     const int64_t per = ceil_div(nb, kScanBlock);
     const int64_t a = min(nb, t * per), e = min(nb, a + per);
+    auto padded = [&](int64_t b) { return PAD == 1 ? total[b] : (total[b] + PAD - 1) / PAD * PAD; };
     int32_t sum = 0;
-    for (int64_t b = a; b < e; ++b) sum += total[b];
+    for (int64_t b = a; b < e; ++b) sum += padded(b);
     part[t] = sum;
     __syncthreads();
     for (int d = 1; d < kScanBlock; d <<= 1) {
@@ -94,8 +114,9 @@ __global__ __launch_bounds__(kScanBlock) void sl_blkscan_kernel(int64_t nb,
     int32_t run = part[t] - sum;
     for (int64_t b = a; b < e; ++b) {
         start[b] = run;
-        run += total[b];
+        run += padded(b);
     }
+    if (PAD > 1 && t == kScanBlock - 1) groups[0] = part[t] / PAD;
 }
 
 __global__ __launch_bounds__(kSchedThreads) void sl_scatter_kernel(
@@ -112,6 +133,38 @@ __global__ __launch_bounds__(kSchedThreads) void sl_scatter_kernel(
         list[dst + (s - a)] = s;
         list_row[dst + (s - a)] = static_cast<int32_t>(r);
     }
+}
+
+// Segments of run (r, b): seg_start = first slot, seg_row = r, seg_count <= S.
+template <int S>
+__global__ __launch_bounds__(kSchedThreads) void sg_scatter_kernel(
+    int64_t M, int64_t nb, const int32_t* __restrict__ lo, const int32_t* __restrict__ off,
+    const int32_t* __restrict__ start, int32_t* __restrict__ seg_start,
+    int32_t* __restrict__ seg_row, int32_t* __restrict__ seg_count) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kSchedThreads + threadIdx.x;
+    if (t >= M * nb) return;
+    const int64_t r = t / nb;
+    const int64_t b = t - r * nb;
+    const int32_t a = lo[r * (nb + 1) + b];
+    const int32_t e = lo[r * (nb + 1) + b + 1];
+    const int64_t dst = static_cast<int64_t>(start[b]) + off[t];
+    for (int32_t s = a, k = 0; s < e; s += S, ++k) {
+        seg_start[dst + k] = s;
+        seg_row[dst + k] = static_cast<int32_t>(r);
+        seg_count[dst + k] = min(S, e - s);
+    }
+}
+
+// Every entry an empty segment (row 0, slot 0, count 0): the padding.
+__global__ __launch_bounds__(kSchedThreads) void sg_fill_kernel(int64_t n,
+                                                                int32_t* __restrict__ seg_start,
+                                                                int32_t* __restrict__ seg_row,
+                                                                int32_t* __restrict__ seg_count) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kSchedThreads + threadIdx.x;
+    if (t >= n) return;
+    seg_start[t] = 0;
+    seg_row[t] = 0;
+    seg_count[t] = 0;
 }
 
 struct ListPlan {
@@ -171,12 +224,101 @@ extern "C" int slk_slot_list_build(const slk_csr* W, int64_t block_cols, void* w
                        dim3(kSchedThreads), 0, st, M, p.nb, block_cols, W->row_start, W->row_nnz,
                        W->col_indices, lo);
     if (int rc = check_launch("slot_list/bounds")) return rc;
-    hipLaunchKernelGGL(sl_rowscan_kernel, dim3(static_cast<unsigned>(p.nb)), dim3(kScanBlock), 0, st,
-                       M, p.nb, lo, off, total);
+    hipLaunchKernelGGL(sl_rowscan_kernel<1>, dim3(static_cast<unsigned>(p.nb)), dim3(kScanBlock), 0,
+                       st, M, p.nb, lo, off, total);
     if (int rc = check_launch("slot_list/rowscan")) return rc;
-    hipLaunchKernelGGL(sl_blkscan_kernel, dim3(1), dim3(kScanBlock), 0, st, p.nb, total, start);
+    hipLaunchKernelGGL(sl_blkscan_kernel<1>, dim3(1), dim3(kScanBlock), 0, st, p.nb, total, start,
+                       nullptr);
     if (int rc = check_launch("slot_list/blkscan")) return rc;
     hipLaunchKernelGGL(sl_scatter_kernel, dim3(static_cast<unsigned>(ceil_div(p.off_ints, kSchedThreads))),
                        dim3(kSchedThreads), 0, st, M, p.nb, lo, off, start, slot_list, slot_list_row);
     return check_launch("slot_list/scatter");
+}
+
+extern "C" int64_t slk_seg_list_capacity(const slk_csr* W, int64_t block_cols, int64_t seg_slots) {
+    if (W == nullptr || W->nrows <= 0 || W->ncols <= 0 || block_cols <= 0 || seg_slots <= 0) return 0;
+    // every run of n slots makes ceil(n/S) <= n/S + 1 segments, and only
+    // non-empty runs make any: at most min(cap, M*nb) of them; each block's
+    // padding adds fewer than SLK_SEG_GROUP
+    const int64_t nb = slk::ceil_div(W->ncols, block_cols);
+    const int64_t cap = W->total_capacity;
+    return cap / seg_slots + std::min(cap, W->nrows * nb) + nb * (SLK_SEG_GROUP - 1) + SLK_SEG_GROUP;
+}
+
+extern "C" int64_t slk_seg_list_workspace_bytes(const slk_csr* W, int64_t block_cols) {
+    return slk_slot_list_workspace_bytes(W, block_cols);
+}
+
+extern "C" int slk_seg_list_build(const slk_csr* W, int64_t block_cols, int64_t seg_slots,
+                                  void* workspace, int64_t workspace_bytes, int32_t* seg_start,
+                                  int32_t* seg_row, int32_t* seg_count, int64_t n_seg,
+                                  int32_t* seg_groups, void* stream) {
+    using namespace slk;
+    clear_error();
+    if (int rc = validate_csr(W, "seg_list")) return rc;
+    if (block_cols != 64 && block_cols != 128) {
+        return fail(SLK_EINVAL, "seg_list: block_cols must be 64 or 128, got " +
+                                    std::to_string(block_cols));
+    }
+    if (seg_slots != 4 && seg_slots != 8) {
+        return fail(SLK_EINVAL, "seg_list: seg_slots must be 4 or 8, got " +
+                                    std::to_string(seg_slots));
+    }
+    const int64_t M = W->nrows, K = W->ncols;
+    if (seg_groups == nullptr) return fail(SLK_EINVAL, "seg_list: NULL seg_groups");
+    hipStream_t st = as_stream(stream);
+    if (M == 0 || K == 0) {
+        hipLaunchKernelGGL(sl_blkscan_kernel<SLK_SEG_GROUP>, dim3(1), dim3(kScanBlock), 0, st,
+                           int64_t{0}, nullptr, nullptr, seg_groups);
+        return check_launch("seg_list/blkscan");
+    }
+    const int64_t need = slk_seg_list_capacity(W, block_cols, seg_slots);
+    if (n_seg < need) {
+        return fail(SLK_EINVAL, "seg_list: n_seg=" + std::to_string(n_seg) +
+                                    " is below the required " + std::to_string(need));
+    }
+    if (seg_start == nullptr || seg_row == nullptr || seg_count == nullptr) {
+        return fail(SLK_EINVAL, "seg_list: NULL output");
+    }
+    if (n_seg > INT32_MAX) return fail(SLK_EINVAL, "seg_list: matrix too large");
+    const ListPlan p = plan_list(M, K, block_cols);
+    if (workspace == nullptr || workspace_bytes < p.bytes) {
+        return fail(SLK_EINVAL, "seg_list: workspace of " + std::to_string(workspace_bytes) +
+                                    " bytes is smaller than the required " +
+                                    std::to_string(p.bytes));
+    }
+    if (p.nb > INT32_MAX || ceil_div(p.lo_ints, kSchedThreads) > INT32_MAX) {
+        return fail(SLK_EINVAL, "seg_list: matrix too large");
+    }
+    int32_t* lo = static_cast<int32_t*>(workspace);
+    int32_t* off = lo + p.lo_ints;
+    int32_t* total = off + p.off_ints;
+    int32_t* start = total + p.nb;
+    hipLaunchKernelGGL(sg_fill_kernel, dim3(static_cast<unsigned>(ceil_div(n_seg, kSchedThreads))),
+                       dim3(kSchedThreads), 0, st, n_seg, seg_start, seg_row, seg_count);
+    if (int rc = check_launch("seg_list/fill")) return rc;
+    hipLaunchKernelGGL(sl_bounds_kernel, dim3(static_cast<unsigned>(ceil_div(p.lo_ints, kSchedThreads))),
+                       dim3(kSchedThreads), 0, st, M, p.nb, block_cols, W->row_start, W->row_nnz,
+                       W->col_indices, lo);
+    if (int rc = check_launch("seg_list/bounds")) return rc;
+    if (seg_slots == 4) {
+        hipLaunchKernelGGL(sl_rowscan_kernel<4>, dim3(static_cast<unsigned>(p.nb)), dim3(kScanBlock),
+                           0, st, M, p.nb, lo, off, total);
+    } else {
+        hipLaunchKernelGGL(sl_rowscan_kernel<8>, dim3(static_cast<unsigned>(p.nb)), dim3(kScanBlock),
+                           0, st, M, p.nb, lo, off, total);
+    }
+    if (int rc = check_launch("seg_list/rowscan")) return rc;
+    hipLaunchKernelGGL(sl_blkscan_kernel<SLK_SEG_GROUP>, dim3(1), dim3(kScanBlock), 0, st, p.nb,
+                       total, start, seg_groups);
+    if (int rc = check_launch("seg_list/blkscan")) return rc;
+    const dim3 sgrid(static_cast<unsigned>(ceil_div(p.off_ints, kSchedThreads)));
+    if (seg_slots == 4) {
+        hipLaunchKernelGGL(sg_scatter_kernel<4>, sgrid, dim3(kSchedThreads), 0, st, M, p.nb, lo,
+                           off, start, seg_start, seg_row, seg_count);
+    } else {
+        hipLaunchKernelGGL(sg_scatter_kernel<8>, sgrid, dim3(kSchedThreads), 0, st, M, p.nb, lo,
+                           off, start, seg_start, seg_row, seg_count);
+    }
+    return check_launch("seg_list/scatter");
 }

@@ -618,6 +618,173 @@ __global__ __launch_bounds__(kBlock) void sddmm_scalar_kernel(
 }
 
 
+
+// SIMD order over a segment list: X from LDS, dY in registers (16-byte path).
+//
+// The tile kernel above reads both operands of every fma from LDS, and on
+// gfx950 a 64-lane 16-byte LDS read costs the same whether its lanes read one
+// row (a broadcast) or sixteen: about 4.6 cycles per CU measured, so two reads
+// per 16 fmas make it LDS-bound. Here a quad of lanes owns a segment, up to S
+// consecutive live slots of one row inside one column block
+// (slk_seg_list_build): the quad loads the row's dY pieces once per step from
+// global memory, one window ahead, and applies them to all S slots, whose X
+// pieces it reads from LDS. That is S + 0 LDS reads and one 64-byte global
+// load per S slot-steps instead of 2S LDS reads. A workgroup of 64 quads takes
+// one group of SLK_SEG_GROUP segments, all in one column block (the list pads
+// each block to whole groups); for every 64-float window it stages the
+// block's C rows of X in LDS (rows padded by four 16-byte pieces, as in the
+// tile kernel), prefetched a window ahead in registers. Per slot the
+// arithmetic is sddmm_simd_kernel's: the 16 running sums advance in step
+// order across the windows, then the same combine and scalar tail. Empty
+// segments (padding, or slots past a short segment's count) compute on a
+// clamped address and store nothing. Workgroups past the groups in use
+// (*groups, read on the device) exit at once; the workgroups after max_groups
+// are one wave per row that zeroes the row's padding slots and, with dbias,
+// sums its dY row.
+constexpr int kSegThreads = SLK_SEG_GROUP * 4;  // one quad per segment
+static_assert(kSegThreads == 256, "four waves per workgroup");
+
+template <int C, int S, bool LEAN>
+__global__ __launch_bounds__(kSegThreads) void sddmm_seg_kernel(
+    int64_t M, int64_t K, int64_t N, const int32_t* __restrict__ row_start,
+    const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ row_cap,
+    const int32_t* __restrict__ col, const float* __restrict__ dY, const float* __restrict__ X,
+    float* __restrict__ dW, float* __restrict__ dbias, const int32_t* __restrict__ seg_start,
+    const int32_t* __restrict__ seg_row, const int32_t* __restrict__ seg_count,
+    const int32_t* __restrict__ groups, int64_t max_groups) {
+    constexpr int kLoads = C * kTilePieces / kSegThreads;  // staged pieces per thread
+    static_assert(kLoads * kSegThreads == C * kTilePieces, "whole rows per pass");
+    __shared__ f32x4 xs[C * kTileStride];
+    const int wv = threadIdx.x >> 6;
+    const int q = threadIdx.x & 3;
+    const int64_t grp = blockIdx.x;
+    if (grp >= max_groups) {  // block-uniform: per-row waves
+        const int64_t row = (grp - max_groups) * (kSegThreads / kWave) + wv;
+        zero_row_padding(row_start, row_nnz, row_cap, M, row, dW);
+        if (dbias != nullptr) bias_row_sum(dY, M, N, row, dbias, N, 1);
+        return;
+    }
+    if (grp >= groups[0]) return;  // block-uniform
+    const int64_t e0 = grp * SLK_SEG_GROUP;
+    const int32_t c_lo = col[seg_start[e0]] / C * C;  // a group's first segment is never empty
+    const int64_t e = e0 + (threadIdx.x >> 2);
+    const int32_t s0 = seg_start[e];
+    const int32_t cnt = seg_count[e];
+    const int64_t row = seg_row[e];
+    int32_t xo[S];
+#pragma unroll
+    for (int k = 0; k < S; ++k) xo[k] = ((k < cnt ? col[s0 + k] : c_lo) - c_lo) * kTileStride + q;
+    // X row of slot k (the epilogue's tail), from xo
+    auto xrow = [&](int k) { return X + static_cast<int64_t>(c_lo + (xo[k] - q) / kTileStride) * N; };
+    const int32_t nC = static_cast<int32_t>(min<int64_t>(C, K - c_lo));
+
+    // staging: thread t copies piece (t mod 16) of block rows t/16 + 16i. Rows
+    // past the matrix (a last block narrower than C) and pieces past n16 (a
+    // last window shorter than 64 floats) load a clamped, in-bounds address
+    // instead: those LDS rows and steps are never read, and the loads stay
+    // branch-free.
+    const int pc = threadIdx.x % kTilePieces;
+    const int rr0 = threadIdx.x / kTilePieces;
+    const float* xband = X + static_cast<int64_t>(c_lo) * N;
+    uint32_t xoff[kLoads];  // byte offsets in the band: C*N*4 < 2^32 (launcher check)
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i)
+        xoff[i] = static_cast<uint32_t>(min(rr0 + i * kTileRowsPerPass, nC - 1)) *
+                  static_cast<uint32_t>(N) * 4u;
+    const float* dyr = dY + row * N + 4 * q;
+    const int64_t n16 = (N / 16) * 16;  // >= 16 (the launcher's bar)
+    const int64_t nwin = ceil_div(n16, kTileWin);
+    float acc[S][4];
+#pragma unroll
+    for (int k = 0; k < S; ++k) acc[k][0] = acc[k][1] = acc[k][2] = acc[k][3] = 0.f;
+    f32x4 pre[kLoads];
+    f32x4 dcur[kTileWin / 16], dnext[kTileWin / 16];
+    auto fetch_x = [&](int64_t w) {
+        const uint32_t jx = static_cast<uint32_t>(min<int64_t>(w * kTileWin + 4 * pc, n16 - 4)) * 4u;
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i)
+            pre[i] = *reinterpret_cast<const f32x4*>(reinterpret_cast<const char*>(xband) + xoff[i] + jx);
+    };
+    auto fetch_dy = [&](int64_t w, f32x4 (&d)[kTileWin / 16]) {
+#pragma unroll
+        for (int t = 0; t < kTileWin / 16; ++t)
+            d[t] = *reinterpret_cast<const f32x4*>(dyr + min<int64_t>(w * kTileWin + 16 * t, n16 - 16));
+    };
+    // LEAN: dY loaded at the start of its own window (its latency overlaps the
+    // LDS store and the barrier) and S/2 X reads in flight, for fewer registers
+    constexpr int SH = LEAN ? S / 2 : S;
+    fetch_x(0);
+    if constexpr (!LEAN) fetch_dy(0, dnext);
+    for (int64_t w = 0; w < nwin; ++w) {
+        if constexpr (LEAN) fetch_dy(w, dcur);
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) xs[(rr0 + i * kTileRowsPerPass) * kTileStride + pc] = pre[i];
+        if constexpr (!LEAN) {
+#pragma unroll
+            for (int t = 0; t < kTileWin / 16; ++t) dcur[t] = dnext[t];
+        }
+        __syncthreads();
+        // the last window refetches itself (unused)
+        fetch_x(min(w + 1, nwin - 1));
+        if constexpr (!LEAN) fetch_dy(min(w + 1, nwin - 1), dnext);
+        const int tn = static_cast<int>(min<int64_t>(kTileWin / 16, n16 / 16 - w * (kTileWin / 16)));
+#pragma unroll
+        for (int t = 0; t < kTileWin / 16; ++t) {
+#pragma unroll
+            for (int k0 = 0; k0 < S; k0 += SH) {
+                if (t < tn) {  // block-uniform
+                    f32x4 x[SH];
+#pragma unroll
+                    for (int k = 0; k < SH; ++k) x[k] = xs[xo[k0 + k] + 4 * t];
+#pragma unroll
+                    for (int k = 0; k < SH; ++k)
+                        fma4x(dcur[t], x[k], acc[k0 + k][0], acc[k0 + k][1], acc[k0 + k][2],
+                              acc[k0 + k][3]);
+                }
+                // SH reads in flight at a time: hoisting the next reads ahead
+                // of these fmas would take 16 registers per read
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        __syncthreads();  // every lane has read this window before it is overwritten
+    }
+    // a[l] = v[l] + v[l+8]: lanes q=0,1 take the partner q^2 (v[8..15]).
+#pragma unroll
+    for (int k = 0; k < S; ++k) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[k][c] = acc[k][c] + __shfl_xor(acc[k][c], 2);
+    }
+    int64_t jt = n16;
+    if (N - n16 >= 8) {
+        if (q < 2) {
+            const int64_t j = n16 + 4 * q;
+            const f32x4 d = *reinterpret_cast<const f32x4*>(dY + row * N + j);
+#pragma unroll
+            for (int k = 0; k < S; ++k) {
+                if (k < cnt) {
+                    fma4x(d, *reinterpret_cast<const f32x4*>(xrow(k) + j), acc[k][0], acc[k][1],
+                          acc[k][2], acc[k][3]);
+                }
+            }
+        }
+        jt += 8;
+    }
+    // s4[k] = a[k] + a[k+4]: lane q=0 holds a[0..3], lane q=1 holds a[4..7].
+#pragma unroll
+    for (int k = 0; k < S; ++k) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[k][c] = acc[k][c] + __shfl_xor(acc[k][c], 1);
+    }
+    if (q == 0) {
+#pragma unroll
+        for (int k = 0; k < S; ++k) {
+            if (k >= cnt) continue;
+            const float rsum = (acc[k][0] + acc[k][2]) + (acc[k][1] + acc[k][3]);
+            dW[s0 + k] = running_sum(dY + row * N + jt, xrow(k) + jt, N - jt, rsum);
+        }
+    }
+}
+
 int sddmm_impl(const slk_csr* W, const float* dY, int64_t dY_rows, const float* X,
                int64_t X_rows, int64_t N, float* dW, float* dbias, int order, void* stream) {
     clear_error();
@@ -679,6 +846,41 @@ int sddmm_impl(const slk_csr* W, const float* dY, int64_t dY_rows, const float* 
 #define SLK_SDDMM_WIN_ARGS                                                                   \
     SLK_SDDMM_ARGS, W->row_capacity, listed ? W->slot_list : nullptr,                         \
         listed ? W->slot_list_row : nullptr, space
+    // A segment list: X through LDS, dY rows in registers.
+    // (C·N floats of a band addressed with 32-bit byte offsets)
+    if (v4 && W->seg_start != nullptr && N >= 16 && W->seg_block * N * 4 < (int64_t{1} << 32)) {
+        const int64_t max_groups = W->n_seg / SLK_SEG_GROUP;
+        const int64_t sblocks = max_groups + ceil_div(W->nrows, int64_t{kSegThreads / kWave});
+        if (sblocks > INT32_MAX) return fail(SLK_EINVAL, std::string(who) + ": problem too large");
+#define SLK_SEG_ARGS                                                                         \
+    W->nrows, W->ncols, N, W->row_start, W->row_nnz, W->row_capacity, W->col_indices, dY, X, \
+        dW, dbias, W->seg_start, W->seg_row, W->seg_count, W->seg_groups, max_groups
+        const dim3 sgrid(static_cast<unsigned>(sblocks));
+        // 8-slot segments: the lean variant (4 waves per SIMD at 64 columns,
+        // 3 at 128; 2-15% faster on the 60M-GPT and 16384^2 layers). 4-slot
+        // segments, used where rows hold few slots per block, keep dY loaded a
+        // window ahead: their quads touch many different dY rows (16384^2 at
+        // 99%: 2.6 ms against 3.6 lean). SLK_SEG_LEAN=0|1 overrides.
+        bool lean = W->seg_slots == 8;
+        if (const char* e = std::getenv("SLK_SEG_LEAN")) lean = e[0] == '1';
+#define SLK_SEG_LAUNCH(CB, SS)                                                                 \
+    do {                                                                                       \
+        if (lean) {                                                                            \
+            hipLaunchKernelGGL((sddmm_seg_kernel<CB, SS, true>), sgrid, dim3(kSegThreads), 0, \
+                               st, SLK_SEG_ARGS);                                              \
+        } else {                                                                               \
+            hipLaunchKernelGGL((sddmm_seg_kernel<CB, SS, false>), sgrid, dim3(kSegThreads), 0, \
+                               st, SLK_SEG_ARGS);                                              \
+        }                                                                                      \
+    } while (0)
+        if (W->seg_block == 64 && W->seg_slots == 4) SLK_SEG_LAUNCH(64, 4);
+        else if (W->seg_block == 64) SLK_SEG_LAUNCH(64, 8);
+        else if (W->seg_slots == 4) SLK_SEG_LAUNCH(128, 4);
+        else SLK_SEG_LAUNCH(128, 8);
+#undef SLK_SEG_LAUNCH
+#undef SLK_SEG_ARGS
+        return check_launch(who);
+    }
     // A slot list in blocks of 64 or 128 columns: both operands through LDS.
     const char* tile_env = std::getenv("SLK_SDDMM_TILE");  // "0": the windowed kernel
     const int64_t cb = W->slot_list_block;

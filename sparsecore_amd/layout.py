@@ -270,6 +270,7 @@ class PaddedCSR:
         self._cview = None
         self._order = None      # (topology_version, device row schedule, heavy rows)
         self._slist = None      # ((topology_version, block_cols), view with a slot list)
+        self._seglist = None    # ((topology_version, block_cols, seg_slots), segmented view)
         self._host_rows = None  # cached numpy (row_start, row_nnz, row_capacity)
         self._heavy_hint = None  # heavy_row_count(row_nnz) when a builder counted it
 
@@ -391,6 +392,25 @@ class PaddedCSR:
                           n_slot_list=int(lst.numel()), slot_list_block=int(block_cols))
             self._slist = (key, _lib.CsrView(**fields), lst, lrow)
         return self._slist[1]
+
+    def _view_segmented(self, block_cols: int, seg_slots: int) -> _lib.CsrView:
+        """The view plus W's live slots cut into segments of at most seg_slots
+        consecutive slots of one row inside one column block (slk_csr.seg_start):
+        a schedule for slk_sddmm that keeps each segment's dY row in registers.
+        Built on the device (slk_seg_list_build, five launches, no host read)
+        once per topology."""
+        base = self._view()
+        key = (self._topology_version, int(block_cols), int(seg_slots), id(base))
+        if self._seglist is None or self._seglist[0] != key:
+            arrays = _lib.seg_list_build(base, int(block_cols), int(seg_slots), self.device)
+            start, row, count, groups = arrays
+            fields = {f: getattr(base, f) for f, _ in _lib.CsrView._fields_}
+            fields.update(seg_start=_lib.ptr(start), seg_row=_lib.ptr(row),
+                          seg_count=_lib.ptr(count), seg_groups=_lib.ptr(groups),
+                          n_seg=int(start.numel()), seg_block=int(block_cols),
+                          seg_slots=int(seg_slots))
+            self._seglist = (key, _lib.CsrView(**fields), arrays)
+        return self._seglist[1]
 
     def _rows_host(self):
         h = self._host_rows

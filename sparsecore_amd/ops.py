@@ -111,10 +111,35 @@ def _slot_block(W: PaddedCSR, K: int, N: int) -> int:
     return min(1024, max(256, N // 32))
 
 
+# Segment schedule for dW (slk_csr.seg_start): from this many live slots at
+# N >= 1024 (measured per layer: 1.4-1.8x on the 60M-GPT layers, 1.35x on the
+# 10M-GPT QKV layer, 1.5x / 1.45x on the 16384^2 layer at 95% / 99%; the
+# windowed kernel stays ahead on the 10M-GPT layers of 44-59 k slots).
+_SEG_MIN_NNZ = 100_000
+
+
+def _seg_shape(W: PaddedCSR, K: int, N: int) -> tuple[int, int]:
+    """(block columns, slots per segment) of the segment list: 128-column
+    blocks where X is far beyond the L2s (fewer workgroups stage each X band),
+    else 64; 8 slots per segment where a row holds at least 4 live slots per
+    block on average, else 4 (fewer empty slots in short runs)."""
+    cols = 128 if 4 * K * N >= _TILE_MIN_X_BYTES else 64
+    density = W.nnz / max(1, W.nrows * W.ncols)
+    return cols, 8 if density * cols >= 4 else 4
+
+
 def _sddmm_view(W: PaddedCSR, X: torch.Tensor):
-    """W's view for slk_sddmm: with a slot list where it pays (see above);
-    SLK_SLOT_BLOCK=<cols> forces a list with that block width, 0 none."""
+    """W's view for slk_sddmm: with a segment list or a slot list where it
+    pays (see above). SLK_SEG=<cols>x<slots> forces a segment list, 0 none;
+    SLK_SLOT_BLOCK=<cols> forces a slot list with that block width, 0 none."""
     K, N = X.shape
+    seg = os.environ.get("SLK_SEG")
+    if seg is not None and seg != "0":
+        cols, slots = (int(v) for v in seg.split("x"))
+        return W._view_segmented(cols, slots)
+    if (seg is None and W.nnz >= _SEG_MIN_NNZ and N >= 1024 and N % 4 == 0
+            and os.environ.get("SLK_SLOT_BLOCK") is None):
+        return W._view_segmented(*_seg_shape(W, K, N))
     forced = os.environ.get("SLK_SLOT_BLOCK")
     if forced is not None:
         return W._view_listed(int(forced)) if int(forced) > 0 else W._view()

@@ -182,3 +182,30 @@ def test_sddmm_bias_rejects_null_dbias_on_the_host():
     rc = lib.slk_sddmm_bias(ctypes.byref(v), None, 4, None, 6, 3, None, None, _lib.SLK_DW_SIMD,
                             None)
     assert rc == _lib.SLK_EINVAL and "dbias" in lib.slk_last_error().decode()
+
+
+def test_segment_list_fields_are_checked_on_the_host():
+    """A view that carries a segment list must carry all of it, with a block
+    width of 64 or 128 and 4 or 8 slots per segment; slk_seg_list_build checks
+    its block width, segment size and output length before any device work."""
+    lib = _lib.load()
+    one = ctypes.c_int32(0)
+    p = ctypes.addressof(one)
+    good = dict(seg_start=p, seg_row=p, seg_count=p, seg_groups=p, n_seg=64, seg_block=64,
+                seg_slots=4)
+    for bad in ({"seg_row": None}, {"seg_groups": None}, {"seg_block": 32}, {"seg_slots": 6},
+                {"n_seg": -1}):
+        f = dict(good, **bad)
+        v = _lib.CsrView(4, 6, 0, None, None, 1, 1, 1, **f)
+        rc = lib.slk_sddmm(ctypes.byref(v), None, 4, None, 6, 3, None, _lib.SLK_DW_SIMD, None)
+        assert rc == _lib.SLK_EINVAL and "segment list" in lib.slk_last_error().decode(), bad
+    v = _view()
+    for cols, slots, word in ((32, 4, "block_cols"), (64, 5, "seg_slots")):
+        rc = lib.slk_seg_list_build(ctypes.byref(v), cols, slots, None, 0, p, p, p, 64, p, None)
+        assert rc == _lib.SLK_EINVAL and word in lib.slk_last_error().decode()
+    need = lib.slk_seg_list_capacity(ctypes.byref(_lib.CsrView(4, 6, 40, None, None, 1, 1, 1)),
+                                     64, 4)
+    assert need == 40 // 4 + min(40, 4 * 1) + 63 + 64
+    vc = _lib.CsrView(4, 6, 40, 1, 1, 1, 1, 1)
+    rc = lib.slk_seg_list_build(ctypes.byref(vc), 64, 4, None, 0, p, p, p, need - 1, p, None)
+    assert rc == _lib.SLK_EINVAL and "n_seg" in lib.slk_last_error().decode()

@@ -267,6 +267,29 @@ def test_row_order_schedule_bit_exact(dev, N):
     assert_bits_equal(Y.cpu().numpy(), want, "Y (natural order)")
 
 
+def test_gather_path_skewed_rows_wide_N_bit_exact(dev):
+    """A skewed matrix too sparse for the LDS kernel, at N >= 1024 (the 16-byte
+    gather kernel over the longest-first order): rows from fully dense to
+    empty give the reference's bits, with and without bias."""
+    print("[gather skewed wide N]", flush=True)
+    c = oracle.zipf_rows(2500, 600, 0.01, 1.1, seed=17, sigma=0.5)
+    assert c.row_nnz.max() == 600 and c.row_nnz.min() == 0
+    rng = np.random.default_rng(17)
+    N = 1040
+    X_np = rng.standard_normal((600, N)).astype(np.float32)
+    b_np = rng.standard_normal(2500).astype(np.float32)
+    W = from_oracle(c, dev)
+    v = W._view()
+    assert v.row_order is not None and v.n_heavy_rows > 0
+    X = _t(X_np, dev)
+    want = oracle.spmm(c, X_np)
+    Y = torch.full((2500, N), float("nan"), device=dev)
+    _lib.spmm(v, X, Y)
+    assert_bits_equal(Y.cpu().numpy(), want, "Y")
+    _lib.spmm(v, X, Y, _t(b_np, dev))
+    assert_bits_equal(Y.cpu().numpy(), want + b_np[:, None], "Y+bias")
+
+
 @pytest.mark.parametrize("h,rw", [(1, 2), (1, 4), (1, 8), (2, 2), (2, 4)])
 def test_row_order_lds_kernel_bit_exact(dev, monkeypatch, h, rw):
     """Every LDS-staged kernel variant gives the natural order's bits whatever
@@ -741,3 +764,113 @@ def test_sddmm_slot_list_order_bit_exact(dev, monkeypatch, G, block):
     db_flat = torch.empty(150, device=dev)
     _lib.sddmm(W._view(), dY, X, torch.empty_like(dW), _lib.SLK_DW_SIMD, db_flat)
     assert torch.equal(db, db_flat)
+
+
+def _expected_seg_list(c, block, S, n):
+    """The padded segment list, restated in numpy: for every column block, for
+    every row, the row's run of live slots in the block cut into segments of at
+    most S slots; each block padded with empty segments (row 0, slot 0, count 0)
+    to a multiple of SEG_GROUP; n entries in all."""
+    G = _lib.SEG_GROUP
+    start, row, cnt = [], [], []
+    nb = -(-c.ncols // block)
+    for b in range(nb):
+        k0 = len(start)
+        for r in range(c.nrows):
+            s0 = int(c.row_start[r])
+            cols = c.col_indices[s0:s0 + int(c.row_nnz[r])]
+            a = s0 + int(np.searchsorted(cols, b * block))
+            e = s0 + int(np.searchsorted(cols, (b + 1) * block))
+            for s in range(a, e, S):
+                start.append(s)
+                row.append(r)
+                cnt.append(min(S, e - s))
+        pad = (-(len(start) - k0)) % G
+        start += [0] * pad
+        row += [0] * pad
+        cnt += [0] * pad
+    groups = len(start) // G
+    assert len(start) <= n
+    fill = n - len(start)
+    as32 = lambda v: np.asarray(v + [0] * fill, dtype=np.int32)
+    return as32(start), as32(row), as32(cnt), groups
+
+
+@pytest.mark.parametrize("S", [4, 8])
+@pytest.mark.parametrize("shape,density,block", [
+    ((150, 300), 0.06, 64),
+    ((150, 300), 0.3, 128),
+    ((3000, 257), 0.02, 64),      # more rows than the scan's 1024 threads
+    ((5, 4100), 0.3, 128),        # 33 blocks, a last block of 4 columns
+    ((64, 64), 1.0, 64),          # fully dense: 16 or 8 full segments per row
+])
+def test_seg_list_build_matches_the_restatement(dev, S, shape, density, block):
+    """slk_seg_list_build writes exactly the numpy restatement's padded list
+    (segments block by block and row by row, runs cut every S slots, blocks
+    padded to whole groups, the rest of the arrays empty) and the group count,
+    for skewed rows including an empty one."""
+    M, K = shape
+    print(f"[seg list] S={S} shape={shape} d={density} block={block}", flush=True)
+    c = oracle.zipf_rows(M, K, density, 1.1, seed=M + K + block + S, sigma=0.5)
+    c.row_nnz[M // 2] = 0
+    c.col_indices[c.row_start[M // 2]:c.row_start[M // 2] + c.row_capacity[M // 2]] = -1
+    W = from_oracle(c, dev)
+    start, row, cnt, groups = _lib.seg_list_build(W._view(), block, S, dev)
+    want = _expected_seg_list(c, block, S, start.numel())
+    assert np.array_equal(start.cpu().numpy(), want[0])
+    assert np.array_equal(row.cpu().numpy(), want[1])
+    assert np.array_equal(cnt.cpu().numpy(), want[2])
+    assert int(groups.item()) == want[3]
+
+
+def test_seg_list_build_rejects_bad_arguments(dev):
+    c = oracle.zipf_rows(16, 32, 0.2, 1.1, seed=3)
+    W = from_oracle(c, dev)
+    with pytest.raises(ValueError, match="block_cols"):
+        _lib.seg_list_build(W._view(), 32, 4, dev)
+    with pytest.raises(ValueError, match="seg_slots"):
+        _lib.seg_list_build(W._view(), 64, 6, dev)
+    lib = _lib.load()
+    view = W._view()
+    n = int(lib.slk_seg_list_capacity(ctypes.byref(view), 64, 4))
+    out = torch.empty(n, dtype=torch.int32, device=dev)
+    rc = lib.slk_seg_list_build(ctypes.byref(view), 64, 4, None, 0, _lib.ptr(out), _lib.ptr(out),
+                                _lib.ptr(out), n - 1, _lib.ptr(out), None)
+    assert rc != 0 and b"n_seg" in lib.slk_last_error()
+
+
+@pytest.mark.parametrize("block,S", [(64, 4), (64, 8), (128, 4), (128, 8)])
+@pytest.mark.parametrize("M,K,density,N", [
+    (200, 256, 0.5, 1024),    # dense rows: several full segments per run
+    (3000, 300, 0.02, 1100),  # sparse skewed rows: many short segments, many groups
+    (700, 200, 0.1, 1032),    # partial last window, 8-wide step
+    (500, 130, 0.2, 1045),    # scalar tail, a last block narrower than the block width
+    (90, 150, 0.3, 16),       # one 16-float step: a single, partial window
+    (90, 150, 0.3, 60),       # 8-wide step and tail after three steps
+])
+def test_sddmm_seg_kernel_bit_exact(dev, block, S, M, K, density, N):
+    """slk_sddmm on a segment list (X staged in LDS per workgroup, each
+    segment's dY row in registers) gives the oracle's bits: full and partial
+    windows, the 8-wide step and scalar tail, narrow last blocks, empty rows,
+    empty padding segments, zeroed padding slots and the fused bias gradient."""
+    print(f"[dW seg] block={block} S={S} M={M} K={K} d={density} N={N}", flush=True)
+    c = oracle.zipf_rows(M, K, density, 0.6, seed=M + N + S, sigma=0.5)
+    c.row_nnz[M // 3] = 0
+    c.col_indices[c.row_start[M // 3]:c.row_start[M // 3] + c.row_capacity[M // 3]] = -1
+    rng = np.random.default_rng(N + S)
+    X_np = rng.standard_normal((K, N)).astype(np.float32)
+    dY_np = rng.standard_normal((M, N)).astype(np.float32)
+    W = from_oracle(c, dev)
+    X, dY = _t(X_np, dev), _t(dY_np, dev)
+    view = W._view_segmented(block, S)
+    assert view.seg_block == block and view.seg_slots == S
+    dW = torch.full((W.total_capacity,), float("nan"), device=dev)
+    db = torch.full((M,), float("nan"), device=dev)
+    _lib.sddmm(view, dY, X, dW, _lib.SLK_DW_SIMD, db)
+    assert_bits_equal(dW.cpu().numpy(), oracle.sddmm(c, dY_np, X_np), "dW seg")
+    db_ref = torch.empty(M, device=dev)
+    _lib.sddmm(W._view(), dY, X, torch.empty_like(dW), _lib.SLK_DW_SIMD, db_ref)
+    assert torch.equal(db, db_ref)
+    dW2 = torch.full((W.total_capacity,), float("nan"), device=dev)
+    _lib.sddmm(view, dY, X, dW2, _lib.SLK_DW_SIMD)
+    assert_bits_equal(dW2.cpu().numpy(), oracle.sddmm(c, dY_np, X_np), "dW seg, no bias")
