@@ -19,7 +19,7 @@ import torch.nn as nn
 import oracle
 import sparsecore_amd as slk
 from helpers import assert_bits_equal, from_oracle, make_sparse_W, to_oracle
-from sparsecore_amd import PaddedCSR, SparseLinear
+from sparsecore_amd import PaddedCSR, SparseLinear, _lib
 from sparsecore_amd.ops import (_SpMMFunction, _cached_transpose, _clear_transpose_cache,
                                 _transpose_cache)
 
@@ -640,3 +640,31 @@ def test_state_dict_topology_roundtrip_on_device(dev):
     ya.backward(up)
     yb.backward(up)
     assert torch.equal(a._values.grad, b._values.grad) and torch.equal(a.bias.grad, b.bias.grad)
+
+
+@pytest.mark.parametrize("sparsity,batch", [(0.7, 1024), (0.95, 1100), (0.9, 1032)])
+def test_sparse_linear_dW_through_the_default_schedules(dev, monkeypatch, sparsity, batch):
+    """SparseLinear's weight gradient through the schedule the library picks
+    for large layers (a segment list from _SEG_MIN_NNZ live slots at N >= 1024,
+    with the block width and segment size _seg_shape gives), with the threshold
+    lowered so a small layer takes it: dW is the oracle's SIMD-order dW of the
+    same layer and upstream gradient, bit for bit, and dbias its row sums."""
+    from sparsecore_amd import ops
+
+    monkeypatch.setattr(ops, "_SEG_MIN_NNZ", 1000)
+    torch.manual_seed(int(sparsity * 100) + batch)
+    layer = SparseLinear(300, 200, sparsity=sparsity).to(dev)
+    W = layer._csr
+    x = torch.randn(batch, 300, device=dev)
+    view = ops._sddmm_view(W, x.t().contiguous())
+    want_shape = ops._seg_shape(W, 300, batch)
+    assert view.seg_start is not None and (view.seg_block, view.seg_slots) == want_shape
+    up = torch.randn(batch, 200, device=dev)
+    layer(x).backward(up)
+    c = to_oracle(W)
+    ref = oracle.sddmm(c, up.t().contiguous().cpu().numpy(), x.t().contiguous().cpu().numpy())
+    assert_bits_equal(layer._values.grad.cpu().numpy(), ref, "dW (segment schedule)")
+    db = torch.empty(200, device=dev)
+    _lib.sddmm(W._view(), up.t().contiguous(), x.t().contiguous(),
+               torch.empty(W.total_capacity, device=dev), _lib.SLK_DW_SIMD, db)
+    assert torch.equal(layer.bias.grad, db)
