@@ -104,8 +104,8 @@ typedef struct slk_csr {
      * int32) holds the number of such groups in use; n_seg is the arrays'
      * length. slk_sddmm then gives each group of segments one workgroup that
      * stages the block's X rows in LDS and keeps each segment's dY row in
-     * registers; results are the same either way. A schedule the caller
-     * caches per topology. */
+     * registers, consecutive groups on one XCD; results are the same either
+     * way. A schedule the caller caches per topology. */
     const int32_t* seg_start;
     const int32_t* seg_row;
     const int32_t* seg_count;

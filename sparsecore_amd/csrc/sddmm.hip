@@ -664,10 +664,16 @@ __global__ __launch_bounds__(kSegThreads) void sddmm_seg_kernel(
         if (dbias != nullptr) bias_row_sum(dY, M, N, row, dbias, N, 1);
         return;
     }
-    if (grp >= groups[0]) return;  // block-uniform
-    const int64_t e0 = grp * SLK_SEG_GROUP;
+    // Groups in use G: workgroups [0, G) take them in XCD-contiguous order
+    // (a bijection on [0, G)), so the groups an XCD runs together mostly lie
+    // in one column block and share its X band in that XCD's L2 (C4 768x3072
+    // layer 281 -> 232 us). Ordering the list by row panels to share dY rows
+    // instead was slower: the concurrent groups then span many X bands.
+    const int64_t G = groups[0];
+    if (grp >= G) return;  // block-uniform
+    const int64_t e0 = xcd_logical_block(grp, G) * SLK_SEG_GROUP;
     const int32_t c_lo = col[seg_start[e0]] / C * C;  // a group's first segment is never empty
-    const int64_t e = e0 + (threadIdx.x >> 2);
+    const int64_t e = e0 + (threadIdx.x >> 2);  // this quad's segment
     const int32_t s0 = seg_start[e];
     const int32_t cnt = seg_count[e];
     const int64_t row = seg_row[e];
