@@ -44,7 +44,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "SpMM fwd+dX+dW achieved HBM GB/s & effective GFLOP/s; train-step tokens/s"
 HBM_PEAK_GBS = 8000.0
-FP32_VALU_PEAK_TFLOPS = 157.3
+VALU_PEAK_TFLOPS = 78.6  # MI355X fp32 vector fma, non-packed (157.3 is the packed-fp32 figure)
 
 
 def parse_args():
@@ -1120,6 +1120,15 @@ def main():
         "roofline": {"bound": "hbm", "kernel": dom["kernel"], "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
+        # The same kernel against the fp32 fma rate of the vector ALUs (the
+        # kernels compute on the VALU; MFMA is not used): 2 flops per fma of
+        # the 2*nnz*N algorithmic flops over the non-packed peak (256 CUs x 64
+        # fma/clk x 2.4 GHz x 2 = 78.6 TFLOP/s).
+        "compute_roofline": {"kernel": dom["kernel"],
+                             "achieved": round(dom["flops"] / (dom["avg_us"] * 1e-6) / 1e12, 3),
+                             "peak": VALU_PEAK_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(dom["flops"] / (dom["avg_us"] * 1e-6) / 1e12 /
+                                           VALU_PEAK_TFLOPS, 4)},
         "cpu_baseline": None,
     }
     if args.calibrate_copy_mib > 0:
