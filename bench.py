@@ -601,7 +601,7 @@ class LayerWork:
         Y = torch.empty(M, N, device=self.dev)
         dW = torch.empty(W.total_capacity, device=self.dev)
         dX = torch.empty(K, N, device=self.dev)
-        v, vT = W._view(), WT._view()
+        v, vT = ops._spmm_view(W, self.X), ops._spmm_view(WT, self.dY)
         return [
             ("spmm_fwd", lambda: _lib.spmm(v, self.X, Y), bytes_fwd(W.nnz, M, K, N),
              flops(W.nnz, N)),

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define SLK_ABI_VERSION 7
+#define SLK_ABI_VERSION 8
 
 #if defined(__GNUC__)
 #define SLK_API __attribute__((visibility("default")))
@@ -113,6 +113,15 @@ typedef struct slk_csr {
     int64_t n_seg;
     int64_t seg_block;
     int64_t seg_slots;
+    /* Optional (may be NULL): phase bounds for slk_spmm's gather kernel, as
+     * built by slk_phase_bounds_build: phase_lo[r*(n_phases+1) + p] is the
+     * first live slot of row r whose column is >= p*ceil(ncols/n_phases). The
+     * kernel then sweeps the columns in n_phases launches, each row's fma
+     * chain continuing from the partial sum the previous phase left in Y, so
+     * the X rows that one phase gathers fit the L2s; the chain, and so every
+     * bit, is the same. A schedule the caller caches per topology. */
+    const int32_t* phase_lo;
+    int64_t n_phases;
 } slk_csr;
 
 /* Segments per group of a segment list (one slk_sddmm workgroup each). */
@@ -333,6 +342,14 @@ SLK_API int slk_seg_list_build(const slk_csr* W, int64_t block_cols, int64_t seg
                                void* workspace, int64_t workspace_bytes, int32_t* seg_start,
                                int32_t* seg_row, int32_t* seg_count, int64_t n_seg,
                                int32_t* seg_groups, void* stream);
+
+/* Builds the optional phase bounds of slk_csr (see phase_lo there) on the
+ * device: phase_lo receives W->nrows * (n_phases + 1) int32 entries, n_phases
+ * >= 1. No counterpart in the reference (csrc/kernels/spmm_avx2.cpp walks
+ * each row's slots in one pass): a visiting schedule for slk_spmm that leaves
+ * every output bit unchanged.                                               */
+SLK_API int slk_phase_bounds_build(const slk_csr* W, int64_t n_phases, int32_t* phase_lo,
+                                   void* stream);
 
 #ifdef __cplusplus
 }

@@ -21,7 +21,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libsparsecore_amd.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 SLK_OK, SLK_EINVAL, SLK_EDEVICE = 0, 1, 2
 SLK_DW_SIMD, SLK_DW_SCALAR = 0, 1
@@ -54,6 +54,7 @@ EXPORTS = (
     "slk_seg_list_capacity",
     "slk_seg_list_workspace_bytes",
     "slk_seg_list_build",
+    "slk_phase_bounds_build",
 )
 
 SEG_GROUP = 64  # SLK_SEG_GROUP
@@ -87,6 +88,8 @@ class CsrView(ctypes.Structure):
         ("n_seg", ctypes.c_int64),
         ("seg_block", ctypes.c_int64),
         ("seg_slots", ctypes.c_int64),
+        ("phase_lo", ctypes.c_void_p),
+        ("n_phases", ctypes.c_int64),
     ]
 
 
@@ -132,6 +135,7 @@ def _declare(lib) -> None:
     lib.slk_seg_list_workspace_bytes.argtypes = [_csrp, _i64]
     lib.slk_seg_list_build.argtypes = [_csrp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp,
                                        _vp]
+    lib.slk_phase_bounds_build.argtypes = [_csrp, _i64, _vp, _vp]
     sized = ("slk_last_error", "slk_abi_version", "slk_transpose_workspace_bytes",
              "slk_drop_grow_workspace_bytes", "slk_slot_list_workspace_bytes",
              "slk_seg_list_capacity", "slk_seg_list_workspace_bytes")
@@ -344,6 +348,18 @@ def seg_list_build(view: CsrView, block_cols: int, seg_slots: int, device):
     if rc:
         _raise(rc)
     return start, row, count, groups
+
+
+def phase_bounds_build(view: CsrView, n_phases: int, device) -> torch.Tensor:
+    """int32 tensor of nrows * (n_phases + 1) entries: for each row the first
+    live slot whose column is >= p * ceil(ncols / n_phases), p = 0..n_phases
+    (slk_phase_bounds_build)."""
+    lib = load()
+    lo = torch.empty(max(1, view.nrows * (int(n_phases) + 1)), dtype=torch.int32, device=device)
+    rc = lib.slk_phase_bounds_build(ctypes.byref(view), int(n_phases), ptr(lo), stream_of(lo))
+    if rc:
+        _raise(rc)
+    return lo
 
 
 def transpose_dense(src: torch.Tensor, dst: torch.Tensor) -> None:

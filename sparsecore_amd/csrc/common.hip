@@ -55,6 +55,10 @@ int validate_csr(const slk_csr* W, const char* who) {
                                     ": a segment list needs seg_row, seg_count, seg_groups, "
                                     "n_seg >= 0, seg_block 64 or 128 and seg_slots 4 or 8");
     }
+    if (W->phase_lo != nullptr && W->n_phases < 1) {
+        return fail(SLK_EINVAL, std::string(who) + ": phase_lo needs n_phases >= 1, got " +
+                                    std::to_string(W->n_phases));
+    }
     return SLK_OK;
 }
 

@@ -322,3 +322,25 @@ extern "C" int slk_seg_list_build(const slk_csr* W, int64_t block_cols, int64_t 
     }
     return check_launch("seg_list/scatter");
 }
+
+extern "C" int slk_phase_bounds_build(const slk_csr* W, int64_t n_phases, int32_t* phase_lo,
+                                      void* stream) {
+    using namespace slk;
+    clear_error();
+    if (int rc = validate_csr(W, "phase_bounds")) return rc;
+    if (n_phases < 1) {
+        return fail(SLK_EINVAL, "phase_bounds: n_phases must be >= 1, got " +
+                                    std::to_string(n_phases));
+    }
+    const int64_t M = W->nrows, K = W->ncols;
+    if (M == 0) return SLK_OK;
+    if (phase_lo == nullptr) return fail(SLK_EINVAL, "phase_bounds: NULL phase_lo");
+    const int64_t n = M * (n_phases + 1);
+    if (ceil_div(n, kSchedThreads) > INT32_MAX) return fail(SLK_EINVAL, "phase_bounds: too large");
+    // the slot list's first pass with blocks of ceil(K / n_phases) columns
+    const int64_t C = std::max<int64_t>(1, ceil_div(K, n_phases));
+    hipLaunchKernelGGL(sl_bounds_kernel, dim3(static_cast<unsigned>(ceil_div(n, kSchedThreads))),
+                       dim3(kSchedThreads), 0, as_stream(stream), M, n_phases, C, W->row_start,
+                       W->row_nnz, W->col_indices, phase_lo);
+    return check_launch("phase_bounds");
+}

@@ -154,12 +154,17 @@ __device__ __forceinline__ void load_meta(const int32_t* __restrict__ col,
 }
 
 // TOUT: Y is stored token-major, Y[i, n] at Y[n·M + i] (slk_spmm_t).
-template <int VEC, int U, bool TOUT = false>
+// PH: phase `ph` of `nph` (slk_csr.phase_lo): the row's slots
+// [plo[row·(nph+1) + ph], plo[row·(nph+1) + ph + 1]) continue the fma chain
+// from the partial sums the previous phase stored in Y (from +0.0 in phase
+// 0); the caller passes bias only with the last phase.
+template <int VEC, int U, bool TOUT = false, bool PH = false>
 __global__ __launch_bounds__(kSpmmBlock) void spmm_wave_kernel(
     int64_t M, int64_t N, int64_t nitems, const int32_t* __restrict__ order,
     const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
     const int32_t* __restrict__ col, const float* __restrict__ val,
-    const float* __restrict__ X, const float* __restrict__ bias, float* __restrict__ Y) {
+    const float* __restrict__ X, const float* __restrict__ bias, float* __restrict__ Y,
+    const int32_t* __restrict__ plo = nullptr, int64_t nph = 1, int64_t ph = 0) {
     typedef typename VecIO<VEC>::T T;
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t item = wave_id();
@@ -169,13 +174,26 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_wave_kernel(
     const int64_t row = order != nullptr ? order[r] : r;
     const int64_t n0 = (tile * kWave + lane) * VEC;
     const bool active = n0 < N;  // N % VEC == 0, so n0 + VEC <= N
-    const int32_t start = row_start[row];
-    const int32_t nnz = row_nnz[row];
+    int32_t start, nnz;
+    if constexpr (PH) {
+        start = plo[row * (nph + 1) + ph];
+        nnz = plo[row * (nph + 1) + ph + 1] - start;
+    } else {
+        start = row_start[row];
+        nnz = row_nnz[row];
+    }
     const uint32_t off = static_cast<uint32_t>(n0) * 4u;  // 4N < 2^31 (launcher check)
 
     float acc[VEC];
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
+    if constexpr (PH) {
+        if (ph > 0 && active) {
+            const typename VecIO<VEC>::T y = VecIO<VEC>::load(Y + row * N + n0);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) acc[e] = VecIO<VEC>::get(y, e);
+        }
+    }
 
     static_assert(kWave % (2 * U) == 0, "a full chunk holds an even number of batches");
     int32_t mc, nmc = 0;
@@ -679,6 +697,23 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
         while (L < 32 && L < N) L <<= 1;
         if (L < kWave && L >= N) return launch_group_L(L, W, X, N, bias, Y, st);
         vec = 1;
+    }
+    if (vec == 4 && W->phase_lo != nullptr && W->n_phases > 1) {
+        // phased sweep: one launch per column phase, stream-ordered, so each
+        // phase reads the partial sums its predecessor stored
+        constexpr int U = 8;
+        const int64_t nitems = M * ceil_div(N, int64_t{kWave} * 4);
+        int64_t blocks;
+        if (int rc = launch_blocks(nitems, &blocks)) return rc;
+        for (int64_t ph = 0; ph < W->n_phases; ++ph) {
+            const float* b = ph + 1 == W->n_phases ? bias : nullptr;
+            hipLaunchKernelGGL((spmm_wave_kernel<4, U, false, true>),
+                               dim3(static_cast<unsigned>(blocks)), dim3(kSpmmBlock), 0, st, M,
+                               N, nitems, W->row_order, W->row_start, W->row_nnz,
+                               W->col_indices, W->values, X, b, Y, W->phase_lo, W->n_phases, ph);
+            if (int rc = check_launch("spmm")) return rc;
+        }
+        return SLK_OK;
     }
     if (vec == 4) return launch_wave<4>(W, X, N, bias, Y, st);
     if (vec == 2) return launch_wave<2>(W, X, N, bias, Y, st);

@@ -271,6 +271,10 @@ class PaddedCSR:
         self._order = None      # (topology_version, device row schedule, heavy rows)
         self._slist = None      # ((topology_version, block_cols), view with a slot list)
         self._seglist = None    # ((topology_version, block_cols, seg_slots), segmented view)
+        self._phased = None     # ((topology_version, n_phases), view with phase bounds)
+        # True when a few columns hold many of the slots (a transpose of a
+        # matrix with heavy rows): its gathers already stay in cache
+        self._cols_skewed = False
         self._host_rows = None  # cached numpy (row_start, row_nnz, row_capacity)
         self._heavy_hint = None  # heavy_row_count(row_nnz) when a builder counted it
 
@@ -411,6 +415,21 @@ class PaddedCSR:
                           seg_slots=int(seg_slots))
             self._seglist = (key, _lib.CsrView(**fields), arrays)
         return self._seglist[1]
+
+    def _view_phased(self, n_phases: int) -> _lib.CsrView:
+        """The view plus phase bounds for slk_spmm's gather kernel
+        (slk_csr.phase_lo): the columns swept in n_phases launches, each row's
+        chain resumed from Y, so the X rows one phase gathers fit the L2s.
+        Built on the device (slk_phase_bounds_build, one launch) once per
+        topology."""
+        base = self._view()
+        key = (self._topology_version, int(n_phases), id(base))
+        if self._phased is None or self._phased[0] != key:
+            lo = _lib.phase_bounds_build(base, int(n_phases), self.device)
+            fields = {f: getattr(base, f) for f, _ in _lib.CsrView._fields_}
+            fields.update(phase_lo=_lib.ptr(lo), n_phases=int(n_phases))
+            self._phased = (key, _lib.CsrView(**fields), lo)
+        return self._phased[1]
 
     def _rows_host(self):
         h = self._host_rows
@@ -811,6 +830,7 @@ def transpose_with_perm(p: PaddedCSR, *, padding_ratio: float = 0.2):
     _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, capT, val_t, col_t, perm)
     WT = PaddedCSR._from_parts(K, M, val_t, col_t, rs_t, nnz_t, cap_t, p.nnz)
     WT._heavy_hint = heavy
+    WT._cols_skewed = view.n_heavy_rows > 0  # WT's columns are p's rows
     return WT, perm
 
 
@@ -866,6 +886,7 @@ def transposes_with_perm(ps, *, padding_ratio: float = 0.2):
         _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, capT, val_t, col_t, perm)
         WT = PaddedCSR._from_parts(p.ncols, p.nrows, val_t, col_t, rs_t, nnz_t, cap_t, p.nnz)
         WT._heavy_hint = heavy
+        WT._cols_skewed = view.n_heavy_rows > 0  # WT's columns are p's rows
         out.append((WT, perm))
     return out
 

@@ -209,3 +209,15 @@ def test_segment_list_fields_are_checked_on_the_host():
     vc = _lib.CsrView(4, 6, 40, 1, 1, 1, 1, 1)
     rc = lib.slk_seg_list_build(ctypes.byref(vc), 64, 4, None, 0, p, p, p, need - 1, p, None)
     assert rc == _lib.SLK_EINVAL and "n_seg" in lib.slk_last_error().decode()
+
+
+def test_phase_bounds_are_checked_on_the_host():
+    """A view with phase bounds needs n_phases >= 1; slk_phase_bounds_build
+    rejects fewer than one phase before any device work."""
+    lib = _lib.load()
+    one = ctypes.c_int32(0)
+    v = _lib.CsrView(4, 6, 0, None, None, 1, 1, 1, phase_lo=ctypes.addressof(one), n_phases=0)
+    rc = lib.slk_spmm(ctypes.byref(v), None, 6, 3, None, None)
+    assert rc == _lib.SLK_EINVAL and "n_phases" in lib.slk_last_error().decode()
+    rc = lib.slk_phase_bounds_build(ctypes.byref(_view()), 0, ctypes.addressof(one), None)
+    assert rc == _lib.SLK_EINVAL and "n_phases" in lib.slk_last_error().decode()

@@ -874,3 +874,52 @@ def test_sddmm_seg_kernel_bit_exact(dev, block, S, M, K, density, N):
     dW2 = torch.full((W.total_capacity,), float("nan"), device=dev)
     _lib.sddmm(view, dY, X, dW2, _lib.SLK_DW_SIMD)
     assert_bits_equal(dW2.cpu().numpy(), oracle.sddmm(c, dY_np, X_np), "dW seg, no bias")
+
+
+@pytest.mark.parametrize("P", [1, 2, 3, 7, 40])
+def test_phase_bounds_build_matches_searchsorted(dev, P):
+    """slk_phase_bounds_build gives, for every row and phase boundary
+    p * ceil(K / P), the first live slot at or past that column (numpy's
+    searchsorted over the row's ascending columns), empty rows included."""
+    c = oracle.zipf_rows(700, 300, 0.05, 1.1, seed=P, sigma=0.5)
+    c.row_nnz[5] = 0
+    c.col_indices[c.row_start[5]:c.row_start[5] + c.row_capacity[5]] = -1
+    W = from_oracle(c, dev)
+    lo = _lib.phase_bounds_build(W._view(), P, dev).cpu().numpy().reshape(700, P + 1)
+    C = -(-300 // P)
+    for r in range(700):
+        s0 = int(c.row_start[r])
+        cols = c.col_indices[s0:s0 + int(c.row_nnz[r])]
+        want = s0 + np.searchsorted(cols, np.arange(P + 1) * C)
+        assert np.array_equal(lo[r], want), r
+
+
+@pytest.mark.parametrize("P", [2, 3, 7])
+@pytest.mark.parametrize("N,order", [(1024, True), (1032, False), (260, True)])
+def test_spmm_phased_sweep_bit_exact(dev, monkeypatch, P, N, order):
+    """The 16-byte gather kernel swept in P column phases, each row's fma chain
+    resumed from the partial sums the previous phase left in Y, gives the
+    one-pass chain's bits — with and without bias (added once, after the last
+    phase), under the longest-first row order and without one, for rows from
+    fully dense to empty."""
+    monkeypatch.setenv("SLK_SPMM_KERNEL", "wave")
+    monkeypatch.setenv("SLK_SPMM_VEC", "4")
+    print(f"[spmm phased] P={P} N={N} order={order}", flush=True)
+    c = oracle.zipf_rows(2500, 600, 0.02, 1.1, seed=P + N, sigma=0.5)
+    c.row_nnz[11] = 0
+    c.col_indices[c.row_start[11]:c.row_start[11] + c.row_capacity[11]] = -1
+    rng = np.random.default_rng(P * N)
+    X_np = rng.standard_normal((600, N)).astype(np.float32)
+    b_np = rng.standard_normal(2500).astype(np.float32)
+    W = from_oracle(c, dev)
+    v = W._view_phased(P)
+    assert v.n_phases == P and v.phase_lo is not None
+    if not order:
+        v = _with_fields(v, row_order=None, n_heavy_rows=0)
+    X = _t(X_np, dev)
+    want = oracle.spmm(c, X_np)
+    Y = torch.full((2500, N), float("nan"), device=dev)
+    _lib.spmm(v, X, Y)
+    assert_bits_equal(Y.cpu().numpy(), want, "Y phased")
+    _lib.spmm(v, X, Y, _t(b_np, dev))
+    assert_bits_equal(Y.cpu().numpy(), want + b_np[:, None], "Y+bias phased")
