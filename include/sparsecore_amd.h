@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define SLK_ABI_VERSION 8
+#define SLK_ABI_VERSION 9
 
 #if defined(__GNUC__)
 #define SLK_API __attribute__((visibility("default")))
@@ -75,18 +75,6 @@ typedef struct slk_csr {
      * grid; results are the same either way. Not part of the reference
      * layout — a schedule the caller caches per topology. */
     const int32_t* row_order;
-    /* Optional (may be NULL): the live slots listed column block by column
-     * block (then by row, then by column), with each entry's row, the number
-     * of entries and the block width in columns (slk_slot_list_build's
-     * block_cols; 0 if unknown). slk_sddmm then visits the slots in that
-     * order, so the waves resident at one moment gather from one band of X
-     * rows, and with a block of at most 128 columns it stages each
-     * workgroup's X and dY rows in LDS; results are the same either way. A
-     * schedule the caller caches per topology. */
-    const int32_t* slot_list;
-    const int32_t* slot_list_row;
-    int64_t n_slot_list;
-    int64_t slot_list_block;
     /* Rows at the head of row_order that are long against the rest (0 = none;
      * needs row_order; at most nrows). When slk_spmm runs its LDS-staged
      * kernel it runs them as a launch of their own, with fewer rows per
@@ -132,6 +120,33 @@ SLK_API const char* slk_last_error(void);
 
 /* SLK_ABI_VERSION of the loaded library. */
 SLK_API int slk_abi_version(void);
+
+/* Kernel-choice overrides, process-wide, for tests and measurement. No
+ * counterpart in the reference (its dispatch is the compile-time
+ * AVX2/NEON/scalar choice of csrc/bindings.cpp). Every launcher chooses its
+ * kernel variant from the problem shape; a knob set to a value >= 0 replaces
+ * that choice for every later launch until it is set back to -1
+ * (automatic). Results are the same bits under every setting; only the
+ * schedule changes. Values:
+ *   SLK_TUNE_SPMM_KERNEL  0 = per-wave gather kernel, 1 = LDS-staged kernel
+ *   SLK_TUNE_SPMM_H       LDS kernel: 1 or 2 column halves per lane
+ *   SLK_TUNE_SPMM_RW      LDS kernel: rows per wave (2, 4 or 8)
+ *   SLK_TUNE_SPMM_SPLIT   LDS kernel: 0 = no separate launch for heavy rows
+ *   SLK_TUNE_SPMM_VEC     gather kernel: floats per lane (1, 2 or 4)
+ *   SLK_TUNE_SDDMM_G      windowed dW kernel: groups per wave (1, 2 or 4)
+ *   SLK_TUNE_SEG_LEAN     segment dW kernel: 1 = lean variant, 0 = not
+ * Returns SLK_EINVAL for an unknown knob.                                   */
+enum slk_tune_knob {
+    SLK_TUNE_SPMM_KERNEL = 0,
+    SLK_TUNE_SPMM_H = 1,
+    SLK_TUNE_SPMM_RW = 2,
+    SLK_TUNE_SPMM_SPLIT = 3,
+    SLK_TUNE_SPMM_VEC = 4,
+    SLK_TUNE_SDDMM_G = 5,
+    SLK_TUNE_SEG_LEAN = 6,
+    SLK_TUNE_COUNT = 7
+};
+SLK_API int slk_set_tuning(int knob, int64_t value);
 
 /* Y = W·X. Replaces `spmm_simd` / `spmm_scalar` (csrc/bindings.cpp:243-272,
  * kernels csrc/kernels/spmm_avx2.cpp:82-263 and spmm.cpp:20-105). Y is fully
@@ -243,20 +258,25 @@ SLK_API int64_t slk_drop_grow_workspace_bytes(const slk_csr* W);
  * :663-732 for RigL, with its PaddedCSR.rewrite_row calls,
  * csrc/kernels/padded_csr.cpp:219-296). For each row with live slots:
  *   keep the slots with |v| > *thr_dev (if none, the first slot of largest
- *   |v|); n_grow = min(dropped, ncols - kept); grow n_grow columns outside
- *   the kept set with value 0 and write the row back sorted by column.
- * Grow choice: SLK_GROW_GRADIENT takes the n_grow largest |G[i*ldg + c]|
- * (ties: lower column first; NaN last); SLK_GROW_RANDOM takes the n_grow
- * smallest 32-bit keys splitmix64(seed, i*ncols + c), which is a uniform
- * random subset (the reference draws it with numpy's Generator.choice, a
- * stream this cannot reproduce). Row nnz, row_start and capacities never
- * change (a row regrows exactly what it dropped), so only `values` and
- * `col_indices` — which must be W's own arrays — are written. ncols is at
- * most 131072.                                                              */
+ *   |v|); grow n_grow = min(dropped, growable columns) columns outside the
+ *   kept set with value 0 and write the row back sorted by column.
+ * Growable columns: SLK_GROW_RANDOM, every column outside the kept set;
+ * SLK_GROW_GRADIENT, those whose |G[i*ldg + c]| is not NaN (the reference
+ * counts only |G| > -inf as available, router.py:704-705). Grow choice:
+ * SLK_GROW_GRADIENT takes the n_grow largest |G| (ties: lower column
+ * first); SLK_GROW_RANDOM takes the n_grow smallest 32-bit keys
+ * splitmix64(seed, i*ncols + c), which is a uniform random subset (the
+ * reference draws it with numpy's Generator.choice, a stream this cannot
+ * reproduce). row_start and the capacities never change. A row regrows what
+ * it dropped, except a RigL row that runs out of growable columns: it
+ * shrinks, its trailing slots become padding and row_nnz[i] is lowered.
+ * values, col_indices and row_nnz must be W's own arrays. *removed (a
+ * device int64) receives the number of live slots the pass removed in total
+ * (0 unless some row shrank). ncols is at most 131072.                       */
 SLK_API int slk_drop_grow(const slk_csr* W, float* values, int32_t* col_indices,
-                          const float* thr_dev, int rule, const float* G, int64_t ldg,
-                          uint64_t seed, void* workspace, int64_t workspace_bytes,
-                          void* stream);
+                          int32_t* row_nnz, const float* thr_dev, int rule, const float* G,
+                          int64_t ldg, uint64_t seed, void* workspace,
+                          int64_t workspace_bytes, int64_t* removed, void* stream);
 
 /* G = dY·X^T, G is M x K row-major: G[i,k] = sum_j dY[i,j]·X[k,j], each
  * element one running sum over j in order, with the arithmetic of the
@@ -307,20 +327,6 @@ SLK_API int slk_spmm_t(const slk_csr* W, const float* X, int64_t K, int64_t N,
 SLK_API int slk_backward_narrow(const slk_csr* W, const float* dYt, int64_t N, const float* X,
                                 int64_t X_rows, float* dW, float* dbias, float* dX, int order,
                                 void* stream);
-
-/* Bytes of device workspace slk_slot_list_build needs for W and block_cols. */
-SLK_API int64_t slk_slot_list_workspace_bytes(const slk_csr* W, int64_t block_cols);
-
-/* Builds the optional slk_csr.slot_list schedule on the device: W's live
- * slots ordered by column block (block b = columns [b*block_cols,
- * (b+1)*block_cols)), then by row, then by column, into slot_list, with each
- * entry's row in slot_list_row (both nnz entries). Deterministic, no atomics.
- * No counterpart in the reference: its dW loop (csrc/kernels/spmm_grad.cpp,
- * csrc/kernels/spmm_grad_avx2.cpp) walks slots in capacity order; this is
- * a visiting order for slk_sddmm that leaves every output bit unchanged.   */
-SLK_API int slk_slot_list_build(const slk_csr* W, int64_t block_cols, void* workspace,
-                                int64_t workspace_bytes, int32_t* slot_list,
-                                int32_t* slot_list_row, void* stream);
 
 /* Length of the segment arrays slk_seg_list_build needs for W, block_cols
  * and seg_slots (an upper bound on the padded segment count, so the list can

@@ -227,6 +227,25 @@ def transpose_with_perm(p: Csr, padding_ratio: float = 0.2):
     return WT, perm
 
 
+def sub_rows(p: Csr, rows) -> tuple[Csr, np.ndarray]:
+    """The matrix made of the given rows of p (each with its own capacity, in
+    the order given), and for each of its slots the slot of p it came from.
+    Every row's arithmetic in spmm / sddmm depends on that row alone, so the
+    sub-matrix reproduces those rows of p's results at a fraction of the
+    cost (used to check full-size workloads on sampled rows)."""
+    rows = np.asarray(rows, dtype=np.int64)
+    cap = p.row_capacity[rows].astype(np.int64)
+    start = np.zeros(rows.size, dtype=np.int64)
+    if rows.size:
+        start[1:] = np.cumsum(cap[:-1])
+    src = np.concatenate([np.arange(int(p.row_start[r]), int(p.row_start[r]) + int(c),
+                                    dtype=np.int64) for r, c in zip(rows, cap)]
+                         + [np.zeros(0, np.int64)])
+    q = Csr(rows.size, p.ncols, p.values[src], p.col_indices[src], start.astype(np.int32),
+            p.row_nnz[rows], p.row_capacity[rows])
+    return q, src
+
+
 def refresh(WT_values: np.ndarray, W_values: np.ndarray, perm: np.ndarray) -> np.ndarray:
     """Cache-hit value refresh (ops.py:83-94): live WT slots re-read W."""
     out = WT_values.copy()
@@ -324,54 +343,70 @@ def splitmix_keys(seed: int, row: int, ncols: int, cols: np.ndarray) -> np.ndarr
 
 
 def _grow_keys_rigl(g_row: np.ndarray) -> np.ndarray:
-    """Smaller key = preferred: ~bits(|G|), NaN last."""
+    """Smaller key = preferred: ~bits(|G|) (largest |G| first). Only taken
+    for columns whose |G| is not NaN."""
     a = np.abs(g_row.astype(np.float32))
-    keys = ~a.view(np.uint32)
-    keys[np.isnan(a)] = np.uint32(0xFFFFFFFF)
-    return keys
+    return ~a.view(np.uint32)
+
+
+def drop_grow_row(cols: np.ndarray, vals: np.ndarray, thr, rule: str, ncols: int,
+                  g_row: np.ndarray | None = None, seed: int = 0, row: int = 0):
+    """One row of a SET ("random") / RigL ("gradient") update: the new live
+    (cols, vals), sorted by column.
+
+    Follows the per-row loop of router.py:414-478 (SET) and :663-732 (RigL):
+    keep |v| > threshold (the row's first largest |v| if none survive), grow
+    n_grow = min(dropped, growable) columns outside the kept set with value 0,
+    rewrite the row sorted by column. Growable: SET, every column outside the
+    kept set; RigL, those whose |G| is not NaN (router.py:704-705 counts
+    ``available`` as the empties with |G| > -inf), so a RigL row short of them
+    shrinks. Grow choice: the n_grow smallest keys, ties to the lower column;
+    keys are ~bits(|G[i]|) (RigL: largest |G| first) or
+    splitmix_keys(seed, row, ...) (SET).
+    """
+    keep = np.abs(vals) > thr
+    if not keep.any():
+        keep[int(np.argmax(np.abs(vals)))] = True
+    kc, kv = cols[keep], vals[keep]
+    n_drop = len(cols) - int(keep.sum())
+    empty = np.setdiff1d(np.arange(ncols, dtype=np.int64), kc.astype(np.int64))
+    if rule == "gradient":
+        empty = empty[~np.isnan(g_row[empty])]
+    n_grow = min(n_drop, empty.size)
+    if n_grow > 0:
+        if rule == "gradient":
+            keys = _grow_keys_rigl(g_row[empty])
+        else:
+            keys = splitmix_keys(seed, row, ncols, empty)
+        order = np.lexsort((empty, keys))  # by key, then column
+        grow = np.sort(empty[order[:n_grow]]).astype(np.int32)
+    else:
+        grow = np.zeros(0, np.int32)
+    mc = np.concatenate([kc, grow])
+    mv = np.concatenate([kv, np.zeros(grow.size, np.float32)])
+    o = np.argsort(mc, kind="stable")
+    return mc[o].astype(np.int32), mv[o].astype(np.float32)
 
 
 def drop_grow(p: Csr, k_drop: int, rule: str, G: np.ndarray | None = None,
               seed: int = 0) -> Csr:
-    """One SET ("random") / RigL ("gradient") update of every row, on a copy.
-
-    Follows the per-row loop of router.py:414-478 (SET) and :663-732 (RigL):
-    keep |v| > threshold (the row's first largest |v| if none survive), grow
-    n_grow = min(dropped, ncols - kept) columns outside the kept set with
-    value 0, rewrite the row sorted by column. Grow choice: the n_grow
-    smallest keys, ties to the lower column; keys are ~bits(|G[i]|) (RigL:
-    largest |G| first) or splitmix_keys(seed, i, ...) (SET).
-    """
+    """One SET / RigL update of every row (drop_grow_row), on a copy: the
+    threshold is the k_drop-th smallest live |v| (router.py:394-412); a row
+    that shrinks pads its tail with (-1, 0) and lowers its row_nnz."""
     q = p.copy()
     thr = live_abs_kth(p, k_drop)
-    all_cols = np.arange(p.ncols, dtype=np.int64)
     for i in range(p.nrows):
         s, n = int(p.row_start[i]), int(p.row_nnz[i])
         if n == 0:
             continue
-        cols = p.col_indices[s:s + n]
-        vals = p.values[s:s + n]
-        keep = np.abs(vals) > thr
-        if not keep.any():
-            keep[int(np.argmax(np.abs(vals)))] = True
-        kc, kv = cols[keep], vals[keep]
-        n_drop = n - int(keep.sum())
-        empty = np.setdiff1d(all_cols, kc.astype(np.int64))
-        n_grow = min(n_drop, empty.size)
-        if n_grow > 0:
-            if rule == "gradient":
-                keys = _grow_keys_rigl(G[i, empty])
-            else:
-                keys = splitmix_keys(seed, i, p.ncols, empty)
-            order = np.lexsort((empty, keys))  # by key, then column
-            grow = np.sort(empty[order[:n_grow]]).astype(np.int32)
-        else:
-            grow = np.zeros(0, np.int32)
-        mc = np.concatenate([kc, grow])
-        mv = np.concatenate([kv, np.zeros(grow.size, np.float32)])
-        o = np.argsort(mc, kind="stable")
-        q.col_indices[s:s + n] = mc[o]
-        q.values[s:s + n] = mv[o]
+        nc, nv = drop_grow_row(p.col_indices[s:s + n], p.values[s:s + n], thr, rule, p.ncols,
+                               None if G is None else G[i], seed, i)
+        m = nc.size
+        q.col_indices[s:s + m] = nc
+        q.values[s:s + m] = nv
+        q.col_indices[s + m:s + n] = -1
+        q.values[s + m:s + n] = 0.0
+        q.row_nnz[i] = m
     return q
 
 

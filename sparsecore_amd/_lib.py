@@ -21,7 +21,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libsparsecore_amd.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 SLK_OK, SLK_EINVAL, SLK_EDEVICE = 0, 1, 2
 SLK_DW_SIMD, SLK_DW_SCALAR = 0, 1
@@ -47,15 +47,18 @@ EXPORTS = (
     "slk_drop_grow",
     "slk_dense_grad",
     "slk_transpose_dense",
-    "slk_slot_list_workspace_bytes",
-    "slk_slot_list_build",
     "slk_spmm_t",
     "slk_backward_narrow",
     "slk_seg_list_capacity",
     "slk_seg_list_workspace_bytes",
     "slk_seg_list_build",
     "slk_phase_bounds_build",
+    "slk_set_tuning",
 )
+
+# Kernel-choice overrides (slk_set_tuning): knob numbers of enum slk_tune_knob.
+TUNE_KNOBS = {"spmm_kernel": 0, "spmm_h": 1, "spmm_rw": 2, "spmm_split": 3, "spmm_vec": 4,
+              "sddmm_g": 5, "seg_lean": 6}
 
 SEG_GROUP = 64  # SLK_SEG_GROUP
 
@@ -76,10 +79,6 @@ class CsrView(ctypes.Structure):
         ("row_nnz", ctypes.c_void_p),
         ("row_capacity", ctypes.c_void_p),
         ("row_order", ctypes.c_void_p),
-        ("slot_list", ctypes.c_void_p),
-        ("slot_list_row", ctypes.c_void_p),
-        ("n_slot_list", ctypes.c_int64),
-        ("slot_list_block", ctypes.c_int64),
         ("n_heavy_rows", ctypes.c_int64),
         ("seg_start", ctypes.c_void_p),
         ("seg_row", ctypes.c_void_p),
@@ -119,13 +118,10 @@ def _declare(lib) -> None:
     lib.slk_live_abs_kth.argtypes = [_csrp, _i64, _vp, _i64, _vp, _vp]
     lib.slk_drop_grow_workspace_bytes.restype = _i64
     lib.slk_drop_grow_workspace_bytes.argtypes = [_csrp]
-    lib.slk_drop_grow.argtypes = [_csrp, _vp, _vp, _vp, ctypes.c_int, _vp, _i64, ctypes.c_uint64,
-                                  _vp, _i64, _vp]
+    lib.slk_drop_grow.argtypes = [_csrp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _i64,
+                                  ctypes.c_uint64, _vp, _i64, _vp, _vp]
     lib.slk_dense_grad.argtypes = [_vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp, _vp]
     lib.slk_transpose_dense.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp]
-    lib.slk_slot_list_workspace_bytes.restype = _i64
-    lib.slk_slot_list_workspace_bytes.argtypes = [_csrp, _i64]
-    lib.slk_slot_list_build.argtypes = [_csrp, _i64, _vp, _i64, _vp, _vp, _vp]
     lib.slk_spmm_t.argtypes = [_csrp, _vp, _i64, _i64, _vp, _vp, _vp]
     lib.slk_backward_narrow.argtypes = [_csrp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, ctypes.c_int,
                                         _vp]
@@ -136,8 +132,9 @@ def _declare(lib) -> None:
     lib.slk_seg_list_build.argtypes = [_csrp, _i64, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp,
                                        _vp]
     lib.slk_phase_bounds_build.argtypes = [_csrp, _i64, _vp, _vp]
+    lib.slk_set_tuning.argtypes = [ctypes.c_int, _i64]
     sized = ("slk_last_error", "slk_abi_version", "slk_transpose_workspace_bytes",
-             "slk_drop_grow_workspace_bytes", "slk_slot_list_workspace_bytes",
+             "slk_drop_grow_workspace_bytes",
              "slk_seg_list_capacity", "slk_seg_list_workspace_bytes")
     for name in EXPORTS:
         if name not in sized:
@@ -273,11 +270,14 @@ def drop_grow_workspace_bytes(view: CsrView) -> int:
 
 
 def drop_grow(view: CsrView, thr: torch.Tensor, rule: int, G: torch.Tensor | None, seed: int,
-              ws: torch.Tensor) -> None:
+              ws: torch.Tensor, removed: torch.Tensor) -> None:
+    """One SET / RigL pass over every row of the view's matrix, in place;
+    ``removed`` (int64, 1 element) receives the live slots removed in total."""
     lib = load()
     ldg = G.stride(0) if G is not None else 0
-    rc = lib.slk_drop_grow(ctypes.byref(view), view.values, view.col_indices, thr.data_ptr(), rule,
-                           ptr(G), ldg, seed & (2**64 - 1), ptr(ws), ws.numel(), stream_of(thr))
+    rc = lib.slk_drop_grow(ctypes.byref(view), view.values, view.col_indices, view.row_nnz,
+                           thr.data_ptr(), rule, ptr(G), ldg, seed & (2**64 - 1), ptr(ws),
+                           ws.numel(), removed.data_ptr(), stream_of(thr))
     if rc:
         _raise(rc)
 
@@ -310,21 +310,6 @@ def backward_narrow(view: CsrView, dYt: torch.Tensor, X: torch.Tensor,
                                  ptr(dW), ptr(dbias), ptr(dX), int(order), stream_of(dYt))
     if rc:
         _raise(rc)
-
-
-def slot_list_build(view: CsrView, block_cols: int, nnz: int, device):
-    """(slot_list, slot_list_row) int32 tensors of nnz entries: W's live slots
-    by column block, row and column (slk_slot_list_build)."""
-    lib = load()
-    lst = torch.empty(nnz, dtype=torch.int32, device=device)
-    lrow = torch.empty(nnz, dtype=torch.int32, device=device)
-    nbytes = int(lib.slk_slot_list_workspace_bytes(ctypes.byref(view), int(block_cols)))
-    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
-    rc = lib.slk_slot_list_build(ctypes.byref(view), int(block_cols), ptr(ws), nbytes, ptr(lst),
-                                 ptr(lrow), stream_of(lst))
-    if rc:
-        _raise(rc)
-    return lst, lrow
 
 
 def seg_list_build(view: CsrView, block_cols: int, seg_slots: int, device):
@@ -369,5 +354,14 @@ def transpose_dense(src: torch.Tensor, dst: torch.Tensor) -> None:
     rows, cols = src.shape
     rc = lib.slk_transpose_dense(ptr(src), rows, cols, src.stride(0) if rows > 1 else cols,
                                  ptr(dst), stream_of(dst))
+    if rc:
+        _raise(rc)
+
+
+def set_tuning(knob: str, value: int | None) -> None:
+    """Override one kernel choice process-wide (slk_set_tuning); None restores
+    the launcher's own choice. For tests and measurement: results keep their
+    bits under every setting."""
+    rc = load().slk_set_tuning(TUNE_KNOBS[knob], -1 if value is None else int(value))
     if rc:
         _raise(rc)

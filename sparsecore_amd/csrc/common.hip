@@ -1,11 +1,17 @@
 // Error state and argument validation shared by every entry point.
 #include "common.hpp"
 
+#include <atomic>
+
 namespace slk {
 
 namespace {
 thread_local std::string g_last_error;
+// Kernel-choice overrides, process-wide; -1 = the launcher's own choice.
+std::atomic<int64_t> g_tuning[SLK_TUNE_COUNT] = {-1, -1, -1, -1, -1, -1, -1};
 }
+
+int64_t tuning(int knob) { return g_tuning[knob].load(std::memory_order_relaxed); }
 
 int fail(int code, const std::string& msg) {
     g_last_error = msg;
@@ -67,3 +73,12 @@ int validate_csr(const slk_csr* W, const char* who) {
 extern "C" const char* slk_last_error(void) { return slk::g_last_error.c_str(); }
 
 extern "C" int slk_abi_version(void) { return SLK_ABI_VERSION; }
+
+extern "C" int slk_set_tuning(int knob, int64_t value) {
+    slk::clear_error();
+    if (knob < 0 || knob >= SLK_TUNE_COUNT) {
+        return slk::fail(SLK_EINVAL, "set_tuning: unknown knob " + std::to_string(knob));
+    }
+    slk::g_tuning[knob].store(value < 0 ? -1 : value, std::memory_order_relaxed);
+    return SLK_OK;
+}

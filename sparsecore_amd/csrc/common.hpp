@@ -26,6 +26,9 @@ inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Current value of a kernel-choice override (slk_set_tuning); -1 = automatic.
+int64_t tuning(int knob);
+
 // Validates the parts of a CSR view every kernel relies on.
 int validate_csr(const slk_csr* W, const char* who);
 

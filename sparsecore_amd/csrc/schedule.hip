@@ -1,32 +1,27 @@
-// Slot-list schedule for the weight gradient on large layers.
+// Visiting schedules for slk_sddmm (segment list) and slk_spmm (phase
+// bounds) on large layers. Neither changes any slot's arithmetic; they only
+// decide which wave computes which slots, and when.
 //
-// slk_sddmm's windowed kernel can visit W's live slots in an order other than
-// the flat capacity order; the order built here takes them column block by
-// column block (block b = columns [b·C, (b+1)·C)), row by row inside a block,
-// by column inside a row. Waves resident at one moment then gather from one
-// band of X rows. The list is a permutation of the live slots, so it changes
-// which wave computes a slot, never the slot's arithmetic.
-//
-// Within a row the live columns ascend, so the row's slots in block b are one
-// run [lo(r, b), lo(r, b+1)), lo(r, b) = first live slot of row r with column
-// >= b·C. The build is a counting sort on (block, row) without atomics:
+// Within a row the live columns ascend, so the row's slots in column block b
+// (columns [b·C, (b+1)·C)) are one run [lo(r, b), lo(r, b+1)), lo(r, b) =
+// first live slot of row r with column >= b·C. The segment list is a
+// counting sort of these runs on (block, row), without atomics:
 //
 //   S1 bounds   one thread per (row, block boundary): lo(r, b) by binary
 //               search over the row's columns.
-//   S2 rowscan  one workgroup per block: exclusive scan over rows of the run
-//               lengths -> each run's offset inside its block, and the block
-//               total.
-//   S3 blkscan  one workgroup: exclusive scan of the block totals.
-//   S4 scatter  one thread per (row, block): copies its run to
-//               list[block start + run offset + i] with the row alongside.
+//   S2 rowscan  one workgroup per block: exclusive scan over rows of the
+//               run's segment counts (a run of n slots is ceil(n / S)
+//               segments of at most S consecutive slots) -> each run's
+//               offset inside its block, and the block total.
+//   S3 blkscan  one workgroup: exclusive scan of the block totals, each
+//               padded to a multiple of SLK_SEG_GROUP (a group of segments
+//               never straddles two blocks); the number of groups in use is
+//               written to device memory.
+//   S4 scatter  one thread per (row, block): writes its run's segments.
 //
-// The segment list (slk_seg_list_build) is the same counting sort over
-// segments instead of slots: run (r, b) of length n becomes ceil(n / S)
-// segments of at most S consecutive slots, each block's segment count is
-// padded to a multiple of SLK_SEG_GROUP (so a group never straddles two
-// blocks), and the padding is left as empty segments by a fill pass that
-// runs first. The list's length is an upper bound the host can compute;
-// the number of groups in use is written to device memory.
+// The padding is left as empty segments by a fill pass that runs first. The
+// list's length is an upper bound the host can compute without a device read.
+// The phase bounds are S1 with the phase width as the block.
 #include "common.hpp"
 
 #include <algorithm>
@@ -119,22 +114,6 @@ __global__ __launch_bounds__(kScanBlock) void sl_blkscan_kernel(int64_t nb,
     if (PAD > 1 && t == kScanBlock - 1) groups[0] = part[t] / PAD;
 }
 
-__global__ __launch_bounds__(kSchedThreads) void sl_scatter_kernel(
-    int64_t M, int64_t nb, const int32_t* __restrict__ lo, const int32_t* __restrict__ off,
-    const int32_t* __restrict__ start, int32_t* __restrict__ list, int32_t* __restrict__ list_row) {
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * kSchedThreads + threadIdx.x;
-    if (t >= M * nb) return;
-    const int64_t r = t / nb;
-    const int64_t b = t - r * nb;
-    const int32_t a = lo[r * (nb + 1) + b];
-    const int32_t e = lo[r * (nb + 1) + b + 1];
-    const int64_t dst = static_cast<int64_t>(start[b]) + off[t];
-    for (int32_t s = a; s < e; ++s) {
-        list[dst + (s - a)] = s;
-        list_row[dst + (s - a)] = static_cast<int32_t>(r);
-    }
-}
-
 // Segments of run (r, b): seg_start = first slot, seg_row = r, seg_count <= S.
 template <int S>
 __global__ __launch_bounds__(kSchedThreads) void sg_scatter_kernel(
@@ -186,55 +165,6 @@ ListPlan plan_list(int64_t M, int64_t K, int64_t C) {
 }  // namespace
 }  // namespace slk
 
-extern "C" int64_t slk_slot_list_workspace_bytes(const slk_csr* W, int64_t block_cols) {
-    if (W == nullptr || W->nrows <= 0 || W->ncols <= 0 || block_cols <= 0) return 0;
-    return slk::plan_list(W->nrows, W->ncols, block_cols).bytes;
-}
-
-extern "C" int slk_slot_list_build(const slk_csr* W, int64_t block_cols, void* workspace,
-                                   int64_t workspace_bytes, int32_t* slot_list,
-                                   int32_t* slot_list_row, void* stream) {
-    using namespace slk;
-    clear_error();
-    if (int rc = validate_csr(W, "slot_list")) return rc;
-    if (block_cols <= 0) {
-        return fail(SLK_EINVAL, "slot_list: block_cols must be positive, got " +
-                                    std::to_string(block_cols));
-    }
-    const int64_t M = W->nrows, K = W->ncols;
-    if (M == 0 || K == 0) return SLK_OK;
-    const ListPlan p = plan_list(M, K, block_cols);
-    if (workspace == nullptr || workspace_bytes < p.bytes) {
-        return fail(SLK_EINVAL, "slot_list: workspace of " + std::to_string(workspace_bytes) +
-                                    " bytes is smaller than the required " +
-                                    std::to_string(p.bytes));
-    }
-    if (slot_list == nullptr || slot_list_row == nullptr) {
-        return fail(SLK_EINVAL, "slot_list: NULL output");
-    }
-    if (p.nb > INT32_MAX || ceil_div(p.lo_ints, kSchedThreads) > INT32_MAX) {
-        return fail(SLK_EINVAL, "slot_list: matrix too large");
-    }
-    int32_t* lo = static_cast<int32_t*>(workspace);
-    int32_t* off = lo + p.lo_ints;
-    int32_t* total = off + p.off_ints;
-    int32_t* start = total + p.nb;
-    hipStream_t st = as_stream(stream);
-    hipLaunchKernelGGL(sl_bounds_kernel, dim3(static_cast<unsigned>(ceil_div(p.lo_ints, kSchedThreads))),
-                       dim3(kSchedThreads), 0, st, M, p.nb, block_cols, W->row_start, W->row_nnz,
-                       W->col_indices, lo);
-    if (int rc = check_launch("slot_list/bounds")) return rc;
-    hipLaunchKernelGGL(sl_rowscan_kernel<1>, dim3(static_cast<unsigned>(p.nb)), dim3(kScanBlock), 0,
-                       st, M, p.nb, lo, off, total);
-    if (int rc = check_launch("slot_list/rowscan")) return rc;
-    hipLaunchKernelGGL(sl_blkscan_kernel<1>, dim3(1), dim3(kScanBlock), 0, st, p.nb, total, start,
-                       nullptr);
-    if (int rc = check_launch("slot_list/blkscan")) return rc;
-    hipLaunchKernelGGL(sl_scatter_kernel, dim3(static_cast<unsigned>(ceil_div(p.off_ints, kSchedThreads))),
-                       dim3(kSchedThreads), 0, st, M, p.nb, lo, off, start, slot_list, slot_list_row);
-    return check_launch("slot_list/scatter");
-}
-
 extern "C" int64_t slk_seg_list_capacity(const slk_csr* W, int64_t block_cols, int64_t seg_slots) {
     if (W == nullptr || W->nrows <= 0 || W->ncols <= 0 || block_cols <= 0 || seg_slots <= 0) return 0;
     // every run of n slots makes ceil(n/S) <= n/S + 1 segments, and only
@@ -246,7 +176,8 @@ extern "C" int64_t slk_seg_list_capacity(const slk_csr* W, int64_t block_cols, i
 }
 
 extern "C" int64_t slk_seg_list_workspace_bytes(const slk_csr* W, int64_t block_cols) {
-    return slk_slot_list_workspace_bytes(W, block_cols);
+    if (W == nullptr || W->nrows <= 0 || W->ncols <= 0 || block_cols <= 0) return 0;
+    return slk::plan_list(W->nrows, W->ncols, block_cols).bytes;
 }
 
 extern "C" int slk_seg_list_build(const slk_csr* W, int64_t block_cols, int64_t seg_slots,

@@ -44,7 +44,6 @@ constexpr int kBlock = 256;
 constexpr int kSlotsPerWave = 16;  // SIMD order: 4 lanes per slot group
 constexpr int64_t kWinMinN = 1024;
 constexpr int64_t kWinMinSlots = 2048 * kSlotsPerWave;  // 2048 waves
-constexpr int64_t kListG4Slots = 1536 * 1024;             // ~8 generations of G=4 waves
 
 template <bool V4>
 __device__ __forceinline__ void load4(const float* p, float& a, float& b, float& c, float& d) {
@@ -178,8 +177,8 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Zeroes the padding slots of one row of dW (one wave): used when the slots are
-// walked through a slot list, which holds live slots only.
+// Zeroes the padding slots of one row of dW (one wave): used where the slots
+// are walked through a schedule that lists live slots only.
 __device__ __forceinline__ void zero_row_padding(const int32_t* __restrict__ row_start,
                                                  const int32_t* __restrict__ row_nnz,
                                                  const int32_t* __restrict__ row_cap, int64_t M,
@@ -191,32 +190,27 @@ __device__ __forceinline__ void zero_row_padding(const int32_t* __restrict__ row
     for (int64_t s = s0 + row_nnz[row] + lane; s < e; s += kWave) dW[s] = 0.0f;
 }
 
-template <int G, int NS>
+template <int G>
 __global__ __launch_bounds__(kBlock) void sddmm_simd_win_kernel(
     int64_t M, int64_t N, int64_t cap_total,
     const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
     const int32_t* __restrict__ col, const float* __restrict__ dY,
     const float* __restrict__ X, float* __restrict__ dW, float* __restrict__ dbias,
-    int64_t slot_waves, const int32_t* __restrict__ row_cap,
-    const int32_t* __restrict__ slot_list, const int32_t* __restrict__ slot_row,
-    int64_t n_list) {
+    int64_t slot_waves) {
     constexpr int kWavesPerBlock = kBlock / kWave;
-    static_assert(NS == 2 || NS == 4, "staged rows per group");
-    __shared__ f32x4 dys[kWavesPerBlock][G][NS][kWave];  // NS KiB per group
+    constexpr int NS = 2;  // staged dY rows per group: its first and its last
+    __shared__ f32x4 dys[kWavesPerBlock][G][NS][kWave];  // 2 KiB per group
     const int lane = threadIdx.x & (kWave - 1);
     const int wv = threadIdx.x >> 6;
     const int g = lane >> 2;
     const int q = lane & 3;
     const int64_t wid = wave_id();
-    const bool listed = slot_list != nullptr;
-    if (wid >= slot_waves) {  // wave-uniform: a per-row wave
-        if (listed) zero_row_padding(row_start, row_nnz, row_cap, M, wid - slot_waves, dW);
+    if (wid >= slot_waves) {  // wave-uniform: a per-row bias wave
         if (dbias != nullptr) bias_row_sum(dY, M, N, wid - slot_waves, dbias, N, 1);
         return;
     }
-    // The wave's 16·G entries: slots of the flat capacity space, or (listed)
-    // entries of the slot list, whose rows come with it.
-    const int64_t space = listed ? n_list : cap_total;
+    // The wave's 16·G slots of the flat capacity space.
+    const int64_t space = cap_total;
     const int64_t base = wid * (kSlotsPerWave * G);
 
     bool in[G], live[G], direct[G];
@@ -225,12 +219,8 @@ __global__ __launch_bounds__(kBlock) void sddmm_simd_win_kernel(
     int64_t slot_of[G];
     const float* dyr[G];
     const float* xr[G];
-    int64_t r = 0;
-    WaveRows rows;
-    if (!listed) {
-        rows = WaveRows(row_start, M, base, min(base + kSlotsPerWave * G - 1, cap_total - 1));
-        r = rows.first_row;
-    }
+    WaveRows rows(row_start, M, base, min(base + kSlotsPerWave * G - 1, cap_total - 1));
+    int64_t r = rows.first_row;
     bool any_direct = false;
 #pragma unroll
     for (int k = 0; k < G; ++k) {
@@ -240,27 +230,16 @@ __global__ __launch_bounds__(kBlock) void sddmm_simd_win_kernel(
         live[k] = false;
         slot_of[k] = e;
         if (in[k]) {
-            if (listed) {
-                slot_of[k] = slot_list[e];
-                r = slot_row[e];
-                live[k] = true;
-            } else {
-                r = rows.of(row_start, r, e);
-                live[k] = (e - row_start[r]) < row_nnz[r];
-            }
+            r = rows.of(row_start, r, e);
+            live[k] = (e - row_start[r]) < row_nnz[r];
         }
         // first and last row of group k (lane 0 holds its first entry)
         const int last = gbase < space
                              ? 4 * static_cast<int>(min<int64_t>(kSlotsPerWave - 1, space - 1 - gbase))
                              : 0;
-        // staged rows: those of the group's entries 0 and last (NS = 2), or
-        // 0, 5, 10 and last (NS = 4: short row runs, as in a slot list)
+        // staged rows: those of the group's first and last entries
         const int32_t ri = static_cast<int32_t>(r);
         rs[k][0] = __builtin_amdgcn_readfirstlane(ri);
-        if constexpr (NS == 4) {
-            rs[k][1] = __builtin_amdgcn_readlane(ri, min(20, last));
-            rs[k][2] = __builtin_amdgcn_readlane(ri, min(40, last));
-        }
         rs[k][NS - 1] = __builtin_amdgcn_readlane(ri, last);
         sel[k] = NS - 1;
         direct[k] = live[k];
@@ -384,214 +363,8 @@ __global__ __launch_bounds__(kBlock) void sddmm_simd_win_kernel(
     }
 }
 
-// SIMD order over a slot list, both operands from LDS (16-byte path).
-//
-// The windowed kernel above runs at the rate its per-lane X gathers issue
-// (about one 1 KB wave load per 20 cycles per CU from L2). A slot list built
-// with a narrow column block (C = 64 or 128 columns) allows more: a workgroup takes
-// 256 consecutive list entries, which lie in one column block and a short run
-// of rows, and for every 64-float window it stages the block's C rows of X and
-// the run's dY rows (at most 64) in LDS, once per workgroup; every lane then
-// reads both of its slot's pieces from LDS, whose read rate is several times
-// the gather rate. Each staged row is padded by four 16-byte pieces (a row
-// then starts 16 banks after the previous one, the width of one slot's four
-// lanes), which measured 2-7% faster than a one-piece pad. Staging goes through
-// registers a window ahead (loads of window w+1 in flight while window w is
-// computed), with a barrier before and after each store. An entry whose column
-// lies outside the block or whose row lies outside the staged run (a
-// workgroup that straddles two blocks) reads that operand from global memory.
-// Per slot, the arithmetic is sddmm_simd_kernel's: the 16 running sums advance
-// in step order across the windows, then the same combine and scalar tail.
-// Where it pays (measured): layers whose X is far larger than the L2s, where
-// the windowed kernel streams from HBM (16384x16384 at N=4096: 16.2 -> 11.9 ms
-// at 95% sparsity with 128-column blocks, 5.0 -> 3.9 ms at 99% with 64). With
-// an L2-resident X (the 60M-GPT layers) the windowed kernel, which splits the
-// operands between the gather path and LDS, stays 10-60% faster. The caller
-// picks by the block width it builds the list with.
-constexpr int kTileWaves = 4;
-constexpr int kTileThreads = kTileWaves * kWave;
-constexpr int kTileG = 4;                                     // groups of 16 slots per wave
-constexpr int kTileEntries = kTileWaves * kTileG * kSlotsPerWave;  // 256 list entries
-constexpr int kTileWin = 64;                                  // floats per window (4 steps)
-constexpr int kTilePieces = kTileWin / 4;                     // 16-byte pieces per row
-constexpr int kTileStride = kTilePieces + 4;                  // pieces per LDS row (padded)
-constexpr int kTileRows = 64;                                 // staged dY rows at most
-constexpr int kTileRowsPerPass = kTileThreads / kTilePieces;  // 16 staged rows per pass
-constexpr int kTileMaxC = 128;                                // column block width at most
-
-template <int C>
-__global__ __launch_bounds__(kTileThreads) void sddmm_tile_kernel(
-    int64_t M, int64_t K, int64_t N, const int32_t* __restrict__ row_start,
-    const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ row_cap,
-    const int32_t* __restrict__ col, const float* __restrict__ dY, const float* __restrict__ X,
-    float* __restrict__ dW, float* __restrict__ dbias, const int32_t* __restrict__ slot_list,
-    const int32_t* __restrict__ slot_row, int64_t n_list, int64_t tile_blocks) {
-    constexpr int kLoads = (C + kTileRows) / kTileRowsPerPass;  // staged pieces per thread
-    __shared__ f32x4 xs[C * kTileStride];          // X rows c_lo .. c_lo + C - 1
-    __shared__ f32x4 ds[kTileRows * kTileStride];  // dY rows r_lo .. r_lo + 63
-    __shared__ int32_t s_rhi[kTileWaves];
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wv = threadIdx.x >> 6;
-    const int g = lane >> 2;
-    const int q = lane & 3;
-    if (static_cast<int64_t>(blockIdx.x) >= tile_blocks) {  // block-uniform: per-row waves
-        const int64_t row = (static_cast<int64_t>(blockIdx.x) - tile_blocks) * kTileWaves + wv;
-        zero_row_padding(row_start, row_nnz, row_cap, M, row, dW);
-        if (dbias != nullptr) bias_row_sum(dY, M, N, row, dbias, N, 1);
-        return;
-    }
-    const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kTileEntries;  // < n_list
-    const int32_t c_lo = col[slot_list[e0]] / C * C;
-    const int32_t r_lo = slot_row[e0];
-
-    int32_t slot[kTileG], row[kTileG], cv[kTileG];
-    bool in[kTileG];
-    int32_t rmax = -1;
-#pragma unroll
-    for (int k = 0; k < kTileG; ++k) {
-        const int64_t e = e0 + (wv * kTileG + k) * kSlotsPerWave + g;
-        in[k] = e < n_list;
-        slot[k] = in[k] ? slot_list[e] : 0;
-        row[k] = in[k] ? slot_row[e] : 0;
-        cv[k] = in[k] ? col[slot[k]] : -1;
-        // rows ascend within a column block: the run ends at c_lo's block's last entry
-        if (in[k] && cv[k] >= c_lo && cv[k] < c_lo + C) rmax = max(rmax, row[k]);
-    }
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) rmax = max(rmax, __shfl_xor(rmax, off));
-    if (lane == 0) s_rhi[wv] = rmax;
-    __syncthreads();
-    int32_t rhi = s_rhi[0];
-#pragma unroll
-    for (int w = 1; w < kTileWaves; ++w) rhi = max(rhi, s_rhi[w]);
-    const int32_t nR = min(kTileRows, max(0, rhi - r_lo + 1));
-    const int32_t nC = static_cast<int32_t>(min<int64_t>(C, K - c_lo));
-
-    // LDS piece offsets of each entry's operands; outsiders read global memory
-    int32_t xo[kTileG], dO[kTileG];
-    bool xdir[kTileG], ddir[kTileG];
-    bool any_direct = false;
-#pragma unroll
-    for (int k = 0; k < kTileG; ++k) {
-        const int32_t xr = cv[k] - c_lo, dr = row[k] - r_lo;
-        xdir[k] = in[k] && !(xr >= 0 && xr < nC);
-        ddir[k] = in[k] && !(dr >= 0 && dr < nR);
-        xo[k] = (xdir[k] || !in[k] ? 0 : xr) * kTileStride + q;
-        dO[k] = (ddir[k] || !in[k] ? 0 : dr) * kTileStride + q;
-        any_direct |= __ballot(xdir[k] || ddir[k]) != 0;
-    }
-
-    // staging: thread t copies piece (t mod 16) of staged rows t/16 + 16i;
-    // rows 0..C-1 of the stage are X rows c_lo.., rows C..C+63 dY rows r_lo..
-    // (i < C/16 picks X), each 16·N floats after the previous one
-    const int pc = threadIdx.x % kTilePieces;
-    const int rr0 = threadIdx.x / kTilePieces;
-    const float* xsrc = X + static_cast<int64_t>(c_lo + rr0) * N + 4 * pc;
-    const float* dsrc = dY + static_cast<int64_t>(r_lo + rr0) * N + 4 * pc;
-    const int64_t rstep = static_cast<int64_t>(kTileRowsPerPass) * N;
-    uint32_t smask = 0;
-#pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-        const int rr = rr0 + i * kTileRowsPerPass;
-        if (rr < C ? rr < nC : rr - C < nR) smask |= 1u << i;
-    }
-    const int64_t n16 = (N / 16) * 16;
-    const int64_t nwin = ceil_div(n16, kTileWin);
-    float acc[kTileG][4];
-#pragma unroll
-    for (int k = 0; k < kTileG; ++k) acc[k][0] = acc[k][1] = acc[k][2] = acc[k][3] = 0.f;
-    f32x4 pre[kLoads];
-    auto fetch = [&](int64_t w) {
-        const int64_t j = w * kTileWin;
-        if (j + 4 * pc < n16) {
-#pragma unroll
-            for (int i = 0; i < kLoads; ++i) {
-                const float* p = i < C / kTileRowsPerPass
-                                     ? xsrc + i * rstep
-                                     : dsrc + (i - C / kTileRowsPerPass) * rstep;
-                if (smask & (1u << i)) pre[i] = *reinterpret_cast<const f32x4*>(p + j);
-            }
-        }
-    };
-    if (nwin > 0) fetch(0);
-    for (int64_t w = 0; w < nwin; ++w) {
-        if (w > 0) __syncthreads();  // every lane has read window w-1
-#pragma unroll
-        for (int i = 0; i < kLoads; ++i) {
-            const int rr = rr0 + i * kTileRowsPerPass;
-            if (smask & (1u << i)) {
-                if (rr < C) xs[rr * kTileStride + pc] = pre[i];
-                else ds[(rr - C) * kTileStride + pc] = pre[i];
-            }
-        }
-        __syncthreads();
-        if (w + 1 < nwin) fetch(w + 1);
-        const int tn = static_cast<int>(min<int64_t>(kTileWin / 16, n16 / 16 - w * (kTileWin / 16)));
-#pragma unroll
-        for (int k = 0; k < kTileG; ++k) {
-            if (!in[k]) continue;
-            if (!any_direct && tn == kTileWin / 16) {
-#pragma unroll
-                for (int t = 0; t < kTileWin / 16; ++t)
-                    fma4x(ds[dO[k] + 4 * t], xs[xo[k] + 4 * t], acc[k][0], acc[k][1], acc[k][2],
-                          acc[k][3]);
-                // one group's 8 reads in flight at a time: hoisting all groups'
-                // reads ahead of their fmas would take 128 registers
-                __builtin_amdgcn_sched_barrier(0);
-            } else {
-                const int64_t j = w * kTileWin + 4 * q;
-                const float* xg = X + static_cast<int64_t>(cv[k]) * N + j;
-                const float* dg = dY + static_cast<int64_t>(row[k]) * N + j;
-                for (int t = 0; t < tn; ++t) {
-                    // LDS pieces read unconditionally, then replaced (see the
-                    // windowed kernel on mixing LDS and global loads)
-                    f32x4 d = ds[dO[k] + 4 * t];
-                    f32x4 x = xs[xo[k] + 4 * t];
-                    if (ddir[k]) d = *reinterpret_cast<const f32x4*>(dg + 16 * t);
-                    if (xdir[k]) x = *reinterpret_cast<const f32x4*>(xg + 16 * t);
-                    fma4x(d, x, acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
-                }
-            }
-        }
-    }
-    // a[l] = v[l] + v[l+8]: lanes q=0,1 take the partner q^2 (v[8..15]).
-#pragma unroll
-    for (int k = 0; k < kTileG; ++k) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[k][e] = acc[k][e] + __shfl_xor(acc[k][e], 2);
-    }
-    int64_t jt = n16;
-    if (N - n16 >= 8) {
-        if (q < 2) {
-            const int64_t j = n16 + 4 * q;
-#pragma unroll
-            for (int k = 0; k < kTileG; ++k) {
-                if (in[k]) {
-                    fma4x(*reinterpret_cast<const f32x4*>(dY + static_cast<int64_t>(row[k]) * N + j),
-                          *reinterpret_cast<const f32x4*>(X + static_cast<int64_t>(cv[k]) * N + j),
-                          acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
-                }
-            }
-        }
-        jt += 8;
-    }
-    // s4[k] = a[k] + a[k+4]: lane q=0 holds a[0..3], lane q=1 holds a[4..7].
-#pragma unroll
-    for (int k = 0; k < kTileG; ++k) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc[k][e] = acc[k][e] + __shfl_xor(acc[k][e], 1);
-    }
-    if (q == 0) {
-#pragma unroll
-        for (int k = 0; k < kTileG; ++k) {
-            if (!in[k]) continue;
-            const float rsum = (acc[k][0] + acc[k][2]) + (acc[k][1] + acc[k][3]);
-            dW[slot[k]] = running_sum(dY + static_cast<int64_t>(row[k]) * N + jt,
-                                      X + static_cast<int64_t>(cv[k]) * N + jt, N - jt, rsum);
-        }
-    }
-}
-
+// Scalar order (csrc/kernels/spmm_grad.cpp:89-108): one lane per slot, one
+// running chain over j.
 __global__ __launch_bounds__(kBlock) void sddmm_scalar_kernel(
     int64_t M, int64_t N, int64_t cap_total,
     const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
@@ -621,28 +394,32 @@ __global__ __launch_bounds__(kBlock) void sddmm_scalar_kernel(
 
 // SIMD order over a segment list: X from LDS, dY in registers (16-byte path).
 //
-// The tile kernel above reads both operands of every fma from LDS, and on
-// gfx950 a 64-lane 16-byte LDS read costs the same whether its lanes read one
-// row (a broadcast) or sixteen: about 4.6 cycles per CU measured, so two reads
-// per 16 fmas make it LDS-bound. Here a quad of lanes owns a segment, up to S
+// On gfx950 a 64-lane 16-byte LDS read costs the same whether its lanes read
+// one row (a broadcast) or sixteen: about 4.6 cycles per CU measured, so a
+// kernel that read both operands of every fma from LDS (two reads per 16
+// fmas) would be LDS-bound. Here a quad of lanes owns a segment, up to S
 // consecutive live slots of one row inside one column block
 // (slk_seg_list_build): the quad loads the row's dY pieces once per step from
 // global memory, one window ahead, and applies them to all S slots, whose X
-// pieces it reads from LDS. That is S + 0 LDS reads and one 64-byte global
-// load per S slot-steps instead of 2S LDS reads. A workgroup of 64 quads takes
-// one group of SLK_SEG_GROUP segments, all in one column block (the list pads
-// each block to whole groups); for every 64-float window it stages the
-// block's C rows of X in LDS (rows padded by four 16-byte pieces, as in the
-// tile kernel), prefetched a window ahead in registers. Per slot the
-// arithmetic is sddmm_simd_kernel's: the 16 running sums advance in step
-// order across the windows, then the same combine and scalar tail. Empty
-// segments (padding, or slots past a short segment's count) compute on a
-// clamped address and store nothing. Workgroups past the groups in use
-// (*groups, read on the device) exit at once; the workgroups after max_groups
-// are one wave per row that zeroes the row's padding slots and, with dbias,
-// sums its dY row.
+// pieces it reads from LDS. That is S LDS reads and one 64-byte global load
+// per S slot-steps. A workgroup of 64 quads takes one group of SLK_SEG_GROUP
+// segments, all in one column block (the list pads each block to whole
+// groups); for every 64-float window it stages the block's C rows of X in LDS
+// (rows padded by four 16-byte pieces, so a row starts 16 banks after the
+// previous one, the width of one slot's four lanes), prefetched a window
+// ahead in registers. Per slot the arithmetic is sddmm_simd_kernel's: the 16
+// running sums advance in step order across the windows, then the same
+// combine and scalar tail. Empty segments (padding, or slots past a short
+// segment's count) compute on a clamped address and store nothing.
+// Workgroups past the groups in use (*groups, read on the device) exit at
+// once; the workgroups after max_groups are one wave per row that zeroes the
+// row's padding slots and, with dbias, sums its dY row.
 constexpr int kSegThreads = SLK_SEG_GROUP * 4;  // one quad per segment
 static_assert(kSegThreads == 256, "four waves per workgroup");
+constexpr int kSegWin = 64;                                 // floats per window (4 steps)
+constexpr int kSegPieces = kSegWin / 4;                     // 16-byte pieces per row
+constexpr int kSegStride = kSegPieces + 4;                  // pieces per LDS row (padded)
+constexpr int kSegRowsPerPass = kSegThreads / kSegPieces;  // 16 staged rows per pass
 
 template <int C, int S, bool LEAN>
 __global__ __launch_bounds__(kSegThreads) void sddmm_seg_kernel(
@@ -652,9 +429,9 @@ __global__ __launch_bounds__(kSegThreads) void sddmm_seg_kernel(
     float* __restrict__ dW, float* __restrict__ dbias, const int32_t* __restrict__ seg_start,
     const int32_t* __restrict__ seg_row, const int32_t* __restrict__ seg_count,
     const int32_t* __restrict__ groups, int64_t max_groups) {
-    constexpr int kLoads = C * kTilePieces / kSegThreads;  // staged pieces per thread
-    static_assert(kLoads * kSegThreads == C * kTilePieces, "whole rows per pass");
-    __shared__ f32x4 xs[C * kTileStride];
+    constexpr int kLoads = C * kSegPieces / kSegThreads;  // staged pieces per thread
+    static_assert(kLoads * kSegThreads == C * kSegPieces, "whole rows per pass");
+    __shared__ f32x4 xs[C * kSegStride];
     const int wv = threadIdx.x >> 6;
     const int q = threadIdx.x & 3;
     const int64_t grp = blockIdx.x;
@@ -679,9 +456,9 @@ __global__ __launch_bounds__(kSegThreads) void sddmm_seg_kernel(
     const int64_t row = seg_row[e];
     int32_t xo[S];
 #pragma unroll
-    for (int k = 0; k < S; ++k) xo[k] = ((k < cnt ? col[s0 + k] : c_lo) - c_lo) * kTileStride + q;
+    for (int k = 0; k < S; ++k) xo[k] = ((k < cnt ? col[s0 + k] : c_lo) - c_lo) * kSegStride + q;
     // X row of slot k (the epilogue's tail), from xo
-    auto xrow = [&](int k) { return X + static_cast<int64_t>(c_lo + (xo[k] - q) / kTileStride) * N; };
+    auto xrow = [&](int k) { return X + static_cast<int64_t>(c_lo + (xo[k] - q) / kSegStride) * N; };
     const int32_t nC = static_cast<int32_t>(min<int64_t>(C, K - c_lo));
 
     // staging: thread t copies piece (t mod 16) of block rows t/16 + 16i. Rows
@@ -689,32 +466,32 @@ __global__ __launch_bounds__(kSegThreads) void sddmm_seg_kernel(
     // last window shorter than 64 floats) load a clamped, in-bounds address
     // instead: those LDS rows and steps are never read, and the loads stay
     // branch-free.
-    const int pc = threadIdx.x % kTilePieces;
-    const int rr0 = threadIdx.x / kTilePieces;
+    const int pc = threadIdx.x % kSegPieces;
+    const int rr0 = threadIdx.x / kSegPieces;
     const float* xband = X + static_cast<int64_t>(c_lo) * N;
     uint32_t xoff[kLoads];  // byte offsets in the band: C*N*4 < 2^32 (launcher check)
 #pragma unroll
     for (int i = 0; i < kLoads; ++i)
-        xoff[i] = static_cast<uint32_t>(min(rr0 + i * kTileRowsPerPass, nC - 1)) *
+        xoff[i] = static_cast<uint32_t>(min(rr0 + i * kSegRowsPerPass, nC - 1)) *
                   static_cast<uint32_t>(N) * 4u;
     const float* dyr = dY + row * N + 4 * q;
     const int64_t n16 = (N / 16) * 16;  // >= 16 (the launcher's bar)
-    const int64_t nwin = ceil_div(n16, kTileWin);
+    const int64_t nwin = ceil_div(n16, kSegWin);
     float acc[S][4];
 #pragma unroll
     for (int k = 0; k < S; ++k) acc[k][0] = acc[k][1] = acc[k][2] = acc[k][3] = 0.f;
     f32x4 pre[kLoads];
-    f32x4 dcur[kTileWin / 16], dnext[kTileWin / 16];
+    f32x4 dcur[kSegWin / 16], dnext[kSegWin / 16];
     auto fetch_x = [&](int64_t w) {
-        const uint32_t jx = static_cast<uint32_t>(min<int64_t>(w * kTileWin + 4 * pc, n16 - 4)) * 4u;
+        const uint32_t jx = static_cast<uint32_t>(min<int64_t>(w * kSegWin + 4 * pc, n16 - 4)) * 4u;
 #pragma unroll
         for (int i = 0; i < kLoads; ++i)
             pre[i] = *reinterpret_cast<const f32x4*>(reinterpret_cast<const char*>(xband) + xoff[i] + jx);
     };
-    auto fetch_dy = [&](int64_t w, f32x4 (&d)[kTileWin / 16]) {
+    auto fetch_dy = [&](int64_t w, f32x4 (&d)[kSegWin / 16]) {
 #pragma unroll
-        for (int t = 0; t < kTileWin / 16; ++t)
-            d[t] = *reinterpret_cast<const f32x4*>(dyr + min<int64_t>(w * kTileWin + 16 * t, n16 - 16));
+        for (int t = 0; t < kSegWin / 16; ++t)
+            d[t] = *reinterpret_cast<const f32x4*>(dyr + min<int64_t>(w * kSegWin + 16 * t, n16 - 16));
     };
     // LEAN: dY loaded at the start of its own window (its latency overlaps the
     // LDS store and the barrier) and S/2 X reads in flight, for fewer registers
@@ -724,18 +501,18 @@ __global__ __launch_bounds__(kSegThreads) void sddmm_seg_kernel(
     for (int64_t w = 0; w < nwin; ++w) {
         if constexpr (LEAN) fetch_dy(w, dcur);
 #pragma unroll
-        for (int i = 0; i < kLoads; ++i) xs[(rr0 + i * kTileRowsPerPass) * kTileStride + pc] = pre[i];
+        for (int i = 0; i < kLoads; ++i) xs[(rr0 + i * kSegRowsPerPass) * kSegStride + pc] = pre[i];
         if constexpr (!LEAN) {
 #pragma unroll
-            for (int t = 0; t < kTileWin / 16; ++t) dcur[t] = dnext[t];
+            for (int t = 0; t < kSegWin / 16; ++t) dcur[t] = dnext[t];
         }
         __syncthreads();
         // the last window refetches itself (unused)
         fetch_x(min(w + 1, nwin - 1));
         if constexpr (!LEAN) fetch_dy(min(w + 1, nwin - 1), dnext);
-        const int tn = static_cast<int>(min<int64_t>(kTileWin / 16, n16 / 16 - w * (kTileWin / 16)));
+        const int tn = static_cast<int>(min<int64_t>(kSegWin / 16, n16 / 16 - w * (kSegWin / 16)));
 #pragma unroll
-        for (int t = 0; t < kTileWin / 16; ++t) {
+        for (int t = 0; t < kSegWin / 16; ++t) {
 #pragma unroll
             for (int k0 = 0; k0 < S; k0 += SH) {
                 if (t < tn) {  // block-uniform
@@ -829,29 +606,18 @@ int sddmm_impl(const slk_csr* W, const float* dY, int64_t dY_rows, const float* 
     // Windowed sweep (G groups per wave) for the 16-byte path at large N:
     // G = 4 from 2048 waves of 4 groups, G = 2 from 1024 waves of 2 (measured
     // on the C3/C4 layer shapes: the 10M-GPT attention-out layer, 53 k slots,
-    // runs 133 -> 105 us with G = 2); SLK_SDDMM_G=1|2|4 overrides G (1 = one
-    // group per wave, whole rows).
+    // runs 133 -> 105 us with G = 2); SLK_TUNE_SDDMM_G = 1|2|4 overrides G
+    // (1 = one group per wave, whole rows).
     int G = 1;
     if (v4 && N >= kWinMinN) G = cap >= 4 * kWinMinSlots ? 4 : cap >= kWinMinSlots ? 2 : 1;
-    if (const char* e = std::getenv("SLK_SDDMM_G")) G = std::atoi(e);
+    if (const int64_t t = tuning(SLK_TUNE_SDDMM_G); t >= 0) G = static_cast<int>(t);
     if (!v4 || (G != 2 && G != 4)) G = 1;
-    // The windowed kernel walks W's slot list when the caller supplies one
-    // (live slots only; one wave per row then also zeroes the row's padding).
-    const bool listed = G > 1 && W->slot_list != nullptr && W->slot_list_row != nullptr;
-    // list order: G = 4 only with many generations of waves (a short last
-    // generation costs more than the extra dY staging of G = 2)
-    if (listed && std::getenv("SLK_SDDMM_G") == nullptr) G = W->n_slot_list >= kListG4Slots ? 4 : 2;
-    const int64_t space = listed ? W->n_slot_list : cap;
-    const int64_t row_waves = listed ? W->nrows : bias_waves;
-    const int64_t slot_waves = ceil_div(space, kSlotsPerWave * G);
-    const int64_t blocks = ceil_div(slot_waves + row_waves, kBlock / kWave);
+    const int64_t slot_waves = ceil_div(cap, kSlotsPerWave * G);
+    const int64_t blocks = ceil_div(slot_waves + bias_waves, kBlock / kWave);
     if (blocks > INT32_MAX) return fail(SLK_EINVAL, std::string(who) + ": problem too large");
     const dim3 grid(static_cast<unsigned>(blocks));
 #define SLK_SDDMM_ARGS \
     W->nrows, N, cap, W->row_start, W->row_nnz, W->col_indices, dY, X, dW, dbias, slot_waves
-#define SLK_SDDMM_WIN_ARGS                                                                   \
-    SLK_SDDMM_ARGS, W->row_capacity, listed ? W->slot_list : nullptr,                         \
-        listed ? W->slot_list_row : nullptr, space
     // A segment list: X through LDS, dY rows in registers.
     // (C·N floats of a band addressed with 32-bit byte offsets)
     if (v4 && W->seg_start != nullptr && N >= 16 && W->seg_block * N * 4 < (int64_t{1} << 32)) {
@@ -866,9 +632,9 @@ int sddmm_impl(const slk_csr* W, const float* dY, int64_t dY_rows, const float* 
         // 3 at 128; 2-15% faster on the 60M-GPT and 16384^2 layers). 4-slot
         // segments, used where rows hold few slots per block, keep dY loaded a
         // window ahead: their quads touch many different dY rows (16384^2 at
-        // 99%: 2.6 ms against 3.6 lean). SLK_SEG_LEAN=0|1 overrides.
+        // 99%: 2.6 ms against 3.6 lean). SLK_TUNE_SEG_LEAN = 0|1 overrides.
         bool lean = W->seg_slots == 8;
-        if (const char* e = std::getenv("SLK_SEG_LEAN")) lean = e[0] == '1';
+        if (const int64_t t = tuning(SLK_TUNE_SEG_LEAN); t >= 0) lean = t == 1;
 #define SLK_SEG_LAUNCH(CB, SS)                                                                 \
     do {                                                                                       \
         if (lean) {                                                                            \
@@ -887,41 +653,15 @@ int sddmm_impl(const slk_csr* W, const float* dY, int64_t dY_rows, const float* 
 #undef SLK_SEG_ARGS
         return check_launch(who);
     }
-    // A slot list in blocks of 64 or 128 columns: both operands through LDS.
-    const char* tile_env = std::getenv("SLK_SDDMM_TILE");  // "0": the windowed kernel
-    const int64_t cb = W->slot_list_block;
-    if (listed && v4 && (cb == 64 || cb == kTileMaxC) && (tile_env == nullptr || tile_env[0] != '0')) {
-        const int64_t tile_blocks = ceil_div(W->n_slot_list, int64_t{kTileEntries});
-        const int64_t tblocks = tile_blocks + ceil_div(W->nrows, int64_t{kTileWaves});
-        if (tblocks > INT32_MAX) return fail(SLK_EINVAL, std::string(who) + ": problem too large");
-#define SLK_TILE_ARGS                                                                        \
-    W->nrows, W->ncols, N, W->row_start, W->row_nnz, W->row_capacity, W->col_indices, dY, X, \
-        dW, dbias, W->slot_list, W->slot_list_row, W->n_slot_list, tile_blocks
-        if (cb == 64) {
-            hipLaunchKernelGGL(sddmm_tile_kernel<64>, dim3(static_cast<unsigned>(tblocks)),
-                               dim3(kTileThreads), 0, st, SLK_TILE_ARGS);
-        } else {
-            hipLaunchKernelGGL(sddmm_tile_kernel<128>, dim3(static_cast<unsigned>(tblocks)),
-                               dim3(kTileThreads), 0, st, SLK_TILE_ARGS);
-        }
-#undef SLK_TILE_ARGS
-        return check_launch(who);
-    }
-    // A slot list has short row runs per column block: stage four rows per group.
-    if (G == 2 && !listed) {
-        hipLaunchKernelGGL((sddmm_simd_win_kernel<2, 2>), grid, dim3(kBlock), 0, st, SLK_SDDMM_WIN_ARGS);
-    } else if (G == 2) {
-        hipLaunchKernelGGL((sddmm_simd_win_kernel<2, 4>), grid, dim3(kBlock), 0, st, SLK_SDDMM_WIN_ARGS);
-    } else if (G == 4 && !listed) {
-        hipLaunchKernelGGL((sddmm_simd_win_kernel<4, 2>), grid, dim3(kBlock), 0, st, SLK_SDDMM_WIN_ARGS);
+    if (G == 2) {
+        hipLaunchKernelGGL(sddmm_simd_win_kernel<2>, grid, dim3(kBlock), 0, st, SLK_SDDMM_ARGS);
     } else if (G == 4) {
-        hipLaunchKernelGGL((sddmm_simd_win_kernel<4, 4>), grid, dim3(kBlock), 0, st, SLK_SDDMM_WIN_ARGS);
+        hipLaunchKernelGGL(sddmm_simd_win_kernel<4>, grid, dim3(kBlock), 0, st, SLK_SDDMM_ARGS);
     } else if (v4) {
         hipLaunchKernelGGL(sddmm_simd_kernel<true>, grid, dim3(kBlock), 0, st, SLK_SDDMM_ARGS);
     } else {
         hipLaunchKernelGGL(sddmm_simd_kernel<false>, grid, dim3(kBlock), 0, st, SLK_SDDMM_ARGS);
     }
-#undef SLK_SDDMM_WIN_ARGS
 #undef SLK_SDDMM_ARGS
     return check_launch(who);
 }

@@ -639,7 +639,7 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
     // when it has enough workgroups to occupy the chip. Among the
     // configurations that pass both bars, lds_cost picks one. The per-wave
     // gather kernels cover everything else (small N is latency-bound).
-    // SLK_SPMM_KERNEL=lds|wave, SLK_SPMM_H=1|2 and SLK_SPMM_RW=2|4|8 override.
+    // SLK_TUNE_SPMM_KERNEL, SLK_TUNE_SPMM_H and SLK_TUNE_SPMM_RW override.
     const bool lds_ok = N % 4 == 0 && align % 16 == 0;
     int rw = 0, h = 1;
     if (lds_ok && N >= kLdsMinN) {
@@ -658,13 +658,14 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
             }
         }
     }
-    if (const char* e = std::getenv("SLK_SPMM_KERNEL")) {
-        if (e[0] == 'w') rw = 0;
-        if (e[0] == 'l' && lds_ok && rw == 0) rw = 8;
+    if (const int64_t t = tuning(SLK_TUNE_SPMM_KERNEL); t >= 0) {
+        if (t == 0) rw = 0;
+        if (t == 1 && lds_ok && rw == 0) rw = 8;
     }
     if (rw != 0) {
-        if (const char* e = std::getenv("SLK_SPMM_H")) h = e[0] == '2' ? 2 : 1;
-        if (const char* e = std::getenv("SLK_SPMM_RW")) rw = std::atoi(e);
+        if (const int64_t t = tuning(SLK_TUNE_SPMM_H); t >= 0) h = t == 2 ? 2 : 1;
+        if (const int64_t t = tuning(SLK_TUNE_SPMM_RW); t >= 0) rw = static_cast<int>(t);
+        if (rw != 2 && rw != 4 && rw != 8) rw = 8;
         if (h == 2 && rw == 8) rw = 4;  // no 8-row variant with 8 columns per lane
         // Heavy rows (the head of the longest-rows-first order) as a launch of
         // their own with two rows per wave, then the rest in that order, so
@@ -672,10 +673,10 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
         // Zipf(1.1) layer at 95% sparsity 12.6 -> 9.1 ms (heavy rows with the
         // rest, a long row stalls its workgroup at every chunk; all rows in
         // one sorted launch, the few workgroups of full rows outlast the rest).
-        // SLK_SPMM_SPLIT=0 runs one launch in natural row order.
+        // SLK_TUNE_SPMM_SPLIT = 0 runs one launch in natural row order.
         const int64_t T = W->n_heavy_rows;
         bool split = T > 0;
-        if (const char* e = std::getenv("SLK_SPMM_SPLIT")) split = split && e[0] != '0';
+        if (const int64_t t = tuning(SLK_TUNE_SPMM_SPLIT); t == 0) split = false;
         if (split) {
             if (int rc = launch_lds_rw<2>(W, W->row_order, T, X, N, bias, Y, st)) return rc;
             return launch_lds(h, rw, W, W->row_order + T, M - T, X, N, bias, Y, st);
@@ -684,7 +685,7 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
     }
 
     int vec = 1;
-    if (const char* e = std::getenv("SLK_SPMM_VEC")) vec = std::atoi(e);
+    if (const int64_t t = tuning(SLK_TUNE_SPMM_VEC); t >= 0) vec = static_cast<int>(t);
     else if (N % 4 == 0 && align % 16 == 0 && M * ceil_div(N, 256) >= kTargetWaves) vec = 4;
     else if (N % 2 == 0 && align % 8 == 0 && M * ceil_div(N, 128) >= kTargetWaves) vec = 2;
     if ((vec == 4 && (N % 4 || align % 16)) || (vec == 2 && (N % 2 || align % 8)) ||

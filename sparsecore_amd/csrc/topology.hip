@@ -7,9 +7,11 @@
 //   per row: keep |v| > threshold (at least the largest slot), then grow as
 //   many columns as were dropped, outside the kept set, zero-initialised, and
 //   rewrite the row sorted by column (PaddedCSR.rewrite_row).
-// A row always regrows exactly what it dropped (ncols - kept >= dropped), so
-// row_nnz, row_start and the capacities never change: only the live parts of
-// col_indices and values are rewritten.
+// A row regrows what it dropped (ncols - kept >= dropped), so row_start and
+// the capacities never change and row_nnz changes only in RigL's one
+// exception: columns whose |G| is NaN are never grown (the reference counts
+// `available` as the empty columns with |G| > -inf, router.py:704-705), and a
+// row that runs out of such columns shrinks by the difference.
 //
 //   kth_*        radix select (digits of 11, 10, 10 bits) over the bit
 //                patterns of |v| of the live slots: for non-negative floats
@@ -156,15 +158,21 @@ __device__ __forceinline__ uint32_t set_key(uint64_t seed, int64_t row, int64_t 
     return static_cast<uint32_t>(z >> 32);
 }
 
+// RigL: ~bits(|G|), largest |G| first (NaN columns are skipped before any
+// key is taken); SET: the splitmix64 key.
 template <bool RIGL>
 __device__ __forceinline__ uint32_t grow_key(const float* __restrict__ g_row, uint64_t seed,
                                              int64_t row, int64_t K, int64_t c) {
-    if (RIGL) {
-        const float a = fabsf(g_row[c]);
-        if (a != a) return 0xFFFFFFFFu;  // NaN: least preferred
-        return ~__float_as_uint(a);
-    }
+    if (RIGL) return ~__float_as_uint(fabsf(g_row[c]));
     return set_key(seed, row, K, c);
+}
+
+// A column RigL may not grow into: |G| is NaN.
+template <bool RIGL>
+__device__ __forceinline__ bool never_grown(const float* __restrict__ g_row, int64_t c) {
+    if (!RIGL) return false;
+    const float g = g_row[c];
+    return g != g;
 }
 
 __device__ __forceinline__ bool bit_of(const uint32_t* bm, int64_t c) {
@@ -174,9 +182,10 @@ __device__ __forceinline__ bool bit_of(const uint32_t* bm, int64_t c) {
 template <bool RIGL>
 __global__ __launch_bounds__(kDgThreads) void drop_grow_kernel(
     int64_t K, int64_t Kw, const int32_t* __restrict__ row_start,
-    const int32_t* __restrict__ row_nnz, float* __restrict__ values, int32_t* __restrict__ cols,
+    int32_t* __restrict__ row_nnz, float* __restrict__ values, int32_t* __restrict__ cols,
     const float* __restrict__ thr_ptr, const float* __restrict__ G, int64_t ldg, uint64_t seed,
-    int32_t* __restrict__ stage_col, float* __restrict__ stage_val) {
+    int32_t* __restrict__ stage_col, float* __restrict__ stage_val,
+    unsigned long long* __restrict__ removed) {
     extern __shared__ uint32_t lds[];
     uint32_t* keep = lds;         // survivors
     uint32_t* grow = lds + Kw;    // grown columns
@@ -229,24 +238,41 @@ __global__ __launch_bounds__(kDgThreads) void drop_grow_kernel(
     }
 
     const int64_t n_drop = n_live - n_keep;
-    const int64_t n_empty = K - n_keep;
-    const int64_t n_grow = n_drop < n_empty ? n_drop : n_empty;
     const float* g_row = RIGL ? G + i * ldg : nullptr;
+    int64_t n_grow = 0;
 
-    if (n_grow > 0) {
-        // Radix select of the n_grow smallest keys among unmarked columns.
+    if (n_drop > 0) {
+        // Radix select of the n_grow smallest keys among the unmarked columns
+        // a row may grow into. Pass 0 also counts the others (RigL: NaN |G|),
+        // which fixes n_grow = min(dropped, growable columns).
         uint32_t prefix = 0;
-        int64_t need = n_grow;
+        int64_t need = 0;
         for (int pass = 0; pass < 4; ++pass) {
             const int shift = 24 - 8 * pass;
             hist[t] = 0;
             __syncthreads();
+            int64_t skipped = 0;
             for (int64_t c = t; c < K; c += kDgThreads) {
                 if (bit_of(keep, c)) continue;
+                if (never_grown<RIGL>(g_row, c)) {
+                    ++skipped;
+                    continue;
+                }
                 const uint32_t u = grow_key<RIGL>(g_row, seed, i, K, c);
                 if (pass == 0 || (u >> (shift + 8)) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
             }
             __syncthreads();
+            if (pass == 0) {
+                int64_t n_growable = K - n_keep;
+                if (RIGL) {
+                    block_inclusive_scan(skipped, tmp);
+                    n_growable -= tmp[kDgThreads - 1];
+                    __syncthreads();
+                }
+                n_grow = n_drop < n_growable ? n_drop : n_growable;
+                need = n_grow;
+                if (n_grow == 0) break;  // block-uniform
+            }
             const int64_t h = hist[t];
             const int64_t incl = block_inclusive_scan(h, tmp);
             if (incl - h < need && need <= incl) {
@@ -262,10 +288,10 @@ __global__ __launch_bounds__(kDgThreads) void drop_grow_kernel(
         // (ascending) whose key equals it.
         const uint32_t T = prefix;
         int64_t taken_eq = 0;
-        for (int64_t c0 = 0; c0 < K; c0 += kDgThreads) {
+        for (int64_t c0 = 0; n_grow > 0 && c0 < K; c0 += kDgThreads) {
             const int64_t c = c0 + t;
             bool lt = false, eq = false;
-            if (c < K && !bit_of(keep, c)) {
+            if (c < K && !bit_of(keep, c) && !never_grown<RIGL>(g_row, c)) {
                 const uint32_t u = grow_key<RIGL>(g_row, seed, i, K, c);
                 lt = u < T;
                 eq = u == T;
@@ -319,11 +345,21 @@ __global__ __launch_bounds__(kDgThreads) void drop_grow_kernel(
         }
     }
     __syncthreads();
+    // The new row is n_keep + n_grow slots; a RigL row short of growable
+    // columns pads the rest (col -1, value 0) and records its new length.
+    const int64_t n_new = n_keep + n_grow;
     for (int32_t s = t; s < n_live; s += kDgThreads) {
-        cols[start + s] = stage_col[start + s];
-        values[start + s] = stage_val[start + s];
+        const bool live_s = s < n_new;
+        cols[start + s] = live_s ? stage_col[start + s] : -1;
+        values[start + s] = live_s ? stage_val[start + s] : 0.0f;
+    }
+    if (t == 0 && n_new < n_live) {
+        row_nnz[i] = static_cast<int32_t>(n_new);
+        atomicAdd(removed, static_cast<unsigned long long>(n_live - n_new));
     }
 }
+
+__global__ void clear_counter_kernel(unsigned long long* __restrict__ c) { *c = 0; }
 
 // ───────────────────────── dense gradient ──────────────────────────────────
 
@@ -483,27 +519,35 @@ extern "C" int64_t slk_drop_grow_workspace_bytes(const slk_csr* W) {
 }
 
 extern "C" int slk_drop_grow(const slk_csr* W, float* values, int32_t* col_indices,
-                             const float* thr_dev, int rule, const float* G, int64_t ldg,
-                             uint64_t seed, void* workspace, int64_t workspace_bytes,
-                             void* stream) {
+                             int32_t* row_nnz, const float* thr_dev, int rule, const float* G,
+                             int64_t ldg, uint64_t seed, void* workspace,
+                             int64_t workspace_bytes, int64_t* removed, void* stream) {
     using namespace slk;
     clear_error();
     if (int rc = validate_csr(W, "drop_grow")) return rc;
-    if (values != W->values || col_indices != W->col_indices)
-        return fail(SLK_EINVAL, "drop_grow: values/col_indices must be W's own arrays");
+    if (values != W->values || col_indices != W->col_indices || row_nnz != W->row_nnz)
+        return fail(SLK_EINVAL, "drop_grow: values/col_indices/row_nnz must be W's own arrays");
     if (rule != SLK_GROW_RANDOM && rule != SLK_GROW_GRADIENT)
         return fail(SLK_EINVAL, "drop_grow: unknown grow rule " + std::to_string(rule));
     if (W->ncols > kDgMaxCols)
         return fail(SLK_EINVAL, "drop_grow: ncols=" + std::to_string(W->ncols) +
                                     " exceeds the supported maximum " + std::to_string(kDgMaxCols));
-    if (W->nrows == 0 || W->total_capacity == 0) return SLK_OK;
-    if (thr_dev == nullptr) return fail(SLK_EINVAL, "drop_grow: NULL threshold");
-    if (rule == SLK_GROW_GRADIENT && (G == nullptr || ldg < W->ncols))
-        return fail(SLK_EINVAL, "drop_grow: the gradient rule needs G with ldg >= ncols");
-    if (workspace == nullptr || workspace_bytes < W->total_capacity * 8)
-        return fail(SLK_EINVAL, "drop_grow: workspace smaller than slk_drop_grow_workspace_bytes");
-    if (W->nrows > INT32_MAX) return fail(SLK_EINVAL, "drop_grow: too many rows for one launch");
+    if (removed == nullptr) return fail(SLK_EINVAL, "drop_grow: NULL removed-slot counter");
+    const bool empty = W->nrows == 0 || W->total_capacity == 0;
+    if (!empty) {
+        if (thr_dev == nullptr) return fail(SLK_EINVAL, "drop_grow: NULL threshold");
+        if (rule == SLK_GROW_GRADIENT && (G == nullptr || ldg < W->ncols))
+            return fail(SLK_EINVAL, "drop_grow: the gradient rule needs G with ldg >= ncols");
+        if (workspace == nullptr || workspace_bytes < W->total_capacity * 8)
+            return fail(SLK_EINVAL,
+                        "drop_grow: workspace smaller than slk_drop_grow_workspace_bytes");
+        if (W->nrows > INT32_MAX) return fail(SLK_EINVAL, "drop_grow: too many rows for one launch");
+    }
     hipStream_t st = as_stream(stream);
+    unsigned long long* removed_u = reinterpret_cast<unsigned long long*>(removed);
+    hipLaunchKernelGGL(clear_counter_kernel, dim3(1), dim3(1), 0, st, removed_u);
+    if (int rc = check_launch("drop_grow")) return rc;
+    if (empty) return SLK_OK;
     const int64_t K = W->ncols;
     const int64_t Kw = ceil_div(K, 32) > 0 ? ceil_div(K, 32) : 1;
     const size_t lds = static_cast<size_t>(3 * Kw) * sizeof(uint32_t);
@@ -512,12 +556,12 @@ extern "C" int slk_drop_grow(const slk_csr* W, float* values, int32_t* col_indic
     const dim3 grid(static_cast<unsigned>(W->nrows));
     if (rule == SLK_GROW_GRADIENT) {
         hipLaunchKernelGGL(drop_grow_kernel<true>, grid, dim3(kDgThreads), lds, st, K, Kw,
-                           W->row_start, W->row_nnz, values, col_indices, thr_dev, G, ldg, seed,
-                           stage_col, stage_val);
+                           W->row_start, row_nnz, values, col_indices, thr_dev, G, ldg, seed,
+                           stage_col, stage_val, removed_u);
     } else {
         hipLaunchKernelGGL(drop_grow_kernel<false>, grid, dim3(kDgThreads), lds, st, K, Kw,
-                           W->row_start, W->row_nnz, values, col_indices, thr_dev, G, ldg, seed,
-                           stage_col, stage_val);
+                           W->row_start, row_nnz, values, col_indices, thr_dev, G, ldg, seed,
+                           stage_col, stage_val, removed_u);
     }
     return check_launch("drop_grow");
 }

@@ -269,9 +269,9 @@ class PaddedCSR:
         self._topology_version = 0
         self._cview = None
         self._order = None      # (topology_version, device row schedule, heavy rows)
-        self._slist = None      # ((topology_version, block_cols), view with a slot list)
-        self._seglist = None    # ((topology_version, block_cols, seg_slots), segmented view)
-        self._phased = None     # ((topology_version, n_phases), view with phase bounds)
+        # derived views: (key, the base view they copy, view, schedule arrays)
+        self._seglist = None    # key (topology_version, block_cols, seg_slots)
+        self._phased = None     # key (topology_version, n_phases)
         # True when a few columns hold many of the slots (a transpose of a
         # matrix with heavy rows): its gathers already stay in cache
         self._cols_skewed = False
@@ -382,54 +382,53 @@ class PaddedCSR:
             self._cview = v
         return v
 
-    def _view_listed(self, block_cols: int) -> _lib.CsrView:
-        """The view plus W's live slots listed column block by column block (then
-        by row and column), with their rows: a slot order for slk_sddmm on large
-        layers (slk_csr.slot_list). Built on the device (slk_slot_list_build,
-        four launches) once per topology."""
-        base = self._view()
-        key = (self._topology_version, int(block_cols), id(base))
-        if self._slist is None or self._slist[0] != key:
-            lst, lrow = _lib.slot_list_build(base, int(block_cols), self._nnz, self.device)
-            fields = {f: getattr(base, f) for f, _ in _lib.CsrView._fields_}
-            fields.update(slot_list=_lib.ptr(lst), slot_list_row=_lib.ptr(lrow),
-                          n_slot_list=int(lst.numel()), slot_list_block=int(block_cols))
-            self._slist = (key, _lib.CsrView(**fields), lst, lrow)
-        return self._slist[1]
+    @staticmethod
+    def _derived(base: _lib.CsrView, **changes) -> _lib.CsrView:
+        fields = {f: getattr(base, f) for f, _ in _lib.CsrView._fields_}
+        fields.update(changes)
+        return _lib.CsrView(**fields)
 
     def _view_segmented(self, block_cols: int, seg_slots: int) -> _lib.CsrView:
         """The view plus W's live slots cut into segments of at most seg_slots
         consecutive slots of one row inside one column block (slk_csr.seg_start):
         a schedule for slk_sddmm that keeps each segment's dY row in registers.
         Built on the device (slk_seg_list_build, five launches, no host read)
-        once per topology."""
+        once per topology. The cached view is rebuilt whenever the base view
+        is (a values rebind, a row-schedule change), so it never carries a
+        stale pointer; the segment arrays survive that as long as the
+        topology does."""
         base = self._view()
-        key = (self._topology_version, int(block_cols), int(seg_slots), id(base))
-        if self._seglist is None or self._seglist[0] != key:
+        key = (self._topology_version, int(block_cols), int(seg_slots))
+        c = self._seglist
+        if c is None or c[0] != key:
             arrays = _lib.seg_list_build(base, int(block_cols), int(seg_slots), self.device)
-            start, row, count, groups = arrays
-            fields = {f: getattr(base, f) for f, _ in _lib.CsrView._fields_}
-            fields.update(seg_start=_lib.ptr(start), seg_row=_lib.ptr(row),
-                          seg_count=_lib.ptr(count), seg_groups=_lib.ptr(groups),
-                          n_seg=int(start.numel()), seg_block=int(block_cols),
-                          seg_slots=int(seg_slots))
-            self._seglist = (key, _lib.CsrView(**fields), arrays)
-        return self._seglist[1]
+            c = (key, None, None, arrays)
+        if c[1] is not base:
+            start, row, count, groups = c[3]
+            view = self._derived(base, seg_start=_lib.ptr(start), seg_row=_lib.ptr(row),
+                                 seg_count=_lib.ptr(count), seg_groups=_lib.ptr(groups),
+                                 n_seg=int(start.numel()), seg_block=int(block_cols),
+                                 seg_slots=int(seg_slots))
+            c = (key, base, view, c[3])
+        self._seglist = c
+        return c[2]
 
     def _view_phased(self, n_phases: int) -> _lib.CsrView:
         """The view plus phase bounds for slk_spmm's gather kernel
         (slk_csr.phase_lo): the columns swept in n_phases launches, each row's
         chain resumed from Y, so the X rows one phase gathers fit the L2s.
         Built on the device (slk_phase_bounds_build, one launch) once per
-        topology."""
+        topology; the cached view follows the base view as above."""
         base = self._view()
-        key = (self._topology_version, int(n_phases), id(base))
-        if self._phased is None or self._phased[0] != key:
-            lo = _lib.phase_bounds_build(base, int(n_phases), self.device)
-            fields = {f: getattr(base, f) for f, _ in _lib.CsrView._fields_}
-            fields.update(phase_lo=_lib.ptr(lo), n_phases=int(n_phases))
-            self._phased = (key, _lib.CsrView(**fields), lo)
-        return self._phased[1]
+        key = (self._topology_version, int(n_phases))
+        c = self._phased
+        if c is None or c[0] != key:
+            c = (key, None, None, _lib.phase_bounds_build(base, int(n_phases), self.device))
+        if c[1] is not base:
+            view = self._derived(base, phase_lo=_lib.ptr(c[3]), n_phases=int(n_phases))
+            c = (key, base, view, c[3])
+        self._phased = c
+        return c[2]
 
     def _rows_host(self):
         h = self._host_rows
@@ -551,9 +550,11 @@ class PaddedCSR:
 
         Drops the live slots with |v| <= the k_drop-th smallest live |v| (each
         row keeps at least its largest slot), regrows as many columns per row
-        (RigL: largest |G| first; SET: a uniform random subset keyed by
-        ``seed``), zero-initialised, rows rewritten sorted by column. Row nnz
-        and capacities do not change. Bumps ``topology_version``.
+        (RigL: largest |G| first, never a column whose |G| is NaN; SET: a
+        uniform random subset keyed by ``seed``), zero-initialised, rows
+        rewritten sorted by column. Capacities do not change; row nnz changes
+        only where a RigL row runs out of non-NaN columns to grow into, which
+        costs one device read. Bumps ``topology_version``.
         """
         self._require_device("drop_grow")
         if not 1 <= k_drop <= self._nnz:
@@ -564,10 +565,19 @@ class PaddedCSR:
         thr = torch.empty(1, dtype=_F32, device=dev)
         _lib.live_abs_kth(view, k_drop, ws, thr)
         stage = torch.empty(_lib.drop_grow_workspace_bytes(view), dtype=torch.uint8, device=dev)
-        _lib.drop_grow(view, thr, rule, G, seed, stage)
-        # row_nnz is unchanged, so the cached row schedule stays valid
+        removed = torch.empty(1, dtype=torch.int64, device=dev)
+        _lib.drop_grow(view, thr, rule, G, seed, stage, removed)
         self._topology_version += 1
-        if self._order is not None:
+        lost = int(removed.item()) if rule == _lib.SLK_GROW_GRADIENT else 0
+        if lost:
+            # some rows shrank: row_nnz changed on the device
+            self._nnz -= lost
+            self._host_rows = None
+            self._heavy_hint = None
+            self._cview = None
+            self._order = None
+        elif self._order is not None:
+            # row_nnz is unchanged, so the cached row schedule stays valid
             self._order = (self._topology_version,) + self._order[1:]
 
     # ─── device movement ───────────────────────────────────────────

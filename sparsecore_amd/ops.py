@@ -19,7 +19,6 @@ non-CPU tensors the same way; this build is GPU-only and has no CPU path).
 
 from __future__ import annotations
 
-import os
 import weakref
 
 import torch
@@ -95,12 +94,18 @@ _PHASE_MIN_X_BYTES = 128 << 20
 _PHASE_X_ROWS = 4096
 
 
+# Schedule overrides for tests and measurement (the launchers' own choices
+# otherwise; results keep their bits either way): "spmm_phases" = n forces
+# n column phases on slk_spmm's gather path (<= 1: none); "seg" = (block
+# columns, slots per segment) forces that segment list on slk_sddmm, () none.
+_overrides: dict[str, object] = {}
+
+
 def _spmm_view(W: PaddedCSR, X: torch.Tensor):
     """W's view for slk_spmm: with phase bounds where X is far beyond the L2s
-    and W's columns are not skewed. SLK_SPMM_PHASES=<n> forces n phases, 0
-    none."""
+    and W's columns are not skewed."""
     K, N = X.shape
-    forced = os.environ.get("SLK_SPMM_PHASES")
+    forced = _overrides.get("spmm_phases")
     if forced is not None:
         return W._view_phased(int(forced)) if int(forced) > 1 else W._view()
     if 4 * K * N >= _PHASE_MIN_X_BYTES and K > _PHASE_X_ROWS and not W._cols_skewed:
@@ -114,34 +119,14 @@ def _launch_spmm(W: PaddedCSR, X: torch.Tensor, bias: torch.Tensor | None = None
     return Y
 
 
-# Slot-list schedule for dW on large layers (measured on the C3/C4/C5 shapes:
-# 1.3-1.8x on every C4 and C5 layer, no gain on the C3 layers, whose X stays
-# cache-resident in flat order): live slots taken column block by column block
-# so the resident waves gather from one band of X rows.
-_SLOT_LIST_MIN_NNZ = 150_000
-_SLOT_LIST_MIN_X_BYTES = 16 << 20
-
-
-_TILE_MIN_X_BYTES = 128 << 20
-
-
-def _slot_block(W: PaddedCSR, K: int, N: int) -> int:
-    """Column-block width of the slot list. Where X (K x N) is far larger than
-    the L2s, 128 or 64 columns: slk_sddmm then stages each workgroup's X and
-    dY rows in LDS (measured 23-27% faster on the 16384x16384 layers; 128
-    where a block row holds >= 4 slots, else 64). Otherwise a wider block for
-    the windowed kernel, which only needs the X band to stay in L2."""
-    if 4 * K * N >= _TILE_MIN_X_BYTES:
-        density = W.nnz / max(1, W.nrows * W.ncols)
-        return 128 if density * 128 >= 4 else 64
-    return min(1024, max(256, N // 32))
-
-
 # Segment schedule for dW (slk_csr.seg_start): from this many live slots at
 # N >= 1024 (measured per layer: 1.4-1.8x on the 60M-GPT layers, 1.35x on the
 # 10M-GPT QKV layer, 1.5x / 1.45x on the 16384^2 layer at 95% / 99%; the
 # windowed kernel stays ahead on the 10M-GPT layers of 44-59 k slots).
 _SEG_MIN_NNZ = 100_000
+# X at least this large (far beyond the 4 MB L2 of an XCD) takes 128-column
+# segment blocks where rows are dense enough.
+_SEG_WIDE_MIN_X_BYTES = 128 << 20
 
 
 def _seg_shape(W: PaddedCSR, K: int, N: int) -> tuple[int, int]:
@@ -152,27 +137,18 @@ def _seg_shape(W: PaddedCSR, K: int, N: int) -> tuple[int, int]:
     against 2.60); 8 slots per segment where a row holds at least 4 live slots
     per block on average, else 4 (fewer empty slots in short runs)."""
     density = W.nnz / max(1, W.nrows * W.ncols)
-    cols = 128 if 4 * K * N >= _TILE_MIN_X_BYTES and density * 128 >= 4 else 64
+    cols = 128 if 4 * K * N >= _SEG_WIDE_MIN_X_BYTES and density * 128 >= 4 else 64
     return cols, 8 if density * cols >= 4 else 4
 
 
 def _sddmm_view(W: PaddedCSR, X: torch.Tensor):
-    """W's view for slk_sddmm: with a segment list or a slot list where it
-    pays (see above). SLK_SEG=<cols>x<slots> forces a segment list, 0 none;
-    SLK_SLOT_BLOCK=<cols> forces a slot list with that block width, 0 none."""
+    """W's view for slk_sddmm: with a segment list where it pays (see above)."""
     K, N = X.shape
-    seg = os.environ.get("SLK_SEG")
-    if seg is not None and seg != "0":
-        cols, slots = (int(v) for v in seg.split("x"))
-        return W._view_segmented(cols, slots)
-    if (seg is None and W.nnz >= _SEG_MIN_NNZ and N >= 1024 and N % 4 == 0
-            and os.environ.get("SLK_SLOT_BLOCK") is None):
-        return W._view_segmented(*_seg_shape(W, K, N))
-    forced = os.environ.get("SLK_SLOT_BLOCK")
+    forced = _overrides.get("seg")
     if forced is not None:
-        return W._view_listed(int(forced)) if int(forced) > 0 else W._view()
-    if W.nnz >= _SLOT_LIST_MIN_NNZ and 4 * K * N >= _SLOT_LIST_MIN_X_BYTES and N >= 1024:
-        return W._view_listed(_slot_block(W, K, N))
+        return W._view_segmented(*forced) if forced else W._view()
+    if W.nnz >= _SEG_MIN_NNZ and N >= 1024 and N % 4 == 0:
+        return W._view_segmented(*_seg_shape(W, K, N))
     return W._view()
 
 

@@ -46,3 +46,30 @@ def dev():
     if not sparsecore_amd.native_available():
         pytest.fail("gpu test selected but libsparsecore_amd.so is not built")
     return torch.device("cuda:0")
+
+
+@pytest.fixture
+def tune():
+    """Forces kernel / schedule choices for one test and restores the
+    launchers' own choices afterwards: tune(spmm_kernel=1, spmm_rw=4, ...)
+    for the library's knobs (slk_set_tuning), tune(spmm_phases=3) or
+    tune(seg=(64, 8)) for the host-side schedule overrides of ops."""
+    from sparsecore_amd import _lib, ops
+
+    host_keys = ("spmm_phases", "seg")
+    touched = []
+
+    def set_(**kw):
+        for k, v in kw.items():
+            if k in host_keys:
+                ops._overrides[k] = v
+            else:
+                _lib.set_tuning(k, v)
+            touched.append(k)
+
+    yield set_
+    for k in touched:
+        if k in host_keys:
+            ops._overrides.pop(k, None)
+        else:
+            _lib.set_tuning(k, None)

@@ -144,18 +144,23 @@ def test_topology_entry_points_check_arguments_on_the_host():
     assert rc == _lib.SLK_EINVAL and "workspace" in lib.slk_last_error().decode()
     rc = lib.slk_live_abs_kth(ctypes.byref(v), 0, 1, _lib.SLK_KTH_WORKSPACE_BYTES, 1, None)
     assert rc == _lib.SLK_EINVAL and "k=0" in lib.slk_last_error().decode()
-    rc = lib.slk_drop_grow(ctypes.byref(v), 16, 8, 1, 0, None, 0, 0, None, 0, None)
+    # (W, values, col_indices, row_nnz, thr, rule, G, ldg, seed, ws, ws_bytes, removed, stream)
+    rc = lib.slk_drop_grow(ctypes.byref(v), 16, 8, 1, 1, 0, None, 0, 0, None, 0, 1, None)
     assert rc == _lib.SLK_EINVAL and "own arrays" in lib.slk_last_error().decode()
-    rc = lib.slk_drop_grow(ctypes.byref(v), 8, 8, 1, 5, None, 0, 0, None, 0, None)
+    rc = lib.slk_drop_grow(ctypes.byref(v), 8, 8, 2, 1, 0, None, 0, 0, None, 0, 1, None)
+    assert rc == _lib.SLK_EINVAL and "own arrays" in lib.slk_last_error().decode()
+    rc = lib.slk_drop_grow(ctypes.byref(v), 8, 8, 1, 1, 5, None, 0, 0, None, 0, 1, None)
     assert rc == _lib.SLK_EINVAL and "rule" in lib.slk_last_error().decode()
     wide = _lib.CsrView(4, 200000, 10, 8, 8, 1, 1, 1)
-    rc = lib.slk_drop_grow(ctypes.byref(wide), 8, 8, 1, 0, None, 0, 0, None, 0, None)
+    rc = lib.slk_drop_grow(ctypes.byref(wide), 8, 8, 1, 1, 0, None, 0, 0, None, 0, 1, None)
     assert rc == _lib.SLK_EINVAL and "ncols" in lib.slk_last_error().decode()
-    rc = lib.slk_drop_grow(ctypes.byref(v), 8, 8, 1, _lib.SLK_GROW_GRADIENT, None, 0, 0,
-                           None, 0, None)
+    rc = lib.slk_drop_grow(ctypes.byref(v), 8, 8, 1, 1, 0, None, 0, 0, None, 0, None, None)
+    assert rc == _lib.SLK_EINVAL and "removed" in lib.slk_last_error().decode()
+    rc = lib.slk_drop_grow(ctypes.byref(v), 8, 8, 1, 1, _lib.SLK_GROW_GRADIENT, None, 0, 0,
+                           None, 0, 1, None)
     assert rc == _lib.SLK_EINVAL and "ldg" in lib.slk_last_error().decode()
-    rc = lib.slk_drop_grow(ctypes.byref(v), 8, 8, 1, _lib.SLK_GROW_RANDOM, None, 0, 0,
-                           None, 79, None)
+    rc = lib.slk_drop_grow(ctypes.byref(v), 8, 8, 1, 1, _lib.SLK_GROW_RANDOM, None, 0, 0,
+                           None, 79, 1, None)
     assert rc == _lib.SLK_EINVAL and "workspace" in lib.slk_last_error().decode()
     assert lib.slk_drop_grow_workspace_bytes(ctypes.byref(v)) == 80
     rc = lib.slk_dense_grad(None, None, -1, 2, 2, 0, None, None)

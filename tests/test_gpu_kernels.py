@@ -116,11 +116,11 @@ def test_unaligned_inputs_take_the_scalar_load_path(dev, N):
 
 @pytest.mark.parametrize("vec", [1, 2, 4])
 @pytest.mark.parametrize("N,per_row", [(300, 9), (1024, 150), (4100, 3)])
-def test_spmm_every_vector_width(dev, monkeypatch, vec, N, per_row):
+def test_spmm_every_vector_width(dev, tune, vec, N, per_row):
     """Each lane width of the one-row-per-wave kernel (the launcher picks it by
-    problem size; SLK_SPMM_VEC forces it), including rows longer than one
+    problem size; tune(spmm_vec=...) forces it), including rows longer than one
     64-slot metadata chunk and partial last batches."""
-    monkeypatch.setenv("SLK_SPMM_VEC", str(vec))
+    tune(spmm_vec=vec)
     c, X_np, _ = _case(40, 200, N, per_row, seed=vec * 7 + N)
     W = from_oracle(c, dev)
     assert_bits_equal(_spmm(W, _t(X_np, dev)).cpu().numpy(), oracle.spmm(c, X_np), "Y")
@@ -131,14 +131,14 @@ def test_spmm_every_vector_width(dev, monkeypatch, vec, N, per_row):
     (1, 1, 4, 1), (63, 127, 64, 40), (64, 128, 256, 128), (65, 129, 260, 100),
     (200, 300, 1000, 37), (130, 1000, 200, 700), (70, 5000, 96, 3000), (33, 260, 132, 0),
     (9, 64, 256, 64), (300, 64, 512, 64), (40, 100, 520, 50)])
-def test_spmm_lds_kernel_bit_exact(dev, monkeypatch, h, rw, M, K, N, per_row):
+def test_spmm_lds_kernel_bit_exact(dev, tune, h, rw, M, K, N, per_row):
     """The LDS-staged kernel (forced, each columns-per-lane and rows-per-wave
     variant): partial row blocks and column tiles (one half of a two-half tile
     past N), K not a multiple of the chunk, rows with more slots in one chunk
     than the chunk's rows (fully dense rows), empty rows."""
-    monkeypatch.setenv("SLK_SPMM_KERNEL", "lds")
-    monkeypatch.setenv("SLK_SPMM_H", str(h))
-    monkeypatch.setenv("SLK_SPMM_RW", str(rw))
+    tune(spmm_kernel=1)
+    tune(spmm_h=h)
+    tune(spmm_rw=rw)
     print(f"[lds h={h} rw={rw}] M={M} K={K} N={N} per_row={per_row}", flush=True)
     c, X_np, _ = _case(M, K, N, per_row, seed=M + K + N)
     W = from_oracle(c, dev)
@@ -146,16 +146,15 @@ def test_spmm_lds_kernel_bit_exact(dev, monkeypatch, h, rw, M, K, N, per_row):
 
 
 @pytest.mark.parametrize("env,N", [
-    ({"SLK_SPMM_VEC": "1"}, 300), ({"SLK_SPMM_VEC": "2"}, 300), ({"SLK_SPMM_VEC": "4"}, 1024),
-    ({}, 5), ({}, 40), ({"SLK_SPMM_KERNEL": "lds"}, 132),
-    ({"SLK_SPMM_KERNEL": "lds", "SLK_SPMM_RW": "2"}, 1024),
-    ({"SLK_SPMM_KERNEL": "lds", "SLK_SPMM_H": "2", "SLK_SPMM_RW": "4"}, 1032)])
-def test_spmm_bias_epilogue_bit_exact(dev, monkeypatch, env, N):
+    ({"spmm_vec": 1}, 300), ({"spmm_vec": 2}, 300), ({"spmm_vec": 4}, 1024),
+    ({}, 5), ({}, 40), ({"spmm_kernel": 1}, 132),
+    ({"spmm_kernel": 1, "spmm_rw": 2}, 1024),
+    ({"spmm_kernel": 1, "spmm_h": 2, "spmm_rw": 4}, 1032)])
+def test_spmm_bias_epilogue_bit_exact(dev, tune, env, N):
     """slk_spmm_bias = slk_spmm followed by one float32 add of bias[i] per row,
     in every kernel (wave kernel at each lane width, packed narrow-N kernel,
     LDS-staged kernel), including rows with no live slot (Y = 0 + bias)."""
-    for k, v in env.items():
-        monkeypatch.setenv(k, v)
+    tune(**env)
     print(f"[bias] env={env} N={N}", flush=True)
     c, X_np, _ = _case(45, 150, N, 20, seed=N + len(env))
     c.row_nnz[3] = 0
@@ -170,8 +169,8 @@ def test_spmm_bias_epilogue_bit_exact(dev, monkeypatch, env, N):
     assert_bits_equal(Y.cpu().numpy(), ref, "Y+bias")
 
 
-def test_spmm_lds_kernel_skewed_rows(dev, monkeypatch):
-    monkeypatch.setenv("SLK_SPMM_KERNEL", "lds")
+def test_spmm_lds_kernel_skewed_rows(dev, tune):
+    tune(spmm_kernel=1)
     c = oracle.zipf_rows(300, 700, 0.08, 1.1, seed=5, sigma=0.5)
     X_np = np.random.default_rng(5).standard_normal((700, 192)).astype(np.float32)
     W = from_oracle(c, dev)
@@ -209,14 +208,14 @@ def test_skewed_rows_bit_exact(dev):
 
 @pytest.mark.parametrize("G", [1, 2, 4])
 @pytest.mark.parametrize("N", [16, 24, 256, 260, 264, 271, 512, 1000, 1031, 2048])
-def test_sddmm_windowed_groups_bit_exact(dev, monkeypatch, G, N):
+def test_sddmm_windowed_groups_bit_exact(dev, tune, G, N):
     """dW with G groups of 16 slots per wave swept through N one window at a
-    time (the launcher's choice for 16-byte-aligned large N; SLK_SDDMM_G forces
+    time (the launcher's choice for 16-byte-aligned large N; tune(sddmm_g=...) forces
     G, 1 = the one-group kernel). Cases: groups inside one row, across rows,
     rows of 1..3 live slots, empty rows, a fully dense row, padding ratios 0
     and 1, an 8-wide tail step, a scalar tail, partial windows, and a capacity
     that is not a multiple of the wave."""
-    monkeypatch.setenv("SLK_SDDMM_G", str(G))
+    tune(sddmm_g=G)
     kernel = f"G={G}"
     print(f"[sddmm {kernel}] N={N}", flush=True)
     rng = np.random.default_rng(N + G)
@@ -291,14 +290,14 @@ def test_gather_path_skewed_rows_wide_N_bit_exact(dev):
 
 
 @pytest.mark.parametrize("h,rw", [(1, 2), (1, 4), (1, 8), (2, 2), (2, 4)])
-def test_row_order_lds_kernel_bit_exact(dev, monkeypatch, h, rw):
+def test_row_order_lds_kernel_bit_exact(dev, tune, h, rw):
     """Every LDS-staged kernel variant gives the natural order's bits whatever
     row schedule the view carries (the longest-first one, a random
     permutation, none): a tall skewed matrix with a partial last row block
     (3000 rows) and a partial column tile, with and without bias."""
-    monkeypatch.setenv("SLK_SPMM_KERNEL", "lds")
-    monkeypatch.setenv("SLK_SPMM_H", str(h))
-    monkeypatch.setenv("SLK_SPMM_RW", str(rw))
+    tune(spmm_kernel=1)
+    tune(spmm_h=h)
+    tune(spmm_rw=rw)
     print(f"[row_order lds h={h} rw={rw}]", flush=True)
     c = oracle.zipf_rows(3000, 400, 0.03, 1.1, seed=rw + h, sigma=0.5)
     rng = np.random.default_rng(rw * h)
@@ -321,15 +320,15 @@ def test_row_order_lds_kernel_bit_exact(dev, monkeypatch, h, rw):
 
 
 @pytest.mark.parametrize("h,rw", [(1, 2), (1, 4), (1, 8), (2, 2), (2, 4)])
-def test_lds_heavy_row_split_bit_exact(dev, monkeypatch, h, rw):
+def test_lds_heavy_row_split_bit_exact(dev, tune, h, rw):
     """A skewed matrix's heavy rows (the head of the longest-first order) run
     as their own LDS launch and the rest as a second one: the bits are the
     oracle's for every split point (none, one row, a partial row block, the
     view's own count, all but one row, all rows), every variant of the second
     launch, with and without bias."""
-    monkeypatch.setenv("SLK_SPMM_KERNEL", "lds")
-    monkeypatch.setenv("SLK_SPMM_H", str(h))
-    monkeypatch.setenv("SLK_SPMM_RW", str(rw))
+    tune(spmm_kernel=1)
+    tune(spmm_h=h)
+    tune(spmm_rw=rw)
     print(f"[heavy split h={h} rw={rw}]", flush=True)
     c = oracle.zipf_rows(3000, 700, 0.03, 1.1, seed=h * 10 + rw, sigma=0.5)
     rng = np.random.default_rng(rw + h)
@@ -497,14 +496,13 @@ def test_transpose_dense_is_a_bitwise_copy(dev, rows, cols, ld):
 
 
 @pytest.mark.parametrize("env,N,order", [
-    ({}, 256, "simd"), ({}, 255, "simd"), ({"SLK_SDDMM_G": "2"}, 1040, "simd"),
-    ({"SLK_SDDMM_G": "4"}, 1024, "simd"), ({}, 37, "scalar"), ({}, 0, "simd")])
-def test_sddmm_bias_fuses_the_bias_gradient(dev, monkeypatch, env, N, order):
+    ({}, 256, "simd"), ({}, 255, "simd"), ({"sddmm_g": 2}, 1040, "simd"),
+    ({"sddmm_g": 4}, 1024, "simd"), ({}, 37, "scalar"), ({}, 0, "simd")])
+def test_sddmm_bias_fuses_the_bias_gradient(dev, tune, env, N, order):
     """slk_sddmm_bias: dW bit-identical to slk_sddmm, dbias = Σ_j dY[i, j] within
     float32 rounding of the float64 sum, repeatable, for every dW kernel
     (including rows with no live slot and the scalar order)."""
-    for k, v in env.items():
-        monkeypatch.setenv(k, v)
+    tune(**env)
     c, X_np, dY_np = _case(70, 90, N, 12, seed=N + 3)
     c.row_nnz[4] = 0
     c.col_indices[c.row_start[4]:c.row_start[4] + c.row_capacity[4]] = -1
@@ -656,116 +654,6 @@ def test_backward_narrow_rejects_wide_layers(dev):
                              _lib.SLK_DW_SIMD)
 
 
-def _expected_slot_list(c, block):
-    """Live slots sorted by (column // block, row, column) with their rows."""
-    slots, rows, cols = oracle.live_slots(c)
-    order = np.lexsort((cols, rows, cols // block))
-    return slots[order], rows[order]
-
-
-@pytest.mark.parametrize("shape,density,block", [
-    ((150, 300), 0.06, 1),        # one block per column
-    ((150, 300), 0.06, 7),
-    ((150, 300), 0.06, 300),      # a single block
-    ((150, 300), 0.06, 5000),     # block wider than the matrix
-    ((3000, 257), 0.02, 64),      # more rows than the scan's 1024 threads
-    ((5, 4100), 0.3, 3),          # more blocks than the block scan's threads
-    ((64, 64), 1.0, 16),          # fully dense
-])
-def test_slot_list_build_order(dev, shape, density, block):
-    """slk_slot_list_build lists every live slot exactly once, ordered by
-    column block, row, column, with the right rows (empty rows included)."""
-    M, K = shape
-    c = oracle.zipf_rows(M, K, density, 1.1, seed=M + K + block, sigma=0.5)
-    c.row_nnz[M // 2] = 0
-    c.col_indices[c.row_start[M // 2]:c.row_start[M // 2] + c.row_capacity[M // 2]] = -1
-    W = from_oracle(c, dev)
-    lst, lrow = _lib.slot_list_build(W._view(), block, W.nnz, dev)
-    want_s, want_r = _expected_slot_list(c, block)
-    assert np.array_equal(lst.cpu().numpy(), want_s.astype(np.int32))
-    assert np.array_equal(lrow.cpu().numpy(), want_r.astype(np.int32))
-
-
-def test_slot_list_build_rejects_bad_arguments(dev):
-    c = oracle.zipf_rows(16, 32, 0.2, 1.1, seed=3)
-    W = from_oracle(c, dev)
-    with pytest.raises(ValueError, match="block_cols"):
-        _lib.slot_list_build(W._view(), 0, W.nnz, dev)
-    lib = _lib.load()
-    view = W._view()
-    out = torch.empty(W.nnz, dtype=torch.int32, device=dev)
-    rc = lib.slk_slot_list_build(ctypes.byref(view), 4, _lib.ptr(out), 4, _lib.ptr(out),
-                                 _lib.ptr(out), None)
-    assert rc != 0 and b"workspace" in lib.slk_last_error()
-
-
-@pytest.mark.parametrize("block", [64, 128])
-@pytest.mark.parametrize("M,K,density,N", [
-    (200, 256, 0.5, 1024),    # dense rows: a workgroup's entries span a few rows
-    (3000, 300, 0.02, 1100),  # sparse rows: runs longer than the 64 staged dY rows
-    (700, 200, 0.1, 1032),    # partial last window, 8-wide step
-    (500, 130, 0.2, 1045),    # scalar tail, a last block narrower than the block width
-])
-def test_sddmm_tile_kernel_bit_exact(dev, block, M, K, density, N):
-    """slk_sddmm on a slot list with 64- or 128-column blocks stages X and dY
-    rows in LDS per workgroup: the bits are the oracle's, including workgroups
-    that straddle two column blocks (X from global memory), rows outside the
-    staged run (dY from global memory), empty rows and the fused bias gradient."""
-    print(f"[dW tile] block={block} M={M} K={K} d={density} N={N}", flush=True)
-    c = oracle.zipf_rows(M, K, density, 0.6, seed=M + N, sigma=0.5)
-    c.row_nnz[M // 3] = 0
-    c.col_indices[c.row_start[M // 3]:c.row_start[M // 3] + c.row_capacity[M // 3]] = -1
-    rng = np.random.default_rng(N)
-    X_np = rng.standard_normal((K, N)).astype(np.float32)
-    dY_np = rng.standard_normal((M, N)).astype(np.float32)
-    W = from_oracle(c, dev)
-    X, dY = _t(X_np, dev), _t(dY_np, dev)
-    view = W._view_listed(block)
-    assert view.slot_list_block == block
-    dW = torch.full((W.total_capacity,), float("nan"), device=dev)
-    db = torch.full((M,), float("nan"), device=dev)
-    _lib.sddmm(view, dY, X, dW, _lib.SLK_DW_SIMD, db)
-    assert_bits_equal(dW.cpu().numpy(), oracle.sddmm(c, dY_np, X_np), "dW tile")
-    db_ref = torch.empty(M, device=dev)
-    _lib.sddmm(W._view(), dY, X, torch.empty_like(dW), _lib.SLK_DW_SIMD, db_ref)
-    assert torch.equal(db, db_ref)
-
-
-@pytest.mark.parametrize("G", [2, 4])
-@pytest.mark.parametrize("block", [1, 7, 64, 1000])
-def test_sddmm_slot_list_order_bit_exact(dev, monkeypatch, G, block):
-    """The windowed dW kernel walking the slot list (live slots by column block,
-    row, column; padding zeroed by the per-row waves) gives the same bits as
-    the flat order, with and without the fused bias gradient, including empty
-    rows and a dense row."""
-    monkeypatch.setenv("SLK_SDDMM_G", str(G))
-    c = oracle.zipf_rows(150, 300, 0.06, 1.1, seed=block, sigma=0.5)
-    c.row_nnz[7] = 0
-    c.col_indices[c.row_start[7]:c.row_start[7] + c.row_capacity[7]] = -1
-    c.values[c.row_start[7]:c.row_start[7] + c.row_capacity[7]] = 0.0
-    rng = np.random.default_rng(block)
-    N = 1032
-    X_np = rng.standard_normal((300, N)).astype(np.float32)
-    dY_np = rng.standard_normal((150, N)).astype(np.float32)
-    W = from_oracle(c, dev)
-    X, dY = _t(X_np, dev), _t(dY_np, dev)
-    view = W._view_listed(block)
-    assert view.n_slot_list == W.nnz
-    lst = W._slist[2].cpu().numpy()
-    assert sorted(lst.tolist()) == sorted(oracle.live_slots(c)[0].tolist())
-    ref = oracle.sddmm(c, dY_np, X_np)
-    dW = torch.full((W.total_capacity,), float("nan"), device=dev)
-    _lib.sddmm(view, dY, X, dW, _lib.SLK_DW_SIMD)
-    assert_bits_equal(dW.cpu().numpy(), ref, "dW listed")
-    dW2 = torch.full((W.total_capacity,), float("nan"), device=dev)
-    db = torch.empty(150, device=dev)
-    _lib.sddmm(view, dY, X, dW2, _lib.SLK_DW_SIMD, db)
-    assert_bits_equal(dW2.cpu().numpy(), ref, "dW listed + bias")
-    db_flat = torch.empty(150, device=dev)
-    _lib.sddmm(W._view(), dY, X, torch.empty_like(dW), _lib.SLK_DW_SIMD, db_flat)
-    assert torch.equal(db, db_flat)
-
-
 def _expected_seg_list(c, block, S, n):
     """The padded segment list, restated in numpy: for every column block, for
     every row, the row's run of live slots in the block cut into segments of at
@@ -896,14 +784,14 @@ def test_phase_bounds_build_matches_searchsorted(dev, P):
 
 @pytest.mark.parametrize("P", [2, 3, 7])
 @pytest.mark.parametrize("N,order", [(1024, True), (1032, False), (260, True)])
-def test_spmm_phased_sweep_bit_exact(dev, monkeypatch, P, N, order):
+def test_spmm_phased_sweep_bit_exact(dev, tune, P, N, order):
     """The 16-byte gather kernel swept in P column phases, each row's fma chain
     resumed from the partial sums the previous phase left in Y, gives the
     one-pass chain's bits — with and without bias (added once, after the last
     phase), under the longest-first row order and without one, for rows from
     fully dense to empty."""
-    monkeypatch.setenv("SLK_SPMM_KERNEL", "wave")
-    monkeypatch.setenv("SLK_SPMM_VEC", "4")
+    tune(spmm_kernel=0)
+    tune(spmm_vec=4)
     print(f"[spmm phased] P={P} N={N} order={order}", flush=True)
     c = oracle.zipf_rows(2500, 600, 0.02, 1.1, seed=P + N, sigma=0.5)
     c.row_nnz[11] = 0

@@ -95,6 +95,32 @@ def test_drop_grow_bit_exact(dev, rule, df):
         assert W._check_device() == ""
 
 
+@pytest.mark.parametrize("nan_frac", [0.3, 0.97])
+def test_rigl_never_grows_nan_columns_and_rows_shrink(dev, nan_frac):
+    """G with NaN entries: no NaN column is grown (the reference's available
+    count, router.py:704-705); a row short of growable columns shrinks, and the
+    host's nnz, the row schedule and later kernels follow the new row_nnz."""
+    for name, c in [("uniform", oracle.uniform_rows(64, 100, 10, seed=1, sigma=1.0)),
+                    ("tall", oracle.zipf_rows(2500, 120, 0.05, 1.1, seed=8, sigma=1.0))]:
+        print(f"[drop_grow NaN] {name} nan_frac={nan_frac}", flush=True)
+        rng = np.random.default_rng(11)
+        G = rng.standard_normal((c.nrows, c.ncols)).astype(np.float32)
+        G[rng.random(G.shape) < nan_frac] = np.nan
+        k = max(1, int(0.5 * c.nnz))
+        want = oracle.drop_grow(c, k, "gradient", G)
+        W = from_oracle(c, dev)
+        W._view()
+        W._drop_grow(k, _lib.SLK_GROW_GRADIENT, torch.from_numpy(G).to(dev))
+        csr_arrays_equal(to_oracle(W), want, name)
+        assert W.nnz == want.nnz
+        if nan_frac > 0.9:
+            assert want.nnz < c.nnz  # rows did shrink
+        assert W._check_device() == ""
+        X = np.random.default_rng(0).standard_normal((c.ncols, 64)).astype(np.float32)
+        Y = ops._launch_spmm(W, torch.from_numpy(X).to(dev)).cpu().numpy()
+        assert_bits_equal(Y, oracle.spmm(want, X), "Y after shrink")
+
+
 def test_drop_grow_on_tall_matrix_keeps_row_schedule(dev):
     c = oracle.zipf_rows(3000, 300, 0.05, 1.1, seed=6, sigma=1.0)
     W = from_oracle(c, dev)
@@ -326,34 +352,60 @@ def test_rigl_training_loop_invariants_and_seed(dev):
     np.testing.assert_array_equal(run(), run())
 
 
-@pytest.mark.parametrize("algo_ctor", [
-    lambda: SET(sparsity=0.8, drop_fraction=0.3, update_freq=2, seed=7),
-    lambda: RigL(sparsity=0.8, drop_fraction=0.3, update_freq=2, seed=7)])
-def test_loss_trajectory_cached_vs_fresh_transpose(dev, algo_ctor):
-    """test_set_rigl_with_cache.py: the cached-transpose run and a run that
-    clears the cache every step follow the same loss trajectory (here: bit
-    for bit)."""
-    def run(clear):
-        torch.manual_seed(0)
-        np.random.seed(0)
-        model = nn.Sequential(SparseLinear(24, 32, sparsity=0.8), nn.ReLU(),
-                              SparseLinear(32, 6, sparsity=0.8)).to(dev)
-        algo = algo_ctor()
-        model.apply(algo)
-        opt = torch.optim.SGD(model.parameters(), lr=0.05)
-        g = torch.Generator().manual_seed(1)
-        losses = []
-        for _ in range(30):
-            x = torch.randn(16, 24, generator=g).to(dev)
-            y = torch.randint(0, 6, (16,), generator=g).to(dev)
-            opt.zero_grad()
-            loss = F.cross_entropy(model(x), y)
-            loss.backward()
-            opt.step()
-            algo.step()
-            if clear:
-                _clear_transpose_cache()
-            losses.append(loss.item())
-        return losses
+def _cache_trajectory(dev, algo_ctor, n_steps, batch, clear_every_step, seed=42):
+    """test_set_rigl_with_cache.py's training loop on the general path: two
+    SparseLinear layers with more than 64 outputs (narrow layers keep no
+    transpose cache) and an input that needs its gradient, so both layers'
+    backward computes dX through _cached_transpose. Returns the losses and
+    the topology versions seen."""
+    torch.manual_seed(seed)
+    np.random.seed(seed)
+    l1 = SparseLinear(32, 96, sparsity=0.8, bias=False)
+    l2 = SparseLinear(96, 80, sparsity=0.8, bias=False)
+    model = nn.Sequential(l1, nn.ReLU(), l2).to(dev)
+    algo = algo_ctor()
+    model.apply(algo)
+    opt = torch.optim.SGD(model.parameters(), lr=0.05)
+    g = torch.Generator().manual_seed(seed + 1000)
+    data_x = torch.randn(n_steps * batch, 32, generator=g).to(dev)
+    data_y = torch.randn(n_steps * batch, 80, generator=g).to(dev)
+    losses, versions = [], []
+    for step in range(n_steps):
+        if clear_every_step:
+            _clear_transpose_cache()
+        x = data_x[step * batch:(step + 1) * batch].clone().requires_grad_(True)
+        y = data_y[step * batch:(step + 1) * batch]
+        opt.zero_grad()
+        loss = F.mse_loss(model(x), y)
+        loss.backward()
+        # both layers went through the transpose cache in this backward
+        for layer in (l1, l2):
+            entry = ops._transpose_cache.get(id(layer._csr))
+            assert entry is not None and entry[0] == layer._csr.topology_version
+        opt.step()
+        algo.step()
+        losses.append(loss.item())
+        versions.append((l1._csr.topology_version, l2._csr.topology_version))
+    return losses, versions
 
-    assert run(False) == run(True)
+
+@pytest.mark.parametrize("algo_ctor,n_steps,batch", [
+    (lambda: SET(sparsity=0.8, drop_fraction=0.3, update_freq=25, seed=123), 250, 16),
+    (lambda: RigL(sparsity=0.8, drop_fraction=0.3, update_freq=25, seed=123), 250, 16),
+    (lambda: SET(sparsity=0.7, drop_fraction=0.4, update_freq=5, seed=7), 100, 8)],
+    ids=["set-250", "rigl-250", "set-aggressive-100"])
+def test_loss_trajectory_cached_vs_fresh_transpose(dev, algo_ctor, n_steps, batch):
+    """test_set_rigl_with_cache.py:109-236 on the general path: the run that
+    keeps the transpose cache and a run that clears it before every step
+    follow the same loss trajectory, here bit for bit, across every SET / RigL
+    rewrite (each bumps topology_version and must invalidate the entry)."""
+    print(f"[cache trajectory] {n_steps} steps batch {batch}", flush=True)
+    _clear_transpose_cache()
+    cached, v_cached = _cache_trajectory(dev, algo_ctor, n_steps, batch, False)
+    _clear_transpose_cache()
+    fresh, v_fresh = _cache_trajectory(dev, algo_ctor, n_steps, batch, True)
+    assert v_cached == v_fresh
+    assert len(set(v_cached)) > 3  # the topology did change, several times
+    diverged = [i for i, (a, b) in enumerate(zip(cached, fresh)) if a != b]
+    assert not diverged, f"cached and fresh trajectories differ from step {diverged[0]}"
+    assert sum(cached[-10:]) / 10 < sum(cached[:10]) / 10  # training happened

@@ -105,26 +105,38 @@ def _reference_rigl_row(cols, vals, thr, g_row, ncols):
     return set(kc.tolist()), set(grow.tolist())
 
 
-@pytest.mark.parametrize("seed,df", [(0, 0.3), (1, 0.5), (2, 0.99), (3, 0.05)])
-def test_rigl_matches_reference_selection(seed, df):
+@pytest.mark.parametrize("seed,df,nan_frac", [(0, 0.3, 0.0), (1, 0.5, 0.0), (2, 0.99, 0.0),
+                                               (3, 0.05, 0.0), (4, 0.5, 0.3), (5, 0.99, 0.9)])
+def test_rigl_matches_reference_selection(seed, df, nan_frac):
+    """The oracle's RigL rows against the reference's own selection expression,
+    including G with NaN entries: the reference never grows a NaN column
+    (available = empties with |G| > -inf) and its row then shrinks."""
     p = oracle.uniform_rows(30, 50, 12, seed=seed, sigma=1.0)
     rng = np.random.default_rng(seed)
     G = rng.standard_normal((30, 50)).astype(np.float32)  # no ties (continuous)
+    G[rng.random((30, 50)) < nan_frac] = np.nan
     k_drop = max(1, int(df * p.nnz))
     thr = oracle.live_abs_kth(p, k_drop)
     q = oracle.drop_grow(p, k_drop, "gradient", G)
+    shrunk = 0
     for i in range(p.nrows):
         cols, vals = _live(p, i)
         kept, grown = _reference_rigl_row(cols, vals, thr, G[i], p.ncols)
         new_cols, new_vals = _live(q, i)
         assert set(new_cols.tolist()) == kept | grown, i
+        assert len(new_cols) == len(kept) + len(grown)
+        shrunk += len(cols) - len(new_cols)
         for c, v in zip(new_cols, new_vals):
             if c in kept:
                 assert v == vals[cols == c][0]
             else:
                 assert v == 0.0
     _check(q)
-    assert q.nnz == p.nnz and np.array_equal(q.row_nnz, p.row_nnz)
+    assert q.nnz == p.nnz - shrunk
+    if nan_frac == 0.0:
+        assert shrunk == 0 and np.array_equal(q.row_nnz, p.row_nnz)
+    if nan_frac == 0.9:
+        assert shrunk > 0  # the case is exercised
 
 
 @pytest.mark.parametrize("df", [0.3, 0.99])
@@ -169,7 +181,7 @@ def test_set_grow_is_uniform_over_empty_columns():
     assert chi2 < 33.7  # chi-square, 8 degrees of freedom, p = 1e-4
 
 
-def test_rigl_ties_go_to_lower_columns_and_nan_last():
+def test_rigl_ties_go_to_lower_columns_and_nan_is_never_grown():
     p = oracle.from_row_lists(1, 8, [np.array([0, 1, 2], np.int32)],
                               [np.array([0.01, 0.02, 0.9], np.float32)])
     G = np.array([[5, 5, 0, 3, 3, np.nan, 3, 3]], np.float32)
@@ -180,6 +192,12 @@ def test_rigl_ties_go_to_lower_columns_and_nan_last():
     G2 = np.array([[0, 0, 0, 3, 3, np.nan, 3, 3]], np.float32)
     q2 = oracle.drop_grow(p, 2, "gradient", G2)
     assert _live(q2, 0)[0].tolist() == [2, 3, 4]
+    # a zero |G| is preferred to a NaN at a lower column
+    G3 = np.array([[np.nan, np.nan, 7, np.nan, np.nan, 0, np.nan, np.nan]], np.float32)
+    q3 = oracle.drop_grow(p, 2, "gradient", G3)
+    assert _live(q3, 0)[0].tolist() == [2, 5]  # one growable column: the row shrinks
+    assert q3.row_nnz.tolist() == [2] and set(q3.col_indices.tolist()[2:]) == {-1}
+    _check(q3)
 
 
 def test_dense_row_regrows_its_dropped_columns():
