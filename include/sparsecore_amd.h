@@ -278,6 +278,27 @@ SLK_API int slk_drop_grow(const slk_csr* W, float* values, int32_t* col_indices,
                           int64_t ldg, uint64_t seed, void* workspace,
                           int64_t workspace_bytes, int64_t* removed, void* stream);
 
+/* slk_drop_grow without a workspace argument and without any allocation:
+ * the row staging lives in a static device array of the library ("scratch",
+ * SLK_DROP_GROW_NOALLOC_MAX_SLOTS * 8 bytes = 16 MiB, one copy per GPU the
+ * library runs on, held until the process ends). No counterpart in the
+ * reference: it is for callers that cannot allocate device memory — code
+ * under HIP graph capture, tight serving or training loops, harnesses that
+ * forbid hipMalloc. Same arguments (minus the workspace), same results bit
+ * for bit as slk_drop_grow. W->total_capacity must be at most
+ * SLK_DROP_GROW_NOALLOC_MAX_SLOTS (SLK_EINVAL otherwise, before any device
+ * work). Every call on one GPU shares that GPU's scratch, which keeps the
+ * last call's contents (each call writes what it reads first): calls that
+ * overlap on one GPU — on two streams, or from two threads — race, so
+ * order them on one stream. The first call on a device looks up that
+ * device's address of the array (hipGetSymbolAddress), with the device
+ * current.                                                                  */
+#define SLK_DROP_GROW_NOALLOC_MAX_SLOTS (1 << 21)
+SLK_API int slk_drop_grow_noalloc(const slk_csr* W, float* values, int32_t* col_indices,
+                                  int32_t* row_nnz, const float* thr_dev, int rule,
+                                  const float* G, int64_t ldg, uint64_t seed, int64_t* removed,
+                                  void* stream);
+
 /* G = dY·X^T, G is M x K row-major: G[i,k] = sum_j dY[i,j]·X[k,j], each
  * element one running sum over j in order, with the arithmetic of the
  * reference build (products of whole 4-element groups rounded, then added;

@@ -54,7 +54,10 @@ EXPORTS = (
     "slk_seg_list_build",
     "slk_phase_bounds_build",
     "slk_set_tuning",
+    "slk_drop_grow_noalloc",
 )
+
+DROP_GROW_NOALLOC_MAX_SLOTS = 1 << 21  # SLK_DROP_GROW_NOALLOC_MAX_SLOTS
 
 # Kernel-choice overrides (slk_set_tuning): knob numbers of enum slk_tune_knob.
 TUNE_KNOBS = {"spmm_kernel": 0, "spmm_h": 1, "spmm_rw": 2, "spmm_split": 3, "spmm_vec": 4,
@@ -133,6 +136,8 @@ def _declare(lib) -> None:
                                        _vp]
     lib.slk_phase_bounds_build.argtypes = [_csrp, _i64, _vp, _vp]
     lib.slk_set_tuning.argtypes = [ctypes.c_int, _i64]
+    lib.slk_drop_grow_noalloc.argtypes = [_csrp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _i64,
+                                          ctypes.c_uint64, _vp, _vp]
     sized = ("slk_last_error", "slk_abi_version", "slk_transpose_workspace_bytes",
              "slk_drop_grow_workspace_bytes",
              "slk_seg_list_capacity", "slk_seg_list_workspace_bytes")

@@ -33,6 +33,8 @@
 //                arithmetic.
 #include "common.hpp"
 
+#include <mutex>
+
 namespace slk {
 namespace {
 
@@ -518,12 +520,15 @@ extern "C" int64_t slk_drop_grow_workspace_bytes(const slk_csr* W) {
     return W->total_capacity * 8;
 }
 
-extern "C" int slk_drop_grow(const slk_csr* W, float* values, int32_t* col_indices,
-                             int32_t* row_nnz, const float* thr_dev, int rule, const float* G,
-                             int64_t ldg, uint64_t seed, void* workspace,
-                             int64_t workspace_bytes, int64_t* removed, void* stream) {
-    using namespace slk;
-    clear_error();
+namespace slk {
+namespace {
+
+// The shared body of slk_drop_grow and slk_drop_grow_noalloc: `stage` holds
+// the row staging (total_capacity int32 columns, then as many floats).
+int drop_grow_impl(const slk_csr* W, float* values, int32_t* col_indices, int32_t* row_nnz,
+                   const float* thr_dev, int rule, const float* G, int64_t ldg, uint64_t seed,
+                   void* stage, int64_t stage_bytes, int64_t* removed, void* stream,
+                   const char* stage_what) {
     if (int rc = validate_csr(W, "drop_grow")) return rc;
     if (values != W->values || col_indices != W->col_indices || row_nnz != W->row_nnz)
         return fail(SLK_EINVAL, "drop_grow: values/col_indices/row_nnz must be W's own arrays");
@@ -538,9 +543,8 @@ extern "C" int slk_drop_grow(const slk_csr* W, float* values, int32_t* col_indic
         if (thr_dev == nullptr) return fail(SLK_EINVAL, "drop_grow: NULL threshold");
         if (rule == SLK_GROW_GRADIENT && (G == nullptr || ldg < W->ncols))
             return fail(SLK_EINVAL, "drop_grow: the gradient rule needs G with ldg >= ncols");
-        if (workspace == nullptr || workspace_bytes < W->total_capacity * 8)
-            return fail(SLK_EINVAL,
-                        "drop_grow: workspace smaller than slk_drop_grow_workspace_bytes");
+        if (stage == nullptr || stage_bytes < W->total_capacity * 8)
+            return fail(SLK_EINVAL, std::string("drop_grow: ") + stage_what);
         if (W->nrows > INT32_MAX) return fail(SLK_EINVAL, "drop_grow: too many rows for one launch");
     }
     hipStream_t st = as_stream(stream);
@@ -551,7 +555,7 @@ extern "C" int slk_drop_grow(const slk_csr* W, float* values, int32_t* col_indic
     const int64_t K = W->ncols;
     const int64_t Kw = ceil_div(K, 32) > 0 ? ceil_div(K, 32) : 1;
     const size_t lds = static_cast<size_t>(3 * Kw) * sizeof(uint32_t);
-    int32_t* stage_col = static_cast<int32_t*>(workspace);
+    int32_t* stage_col = static_cast<int32_t*>(stage);
     float* stage_val = reinterpret_cast<float*>(stage_col + W->total_capacity);
     const dim3 grid(static_cast<unsigned>(W->nrows));
     if (rule == SLK_GROW_GRADIENT) {
@@ -564,6 +568,76 @@ extern "C" int slk_drop_grow(const slk_csr* W, float* values, int32_t* col_indic
                            stage_col, stage_val, removed_u);
     }
     return check_launch("drop_grow");
+}
+
+// Row staging of slk_drop_grow_noalloc: a file-scope device array, one copy
+// per GPU, held until the process ends. Host code never passes the array's
+// name to a kernel (on the host it is only a stand-in for the symbol): the
+// device address of each GPU's copy is looked up once per device with
+// hipGetSymbolAddress and kept in scratch_dev[].
+constexpr int64_t kNoallocMaxSlots = SLK_DROP_GROW_NOALLOC_MAX_SLOTS;
+__device__ __align__(256) unsigned char scratch[kNoallocMaxSlots * 8];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void* scratch_dev[kMaxDevices] = {};
+
+// This device's address of `scratch` (the current device's), or NULL with
+// the error recorded.
+void* scratch_for_current_device() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        fail(SLK_EDEVICE, "drop_grow_noalloc: no current HIP device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (scratch_dev[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            fail(SLK_EDEVICE, std::string("drop_grow_noalloc: hipGetSymbolAddress(scratch) "
+                                          "failed: ") + hipGetErrorString(e));
+            return nullptr;
+        }
+        scratch_dev[dev] = p;
+    }
+    return scratch_dev[dev];
+}
+
+}  // namespace
+}  // namespace slk
+
+extern "C" int slk_drop_grow(const slk_csr* W, float* values, int32_t* col_indices,
+                             int32_t* row_nnz, const float* thr_dev, int rule, const float* G,
+                             int64_t ldg, uint64_t seed, void* workspace,
+                             int64_t workspace_bytes, int64_t* removed, void* stream) {
+    slk::clear_error();
+    return slk::drop_grow_impl(W, values, col_indices, row_nnz, thr_dev, rule, G, ldg, seed,
+                               workspace, workspace_bytes, removed, stream,
+                               "workspace smaller than slk_drop_grow_workspace_bytes");
+}
+
+extern "C" int slk_drop_grow_noalloc(const slk_csr* W, float* values, int32_t* col_indices,
+                                     int32_t* row_nnz, const float* thr_dev, int rule,
+                                     const float* G, int64_t ldg, uint64_t seed,
+                                     int64_t* removed, void* stream) {
+    using namespace slk;
+    clear_error();
+    if (W != nullptr && W->total_capacity > kNoallocMaxSlots) {
+        return fail(SLK_EINVAL, "drop_grow_noalloc: total_capacity=" +
+                                    std::to_string(W->total_capacity) +
+                                    " exceeds the static scratch of " +
+                                    std::to_string(kNoallocMaxSlots) +
+                                    " slots; use slk_drop_grow with a workspace");
+    }
+    if (int rc = validate_csr(W, "drop_grow")) return rc;
+    void* stage = nullptr;
+    if (W->nrows > 0 && W->total_capacity > 0) {
+        stage = scratch_for_current_device();
+        if (stage == nullptr) return SLK_EDEVICE;
+    }
+    return drop_grow_impl(W, values, col_indices, row_nnz, thr_dev, rule, G, ldg, seed, stage,
+                          kNoallocMaxSlots * 8, removed, stream, "static scratch unavailable");
 }
 
 extern "C" int slk_dense_grad(const float* dY, const float* X, int64_t M, int64_t K, int64_t N,
