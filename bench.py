@@ -74,6 +74,12 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU-baseline budget")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--only-kernel", default=None,
+                    help="build the workload, then time only this kernel label (e.g. spmm_fwd, "
+                         "sddmm_dw, 'spmm_dx[qkv 768x2304]') and print its timing: a short "
+                         "run for profiler counter passes")
+    ap.add_argument("--kernel-reps", type=int, default=200,
+                    help="most launches per kernel in the kernel-timing phase")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after the run, copy a buffer of this many MiB three times (a "
                          "known-size reference dispatch for HBM byte counters)")
@@ -101,8 +107,12 @@ def flops(nnz, N):
 
 # ───────────────────────────── timing helpers ────────────────────────────────
 
-def kernel_avg_ms(fn, reps: int = 200) -> float:
-    """Average device time of `fn` (one kernel launch) over back-to-back launches."""
+KERNEL_REPS = 200
+
+
+def kernel_avg_ms(fn, reps: int | None = None, with_reps: bool = False):
+    """Average device time of `fn` (one kernel launch) over back-to-back launches
+    (and, with_reps, how many launches were timed)."""
     import torch
 
     fn()
@@ -114,14 +124,16 @@ def kernel_avg_ms(fn, reps: int = 200) -> float:
     end.record()
     torch.cuda.synchronize()
     one = start.elapsed_time(end)
-    reps = max(5, min(reps, int(100.0 / max(one, 1e-3))))  # ~0.1 s of launches at most
+    reps = KERNEL_REPS if reps is None else reps
+    reps = max(min(5, reps), min(reps, int(100.0 / max(one, 1e-3))))  # ~0.1 s at most
     torch.cuda._sleep(int(2e7))  # keeps the GPU busy while the launches queue up
     start.record()
     for _ in range(reps):
         fn()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / reps
+    ms = start.elapsed_time(end) / reps
+    return (ms, reps) if with_reps else ms
 
 
 def stage(msg: str) -> None:
@@ -1034,6 +1046,23 @@ def build_work(name: str, dev, seed: int):
                    rigl=name.endswith("rigl"))
 
 
+def calibrate_copy(args, dev) -> None:
+    """A known-size reference dispatch for HBM byte counters: three copies of
+    --calibrate-copy-mib MiB."""
+    import torch
+
+    if args.calibrate_copy_mib <= 0:
+        return
+    stage(f"copy calibration: {args.calibrate_copy_mib} MiB x 3")
+    n = args.calibrate_copy_mib * (1 << 20) // 4
+    src = torch.ones(n, device=dev)
+    dst = torch.empty(n, device=dev)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def measure(work, args):
     """Warmup, graph capture (where the topology is fixed), the timed region
     and the per-kernel timings of one workload. Returns the fields of its
@@ -1112,9 +1141,10 @@ def measure(work, args):
     kern = []
     for name, fn, nbytes, nflops in work.kernels():
         stage(f"kernel timing: {name}")
-        ms = kernel_avg_ms(fn)
+        ms, reps = kernel_avg_ms(fn, with_reps=True)
         kern.append({"kernel": name, "avg_us": round(ms * 1e3, 3), "bytes": nbytes,
-                     "flops": nflops, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)})
+                     "flops": nflops, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "timed_calls": reps})
     # roofline on the path's dominant kernel (forward SpMM, dX SpMM or dW SDDMM)
     dom = max((k for k in kern if k["kernel"].startswith(("spmm", "sddmm", "backward_narrow"))),
               key=lambda k: k["avg_us"])
@@ -1124,6 +1154,8 @@ def measure(work, args):
     # rocprofv3 FETCH_SIZE/WRITE_SIZE summary of this workload (if any)
     traffic = None
     tf = ROOT / "profiles" / f"traffic_{work.name}.json"
+    if not tf.exists():  # a RigL workload's layer is the static workload's layer
+        tf = ROOT / "profiles" / f"traffic_{work.name.removesuffix('-rigl')}.json"
     if tf.exists():
         tj = json.loads(tf.read_text())
         traffic = tj.get(dom["kernel"], tj.get(dom["kernel"].split("[")[0]))
@@ -1212,8 +1244,22 @@ def main():
     if not sparsecore_amd.native_available():
         sys.exit("bench.py: libsparsecore_amd.so is not built (python -m sparsecore_amd.build)")
     dev = torch.device("cuda:0")
+    global KERNEL_REPS
+    KERNEL_REPS = max(1, args.kernel_reps)
     stage(f"workload {args.workload}: building")
     work = build_work(args.workload, dev, args.seed)
+    if args.only_kernel is not None:
+        got = [k for k in work.kernels() if k[0] == args.only_kernel]
+        if not got:
+            sys.exit(f"bench.py: no kernel label {args.only_kernel!r} in {args.workload}: "
+                     f"{[k[0] for k in work.kernels()]}")
+        name, fn, nbytes, nflops = got[0]
+        stage(f"kernel timing: {name}")
+        ms = kernel_avg_ms(fn)
+        calibrate_copy(args, dev)
+        print(json.dumps({"workload": args.workload, "kernel": name, "avg_us": round(ms * 1e3, 3),
+                          "bytes": nbytes, "flops": nflops, "reps": KERNEL_REPS}), flush=True)
+        return
     m = measure(work, args)
     line = {
         "metric": METRIC,
@@ -1234,15 +1280,7 @@ def main():
         "roofline": m["roofline"],
         "cpu_baseline": None,
     }
-    if args.calibrate_copy_mib > 0:
-        stage(f"copy calibration: {args.calibrate_copy_mib} MiB x 3")
-        n = args.calibrate_copy_mib * (1 << 20) // 4
-        src = torch.ones(n, device=dev)
-        dst = torch.empty(n, device=dev)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+    calibrate_copy(args, dev)
     if not args.no_cpu:
         stage("cpu baseline")
         try:
