@@ -587,13 +587,13 @@ class LayerWork:
         return Y, dW, dX
 
     def topology_update(self):
-        """RigL: G = dY·Xᵀ, drop the 30% smallest |w|, regrow at the top-|G|
-        dead positions, then rebuild the transpose on the device."""
-        from sparsecore_amd import _lib, ops
+        """RigL: drop the 30% smallest |w|, regrow at the top-|G| dead
+        positions, G = dY·Xᵀ (the grows certified from the matrix-core
+        approximation, exact G where it cannot decide), then rebuild the
+        transpose on the device."""
+        from sparsecore_amd import ops
 
-        G = ops.dense_grad(self.dY, self.X)
-        self.W._drop_grow(max(1, int(0.3 * self.W.nnz)), _lib.SLK_GROW_GRADIENT, G)
-        del G
+        self.W._rigl_update(max(1, int(0.3 * self.W.nnz)), self.dY, self.X)
         ops._cached_transpose(self.W)
 
     def params(self):
@@ -646,17 +646,20 @@ class LayerWork:
         W = self.W
         M, K, N = self.M, self.K, self.N
         G = torch.empty(M, K, device=self.dev)
+        nd = torch.empty(M, device=self.dev)
+        nx = torch.empty(K, device=self.dev)
         k = max(1, int(0.3 * W.nnz))
-        Gd = ops.dense_grad(self.dY, self.X)
 
         def rebuild():
             ops._transpose_cache.pop(id(W), None)
             ops._cached_transpose(W)
 
         return [
-            ("dense_grad", lambda: _lib.dense_grad(self.dY, self.X, M, K, N, False, G),
+            ("rigl_norms", lambda: _lib.rigl_norms(self.dY, self.X, nd, nx),
+             4 * (M * N + K * N + M + K), 0),
+            ("dense_grad_approx", lambda: _lib.dense_grad_approx(self.dY, self.X, G),
              4 * (M * N + K * N + M * K), 2 * M * K * N),
-            ("rigl_drop_grow", lambda: W._drop_grow(k, _lib.SLK_GROW_GRADIENT, Gd), 0, 0),
+            ("rigl_update", lambda: W._rigl_update(k, self.dY, self.X), 0, 0),
             ("transpose_rebuild", rebuild,
              8 * M + 8 * W.nnz + 16 * int(1.2 * W.nnz + K) + 12 * K, 0),
         ]
@@ -693,8 +696,10 @@ def make_c5(dev, seed, density, rigl=False):
     X = torch.randn(K, N, generator=g, device=dev)
     dY = torch.randn(M, N, generator=g, device=dev)
     pct = int(round(100 * (1 - density)))
-    extra = ("; step = fwd + dW + dX + RigL rewrite (G = dY.X^T, drop 30% smallest |w|, "
-             "regrow at top-|G| dead positions) + device transpose rebuild") if rigl else ""
+    extra = ("; step = fwd + dW + dX + RigL rewrite (drop 30% smallest |w|, regrow at the "
+             "top-|G| dead positions, G = dY.X^T with the reference's dense_grad arithmetic: "
+             "certified from a matrix-core approximation, exact where undecided) + device "
+             "transpose rebuild") if rigl else ""
     return LayerWork(f"c5-{pct}" + ("-rigl" if rigl else ""),
                      f"16384x16384 at {pct}% sparsity, Zipf(1.1) rows (max {int(counts.max())}, "
                      f"min {int(counts.min())}), values N(0,0.01), N=4096" + extra, W, X, dY,

@@ -310,6 +310,64 @@ SLK_API int slk_drop_grow_noalloc(const slk_csr* W, float* values, int32_t* col_
 SLK_API int slk_dense_grad(const float* dY, const float* X, int64_t M, int64_t K,
                            int64_t N, int token_major, float* G, void* stream);
 
+/* ─── RigL grow choice from a certified approximate gradient ──────────────
+ *
+ * The same rows as slk_drop_grow with SLK_GROW_GRADIENT on G = dY·X^T (the
+ * reference build's dense_grad arithmetic), bit for bit, without computing
+ * that G everywhere. No counterpart entry in the reference; replaces its
+ * RigL._update_layer (sparselab/router.py:598-732) with _core.dense_grad.
+ * Four calls, in stream order:
+ *   slk_rigl_norms         row norms of dY (M x N) and X (K x N), row-major;
+ *   slk_dense_grad_approx  G' = dY·X^T on the matrix cores (fp32 split into
+ *                          bf16 parts), M x K row-major;
+ *   slk_rigl_count         per row: survivors, and the empty columns whose
+ *                          rank |G'| cannot certify; their exclusive scan;
+ *   slk_rigl_finish        per row: exact G of the undecided columns, the
+ *                          grow choice, the rewrite (as slk_drop_grow).
+ * The caller reads *amb_total after slk_rigl_count to size the finish
+ * workspace (8 bytes per undecided column). |G'[i,k] - G[i,k]| <=
+ * slk_rigl_bound_factor(N)·nrm_dY[i]·nrm_X[k] + 2^-100·(1 + nrm_dY[i] +
+ * nrm_X[k]) for norms up to 2^60 (larger or non-finite norms make the row
+ * exact: every empty column is computed exactly).                           */
+
+/* nrm_dY[i] >= ||dY_i||_2, nrm_X[k] >= ||X_k||_2 (+inf where not finite). */
+SLK_API int slk_rigl_norms(const float* dY, int64_t M, const float* X, int64_t K, int64_t N,
+                           float* nrm_dY, float* nrm_X, void* stream);
+
+/* Bytes of device workspace slk_dense_grad_approx needs: both operands split
+ * into bf16 parts, (M + K) * ceil(N / 32) * 128.                            */
+SLK_API int64_t slk_dense_grad_approx_workspace_bytes(int64_t M, int64_t K, int64_t N);
+
+/* G' = dY·X^T within the bound above; dY is M x N and X is K x N, row-major. */
+SLK_API int slk_dense_grad_approx(const float* dY, const float* X, int64_t M, int64_t K,
+                                  int64_t N, float* G, void* workspace,
+                                  int64_t workspace_bytes, void* stream);
+
+/* The factor c_N of the bound above (host function, no device work). */
+SLK_API double slk_rigl_bound_factor(int64_t N);
+
+/* Per row of W: survivors of *thr_dev (the global drop threshold, as for
+ * slk_drop_grow) and the empty columns the bound leaves undecided. info:
+ * 32 bytes per row (opaque to the caller, read by slk_rigl_finish); amb_off:
+ * 2*nrows + 1 int64: [0, nrows] receive the exclusive scan of the undecided
+ * counts, the rest is scratch; *amb_total = amb_off[nrows] (device int64).
+ * ncols at most 131072.                                                     */
+SLK_API int slk_rigl_count(const slk_csr* W, const float* thr_dev, const float* G_approx,
+                           int64_t ldg, const float* nrm_dY, const float* nrm_X, int64_t N,
+                           void* info, int64_t* amb_off, int64_t* amb_total, void* stream);
+
+/* Finishes the RigL pass slk_rigl_count began: values, col_indices and
+ * row_nnz must be W's own arrays (rewritten as slk_drop_grow rewrites them);
+ * amb_ws holds 8 bytes per undecided column (amb_ws_bytes >= 8 * *amb_total);
+ * workspace as slk_drop_grow's; *removed as slk_drop_grow's.                */
+SLK_API int slk_rigl_finish(const slk_csr* W, float* values, int32_t* col_indices,
+                            int32_t* row_nnz, const float* thr_dev, const float* G_approx,
+                            int64_t ldg, const float* nrm_dY, const float* nrm_X,
+                            const float* dY, const float* X, int64_t N, const void* info,
+                            const int64_t* amb_off, void* amb_ws, int64_t amb_ws_bytes,
+                            void* workspace, int64_t workspace_bytes, int64_t* removed,
+                            void* stream);
+
 /* ─── Dense layout ─────────────────────────────────────────────────────── */
 
 /* dst = src^T for a float32 matrix: src is rows x cols with row stride

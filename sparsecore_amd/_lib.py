@@ -55,7 +55,15 @@ EXPORTS = (
     "slk_phase_bounds_build",
     "slk_set_tuning",
     "slk_drop_grow_noalloc",
+    "slk_rigl_norms",
+    "slk_dense_grad_approx_workspace_bytes",
+    "slk_dense_grad_approx",
+    "slk_rigl_bound_factor",
+    "slk_rigl_count",
+    "slk_rigl_finish",
 )
+
+RIGL_INFO_BYTES = 32  # per row, slk_rigl_count's info
 
 DROP_GROW_NOALLOC_MAX_SLOTS = 1 << 21  # SLK_DROP_GROW_NOALLOC_MAX_SLOTS
 
@@ -136,10 +144,20 @@ def _declare(lib) -> None:
                                        _vp]
     lib.slk_phase_bounds_build.argtypes = [_csrp, _i64, _vp, _vp]
     lib.slk_set_tuning.argtypes = [ctypes.c_int, _i64]
+    lib.slk_rigl_norms.argtypes = [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp]
+    lib.slk_dense_grad_approx_workspace_bytes.restype = _i64
+    lib.slk_dense_grad_approx_workspace_bytes.argtypes = [_i64, _i64, _i64]
+    lib.slk_dense_grad_approx.argtypes = [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp]
+    lib.slk_rigl_bound_factor.restype = ctypes.c_double
+    lib.slk_rigl_bound_factor.argtypes = [_i64]
+    lib.slk_rigl_count.argtypes = [_csrp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp]
+    lib.slk_rigl_finish.argtypes = [_csrp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
+                                    _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp]
     lib.slk_drop_grow_noalloc.argtypes = [_csrp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _i64,
                                           ctypes.c_uint64, _vp, _vp]
     sized = ("slk_last_error", "slk_abi_version", "slk_transpose_workspace_bytes",
-             "slk_drop_grow_workspace_bytes",
+             "slk_drop_grow_workspace_bytes", "slk_rigl_bound_factor",
+             "slk_dense_grad_approx_workspace_bytes",
              "slk_seg_list_capacity", "slk_seg_list_workspace_bytes")
     for name in EXPORTS:
         if name not in sized:
@@ -368,5 +386,55 @@ def set_tuning(knob: str, value: int | None) -> None:
     the launcher's own choice. For tests and measurement: results keep their
     bits under every setting."""
     rc = load().slk_set_tuning(TUNE_KNOBS[knob], -1 if value is None else int(value))
+    if rc:
+        _raise(rc)
+
+
+def rigl_norms(dY: torch.Tensor, X: torch.Tensor, nrm_dY: torch.Tensor,
+               nrm_X: torch.Tensor) -> None:
+    """Row norms (upper bounds) of dY (M x N) and X (K x N) (slk_rigl_norms)."""
+    rc = load().slk_rigl_norms(ptr(dY), dY.shape[0], ptr(X), X.shape[0], dY.shape[1],
+                               ptr(nrm_dY), ptr(nrm_X), stream_of(nrm_dY))
+    if rc:
+        _raise(rc)
+
+
+def dense_grad_approx(dY: torch.Tensor, X: torch.Tensor, G: torch.Tensor) -> None:
+    """G' = dY·Xᵀ on the matrix cores within the certified bound
+    (slk_dense_grad_approx); dY (M x N), X (K x N) row-major."""
+    lib = load()
+    M, N = dY.shape
+    K = X.shape[0]
+    nbytes = int(lib.slk_dense_grad_approx_workspace_bytes(M, K, N))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=G.device)
+    rc = lib.slk_dense_grad_approx(ptr(dY), ptr(X), M, K, N, ptr(G), ptr(ws), nbytes,
+                                   stream_of(G))
+    if rc:
+        _raise(rc)
+
+
+def rigl_bound_factor(N: int) -> float:
+    return float(load().slk_rigl_bound_factor(int(N)))
+
+
+def rigl_count(view: CsrView, thr: torch.Tensor, G: torch.Tensor, nrm_dY: torch.Tensor,
+               nrm_X: torch.Tensor, N: int, info: torch.Tensor, amb_off: torch.Tensor,
+               amb_total: torch.Tensor) -> None:
+    rc = load().slk_rigl_count(ctypes.byref(view), thr.data_ptr(), ptr(G), G.stride(0),
+                               ptr(nrm_dY), ptr(nrm_X), int(N), ptr(info), amb_off.data_ptr(),
+                               amb_total.data_ptr(), stream_of(amb_total))
+    if rc:
+        _raise(rc)
+
+
+def rigl_finish(view: CsrView, thr: torch.Tensor, G: torch.Tensor, nrm_dY: torch.Tensor,
+                nrm_X: torch.Tensor, dY: torch.Tensor, X: torch.Tensor, info: torch.Tensor,
+                amb_off: torch.Tensor, amb_ws: torch.Tensor, ws: torch.Tensor,
+                removed: torch.Tensor) -> None:
+    rc = load().slk_rigl_finish(ctypes.byref(view), view.values, view.col_indices, view.row_nnz,
+                                thr.data_ptr(), ptr(G), G.stride(0), ptr(nrm_dY), ptr(nrm_X),
+                                ptr(dY), ptr(X), dY.shape[1], ptr(info), amb_off.data_ptr(),
+                                ptr(amb_ws), amb_ws.numel(), ptr(ws), ws.numel(),
+                                removed.data_ptr(), stream_of(removed))
     if rc:
         _raise(rc)

@@ -32,6 +32,7 @@
 //                running sum over j in order with the reference build's
 //                arithmetic.
 #include "common.hpp"
+#include "row_rewrite.hpp"
 
 #include <mutex>
 
@@ -87,22 +88,6 @@ __global__ __launch_bounds__(kSelThreads) void kth_hist_kernel(
         if (h[b] != 0) atomicAdd(&st->hist[b], h[b]);
 }
 
-// Inclusive scan of one int64 per thread over a 256-thread workgroup.
-__device__ int64_t block_inclusive_scan(int64_t v, int64_t* tmp) {
-    const int t = threadIdx.x;
-    tmp[t] = v;
-    __syncthreads();
-    for (int off = 1; off < static_cast<int>(blockDim.x); off <<= 1) {
-        const int64_t add = t >= off ? tmp[t - off] : 0;
-        __syncthreads();
-        tmp[t] += add;
-        __syncthreads();
-    }
-    const int64_t r = tmp[t];
-    __syncthreads();
-    return r;
-}
-
 __global__ __launch_bounds__(kSelThreads) void kth_pick_kernel(SelState* __restrict__ st, int pass,
                                                               float* __restrict__ thr_out) {
     __shared__ int64_t tmp[kSelThreads];
@@ -148,7 +133,7 @@ __global__ __launch_bounds__(kSelThreads) void kth_pick_kernel(SelState* __restr
 
 // ───────────────────────── drop / grow ─────────────────────────────────────
 
-constexpr int kDgThreads = 256;
+constexpr int kDgThreads = kRowThreads;
 constexpr int64_t kDgMaxCols = 131072;
 
 __device__ __forceinline__ uint32_t set_key(uint64_t seed, int64_t row, int64_t K, int64_t c) {
@@ -177,9 +162,6 @@ __device__ __forceinline__ bool never_grown(const float* __restrict__ g_row, int
     return g != g;
 }
 
-__device__ __forceinline__ bool bit_of(const uint32_t* bm, int64_t c) {
-    return (bm[c >> 5] >> (c & 31)) & 1u;
-}
 
 template <bool RIGL>
 __global__ __launch_bounds__(kDgThreads) void drop_grow_kernel(
@@ -203,162 +185,39 @@ __global__ __launch_bounds__(kDgThreads) void drop_grow_kernel(
     const int32_t n_live = row_nnz[i];
     if (n_live <= 0) return;  // the reference skips empty rows
     const int32_t start = row_start[i];
-    const float thr = thr_ptr[0];
 
     for (int64_t w = t; w < Kw; w += kDgThreads) keep[w] = grow[w] = 0;
-    if (t == 0) s_best = 0;
     __syncthreads();
-
-    // Survivors: |v| strictly above the threshold.
-    int64_t kept = 0;
-    unsigned long long best = 0;
-    for (int32_t s = t; s < n_live; s += kDgThreads) {
-        const uint32_t u = __float_as_uint(fabsf(values[start + s]));
-        if (__uint_as_float(u) > thr) {
-            ++kept;
-            const int32_t c = cols[start + s];
-            atomicOr(&keep[c >> 5], 1u << (c & 31));
-        }
-        // np.argmax: largest |v| (NaN above all), first slot among equals
-        const unsigned long long key =
-            (static_cast<unsigned long long>(u) << 32) | (0xFFFFFFFFull - static_cast<uint32_t>(s));
-        if (key > best) best = key;
-    }
-    int64_t n_keep = block_inclusive_scan(kept, tmp);
-    n_keep = tmp[kDgThreads - 1];
-    __syncthreads();
-    if (n_keep == 0) {
-        atomicMax(&s_best, best);
-        __syncthreads();
-        if (t == 0) {
-            const int32_t s = static_cast<int32_t>(0xFFFFFFFFull - (s_best & 0xFFFFFFFFull));
-            const int32_t c = cols[start + s];
-            keep[c >> 5] |= 1u << (c & 31);
-        }
-        n_keep = 1;
-        __syncthreads();
-    }
-
+    const int64_t n_keep = mark_survivors(values, cols, start, n_live, thr_ptr[0], keep, tmp,
+                                          &s_best);
     const int64_t n_drop = n_live - n_keep;
     const float* g_row = RIGL ? G + i * ldg : nullptr;
     int64_t n_grow = 0;
-
     if (n_drop > 0) {
-        // Radix select of the n_grow smallest keys among the unmarked columns
-        // a row may grow into. Pass 0 also counts the others (RigL: NaN |G|),
-        // which fixes n_grow = min(dropped, growable columns).
-        uint32_t prefix = 0;
-        int64_t need = 0;
-        for (int pass = 0; pass < 4; ++pass) {
-            const int shift = 24 - 8 * pass;
-            hist[t] = 0;
-            __syncthreads();
+        // n_grow = min(dropped, growable columns); RigL never grows a column
+        // whose |G| is NaN
+        int64_t growable = K - n_keep;
+        if (RIGL) {
             int64_t skipped = 0;
-            for (int64_t c = t; c < K; c += kDgThreads) {
-                if (bit_of(keep, c)) continue;
-                if (never_grown<RIGL>(g_row, c)) {
-                    ++skipped;
-                    continue;
-                }
-                const uint32_t u = grow_key<RIGL>(g_row, seed, i, K, c);
-                if (pass == 0 || (u >> (shift + 8)) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
-            }
-            __syncthreads();
-            if (pass == 0) {
-                int64_t n_growable = K - n_keep;
-                if (RIGL) {
-                    block_inclusive_scan(skipped, tmp);
-                    n_growable -= tmp[kDgThreads - 1];
-                    __syncthreads();
-                }
-                n_grow = n_drop < n_growable ? n_drop : n_growable;
-                need = n_grow;
-                if (n_grow == 0) break;  // block-uniform
-            }
-            const int64_t h = hist[t];
-            const int64_t incl = block_inclusive_scan(h, tmp);
-            if (incl - h < need && need <= incl) {
-                s_digit = static_cast<uint32_t>(t);
-                s_below = incl - h;
-            }
-            __syncthreads();
-            prefix = (prefix << 8) | s_digit;
-            need -= s_below;
+            for (int64_t c = t; c < K; c += kDgThreads)
+                if (!bit_of(keep, c) && never_grown<RIGL>(g_row, c)) ++skipped;
+            block_inclusive_scan(skipped, tmp);
+            growable -= tmp[kDgThreads - 1];
             __syncthreads();
         }
-        // Take every key below the selected one and the first `need` columns
-        // (ascending) whose key equals it.
-        const uint32_t T = prefix;
-        int64_t taken_eq = 0;
-        for (int64_t c0 = 0; n_grow > 0 && c0 < K; c0 += kDgThreads) {
-            const int64_t c = c0 + t;
-            bool lt = false, eq = false;
-            if (c < K && !bit_of(keep, c) && !never_grown<RIGL>(g_row, c)) {
-                const uint32_t u = grow_key<RIGL>(g_row, seed, i, K, c);
-                lt = u < T;
-                eq = u == T;
-            }
-            const int64_t e = eq ? 1 : 0;
-            const int64_t incl = block_inclusive_scan(e, tmp);
-            const int64_t chunk_eq = tmp[kDgThreads - 1];
-            if (lt || (eq && taken_eq + incl - 1 < need)) atomicOr(&grow[c >> 5], 1u << (c & 31));
-            taken_eq += chunk_eq;
-            __syncthreads();
-        }
-        __syncthreads();
+        n_grow = n_drop < growable ? n_drop : growable;
+        // the n_grow smallest keys among the growable columns, ties to the
+        // lower column
+        auto cand = [&](int64_t c, int64_t& col, uint32_t& key) -> bool {
+            col = c;
+            if (bit_of(keep, c) || never_grown<RIGL>(g_row, c)) return false;
+            key = grow_key<RIGL>(g_row, seed, i, K, c);
+            return true;
+        };
+        select_smallest_keys(cand, K, n_grow, grow, hist, &s_digit, &s_below, tmp);
     }
-
-    // Slot of column c in the new row = number of marked columns below c.
-    const int64_t per = ceil_div(Kw, kDgThreads);
-    const int64_t w0 = t * per;
-    const int64_t w1 = w0 + per < Kw ? w0 + per : Kw;
-    int64_t cnt = 0;
-    for (int64_t w = w0; w < w1; ++w) cnt += __popc(keep[w] | grow[w]);
-    const int64_t incl = block_inclusive_scan(cnt, tmp);
-    int64_t run = incl - cnt;
-    for (int64_t w = w0; w < w1; ++w) {
-        wpre[w] = static_cast<uint32_t>(run);
-        run += __popc(keep[w] | grow[w]);
-    }
-    __syncthreads();
-
-    auto rank_of = [&](int64_t c) -> int64_t {
-        const uint32_t word = keep[c >> 5] | grow[c >> 5];
-        const uint32_t below_mask = (c & 31) ? (0xFFFFFFFFu >> (32 - (c & 31))) : 0u;
-        return static_cast<int64_t>(wpre[c >> 5]) + __popc(word & below_mask);
-    };
-    for (int32_t s = t; s < n_live; s += kDgThreads) {
-        const int32_t c = cols[start + s];
-        if (bit_of(keep, c)) {
-            const int64_t p = start + rank_of(c);
-            stage_col[p] = c;
-            stage_val[p] = values[start + s];
-        }
-    }
-    for (int64_t w = t; w < Kw; w += kDgThreads) {
-        uint32_t bits = grow[w];
-        while (bits) {
-            const int b = __builtin_ctz(bits);
-            bits &= bits - 1;
-            const int64_t c = w * 32 + b;
-            const int64_t p = start + rank_of(c);
-            stage_col[p] = static_cast<int32_t>(c);
-            stage_val[p] = 0.0f;
-        }
-    }
-    __syncthreads();
-    // The new row is n_keep + n_grow slots; a RigL row short of growable
-    // columns pads the rest (col -1, value 0) and records its new length.
-    const int64_t n_new = n_keep + n_grow;
-    for (int32_t s = t; s < n_live; s += kDgThreads) {
-        const bool live_s = s < n_new;
-        cols[start + s] = live_s ? stage_col[start + s] : -1;
-        values[start + s] = live_s ? stage_val[start + s] : 0.0f;
-    }
-    if (t == 0 && n_new < n_live) {
-        row_nnz[i] = static_cast<int32_t>(n_new);
-        atomicAdd(removed, static_cast<unsigned long long>(n_live - n_new));
-    }
+    write_back_row(keep, grow, wpre, Kw, i, start, n_live, n_keep, n_grow, values, cols, row_nnz,
+                   stage_col, stage_val, removed, tmp);
 }
 
 __global__ void clear_counter_kernel(unsigned long long* __restrict__ c) { *c = 0; }

@@ -567,10 +567,66 @@ class PaddedCSR:
         stage = torch.empty(_lib.drop_grow_workspace_bytes(view), dtype=torch.uint8, device=dev)
         removed = torch.empty(1, dtype=torch.int64, device=dev)
         _lib.drop_grow(view, thr, rule, G, seed, stage, removed)
+        self._after_topology_pass(int(removed.item()) if rule == _lib.SLK_GROW_GRADIENT else 0)
+
+    # Above this many undecided columns per empty column, the exact dense
+    # gradient (every element recomputed in one GEMM-shaped pass) is cheaper
+    # than recomputing the undecided ones one by one.
+    _RIGL_EXACT_SHARE = 0.125
+
+    def _rigl_update(self, k_drop: int, dY: torch.Tensor, X: torch.Tensor) -> None:
+        """One RigL drop-and-grow pass, grows ranked by |G|, G = dY·Xᵀ with the
+        reference's dense_grad arithmetic, without computing G everywhere.
+
+        dY (nrows x N) and X (ncols x N) are row-major float32 on the device.
+        G' = dY·Xᵀ runs on the matrix cores; its certified error bound decides
+        most empty columns, and only the undecided ones are computed exactly
+        (slk_rigl_norms, slk_dense_grad_approx, slk_rigl_count,
+        slk_rigl_finish). The rows come out exactly as
+        ``_drop_grow(k_drop, SLK_GROW_GRADIENT, dense_grad(dY, X))`` writes
+        them. Two device reads: the undecided count and the removed slots.
+        """
+        self._require_device("rigl")
+        if not 1 <= k_drop <= self._nnz:
+            raise ValueError(f"drop_grow: k_drop={k_drop} outside [1, nnz={self._nnz}]")
+        M, K = self._nrows, self._ncols
+        if dY.shape[0] != M or X.shape[0] != K or dY.shape[1] != X.shape[1]:
+            raise ValueError(f"rigl: dY {tuple(dY.shape)} and X {tuple(X.shape)} do not match "
+                             f"W ({M}, {K})")
+        dev = self._values.device
+        dY = dY.to(_F32).contiguous()
+        X = X.to(_F32).contiguous()
+        view = self._view()
+        ws = torch.empty(_lib.SLK_KTH_WORKSPACE_BYTES, dtype=torch.uint8, device=dev)
+        thr = torch.empty(1, dtype=_F32, device=dev)
+        _lib.live_abs_kth(view, k_drop, ws, thr)
+        nrm_dY = torch.empty(M, dtype=_F32, device=dev)
+        nrm_X = torch.empty(K, dtype=_F32, device=dev)
+        _lib.rigl_norms(dY, X, nrm_dY, nrm_X)
+        Gp = torch.empty(M, K, dtype=_F32, device=dev)
+        _lib.dense_grad_approx(dY, X, Gp)
+        info = torch.empty(M * _lib.RIGL_INFO_BYTES, dtype=torch.uint8, device=dev)
+        amb_off = torch.empty(2 * M + 1, dtype=torch.int64, device=dev)
+        total = torch.empty(1, dtype=torch.int64, device=dev)
+        _lib.rigl_count(view, thr, Gp, nrm_dY, nrm_X, dY.shape[1], info, amb_off, total)
+        n_amb = int(total.item())
+        if n_amb > self._RIGL_EXACT_SHARE * max(1, M * K - self._nnz):
+            del Gp
+            from .ops import dense_grad
+            self._drop_grow(k_drop, _lib.SLK_GROW_GRADIENT, dense_grad(dY, X))
+            return
+        amb = torch.empty(max(8, 8 * n_amb), dtype=torch.uint8, device=dev)
+        stage = torch.empty(_lib.drop_grow_workspace_bytes(view), dtype=torch.uint8, device=dev)
+        removed = torch.empty(1, dtype=torch.int64, device=dev)
+        _lib.rigl_finish(view, thr, Gp, nrm_dY, nrm_X, dY, X, info, amb_off, amb, stage, removed)
+        self._after_topology_pass(int(removed.item()))
+
+    def _after_topology_pass(self, lost: int) -> None:
+        """Bookkeeping after a drop/grow pass: the version bump, and where rows
+        shrank (RigL rows short of non-NaN columns), the host nnz and the row
+        schedule."""
         self._topology_version += 1
-        lost = int(removed.item()) if rule == _lib.SLK_GROW_GRADIENT else 0
         if lost:
-            # some rows shrank: row_nnz changed on the device
             self._nnz -= lost
             self._host_rows = None
             self._heavy_hint = None

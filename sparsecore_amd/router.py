@@ -190,7 +190,7 @@ class RigL(DynamicSparsityAlgorithm):
         self._rebuild_transposes()
 
     def _update_layer(self, layer, rng) -> None:
-        from .ops import _dense_grad_token_major
+        from .ops import _as_row_major
 
         captured = self._captured.get(id(layer))
         if captured is None or "X" not in captured or "dY" not in captured:
@@ -203,6 +203,7 @@ class RigL(DynamicSparsityAlgorithm):
         dev = csr.device
         x = captured["X"].reshape(-1, layer.in_features).to(dev)
         dy = captured["dY"].reshape(-1, layer.out_features).to(dev)
-        G = _dense_grad_token_major(dy, x)  # (out, in) = (M, K)
-        csr._drop_grow(self._k_drop(total_nnz), _lib.SLK_GROW_GRADIENT, G)
+        # grows ranked by |G|, G = dyᵀ·x = (out, in): certified from the
+        # matrix-core approximation, exact where it cannot decide
+        csr._rigl_update(self._k_drop(total_nnz), _as_row_major(dy.t()), _as_row_major(x.t()))
         self._captured.pop(id(layer), None)

@@ -205,9 +205,11 @@ def test_c5_layer_at_full_size(dev, c5_layers, density):
 
 @pytest.mark.parametrize("density", [0.05, 0.01], ids=["95", "99"])
 def test_c5_rigl_rewrite_at_full_size(dev, c5_layers, density):
-    """One RigL step of the C5 workload: G = dY·Xᵀ (checked on 4 sampled rows),
-    the global threshold (checked exactly), drop/grow on the device (checked
-    on sampled rows against the oracle's row rule with the device's G row),
+    """One RigL step of the C5 workload as bench.py runs it: the exact G = dY·Xᵀ
+    (checked on 4 sampled rows against the oracle), the global threshold
+    (checked exactly), the certified RigL update (matrix-core G', exact G
+    where undecided; checked on sampled rows against the oracle's row rule
+    with the exact G row),
     then the rebuilt transpose (checked in full) and the forward on the new
     topology (sampled rows)."""
     W, X, dY = c5_layers(density)
@@ -227,8 +229,8 @@ def test_c5_rigl_rewrite_at_full_size(dev, c5_layers, density):
                       thr_dev)
     thr = thr_dev.cpu().numpy()[0]
     assert thr.view(np.uint32) == np.float32(oracle.live_abs_kth(c, k)).view(np.uint32)
-    print(f"[config c5 RigL] density={density} drop_grow", flush=True)
-    W._drop_grow(k, _lib.SLK_GROW_GRADIENT, G)
+    print(f"[config c5 RigL] density={density} certified RigL update", flush=True)
+    W._rigl_update(k, dY, X)
     after = to_oracle(W)
     rows = _sample(c.row_nnz, 13)
     G_rows = G[torch.from_numpy(rows).to(dev)].cpu().numpy()

@@ -409,3 +409,99 @@ def test_loss_trajectory_cached_vs_fresh_transpose(dev, algo_ctor, n_steps, batc
     diverged = [i for i, (a, b) in enumerate(zip(cached, fresh)) if a != b]
     assert not diverged, f"cached and fresh trajectories differ from step {diverged[0]}"
     assert sum(cached[-10:]) / 10 < sum(cached[:10]) / 10  # training happened
+
+
+# ─────────────────── RigL from the certified approximate gradient ──────────
+
+def _rigl_inputs(M, K, N, seed, kind="normal"):
+    rng = np.random.default_rng(seed)
+    dY = rng.standard_normal((M, N)).astype(np.float32)
+    X = rng.standard_normal((K, N)).astype(np.float32)
+    if kind == "ties":  # small integers: many exactly equal |G|, exact G' parts
+        dY = rng.integers(-2, 3, (M, N)).astype(np.float32)
+        X = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    elif kind == "scaled":  # rows and columns over many orders of magnitude
+        dY *= (10.0 ** rng.integers(-15, 15, (M, 1))).astype(np.float32)
+        X *= (10.0 ** rng.integers(-15, 15, (K, 1))).astype(np.float32)
+    elif kind == "nonfinite-rows":  # exact rows: every empty column computed exactly
+        dY[1, 3] = np.nan   # the whole G row is NaN: nothing growable, the row shrinks
+        dY[4, 0] = np.inf   # |G| = inf (NaN where X[k, 0] = 0)
+        dY[6, :] *= 1e30    # a norm beyond the certified range
+    elif kind == "nonfinite-cols":  # a NaN column leaves no row certifiable
+        X[2, 5] = np.nan
+        X[7, 1] = -np.inf
+    return dY, X
+
+
+@pytest.mark.parametrize("M,K,N,kind", [
+    (256, 384, 4096, "normal"), (130, 257, 1000, "normal"), (64, 64, 7, "normal"),
+    (300, 200, 513, "scaled"), (128, 128, 1, "normal"), (200, 300, 96, "ties")])
+def test_dense_grad_approx_within_certified_bound(dev, M, K, N, kind):
+    """|G' - G| <= c_N·n_i·n_k + 2^-100·(1 + n_i + n_k) for every element, G
+    the reference-arithmetic dense gradient (itself pinned to the reference
+    build); the norms bound the true row norms."""
+    print(f"[rigl bound] {M}x{K} N={N} {kind}", flush=True)
+    dY_np, X_np = _rigl_inputs(M, K, N, M + K + N, kind)
+    dY, X = torch.from_numpy(dY_np).to(dev), torch.from_numpy(X_np).to(dev)
+    nd = torch.empty(M, device=dev)
+    nx = torch.empty(K, device=dev)
+    _lib.rigl_norms(dY, X, nd, nx)
+    nd64 = np.linalg.norm(dY_np.astype(np.float64), axis=1)
+    nx64 = np.linalg.norm(X_np.astype(np.float64), axis=1)
+    assert np.all(nd.cpu().numpy().astype(np.float64) >= nd64)
+    assert np.all(nx.cpu().numpy().astype(np.float64) >= nx64)
+    Gp = torch.empty(M, K, device=dev)
+    _lib.dense_grad_approx(dY, X, Gp)
+    G = ops.dense_grad(dY, X).cpu().numpy().astype(np.float64)
+    c = _lib.rigl_bound_factor(N)
+    E = (c * nd.cpu().numpy().astype(np.float64)[:, None] * nx.cpu().numpy().astype(np.float64)[None, :]
+         + 2.0 ** -100 * (1 + nd.cpu().numpy()[:, None] + nx.cpu().numpy()[None, :]))
+    err = np.abs(Gp.cpu().numpy().astype(np.float64) - G)
+    assert np.all(err <= E), float(np.max(err / E))
+    # the bound is a bound, not noise: the approximation is far inside it
+    assert float(np.max(err / E)) < 0.5
+
+
+def _rigl_case(name):
+    if name == "uniform":
+        return oracle.uniform_rows(96, 300, 40, seed=31, sigma=1.0), 512, "normal"
+    if name == "zipf":
+        return oracle.zipf_rows(400, 700, 0.06, 1.1, seed=32, sigma=1.0), 1024, "normal"
+    if name == "ties":
+        return oracle.uniform_rows(64, 200, 30, seed=33, sigma=1.0), 96, "ties"
+    if name == "scaled":
+        return oracle.uniform_rows(80, 260, 50, seed=34, sigma=1.0), 513, "scaled"
+    if name == "nonfinite-rows":
+        return oracle.uniform_rows(200, 90, 20, seed=35, sigma=1.0), 64, "nonfinite-rows"
+    if name == "nonfinite-cols":
+        return oracle.uniform_rows(40, 90, 20, seed=39, sigma=1.0), 64, "nonfinite-cols"
+    if name == "n-odd":
+        return oracle.zipf_rows(150, 129, 0.2, 1.1, seed=36, sigma=1.0), 37, "normal"
+    if name == "dense-rows":
+        W = np.random.default_rng(37).standard_normal((30, 50)).astype(np.float32)
+        W[::3, :] *= (np.random.default_rng(38).random((10, 50)) < 0.1)  # some sparse rows
+        return oracle.from_dense(W), 256, "normal"
+    raise KeyError(name)
+
+
+@pytest.mark.parametrize("df", [0.3, 0.9])
+@pytest.mark.parametrize("name", ["uniform", "zipf", "ties", "scaled", "nonfinite-rows",
+                                  "nonfinite-cols", "n-odd", "dense-rows"])
+def test_rigl_certified_matches_exact_drop_grow(dev, name, df):
+    """The certified path (matrix-core G', exact G only where the bound cannot
+    decide) rewrites every row exactly as the exact-G drop/grow does, and as
+    the oracle's RigL rule does with the oracle's G."""
+    c, N, kind = _rigl_case(name)
+    print(f"[rigl certified] {name} df={df} {c.nrows}x{c.ncols} N={N}", flush=True)
+    dY_np, X_np = _rigl_inputs(c.nrows, c.ncols, N, 40 + c.nrows, kind)
+    dY, X = torch.from_numpy(dY_np).to(dev), torch.from_numpy(X_np).to(dev)
+    k = max(1, int(df * c.nnz))
+    W_exact, W_cert = from_oracle(c, dev), from_oracle(c, dev)
+    W_exact._drop_grow(k, _lib.SLK_GROW_GRADIENT, ops.dense_grad(dY, X))
+    W_cert._rigl_update(k, dY, X)
+    csr_arrays_equal(to_oracle(W_cert), to_oracle(W_exact), f"{name} certified vs exact")
+    assert W_cert.nnz == W_exact.nnz and W_cert.topology_version == 1
+    want = oracle.drop_grow(c, k, "gradient", oracle.dense_grad(dY_np, X_np))
+    csr_arrays_equal(to_oracle(W_cert), want, f"{name} certified vs oracle")
+    if name == "nonfinite-rows":
+        assert want.nnz < c.nnz  # the NaN row shrank
