@@ -41,6 +41,9 @@
 #include "common.hpp"
 #include "row_rewrite.hpp"
 
+#include <cmath>
+#include <type_traits>
+
 namespace slk {
 namespace {
 
@@ -165,71 +168,93 @@ __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64
 #pragma unroll
             for (int r = 0; r < 16; ++r) cm[a][b][r] = mm[a][b][r] = cx[a][b][r] = 0.0f;
 
-    f32x4 ra[4], rb[4];
-    auto fetch = [&](int64_t st) {
+    // Pipeline: stage st+2's loads are issued while stage st is computed from
+    // LDS buffer st&1; stage st+1 (loaded during stage st-1) is written into
+    // the other buffer after this stage's MFMAs; one barrier per stage.
+    f32x4 ra[2][4], rb[2][4];
+    auto fetch = [&](int reg, int64_t st) {
+        const unsigned char* pa = ga + st * kAStageBytes;
+        const unsigned char* pb = gb + st * kAStageBytes;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            ra[q] = *reinterpret_cast<const f32x4*>(ga + st * kAStageBytes + 16 * q);
-            rb[q] = *reinterpret_cast<const f32x4*>(gb + st * kAStageBytes + 16 * q);
+            ra[reg][q] = *reinterpret_cast<const f32x4*>(pa + 16 * q);
+            rb[reg][q] = *reinterpret_cast<const f32x4*>(pb + 16 * q);
         }
     };
-    if (nst > 0) fetch(0);
-    const int half = 16 * (lane >> 5);
-    for (int64_t st = 0; st < nst; ++st) {
-        const int buf = static_cast<int>(st & 1);
+    const int st_off = lr * kALdsRow + lh;
+    auto stage_to_lds = [&](int reg, int b) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            *reinterpret_cast<f32x4*>(&sA[buf][lr * kALdsRow + lh + 16 * q]) = ra[q];
-            *reinterpret_cast<f32x4*>(&sB[buf][lr * kALdsRow + lh + 16 * q]) = rb[q];
+            *reinterpret_cast<f32x4*>(&sA[b][st_off + 16 * q]) = ra[reg][q];
+            *reinterpret_cast<f32x4*>(&sB[b][st_off + 16 * q]) = rb[reg][q];
         }
-        __syncthreads();
-        if (st + 1 < nst) fetch(st + 1);  // in flight during this stage's MFMAs
-        // both k-steps' fragments: [k-step][block][high, low]
-        bf16x8 af[2][2][2], bf[2][2][2];
+    };
+    if (nst > 0) fetch(0, 0);
+    if (nst > 1) fetch(1, 1);
+    if (nst > 0) stage_to_lds(0, 0);
+    __syncthreads();
+    const int half = 16 * (lane >> 5);
+    const int ra0 = (wm * 64 + (lane & 31)) * kALdsRow + half;
+    const int rb0 = (wn * 64 + (lane & 31)) * kALdsRow + half;
+    // stage st lives in register set st & 1 and LDS buffer st & 1; the two
+    // parities are unrolled so both indexes are compile-time constants
+    auto stage = [&](auto R, int64_t st) {
+        constexpr int reg = decltype(R)::value;
+        if (st + 2 < nst) fetch(reg, st + 2);  // register set of stage st: already in LDS
+        const unsigned char* la = sA[reg];
+        const unsigned char* lb = sB[reg];
 #pragma unroll
-        for (int s = 0; s < 2; ++s)
+        for (int s = 0; s < 2; ++s) {
+            bf16x8 af[2][2], bf[2][2];  // [block][high, low]
 #pragma unroll
             for (int b = 0; b < 2; ++b)
 #pragma unroll
                 for (int p = 0; p < 2; ++p) {
-                    const int ra_ = wm * 64 + b * 32 + (lane & 31);
-                    const int rb_ = wn * 64 + b * 32 + (lane & 31);
-                    const int o = p * (kAStageBytes / 2) + 32 * s + half;
-                    af[s][b][p] = *reinterpret_cast<const bf16x8*>(&sA[buf][ra_ * kALdsRow + o]);
-                    bf[s][b][p] = *reinterpret_cast<const bf16x8*>(&sB[buf][rb_ * kALdsRow + o]);
+                    const int o = b * 32 * kALdsRow + p * (kAStageBytes / 2) + 32 * s;
+                    af[b][p] = *reinterpret_cast<const bf16x8*>(la + ra0 + o);
+                    bf[b][p] = *reinterpret_cast<const bf16x8*>(lb + rb0 + o);
                 }
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
 #pragma unroll
             for (int a = 0; a < 2; ++a)
 #pragma unroll
                 for (int b = 0; b < 2; ++b)
-                    cm[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s][a][0], bf[s][b][0],
+                    cm[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a][0], bf[b][0],
                                                                         cm[a][b], 0, 0, 0);
 #pragma unroll
             for (int a = 0; a < 2; ++a)
 #pragma unroll
                 for (int b = 0; b < 2; ++b)
-                    cx[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s][a][0], bf[s][b][1],
+                    cx[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a][0], bf[b][1],
                                                                         cx[a][b], 0, 0, 0);
 #pragma unroll
             for (int a = 0; a < 2; ++a)
 #pragma unroll
                 for (int b = 0; b < 2; ++b)
-                    cx[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s][a][1], bf[s][b][0],
+                    cx[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a][1], bf[b][0],
                                                                         cx[a][b], 0, 0, 0);
         }
-        if ((st + 1) % (kAChunk / kAJ) == 0 || st + 1 == nst) {
-#pragma unroll
-            for (int a = 0; a < 2; ++a)
-#pragma unroll
-                for (int b = 0; b < 2; ++b)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        mm[a][b][r] = mm[a][b][r] + cm[a][b][r];
-                        cm[a][b][r] = 0.0f;
-                    }
+        // stage st+1 into the other buffer (its last readers, stage st-1,
+        // passed the previous barrier)
+        if (st + 1 < nst) stage_to_lds(reg ^ 1, reg ^ 1);
+        __syncthreads();
+    };
+    static_assert((kAChunk / kAJ) % 2 == 0, "chunks hold whole stage pairs");
+    for (int64_t c0 = 0; c0 < nst; c0 += kAChunk / kAJ) {
+        const int64_t c1 = c0 + kAChunk / kAJ < nst ? c0 + kAChunk / kAJ : nst;
+        for (int64_t st = c0; st < c1; st += 2) {
+            stage(std::integral_constant<int, 0>{}, st);
+            if (st + 1 < c1) stage(std::integral_constant<int, 1>{}, st + 1);
         }
+        // a chunk of x_h·y_h done: add its sums on the VALU
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    mm[a][b][r] = mm[a][b][r] + cm[a][b][r];
+                    cm[a][b][r] = 0.0f;
+                }
     }
     // lane l, register 4g + q of a 32x32 block: row 8g + 4(l/32) + q, column l % 32
 #pragma unroll
@@ -250,33 +275,30 @@ __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64
 struct RowInfo {
     int32_t n_grow;  // grows of the row (exact rows: decided in finish)
     int32_t n_in;    // columns certainly grown
-    float t_lo;      // the n_grow-th largest lower bound
-    float t_hi;      // the n_grow-th largest upper bound
+    float t_in;      // a column is certainly grown if its lower bound exceeds this
+    float t_out;     // a column is certainly not grown if its upper bound is below this
     int32_t flags;   // kRowExact, kRowKeep
     int32_t n_keep;
-    int32_t pad[2];
+    float cni;       // an upper bound of c_N·n_i
+    float delta;     // the absolute part of the bound, for every column of the row
 };
 constexpr int32_t kRowExact = 1;  // every empty column undecided
 constexpr int32_t kRowKeep = 2;   // nothing to grow: the row is left as it is
 static_assert(sizeof(RowInfo) == 32, "RowInfo is 32 bytes");
 
-// Certified bounds of |G[i, c]| from |G'[i, c]|: false if the column must be
-// decided exactly (norms not finite or too large).
-__device__ __forceinline__ bool bounds_of(float g, float ni, float nk, double c_bound, float& lo,
-                                          float& hi) {
-    if (!(ni <= 0x1p60f) || !(nk <= 0x1p60f)) return false;
-    const double e = c_bound * static_cast<double>(ni) * static_cast<double>(nk) *
-                         (1.0 + 0x1p-30) +
-                     0x1p-100 * (1.0 + static_cast<double>(ni) + static_cast<double>(nk));
-    const double a = fabs(static_cast<double>(g));
-    if (!(a <= 0x1p125)) return false;  // G' not finite (cannot happen below the norm cap)
-    const double l = (a - e) * (1.0 - 0x1p-40), h = (a + e) * (1.0 + 0x1p-40);
-    lo = l > 0.0 ? __double2float_rd(l) : 0.0f;
-    hi = __double2float_ru(h);
-    return true;
+// Float bounds, each rounded outward by a relative 2^-20 (every float
+// operation rounds by at most 2^-24) and an absolute 2^-120 (subnormals).
+__device__ __forceinline__ float up_(float x) { return x * (1.0f + 0x1p-20f) + 0x1p-120f; }
+__device__ __forceinline__ float dn_(float x) { return x * (1.0f - 0x1p-20f) - 0x1p-120f; }
+constexpr float kNormCap = 0x1p60f;  // norms above this make the row exact
+
+// The per-column error E_k = up(cni·n_k) + delta >= c_N·n_i·n_k + the
+// absolute part (delta = up(2^-100·(1 + n_i + max n_k))).
+__device__ __forceinline__ float col_err(float cni, float nk, float delta) {
+    return up_(cni * nk) + delta;
 }
 
-// Largest-first selection keys of a non-negative float.
+// Largest-first selection key of a non-negative float.
 __device__ __forceinline__ uint32_t desc_key(float v) { return ~__float_as_uint(v); }
 
 // The need-th smallest key among n candidates (cand(e, key) -> bool): a radix
@@ -290,10 +312,11 @@ __device__ uint32_t kth_smallest_key(Cand cand, int64_t n, int64_t need, uint32_
         const int shift = 24 - 8 * pass;
         hist[t] = 0;
         __syncthreads();
-        for (int64_t e = t; e < n; e += kRowThreads) {
-            uint32_t u;
-            if (!cand(e, u)) continue;
-            if (pass == 0 || (u >> (shift + 8)) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
+        const int64_t n_pad = ceil_div(n, kRowThreads) * kRowThreads;  // uniform trip count
+        for (int64_t e = t; e < n_pad; e += kRowThreads) {
+            uint32_t u = 0;
+            const bool ok = e < n && cand(e, u) && (pass == 0 || (u >> (shift + 8)) == prefix);
+            hist_add(hist, (u >> shift) & 255u, ok);
         }
         __syncthreads();
         const int64_t h = hist[t];
@@ -310,108 +333,142 @@ __device__ uint32_t kth_smallest_key(Cand cand, int64_t n, int64_t need, uint32_
     return prefix;
 }
 
+constexpr int64_t kStageMaxK = 16384;  // G' rows up to this length are staged in LDS
+constexpr int kColBlock = 8;            // float4 loads per thread in flight per block
+
+// Calls f(c, g, nk) for every column c < K of a row: g = G'[c] of the row,
+// nk = nrm_c[c]. V4 (K % 4 == 0, 16-byte aligned rows): each thread issues
+// kColBlock float4 loads of both before using any, so a row streams with one
+// memory latency per block instead of one per column.
+template <bool V4, class F>
+__device__ __forceinline__ void for_each_col(const float* __restrict__ g_row,
+                                             const float* __restrict__ nrm_c, int64_t K, F f) {
+    const int t = threadIdx.x;
+    if (V4) {
+        constexpr int64_t step = int64_t{kRowThreads} * 4 * kColBlock;
+        for (int64_t base = 0; base < K; base += step) {
+            f32x4 g[kColBlock], n[kColBlock];
+#pragma unroll
+            for (int u = 0; u < kColBlock; ++u) {
+                const int64_t c = base + 4 * (t + int64_t{kRowThreads} * u);
+                if (c < K) {
+                    g[u] = *reinterpret_cast<const f32x4*>(g_row + c);
+                    n[u] = *reinterpret_cast<const f32x4*>(nrm_c + c);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kColBlock; ++u) {
+                const int64_t c = base + 4 * (t + int64_t{kRowThreads} * u);
+                if (c < K) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) f(c + e, g[u][e], n[u][e]);
+                }
+            }
+        }
+    } else {
+        for (int64_t c = t; c < K; c += kRowThreads) f(c, g_row[c], nrm_c[c]);
+    }
+}
+
+// Per row: survivors (as the exact kernel), then, over the empty columns,
+// T' = the n_grow-th largest |G'| and E_max = the largest E_k. Every |G_k|
+// lies below |G'_k| + E_max, so the n_grow-th largest |G| is at most
+// t_in = T' + E_max; and |G'_k| >= T' holds for n_grow columns, so it is at
+// least t_out = T' - E_max. A column is certainly grown if |G'_k| - E_k >
+// t_in (at most n_grow - 1 of them: they all have |G'_k| > T'), certainly
+// not grown if |G'_k| + E_k < t_out, and undecided otherwise (with the
+// certain ones, at least n_grow: every column with |G'_k| >= T' is one).
+template <bool STAGED, bool V4>
 __global__ __launch_bounds__(kRowThreads) void rigl_count_kernel(
     int64_t K, int64_t Kw, const int32_t* __restrict__ row_start,
     const int32_t* __restrict__ row_nnz, const float* __restrict__ values,
     const int32_t* __restrict__ cols, const float* __restrict__ thr_ptr,
     const float* __restrict__ Gp, int64_t ldg, const float* __restrict__ nrm_r,
-    const float* __restrict__ nrm_c, double c_bound, RowInfo* __restrict__ info,
+    const float* __restrict__ nrm_c, float c_bound, RowInfo* __restrict__ info,
     int64_t* __restrict__ amb_count) {
     extern __shared__ uint32_t lds[];
     uint32_t* keep = lds;
+    float* ag = reinterpret_cast<float*>(lds + Kw);  // |G'| of the row (STAGED)
     __shared__ int64_t tmp[kRowThreads];
     __shared__ uint32_t hist[256];
     __shared__ uint32_t s_digit;
     __shared__ int64_t s_below;
     __shared__ unsigned long long s_best;
+    __shared__ uint32_t s_nmax;
 
     const int64_t i = blockIdx.x;
     const int t = threadIdx.x;
     RowInfo ri{};
     const int32_t n_live = row_nnz[i];
-    if (n_live <= 0) {  // the reference skips empty rows
+    auto finish_row = [&](int32_t flags, int64_t n_amb) {
         if (t == 0) {
-            ri.flags = kRowKeep;
+            ri.flags = flags;
             info[i] = ri;
-            amb_count[i] = 0;
+            amb_count[i] = n_amb;
         }
-        return;
-    }
+    };
+    if (n_live <= 0) return finish_row(kRowKeep, 0);  // the reference skips empty rows
     const int32_t start = row_start[i];
     for (int64_t w = t; w < Kw; w += kRowThreads) keep[w] = 0;
+    if (t == 0) s_nmax = 0;
     __syncthreads();
     const int64_t n_keep = mark_survivors(values, cols, start, n_live, thr_ptr[0], keep, tmp,
                                           &s_best);
     const int64_t n_drop = n_live - n_keep;
     ri.n_keep = static_cast<int32_t>(n_keep);
-    if (n_drop == 0) {
-        if (t == 0) {
-            ri.flags = kRowKeep;
-            info[i] = ri;
-            amb_count[i] = 0;
-        }
-        return;
-    }
+    if (n_drop == 0) return finish_row(kRowKeep, 0);
+    const int64_t n_empty = K - n_keep;
     const float ni = nrm_r[i];
     const float* g_row = Gp + i * ldg;
-    // a column without a certified bound makes the whole row exact
+
+    // stage |G'|, the largest candidate norm, and whether every bound exists
     int64_t unbounded = 0;
-    for (int64_t c = t; c < K; c += kRowThreads) {
-        float lo, hi;
-        if (!bit_of(keep, c) && !bounds_of(g_row[c], ni, nrm_c[c], c_bound, lo, hi)) ++unbounded;
-    }
+    uint32_t nmax = 0;
+    for_each_col<V4>(g_row, nrm_c, K, [&](int64_t c, float g, float nk) {
+        const float a = fabsf(g);
+        if (STAGED) ag[c] = a;
+        if (bit_of(keep, c)) return;
+        if (!(nk <= kNormCap) || !(a <= 0x1p125f)) ++unbounded;
+        else nmax = max(nmax, __float_as_uint(nk));
+    });
+    atomicMax(&s_nmax, nmax);
     block_inclusive_scan(unbounded, tmp);
     unbounded = tmp[kRowThreads - 1];
-    __syncthreads();
-    const int64_t n_empty = K - n_keep;
-    if (unbounded > 0) {
-        if (t == 0) {
-            ri.flags = kRowExact;
-            info[i] = ri;
-            amb_count[i] = n_empty;
-        }
-        return;
-    }
+    if (unbounded > 0 || !(ni <= kNormCap)) return finish_row(kRowExact, n_empty);
+    const float nm = __uint_as_float(s_nmax);
     const int64_t n_grow = n_drop < n_empty ? n_drop : n_empty;
-    auto lower = [&](int64_t c, uint32_t& key) -> bool {
+    auto absg = [&](int64_t c) -> float { return STAGED ? ag[c] : fabsf(g_row[c]); };
+    auto key_of = [&](int64_t c, uint32_t& key) -> bool {
         if (bit_of(keep, c)) return false;
-        float lo, hi;
-        bounds_of(g_row[c], ni, nrm_c[c], c_bound, lo, hi);
-        key = desc_key(lo);
+        key = desc_key(absg(c));
         return true;
     };
-    auto upper = [&](int64_t c, uint32_t& key) -> bool {
-        if (bit_of(keep, c)) return false;
-        float lo, hi;
-        bounds_of(g_row[c], ni, nrm_c[c], c_bound, lo, hi);
-        key = desc_key(hi);
-        return true;
-    };
-    const float t_lo = __uint_as_float(~kth_smallest_key(lower, K, n_grow, hist, &s_digit,
-                                                         &s_below, tmp));
-    const float t_hi = __uint_as_float(~kth_smallest_key(upper, K, n_grow, hist, &s_digit,
-                                                         &s_below, tmp));
+    const float Tp = __uint_as_float(~kth_smallest_key(key_of, K, n_grow, hist, &s_digit,
+                                                       &s_below, tmp));
+    const float cni = up_(c_bound * ni);
+    const float delta = up_(0x1p-100f * up_(1.0f + ni + nm));
+    const float e_max = col_err(cni, nm, delta);
+    const float t_in = up_(Tp + e_max);
+    const float t_out = dn_(Tp - e_max);
     int64_t n_in = 0, n_amb = 0;
-    for (int64_t c = t; c < K; c += kRowThreads) {
-        if (bit_of(keep, c)) continue;
-        float lo, hi;
-        bounds_of(g_row[c], ni, nrm_c[c], c_bound, lo, hi);
-        if (lo > t_hi) ++n_in;
-        else if (hi >= t_lo) ++n_amb;
-    }
+    for_each_col<V4>(g_row, nrm_c, K, [&](int64_t c, float g, float nk) {
+        if (bit_of(keep, c)) return;
+        const float a = fabsf(g);
+        const float e = col_err(cni, nk, delta);
+        if (dn_(a - e) > t_in) ++n_in;
+        else if (!(up_(a + e) < t_out)) ++n_amb;
+    });
     block_inclusive_scan(n_in, tmp);
     n_in = tmp[kRowThreads - 1];
-    __syncthreads();
     block_inclusive_scan(n_amb, tmp);
     n_amb = tmp[kRowThreads - 1];
-    if (t == 0) {
-        ri.n_grow = static_cast<int32_t>(n_grow);
-        ri.n_in = static_cast<int32_t>(n_in);
-        ri.t_lo = t_lo;
-        ri.t_hi = t_hi;
-        info[i] = ri;
-        amb_count[i] = n_amb;
-    }
+    ri.n_grow = static_cast<int32_t>(n_grow);
+    ri.n_in = static_cast<int32_t>(n_in);
+    ri.t_in = t_in;
+    ri.t_out = t_out;
+    ri.cni = cni;
+    ri.delta = delta;
+    finish_row(0, n_amb);
 }
 
 // off[0..M] = exclusive scan of cnt[0..M-1]; *total = off[M]. One workgroup.
@@ -449,13 +506,42 @@ constexpr int64_t kRiglMaxCols = 131072;  // bitmaps of 3 x 16 KiB in LDS
 // Exact G[i, c] with the reference's arithmetic: one running sum over j,
 // products rounded then added, the last N mod 4 terms fused. y: dY_i (LDS
 // or global), x: X_c (global); V4: both 16-byte aligned and N % 4 == 0.
+constexpr int kDotBlock = 8;  // float4 of X in flight per block of the exact dot
+
+// Exact G[i, c] with the reference's arithmetic: one running sum over j,
+// products rounded then added, the last N mod 4 terms fused. y: dY_i (LDS
+// or global), x: X_c (global); V4: both 16-byte aligned and N % 4 == 0, and
+// the next block of x is loaded while the current one is summed.
 template <bool V4>
 __device__ __forceinline__ float exact_dot(const float* y, const float* __restrict__ x, int64_t N) {
     float acc = 0.0f;
     const int64_t n4 = N & ~int64_t{3};
     int64_t j = 0;
     if (V4) {
-        for (; j < n4; j += 4) {
+        const int64_t nb = n4 / (4 * kDotBlock);
+        f32x4 cur[kDotBlock], nxt[kDotBlock];
+        if (nb > 0) {
+#pragma unroll
+            for (int u = 0; u < kDotBlock; ++u) cur[u] = *reinterpret_cast<const f32x4*>(x + 4 * u);
+        }
+        for (int64_t b = 0; b < nb; ++b) {
+            if (b + 1 < nb) {
+#pragma unroll
+                for (int u = 0; u < kDotBlock; ++u)
+                    nxt[u] = *reinterpret_cast<const f32x4*>(x + 4 * (kDotBlock * (b + 1) + u));
+            }
+#pragma unroll
+            for (int u = 0; u < kDotBlock; ++u) {
+                const f32x4 a = *reinterpret_cast<const f32x4*>(y + 4 * (kDotBlock * b + u));
+                acc = acc + a[0] * cur[u][0];
+                acc = acc + a[1] * cur[u][1];
+                acc = acc + a[2] * cur[u][2];
+                acc = acc + a[3] * cur[u][3];
+            }
+#pragma unroll
+            for (int u = 0; u < kDotBlock; ++u) cur[u] = nxt[u];
+        }
+        for (j = nb * 4 * kDotBlock; j < n4; j += 4) {
             const f32x4 a = *reinterpret_cast<const f32x4*>(y + j);
             const f32x4 b = *reinterpret_cast<const f32x4*>(x + j);
             acc = acc + a[0] * b[0];
@@ -473,13 +559,13 @@ __device__ __forceinline__ float exact_dot(const float* y, const float* __restri
     return acc;
 }
 
-template <bool V4>
+template <bool V4, bool VG>
 __global__ __launch_bounds__(kRowThreads) void rigl_finish_kernel(
     int64_t K, int64_t Kw, int64_t N, const int32_t* __restrict__ row_start,
     int32_t* __restrict__ row_nnz, float* __restrict__ values, int32_t* __restrict__ cols,
     const float* __restrict__ thr_ptr, const float* __restrict__ Gp, int64_t ldg,
-    const float* __restrict__ nrm_r, const float* __restrict__ nrm_c, double c_bound,
-    const RowInfo* __restrict__ info, const int64_t* __restrict__ amb_off,
+    const float* __restrict__ nrm_c, const RowInfo* __restrict__ info,
+    const int64_t* __restrict__ amb_off,
     int32_t* __restrict__ amb_col, uint32_t* __restrict__ amb_key,
     const float* __restrict__ dY, const float* __restrict__ X,
     int32_t* __restrict__ stage_col, float* __restrict__ stage_val,
@@ -507,33 +593,48 @@ __global__ __launch_bounds__(kRowThreads) void rigl_finish_kernel(
                                           &s_best);
     const int64_t n_drop = n_live - n_keep;
     const bool exact_row = (ri.flags & kRowExact) != 0;
-    const float ni = nrm_r[i];
     const float* g_row = Gp + i * ldg;
     const int64_t off = amb_off[i];
     const int64_t n_amb = amb_off[i + 1] - off;
 
-    // undecided columns, ascending; certainly grown ones straight into `grow`
-    int64_t run = 0;
-    for (int64_t c0 = 0; c0 < K; c0 += kRowThreads) {
-        const int64_t c = c0 + t;
-        bool amb = false;
-        if (c < K && !bit_of(keep, c)) {
-            if (exact_row) {
-                amb = true;
-            } else {
-                float lo, hi;
-                bounds_of(g_row[c], ni, nrm_c[c], c_bound, lo, hi);
-                if (lo > ri.t_hi) atomicOr(&grow[c >> 5], 1u << (c & 31));
-                else amb = hi >= ri.t_lo;
+    // undecided columns into a bitmap (in wpre, free until the write-back),
+    // certainly grown ones straight into `grow`; then listed in ascending
+    // order with one scan over the bitmap's words
+    uint32_t* ambm = wpre;
+    for (int64_t w = t; w < Kw; w += kRowThreads) ambm[w] = 0;
+    __syncthreads();
+    if (exact_row) {
+        for (int64_t c = t; c < K; c += kRowThreads)
+            if (!bit_of(keep, c)) atomicOr(&ambm[c >> 5], 1u << (c & 31));
+    } else {
+        for_each_col<VG>(g_row, nrm_c, K, [&](int64_t c, float g, float nk) {
+            if (bit_of(keep, c)) return;
+            const float a = fabsf(g);
+            const float e = col_err(ri.cni, nk, ri.delta);
+            if (dn_(a - e) > ri.t_in) atomicOr(&grow[c >> 5], 1u << (c & 31));
+            else if (!(up_(a + e) < ri.t_out)) atomicOr(&ambm[c >> 5], 1u << (c & 31));
+        });
+    }
+    __syncthreads();
+    {
+        const int64_t per = ceil_div(Kw, kRowThreads);
+        const int64_t w0 = t * per < Kw ? t * per : Kw, w1 = w0 + per < Kw ? w0 + per : Kw;
+        int64_t cnt = 0;
+        for (int64_t w = w0; w < w1; ++w) cnt += __popc(ambm[w]);
+        int64_t pos = block_inclusive_scan(cnt, tmp) - cnt;
+        // (the count pass classified the same columns the same way, so every
+        // position is below n_amb; the guard keeps a mismatch inside the row)
+        for (int64_t w = w0; w < w1; ++w) {
+            uint32_t bits = ambm[w];
+            while (bits) {
+                const int b = __builtin_ctz(bits);
+                bits &= bits - 1;
+                if (pos < n_amb) amb_col[off + pos] = static_cast<int32_t>(w * 32 + b);
+                ++pos;
             }
         }
-        const int64_t incl = block_inclusive_scan(amb ? 1 : 0, tmp);
-        // (the count pass classified the same columns the same way, so
-        // run + incl <= n_amb; the guard keeps a mismatch inside the row)
-        if (amb && run + incl - 1 < n_amb) amb_col[off + run + incl - 1] = static_cast<int32_t>(c);
-        run += tmp[kRowThreads - 1];
-        __syncthreads();
     }
+    __syncthreads();
 
     // exact keys of the undecided columns (0 marks a NaN |G|)
     const float* y = dY + i * N;
@@ -677,10 +778,30 @@ extern "C" int slk_rigl_count(const slk_csr* W, const float* thr_dev, const floa
     const int64_t Kw = ceil_div(K, 32) > 0 ? ceil_div(K, 32) : 1;
     // amb_off doubles as the per-row counts before the scan
     if (M > 0) {
-        hipLaunchKernelGGL(rigl_count_kernel, dim3(static_cast<unsigned>(M)), dim3(kRowThreads),
-                           static_cast<size_t>(Kw) * 4, st, K, Kw, W->row_start, W->row_nnz,
-                           W->values, W->col_indices, thr_dev, G_approx, ldg, nrm_dY, nrm_X,
-                           certified_c(N), static_cast<RowInfo*>(info), amb_off + M + 1);
+        // c_N rounded up to a float
+        const float c_f = std::nextafter(static_cast<float>(certified_c(N)), INFINITY);
+        const bool vg = K % 4 == 0 && ldg % 4 == 0 &&
+                        reinterpret_cast<uintptr_t>(G_approx) % 16 == 0 &&
+                        reinterpret_cast<uintptr_t>(nrm_X) % 16 == 0;
+        const dim3 grid(static_cast<unsigned>(M));
+        const size_t lds_st = static_cast<size_t>(Kw + K) * 4, lds_un = static_cast<size_t>(Kw) * 4;
+#define SLK_COUNT_ARGS                                                                       \
+    K, Kw, W->row_start, W->row_nnz, W->values, W->col_indices, thr_dev, G_approx, ldg, nrm_dY, \
+        nrm_X, c_f, static_cast<RowInfo*>(info), amb_off + M + 1
+        if (K <= kStageMaxK && vg) {
+            hipLaunchKernelGGL((rigl_count_kernel<true, true>), grid, dim3(kRowThreads), lds_st, st,
+                               SLK_COUNT_ARGS);
+        } else if (K <= kStageMaxK) {
+            hipLaunchKernelGGL((rigl_count_kernel<true, false>), grid, dim3(kRowThreads), lds_st, st,
+                               SLK_COUNT_ARGS);
+        } else if (vg) {
+            hipLaunchKernelGGL((rigl_count_kernel<false, true>), grid, dim3(kRowThreads), lds_un, st,
+                               SLK_COUNT_ARGS);
+        } else {
+            hipLaunchKernelGGL((rigl_count_kernel<false, false>), grid, dim3(kRowThreads), lds_un,
+                               st, SLK_COUNT_ARGS);
+        }
+#undef SLK_COUNT_ARGS
         if (int rc = check_launch("rigl_count")) return rc;
     }
     hipLaunchKernelGGL(rigl_scan_kernel, dim3(1), dim3(1024), 0, st, M, amb_off + M + 1, amb_off,
@@ -732,18 +853,26 @@ extern "C" int slk_rigl_finish(const slk_csr* W, float* values, int32_t* col_ind
     const size_t lds = static_cast<size_t>(words) * 4;
     int32_t* stage_col = static_cast<int32_t*>(workspace);
     float* stage_val = reinterpret_cast<float*>(stage_col + W->total_capacity);
-    if (v4) {
-        hipLaunchKernelGGL(rigl_finish_kernel<true>, dim3(static_cast<unsigned>(M)),
-                           dim3(kRowThreads), lds, st, K, Kw, N, W->row_start, row_nnz, values,
-                           col_indices, thr_dev, G_approx, ldg, nrm_dY, nrm_X, certified_c(N),
-                           static_cast<const RowInfo*>(info), amb_off, amb_col, amb_key, dY, X,
-                           stage_col, stage_val, removed_u);
+    const bool vg = K % 4 == 0 && ldg % 4 == 0 && reinterpret_cast<uintptr_t>(G_approx) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(nrm_X) % 16 == 0;
+    const dim3 grid(static_cast<unsigned>(M));
+#define SLK_FINISH_ARGS                                                                      \
+    K, Kw, N, W->row_start, row_nnz, values, col_indices, thr_dev, G_approx, ldg, nrm_X,     \
+        static_cast<const RowInfo*>(info), amb_off, amb_col, amb_key, dY, X, stage_col, stage_val, \
+        removed_u
+    if (v4 && vg) {
+        hipLaunchKernelGGL((rigl_finish_kernel<true, true>), grid, dim3(kRowThreads), lds, st,
+                           SLK_FINISH_ARGS);
+    } else if (v4) {
+        hipLaunchKernelGGL((rigl_finish_kernel<true, false>), grid, dim3(kRowThreads), lds, st,
+                           SLK_FINISH_ARGS);
+    } else if (vg) {
+        hipLaunchKernelGGL((rigl_finish_kernel<false, true>), grid, dim3(kRowThreads), lds, st,
+                           SLK_FINISH_ARGS);
     } else {
-        hipLaunchKernelGGL(rigl_finish_kernel<false>, dim3(static_cast<unsigned>(M)),
-                           dim3(kRowThreads), lds, st, K, Kw, N, W->row_start, row_nnz, values,
-                           col_indices, thr_dev, G_approx, ldg, nrm_dY, nrm_X, certified_c(N),
-                           static_cast<const RowInfo*>(info), amb_off, amb_col, amb_key, dY, X,
-                           stage_col, stage_val, removed_u);
+        hipLaunchKernelGGL((rigl_finish_kernel<false, false>), grid, dim3(kRowThreads), lds, st,
+                           SLK_FINISH_ARGS);
     }
+#undef SLK_FINISH_ARGS
     return check_launch("rigl_finish");
 }

@@ -16,21 +16,26 @@ namespace {
 
 constexpr int kRowThreads = 256;
 
-// Inclusive scan of one int64 per thread over a workgroup (blockDim.x
-// threads); tmp holds blockDim.x entries and keeps the scan on return.
+// Inclusive scan of one int64 per thread over a workgroup of kRowThreads
+// threads: a shuffle scan inside each wave, then the wave totals. tmp holds
+// kRowThreads entries and keeps the scan on return (tmp[kRowThreads - 1] is
+// the total).
 __device__ int64_t block_inclusive_scan(int64_t v, int64_t* tmp) {
     const int t = threadIdx.x;
+    const int lane = t & (kWave - 1);
+    const int w = t / kWave;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int64_t up = __shfl_up(v, off);
+        if (lane >= off) v += up;
+    }
+    __shared__ int64_t wsum[kRowThreads / kWave];
+    if (lane == kWave - 1) wsum[w] = v;
+    __syncthreads();
+    for (int q = 0; q < w; ++q) v += wsum[q];
     tmp[t] = v;
     __syncthreads();
-    for (int off = 1; off < static_cast<int>(blockDim.x); off <<= 1) {
-        const int64_t add = t >= off ? tmp[t - off] : 0;
-        __syncthreads();
-        tmp[t] += add;
-        __syncthreads();
-    }
-    const int64_t r = tmp[t];
-    __syncthreads();
-    return r;
+    return v;
 }
 
 __device__ __forceinline__ bool bit_of(const uint32_t* bm, int64_t c) {
@@ -147,6 +152,26 @@ __device__ void write_back_row(const uint32_t* keep, const uint32_t* grow, uint3
     }
 }
 
+// hist[bin] += 1 for every lane with `valid`, the wave's lanes sharing a bin
+// folded into one atomic (radix digits of float magnitudes are often one
+// value across a whole row: one atomic per lane would serialize on it). Two
+// folding rounds, then one atomic per remaining lane. Every lane of the wave
+// must call it.
+__device__ __forceinline__ void hist_add(uint32_t* hist, uint32_t bin, bool valid) {
+    const int lane = threadIdx.x & (kWave - 1);
+    uint64_t pend = __ballot(valid);
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        if (pend == 0) break;
+        const int leader = __ffsll(static_cast<unsigned long long>(pend)) - 1;
+        const uint32_t b = __shfl(bin, leader);
+        const uint64_t same = __ballot(valid && bin == b) & pend;
+        if (lane == leader) atomicAdd(&hist[b], static_cast<uint32_t>(__popcll(same)));
+        pend &= ~same;
+    }
+    if ((pend >> lane) & 1ull) atomicAdd(&hist[bin], 1u);
+}
+
 // Selects, among `n` candidates given by cand(e) -> (column, key, ok), the
 // `need` with the smallest 32-bit keys, ties to the lower column, and sets
 // their columns in `grow`. Candidates must be enumerated in ascending column
@@ -163,11 +188,13 @@ __device__ void select_smallest_keys(Cand cand, int64_t n, int64_t need, uint32_
         const int shift = 24 - 8 * pass;
         hist[t] = 0;
         __syncthreads();
-        for (int64_t e = t; e < n; e += kRowThreads) {
-            int64_t c;
-            uint32_t u;
-            if (!cand(e, c, u)) continue;
-            if (pass == 0 || (u >> (shift + 8)) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
+        const int64_t n_pad = ceil_div(n, kRowThreads) * kRowThreads;  // uniform trip count
+        for (int64_t e = t; e < n_pad; e += kRowThreads) {
+            int64_t c = 0;
+            uint32_t u = 0;
+            const bool ok = e < n && cand(e, c, u) &&
+                            (pass == 0 || (u >> (shift + 8)) == prefix);
+            hist_add(hist, (u >> shift) & 255u, ok);
         }
         __syncthreads();
         const int64_t h = hist[t];
