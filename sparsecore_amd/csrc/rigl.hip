@@ -74,9 +74,8 @@ __global__ __launch_bounds__(256) void rigl_norm_kernel(const float* __restrict_
 
 constexpr int kAT = 128;        // output tile edge (rows of dY, rows of X)
 constexpr int kAJ = 32;         // j per LDS stage: two MFMA k-steps of 16
-constexpr int kARow = 40;       // bf16 per LDS row: 32 + 8 padding (80 bytes)
 constexpr int kAChunk = 512;    // j per matrix-core partial sum of x_h·y_h
-constexpr int kAThreads = 256;  // 4 waves, 2 x 2, each 64 x 64 of the tile
+constexpr int kAThreads = 512;  // 8 waves, 4 x 2, each 32 x 64 of the tile
 constexpr int kAGroup = 8;      // tile rows per group of the tile order
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -132,6 +131,11 @@ __global__ __launch_bounds__(256) void rigl_split_kernel(const float* __restrict
 
 constexpr int kALdsRow = kAStageBytes + 16;  // bytes per staged row (padded)
 
+// G'[i0 + 128 tile] = x_h·y_h (fp32 matrix-core sums over chunks of kAChunk
+// j, the chunk sums added on the VALU) + (x_h·y_l + x_l·y_h) (one fp32
+// matrix-core sum), where x = dY row i, y = X row k. Eight waves in a 4 x 2
+// grid, each 32 rows x 64 columns (two 32 x 32 MFMA blocks): two waves per
+// SIMD, so one wave's LDS waits and barrier are covered by the other's MFMAs.
 __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64_t K, int64_t nst,
                                                                 const uint16_t* __restrict__ PA,
                                                                 const uint16_t* __restrict__ PB,
@@ -152,31 +156,31 @@ __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wv = t >> 6;
-    const int wm = wv >> 1, wn = wv & 1;
-    // staging: thread t moves bytes [64h, 64h + 64) of staged row t/2
-    const int lr = t >> 1, lh = (t & 1) * 64;
+    const int wm = wv >> 1, wn = wv & 1;  // rows wm*32 .. +32, columns wn*64 .. +64
+    // staging: thread t moves bytes [32h, 32h + 32) of staged row t/4, of A and of B
+    constexpr int kPieces = kAStageBytes / 16 * kAT / kAThreads;  // 16-byte pieces per thread
+    static_assert(kPieces * kAThreads * 16 == kAT * kAStageBytes, "whole rows per stage");
+    const int lr = t >> 2, lh = (t & 3) * (16 * kPieces);
     const unsigned char* ga = reinterpret_cast<const unsigned char*>(
         PA + (i0 + lr < M ? i0 + lr : M - 1) * nst * (2 * kAJ)) + lh;
     const unsigned char* gb = reinterpret_cast<const unsigned char*>(
         PB + (k0 + lr < K ? k0 + lr : K - 1) * nst * (2 * kAJ)) + lh;
 
-    f32x16 cm[2][2], mm[2][2], cx[2][2];
+    f32x16 cm[2], mm[2], cx[2];  // [column block]
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int b = 0; b < 2; ++b)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) cm[a][b][r] = mm[a][b][r] = cx[a][b][r] = 0.0f;
+        for (int r = 0; r < 16; ++r) cm[b][r] = mm[b][r] = cx[b][r] = 0.0f;
 
     // Pipeline: stage st+2's loads are issued while stage st is computed from
     // LDS buffer st&1; stage st+1 (loaded during stage st-1) is written into
     // the other buffer after this stage's MFMAs; one barrier per stage.
-    f32x4 ra[2][4], rb[2][4];
+    f32x4 ra[2][kPieces], rb[2][kPieces];
     auto fetch = [&](int reg, int64_t st) {
         const unsigned char* pa = ga + st * kAStageBytes;
         const unsigned char* pb = gb + st * kAStageBytes;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < kPieces; ++q) {
             ra[reg][q] = *reinterpret_cast<const f32x4*>(pa + 16 * q);
             rb[reg][q] = *reinterpret_cast<const f32x4*>(pb + 16 * q);
         }
@@ -184,7 +188,7 @@ __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64
     const int st_off = lr * kALdsRow + lh;
     auto stage_to_lds = [&](int reg, int b) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < kPieces; ++q) {
             *reinterpret_cast<f32x4*>(&sA[b][st_off + 16 * q]) = ra[reg][q];
             *reinterpret_cast<f32x4*>(&sB[b][st_off + 16 * q]) = rb[reg][q];
         }
@@ -194,7 +198,7 @@ __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64
     if (nst > 0) stage_to_lds(0, 0);
     __syncthreads();
     const int half = 16 * (lane >> 5);
-    const int ra0 = (wm * 64 + (lane & 31)) * kALdsRow + half;
+    const int ra0 = (wm * 32 + (lane & 31)) * kALdsRow + half;
     const int rb0 = (wn * 64 + (lane & 31)) * kALdsRow + half;
     // stage st lives in register set st & 1 and LDS buffer st & 1; the two
     // parities are unrolled so both indexes are compile-time constants
@@ -204,34 +208,25 @@ __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64
         const unsigned char* la = sA[reg];
         const unsigned char* lb = sB[reg];
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            bf16x8 af[2][2], bf[2][2];  // [block][high, low]
+        for (int s = 0; s < kAJ / 16; ++s) {
+            bf16x8 af[2], bf[2][2];  // [high, low], [block][high, low]
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const int o = p * (kAStageBytes / 2) + 32 * s;
+                af[p] = *reinterpret_cast<const bf16x8*>(la + ra0 + o);
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+                    bf[b][p] = *reinterpret_cast<const bf16x8*>(lb + rb0 + b * 32 * kALdsRow + o);
+            }
 #pragma unroll
             for (int b = 0; b < 2; ++b)
+                cm[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0], bf[b][0], cm[b], 0, 0, 0);
 #pragma unroll
-                for (int p = 0; p < 2; ++p) {
-                    const int o = b * 32 * kALdsRow + p * (kAStageBytes / 2) + 32 * s;
-                    af[b][p] = *reinterpret_cast<const bf16x8*>(la + ra0 + o);
-                    bf[b][p] = *reinterpret_cast<const bf16x8*>(lb + rb0 + o);
-                }
+            for (int b = 0; b < 2; ++b)
+                cx[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0], bf[b][1], cx[b], 0, 0, 0);
 #pragma unroll
-            for (int a = 0; a < 2; ++a)
-#pragma unroll
-                for (int b = 0; b < 2; ++b)
-                    cm[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a][0], bf[b][0],
-                                                                        cm[a][b], 0, 0, 0);
-#pragma unroll
-            for (int a = 0; a < 2; ++a)
-#pragma unroll
-                for (int b = 0; b < 2; ++b)
-                    cx[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a][0], bf[b][1],
-                                                                        cx[a][b], 0, 0, 0);
-#pragma unroll
-            for (int a = 0; a < 2; ++a)
-#pragma unroll
-                for (int b = 0; b < 2; ++b)
-                    cx[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a][1], bf[b][0],
-                                                                        cx[a][b], 0, 0, 0);
+            for (int b = 0; b < 2; ++b)
+                cx[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[1], bf[b][0], cx[b], 0, 0, 0);
         }
         // stage st+1 into the other buffer (its last readers, stage st-1,
         // passed the previous barrier)
@@ -247,27 +242,23 @@ __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64
         }
         // a chunk of x_h·y_h done: add its sums on the VALU
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
+        for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int b = 0; b < 2; ++b)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    mm[a][b][r] = mm[a][b][r] + cm[a][b][r];
-                    cm[a][b][r] = 0.0f;
-                }
+            for (int r = 0; r < 16; ++r) {
+                mm[b][r] = mm[b][r] + cm[b][r];
+                cm[b][r] = 0.0f;
+            }
     }
     // lane l, register 4g + q of a 32x32 block: row 8g + 4(l/32) + q, column l % 32
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int b = 0; b < 2; ++b) {
+        const int64_t col = k0 + wn * 64 + b * 32 + (lane & 31);
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            const int64_t col = k0 + wn * 64 + b * 32 + (lane & 31);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = i0 + wm * 64 + a * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (row < M && col < K) G[row * K + col] = mm[a][b][r] + cx[a][b][r];
-            }
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = i0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (row < M && col < K) G[row * K + col] = mm[b][r] + cx[b][r];
         }
+    }
 }
 
 // ───────────────────────────── certified selection ─────────────────────────

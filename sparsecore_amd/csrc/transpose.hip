@@ -17,12 +17,16 @@
 //   (host)     reads capT, allocates the WT slot arrays.
 //   T4 pad     writes padding slots (col -1, value 0, perm -1), one wave
 //              per WT row.
-//   T5 scatter one wave per block walks its rows in ascending order and
-//              places every live slot at WT row_start[c] + rank, with the
-//              running rank kept per column in LDS. A row's columns are
-//              distinct, so one row's 64-slot batch never collides on a
-//              counter; rows are visited in order, which makes the scatter
-//              stable and the result deterministic.
+//   T5 scatter places every live slot at WT row_start[c] + rank. With at
+//              most 32 rows per block (every shape up to 2^29 entries of
+//              M x K), one workgroup per block marks, per column, which of
+//              its rows hold it (bit r - r0 of an LDS word; a row's columns
+//              are distinct), and the rank of slot (r, c) is the block's
+//              start in WT row c plus the number of earlier rows of the
+//              block marked at c: every slot is placed in parallel, and the
+//              order (rows ascending within a WT row) is the stable one.
+//              Larger blocks use one wave that walks the rows in order with
+//              a running rank per column in LDS.
 //
 // Integer atomics appear only in T1's LDS histogram (counts are
 // order-independent). Columns are processed in chunks of kColChunk so the LDS
@@ -207,6 +211,57 @@ __global__ __launch_bounds__(kWave) void tr_scatter_kernel(
     }
 }
 
+// T5 for blocks of at most 32 rows (see above): one 256-thread workgroup per
+// block, LDS holds one mask word per column of the current column chunk.
+constexpr int kParScatterThreads = 256;
+constexpr int64_t kParScatterMaxRows = 32;
+
+__global__ __launch_bounds__(kParScatterThreads) void tr_scatter_par_kernel(
+    int64_t M, int64_t K, int64_t B, const int32_t* __restrict__ row_start,
+    const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ col,
+    const float* __restrict__ val, const int32_t* __restrict__ bh,
+    const int32_t* __restrict__ start_t, float* __restrict__ val_t,
+    int32_t* __restrict__ col_t, int64_t* __restrict__ perm) {
+    extern __shared__ uint32_t mask[];
+    const int t = threadIdx.x;
+    const int64_t b = blockIdx.x;
+    const int64_t r0 = b * B;
+    const int64_t r1 = (r0 + B < M) ? r0 + B : M;
+    for (int64_t c0 = 0; c0 < K; c0 += kColChunk) {
+        const int64_t kc = (K - c0 < kColChunk) ? K - c0 : kColChunk;
+        for (int64_t u = t; u < kc; u += kParScatterThreads) mask[u] = 0;
+        __syncthreads();
+        for (int64_t r = r0; r < r1; ++r) {
+            const int64_t s0 = row_start[r];
+            const int32_t n = row_nnz[r];
+            const uint32_t bit = 1u << (r - r0);
+            for (int32_t k = t; k < n; k += kParScatterThreads) {
+                const int64_t c = col[s0 + k] - c0;
+                if (c >= 0 && c < kc) atomicOr(&mask[c], bit);
+            }
+        }
+        __syncthreads();
+        for (int64_t r = r0; r < r1; ++r) {
+            const int64_t s0 = row_start[r];
+            const int32_t n = row_nnz[r];
+            const uint32_t below = (1u << (r - r0)) - 1u;
+            for (int32_t k = t; k < n; k += kParScatterThreads) {
+                const int64_t s = s0 + k;
+                const int32_t c = col[s];
+                const int64_t cc = c - c0;
+                if (cc >= 0 && cc < kc) {
+                    const int64_t pos = static_cast<int64_t>(start_t[c]) + bh[b * K + c] +
+                                        __popc(mask[cc] & below);
+                    perm[pos] = s;
+                    col_t[pos] = static_cast<int32_t>(r);
+                    val_t[pos] = val[s];
+                }
+            }
+        }
+        __syncthreads();  // every read of this chunk's masks is done
+    }
+}
+
 __global__ __launch_bounds__(256) void tr_refresh_kernel(const float* __restrict__ w_val,
                                                          int64_t w_cap,
                                                          const int64_t* __restrict__ perm,
@@ -303,6 +358,14 @@ extern "C" int slk_transpose_fill(const slk_csr* W, const void* workspace, int64
     if (int rc = check_launch("transpose_fill/pad")) return rc;
     if (p.nblk == 0) return SLK_OK;
     const size_t lds = static_cast<size_t>(K < kColChunk ? K : kColChunk) * sizeof(int32_t);
+    if (p.rows_per_block <= kParScatterMaxRows) {
+        hipLaunchKernelGGL(tr_scatter_par_kernel, dim3(static_cast<unsigned>(p.nblk)),
+                           dim3(kParScatterThreads), lds, st, M, K, p.rows_per_block,
+                           W->row_start, W->row_nnz, W->col_indices, W->values,
+                           static_cast<const int32_t*>(workspace), WT_row_start, WT_values,
+                           WT_col_indices, perm);
+        return check_launch("transpose_fill/scatter");
+    }
     hipLaunchKernelGGL(tr_scatter_kernel, dim3(static_cast<unsigned>(p.nblk)), dim3(kWave), lds,
                        st, M, K, p.rows_per_block, W->row_start, W->row_nnz, W->col_indices,
                        W->values, static_cast<const int32_t*>(workspace), WT_row_start, WT_values,
