@@ -340,12 +340,11 @@ __device__ __forceinline__ void for_each_col(const float* __restrict__ g_row,
         for (int64_t base = 0; base < K; base += step) {
             f32x4 g[kColBlock], n[kColBlock];
 #pragma unroll
-            for (int u = 0; u < kColBlock; ++u) {
+            for (int u = 0; u < kColBlock; ++u) {  // no branch: all loads issued at once
                 const int64_t c = base + 4 * (t + int64_t{kRowThreads} * u);
-                if (c < K) {
-                    g[u] = *reinterpret_cast<const f32x4*>(g_row + c);
-                    n[u] = *reinterpret_cast<const f32x4*>(nrm_c + c);
-                }
+                const int64_t cl = c < K ? c : K - 4;  // in bounds, unused past K
+                g[u] = *reinterpret_cast<const f32x4*>(g_row + cl);
+                n[u] = *reinterpret_cast<const f32x4*>(nrm_c + cl);
             }
 #pragma unroll
             for (int u = 0; u < kColBlock; ++u) {
@@ -359,6 +358,153 @@ __device__ __forceinline__ void for_each_col(const float* __restrict__ g_row,
     } else {
         for (int64_t c = t; c < K; c += kRowThreads) f(c, g_row[c], nrm_c[c]);
     }
+}
+
+// rigl_count_kernel with the row's |G'| in registers: thread t owns columns
+// 4(t + 256u) + e (u < U, e < 4), so the radix passes read no memory and the
+// kernel needs 2 KiB of LDS instead of 4K + K/8 bytes (five workgroups per
+// CU instead of two). For K <= 1024·U, K % 4 == 0 and 16-byte aligned rows of
+// G' and nrm_c. Same counts, thresholds and flags as rigl_count_kernel: the
+// select visits the same candidates with the same keys.
+template <int U>
+__global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
+    int64_t K, int64_t Kw, const int32_t* __restrict__ row_start,
+    const int32_t* __restrict__ row_nnz, const float* __restrict__ values,
+    const int32_t* __restrict__ cols, const float* __restrict__ thr_ptr,
+    const float* __restrict__ Gp, int64_t ldg, const float* __restrict__ nrm_r,
+    const float* __restrict__ nrm_c, float c_bound, RowInfo* __restrict__ info,
+    int64_t* __restrict__ amb_count) {
+    __shared__ uint32_t keep[U * kRowThreads * 4 / 32];
+    __shared__ int64_t tmp[kRowThreads];
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t s_digit;
+    __shared__ int64_t s_below;
+    __shared__ unsigned long long s_best;
+    __shared__ uint32_t s_nmax;
+
+    const int64_t i = blockIdx.x;
+    const int t = threadIdx.x;
+    RowInfo ri{};
+    const int32_t n_live = row_nnz[i];
+    auto finish_row = [&](int32_t flags, int64_t n_amb) {
+        if (t == 0) {
+            ri.flags = flags;
+            info[i] = ri;
+            amb_count[i] = n_amb;
+        }
+    };
+    if (n_live <= 0) return finish_row(kRowKeep, 0);  // the reference skips empty rows
+    const int32_t start = row_start[i];
+    for (int64_t w = t; w < Kw; w += kRowThreads) keep[w] = 0;
+    if (t == 0) s_nmax = 0;
+    __syncthreads();
+    const int64_t n_keep = mark_survivors(values, cols, start, n_live, thr_ptr[0], keep, tmp,
+                                          &s_best);
+    const int64_t n_drop = n_live - n_keep;
+    ri.n_keep = static_cast<int32_t>(n_keep);
+    if (n_drop == 0) return finish_row(kRowKeep, 0);
+    const int64_t n_empty = K - n_keep;
+    const float ni = nrm_r[i];
+    const float* g_row = Gp + i * ldg;
+
+    // the row's |G'| and empty-column mask (bit 4u + e), the largest
+    // candidate norm, and whether every bound exists
+    // (every load is issued before the first use: clamped addresses instead
+    // of branches, the columns past K masked out of `cand`)
+    f32x4 a[U], nr[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int64_t c = 4 * (t + int64_t{kRowThreads} * u);
+        const int64_t cl = c < K ? c : K - 4;
+        a[u] = *reinterpret_cast<const f32x4*>(g_row + cl);
+        nr[u] = *reinterpret_cast<const f32x4*>(nrm_c + cl);
+    }
+    uint64_t cand = 0;
+    int64_t unbounded = 0;
+    uint32_t nmax = 0;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int64_t c = 4 * (t + int64_t{kRowThreads} * u);
+        const uint32_t kw = c < K ? keep[c >> 5] >> (c & 31) : 15u;  // c % 4 == 0: one word
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            a[u][e] = fabsf(a[u][e]);
+            if ((kw >> e) & 1u) continue;
+            cand |= 1ull << (4 * u + e);
+            if (!(nr[u][e] <= kNormCap) || !(a[u][e] <= 0x1p125f)) ++unbounded;
+            else nmax = max(nmax, __float_as_uint(nr[u][e]));
+        }
+    }
+    atomicMax(&s_nmax, nmax);
+    block_inclusive_scan(unbounded, tmp);
+    unbounded = tmp[kRowThreads - 1];
+    if (unbounded > 0 || !(ni <= kNormCap)) return finish_row(kRowExact, n_empty);
+    const float nm = __uint_as_float(s_nmax);
+    const int64_t n_grow = n_drop < n_empty ? n_drop : n_empty;
+
+    // T' = the n_grow-th largest |G'| of the empty columns (kth_smallest_key
+    // over the registers)
+    uint32_t prefix = 0;
+    int64_t need = n_grow;
+    for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 24 - 8 * pass;
+        hist[t] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t key = desc_key(a[u][e]);
+                const bool ok = ((cand >> (4 * u + e)) & 1ull) &&
+                                (pass == 0 || (key >> (shift + 8)) == prefix);
+                hist_add(hist, (key >> shift) & 255u, ok);
+            }
+        }
+        __syncthreads();
+        const int64_t h = hist[t];
+        const int64_t incl = block_inclusive_scan(h, tmp);
+        if (incl - h < need && need <= incl) {
+            s_digit = static_cast<uint32_t>(t);
+            s_below = incl - h;
+        }
+        __syncthreads();
+        prefix = (prefix << 8) | s_digit;
+        need -= s_below;
+        __syncthreads();
+    }
+    const float Tp = __uint_as_float(~prefix);
+    const float cni = up_(c_bound * ni);
+    const float delta = up_(0x1p-100f * up_(1.0f + ni + nm));
+    const float e_max = col_err(cni, nm, delta);
+    const float t_in = up_(Tp + e_max);
+    const float t_out = dn_(Tp - e_max);
+    int64_t n_in = 0, n_amb = 0;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int64_t c = 4 * (t + int64_t{kRowThreads} * u);
+        nr[u] = *reinterpret_cast<const f32x4*>(nrm_c + (c < K ? c : K - 4));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (!((cand >> (4 * u + e)) & 1ull)) continue;
+            const float ek = col_err(cni, nr[u][e], delta);
+            if (dn_(a[u][e] - ek) > t_in) ++n_in;
+            else if (!(up_(a[u][e] + ek) < t_out)) ++n_amb;
+        }
+    }
+    block_inclusive_scan(n_in, tmp);
+    n_in = tmp[kRowThreads - 1];
+    block_inclusive_scan(n_amb, tmp);
+    n_amb = tmp[kRowThreads - 1];
+    ri.n_grow = static_cast<int32_t>(n_grow);
+    ri.n_in = static_cast<int32_t>(n_in);
+    ri.t_in = t_in;
+    ri.t_out = t_out;
+    ri.cni = cni;
+    ri.delta = delta;
+    finish_row(0, n_amb);
 }
 
 // Per row: survivors (as the exact kernel), then, over the empty columns,
@@ -779,7 +925,16 @@ extern "C" int slk_rigl_count(const slk_csr* W, const float* thr_dev, const floa
 #define SLK_COUNT_ARGS                                                                       \
     K, Kw, W->row_start, W->row_nnz, W->values, W->col_indices, thr_dev, G_approx, ldg, nrm_dY, \
         nrm_X, c_f, static_cast<RowInfo*>(info), amb_off + M + 1
-        if (K <= kStageMaxK && vg) {
+        if (vg && K <= 4 * kRowThreads * 4) {
+            hipLaunchKernelGGL(rigl_count_reg_kernel<4>, grid, dim3(kRowThreads), 0, st,
+                               SLK_COUNT_ARGS);
+        } else if (vg && K <= 4 * kRowThreads * 8) {
+            hipLaunchKernelGGL(rigl_count_reg_kernel<8>, grid, dim3(kRowThreads), 0, st,
+                               SLK_COUNT_ARGS);
+        } else if (vg && K <= 4 * kRowThreads * 16) {
+            hipLaunchKernelGGL(rigl_count_reg_kernel<16>, grid, dim3(kRowThreads), 0, st,
+                               SLK_COUNT_ARGS);
+        } else if (K <= kStageMaxK && vg) {
             hipLaunchKernelGGL((rigl_count_kernel<true, true>), grid, dim3(kRowThreads), lds_st, st,
                                SLK_COUNT_ARGS);
         } else if (K <= kStageMaxK) {

@@ -164,7 +164,8 @@ __device__ __forceinline__ void hist_add(uint32_t* hist, uint32_t bin, bool vali
     for (int r = 0; r < 2; ++r) {
         if (pend == 0) break;
         const int leader = __ffsll(static_cast<unsigned long long>(pend)) - 1;
-        const uint32_t b = __shfl(bin, leader);
+        // (a lane read into a scalar register: no LDS round trip, unlike a shuffle)
+        const uint32_t b = __builtin_amdgcn_readlane(bin, leader);
         const uint64_t same = __ballot(valid && bin == b) & pend;
         if (lane == leader) atomicAdd(&hist[b], static_cast<uint32_t>(__popcll(same)));
         pend &= ~same;
