@@ -342,7 +342,6 @@ constexpr int kLdsWaves = 16;
 constexpr int kLdsThreads = kLdsWaves * kWave;          // 1024
 constexpr int kLdsK = 64;                               // X rows per chunk
 constexpr int kLdsCols = 4 * kWave;                     // 256 columns per workgroup
-constexpr int kLdsStage = kLdsK * kWave / kLdsThreads;  // 16-byte loads per thread per chunk
 
 __device__ __forceinline__ void lds_window(const int32_t* __restrict__ col,
                                            const float* __restrict__ val, int32_t at,
@@ -368,6 +367,8 @@ __global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
     // H halves of 256 columns per workgroup, each lane 4 columns of each half;
     // chunks of KC X rows keep the double buffer at 128 KiB
     constexpr int KC = kLdsK / H;
+    constexpr int kStage = KC * H * kWave / kLdsThreads;  // 16-byte loads per thread per chunk
+    static_assert(kStage * kLdsWaves == KC * H, "whole X rows per thread group");
     __shared__ f32x4 xs[2][KC][H][kWave];  // 128 KiB
     const int lane = threadIdx.x & (kWave - 1);
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -401,24 +402,39 @@ __global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
         for (int h = 0; h < H; ++h) acc[j][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    // thread t stages piece t + 1024i (i < kLdsStage) of the chunk: X row
+    // thread t stages piece t + 1024i (i < kStage) of the chunk: X row
     // p / (64H), half (p / 64) mod H, lane p mod 64
-    f32x4 pre[kLdsStage];
-    auto prefetch = [&](int64_t k0) {
+    f32x4 pre[kStage];
+    // Piece i's byte offset from the chunk's first X row (KC·N·4 < 2^32: the
+    // launcher's bar), its columns clamped into the row where they pass N
+    // (lanes whose columns pass N never store theirs): a full chunk is a
+    // scalar base plus one 32-bit offset per load. Rows past K (the last
+    // chunk) are clamped to row K - 1: no slot has a column >= K.
+    uint32_t poff[kStage];
 #pragma unroll
-        for (int i = 0; i < kLdsStage; ++i) {
-            const int p = threadIdx.x + i * kLdsThreads;
-            const int kr = p / (H * kWave);
-            const int h = (p / kWave) % H;
-            const int64_t k = k0 + kr;
-            const int64_t nn = tile * (H * kLdsCols) + h * kLdsCols + 4 * (p % kWave);
-            pre[i] = (k < K && nn < N) ? *reinterpret_cast<const f32x4*>(X + k * N + nn)
-                                       : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < kStage; ++i) {
+        const int p = threadIdx.x + i * kLdsThreads;
+        const int64_t nn = tile * (H * kLdsCols) + ((p / kWave) % H) * kLdsCols + 4 * (p % kWave);
+        poff[i] = static_cast<uint32_t>(((p / (H * kWave)) * N + (nn < N ? nn : N - 4)) * 4);
+    }
+    auto prefetch = [&](int64_t k0) {
+        const char* xb = reinterpret_cast<const char*>(X + k0 * N);
+        if (k0 + KC <= K) {  // workgroup-uniform
+#pragma unroll
+            for (int i = 0; i < kStage; ++i)
+                pre[i] = *reinterpret_cast<const f32x4*>(xb + poff[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < kStage; ++i) {
+                const int64_t kr = (threadIdx.x + i * kLdsThreads) / (H * kWave);
+                const int64_t back = k0 + kr < K ? 0 : (k0 + kr - (K - 1)) * N * 4;
+                pre[i] = *reinterpret_cast<const f32x4*>(xb + poff[i] - back);
+            }
         }
     };
     auto stage = [&](int b) {
 #pragma unroll
-        for (int i = 0; i < kLdsStage; ++i) {
+        for (int i = 0; i < kStage; ++i) {
             const int p = threadIdx.x + i * kLdsThreads;
             xs[b][p / (H * kWave)][(p / kWave) % H][p % kWave] = pre[i];
         }
@@ -437,7 +453,12 @@ __global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
         for (int j = 0; j < RW; ++j) {
             int32_t first = pos[j] - base[j];
             while (true) {
-                const int32_t cnt = __popcll(__ballot(lane >= first && mc[j] < k1));
+                // slots of the window at or after `first` (first < 64) below the chunk end:
+                // one compare on the VALU, the mask on the scalar unit
+                const uint64_t run = __ballot(mc[j] < k1) & (~0ull << first);
+                // (two 32-bit counts keep the loop bounds 32-bit scalar compares)
+                const int32_t cnt = __popc(static_cast<uint32_t>(run)) +
+                                    __popc(static_cast<uint32_t>(run >> 32));
                 int32_t k = 0;
                 for (; k + 4 <= cnt; k += 4) {  // four slots' LDS reads in flight
                     const int32_t s0 = first + k;
@@ -455,7 +476,19 @@ __global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
                         fma4(bcast_f(mv[j], s0 + 3), x3, acc[j][h]);
                     }
                 }
-                for (; k < cnt; ++k) {
+                if (k + 2 <= cnt) {  // a pair: both reads in flight
+                    const int32_t s0 = first + k;
+                    const int32_t c0 = bcast_i(mc[j], s0) - k0, c1 = bcast_i(mc[j], s0 + 1) - k0;
+#pragma unroll
+                    for (int h = 0; h < H; ++h) {
+                        const f32x4 x0 = xs[b][c0][h][lane];
+                        const f32x4 x1 = xs[b][c1][h][lane];
+                        fma4(bcast_f(mv[j], s0), x0, acc[j][h]);
+                        fma4(bcast_f(mv[j], s0 + 1), x1, acc[j][h]);
+                    }
+                    k += 2;
+                }
+                if (k < cnt) {
                     const int32_t c0 = bcast_i(mc[j], first + k) - k0;
                     const float v = bcast_f(mv[j], first + k);
 #pragma unroll
@@ -640,7 +673,8 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
     // configurations that pass both bars, lds_cost picks one. The per-wave
     // gather kernels cover everything else (small N is latency-bound).
     // SLK_TUNE_SPMM_KERNEL, SLK_TUNE_SPMM_H and SLK_TUNE_SPMM_RW override.
-    const bool lds_ok = N % 4 == 0 && align % 16 == 0;
+    // (N < 2^24: a chunk of X rows is addressed with 32-bit byte offsets)
+    const bool lds_ok = N % 4 == 0 && align % 16 == 0 && N < (int64_t{1} << 24);
     int rw = 0, h = 1;
     if (lds_ok && N >= kLdsMinN) {
         const double density =
