@@ -340,7 +340,7 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_group_kernel(
 // rows of similar length (see spmm_impl).
 constexpr int kLdsWaves = 16;
 constexpr int kLdsThreads = kLdsWaves * kWave;          // 1024
-constexpr int kLdsK = 64;                               // X rows per chunk
+constexpr int kLdsK = 80;                               // X rows per chunk
 constexpr int kLdsCols = 4 * kWave;                     // 256 columns per workgroup
 
 __device__ __forceinline__ void lds_window(const int32_t* __restrict__ col,
@@ -384,8 +384,14 @@ __global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
     }
     const int64_t r0 = rb * (kLdsWaves * RW) + w;
 
-    int32_t rows[RW], pos[RW], end[RW], base[RW], mc[RW], nmc[RW];  // rows[j] < 0: none
-    float mv[RW], nmv[RW];
+    // PREF: the next window is requested as soon as a window is entered; the
+    // 8-row, 8-column-per-lane variant loads it when needed instead (its
+    // registers are spent on the wider accumulators; its rows are the light ones)
+    constexpr bool PREF = !(RW == 8 && H == 2);
+    constexpr int G = PREF ? 4 : 2;  // slots per group of LDS reads
+    constexpr int RN = PREF ? RW : 1;
+    int32_t rows[RW], pos[RW], end[RW], base[RW], mc[RW], nmc[RN];  // rows[j] < 0: none
+    float mv[RW], nmv[RN];
     f32x4 acc[RW][H];
 #pragma unroll
     for (int j = 0; j < RW; ++j) {
@@ -397,7 +403,7 @@ __global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
         pos[j] = base[j] = s;
         end[j] = e;
         lds_window(col, val, s, e, lane, mc[j], mv[j]);
-        lds_window(col, val, s + kWave, e, lane, nmc[j], nmv[j]);
+        if constexpr (PREF) lds_window(col, val, s + kWave, e, lane, nmc[j], nmv[j]);
 #pragma unroll
         for (int h = 0; h < H; ++h) acc[j][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
@@ -460,23 +466,21 @@ __global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
                 const int32_t cnt = __popc(static_cast<uint32_t>(run)) +
                                     __popc(static_cast<uint32_t>(run >> 32));
                 int32_t k = 0;
-                for (; k + 4 <= cnt; k += 4) {  // four slots' LDS reads in flight
+                for (; k + G <= cnt; k += G) {  // G slots' LDS reads in flight
                     const int32_t s0 = first + k;
-                    const int32_t c0 = bcast_i(mc[j], s0) - k0, c1 = bcast_i(mc[j], s0 + 1) - k0;
-                    const int32_t c2 = bcast_i(mc[j], s0 + 2) - k0, c3 = bcast_i(mc[j], s0 + 3) - k0;
+                    int32_t c[G];
+#pragma unroll
+                    for (int g = 0; g < G; ++g) c[g] = bcast_i(mc[j], s0 + g) - k0;
 #pragma unroll
                     for (int h = 0; h < H; ++h) {
-                        const f32x4 x0 = xs[b][c0][h][lane];
-                        const f32x4 x1 = xs[b][c1][h][lane];
-                        const f32x4 x2 = xs[b][c2][h][lane];
-                        const f32x4 x3 = xs[b][c3][h][lane];
-                        fma4(bcast_f(mv[j], s0), x0, acc[j][h]);
-                        fma4(bcast_f(mv[j], s0 + 1), x1, acc[j][h]);
-                        fma4(bcast_f(mv[j], s0 + 2), x2, acc[j][h]);
-                        fma4(bcast_f(mv[j], s0 + 3), x3, acc[j][h]);
+                        f32x4 x[G];
+#pragma unroll
+                        for (int g = 0; g < G; ++g) x[g] = xs[b][c[g]][h][lane];
+#pragma unroll
+                        for (int g = 0; g < G; ++g) fma4(bcast_f(mv[j], s0 + g), x[g], acc[j][h]);
                     }
                 }
-                if (k + 2 <= cnt) {  // a pair: both reads in flight
+                if (G > 2 && k + 2 <= cnt) {  // a pair: both reads in flight
                     const int32_t s0 = first + k;
                     const int32_t c0 = bcast_i(mc[j], s0) - k0, c1 = bcast_i(mc[j], s0 + 1) - k0;
 #pragma unroll
@@ -498,9 +502,13 @@ __global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
                 if (first + cnt < kWave) break;  // the run ended inside this window
                 // window used up: shift the next one in and request the one after
                 base[j] += kWave;
-                mc[j] = nmc[j];
-                mv[j] = nmv[j];
-                lds_window(col, val, base[j] + kWave, end[j], lane, nmc[j], nmv[j]);
+                if constexpr (PREF) {
+                    mc[j] = nmc[j];
+                    mv[j] = nmv[j];
+                    lds_window(col, val, base[j] + kWave, end[j], lane, nmc[j], nmv[j]);
+                } else {
+                    lds_window(col, val, base[j], end[j], lane, mc[j], mv[j]);
+                }
                 first = 0;
             }
         }
@@ -549,8 +557,13 @@ int launch_lds_rw(const slk_csr* W, const int32_t* order, int64_t P, const float
 
 int launch_lds(int h, int rw, const slk_csr* W, const int32_t* order, int64_t P, const float* X,
                int64_t N, const float* bias, float* Y, hipStream_t st) {
-    if (h == 2) return rw == 2 ? launch_lds_rw<2, 2>(W, order, P, X, N, bias, Y, st)
-                               : launch_lds_rw<4, 2>(W, order, P, X, N, bias, Y, st);
+    if (h == 2) {
+        switch (rw) {
+            case 2: return launch_lds_rw<2, 2>(W, order, P, X, N, bias, Y, st);
+            case 4: return launch_lds_rw<4, 2>(W, order, P, X, N, bias, Y, st);
+            default: return launch_lds_rw<8, 2>(W, order, P, X, N, bias, Y, st);
+        }
+    }
     switch (rw) {
         case 2: return launch_lds_rw<2>(W, order, P, X, N, bias, Y, st);
         case 4: return launch_lds_rw<4>(W, order, P, X, N, bias, Y, st);
@@ -680,8 +693,13 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
         const double density =
             K > 0 ? static_cast<double>(W->total_capacity) / (1.2 * M * K) : 0.0;
         double best = 0.0;
-        for (const int cfg : {18, 14, 12, 24, 22}) {  // h * 10 + rw
+        for (const int cfg : {18, 14, 12, 28, 24, 22}) {  // h * 10 + rw
             const int ch = cfg / 10, crw = cfg % 10;
+            // 8 rows x 8 columns per lane: rows of uniform length only (the
+            // light rows of a skewed matrix run slower with it: 16384^2
+            // Zipf(1.1) forward 8.24 -> 8.51 ms, while its transpose runs
+            // 7.05 -> 6.60 ms)
+            if (cfg == 28 && W->n_heavy_rows > 0) continue;
             if (density * kLdsWaves * crw < kLdsMinReuse) continue;
             if (lds_blocks(M, N, ch, crw) < kLdsMinBlocks) continue;
             const double c = lds_cost(M, K, N, density, ch, crw);
@@ -700,7 +718,6 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
         if (const int64_t t = tuning(SLK_TUNE_SPMM_H); t >= 0) h = t == 2 ? 2 : 1;
         if (const int64_t t = tuning(SLK_TUNE_SPMM_RW); t >= 0) rw = static_cast<int>(t);
         if (rw != 2 && rw != 4 && rw != 8) rw = 8;
-        if (h == 2 && rw == 8) rw = 4;  // no 8-row variant with 8 columns per lane
         // Heavy rows (the head of the longest-rows-first order) as a launch of
         // their own with two rows per wave, then the rest in that order, so
         // every workgroup holds rows of similar length: on the 16384^2
