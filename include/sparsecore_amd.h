@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define SLK_ABI_VERSION 9
+#define SLK_ABI_VERSION 10
 
 #if defined(__GNUC__)
 #define SLK_API __attribute__((visibility("default")))
@@ -112,8 +112,9 @@ typedef struct slk_csr {
     int64_t n_phases;
 } slk_csr;
 
-/* Segments per group of a segment list (one slk_sddmm workgroup each). */
-#define SLK_SEG_GROUP 64
+/* Padding unit of a segment list: each column block's segments are padded
+ * to a multiple of this. slk_sddmm workgroups take 64 or 128 segments. */
+#define SLK_SEG_GROUP 128
 
 /* Thread-local description of the last failure of this thread ("" if none). */
 SLK_API const char* slk_last_error(void);
@@ -135,6 +136,7 @@ SLK_API int slk_abi_version(void);
  *   SLK_TUNE_SPMM_VEC     gather kernel: floats per lane (1, 2 or 4)
  *   SLK_TUNE_SDDMM_G      windowed dW kernel: groups per wave (1, 2 or 4)
  *   SLK_TUNE_SEG_LEAN     segment dW kernel: 1 = lean variant, 0 = not
+ *   SLK_TUNE_SEG_GROUP    segment dW kernel: segments per workgroup (64 or 128)
  * Returns SLK_EINVAL for an unknown knob.                                   */
 enum slk_tune_knob {
     SLK_TUNE_SPMM_KERNEL = 0,
@@ -144,7 +146,8 @@ enum slk_tune_knob {
     SLK_TUNE_SPMM_VEC = 4,
     SLK_TUNE_SDDMM_G = 5,
     SLK_TUNE_SEG_LEAN = 6,
-    SLK_TUNE_COUNT = 7
+    SLK_TUNE_SEG_GROUP = 7,
+    SLK_TUNE_COUNT = 8
 };
 SLK_API int slk_set_tuning(int knob, int64_t value);
 

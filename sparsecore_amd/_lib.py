@@ -21,7 +21,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libsparsecore_amd.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 SLK_OK, SLK_EINVAL, SLK_EDEVICE = 0, 1, 2
 SLK_DW_SIMD, SLK_DW_SCALAR = 0, 1
@@ -69,9 +69,9 @@ DROP_GROW_NOALLOC_MAX_SLOTS = 1 << 21  # SLK_DROP_GROW_NOALLOC_MAX_SLOTS
 
 # Kernel-choice overrides (slk_set_tuning): knob numbers of enum slk_tune_knob.
 TUNE_KNOBS = {"spmm_kernel": 0, "spmm_h": 1, "spmm_rw": 2, "spmm_split": 3, "spmm_vec": 4,
-              "sddmm_g": 5, "seg_lean": 6}
+              "sddmm_g": 5, "seg_lean": 6, "seg_group": 7}
 
-SEG_GROUP = 64  # SLK_SEG_GROUP
+SEG_GROUP = 128  # SLK_SEG_GROUP
 
 NARROW_MAX_ROWS = 64        # SLK_NARROW_MAX_ROWS
 NARROW_MAX_CAPACITY = 8192  # SLK_NARROW_MAX_CAPACITY

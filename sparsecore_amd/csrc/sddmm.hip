@@ -402,9 +402,10 @@ __global__ __launch_bounds__(kBlock) void sddmm_scalar_kernel(
 // (slk_seg_list_build): the quad loads the row's dY pieces once per step from
 // global memory, one window ahead, and applies them to all S slots, whose X
 // pieces it reads from LDS. That is S LDS reads and one 64-byte global load
-// per S slot-steps. A workgroup of 64 quads takes one group of SLK_SEG_GROUP
-// segments, all in one column block (the list pads each block to whole
-// groups); for every 64-float window it stages the block's C rows of X in LDS
+// per S slot-steps. A workgroup of GS quads takes one group of GS segments,
+// all in one column block (the list pads each block to a multiple of
+// SLK_SEG_GROUP, itself a multiple of GS); for every 64-float window it
+// stages the block's C rows of X in LDS
 // (rows padded by four 16-byte pieces, so a row starts 16 banks after the
 // previous one, the width of one slot's four lanes), prefetched a window
 // ahead in registers. Per slot the arithmetic is sddmm_simd_kernel's: the 16
@@ -412,24 +413,28 @@ __global__ __launch_bounds__(kBlock) void sddmm_scalar_kernel(
 // combine and scalar tail. Empty segments (padding, or slots past a short
 // segment's count) compute on a clamped address and store nothing.
 // Workgroups past the groups in use (*groups, read on the device) exit at
-// once; the workgroups after max_groups are one wave per row that zeroes the
-// row's padding slots and, with dbias, sums its dY row.
-constexpr int kSegThreads = SLK_SEG_GROUP * 4;  // one quad per segment
-static_assert(kSegThreads == 256, "four waves per workgroup");
-constexpr int kSegWin = 64;                                 // floats per window (4 steps)
-constexpr int kSegPieces = kSegWin / 4;                     // 16-byte pieces per row
-constexpr int kSegStride = kSegPieces + 4;                  // pieces per LDS row (padded)
-constexpr int kSegRowsPerPass = kSegThreads / kSegPieces;  // 16 staged rows per pass
+// once, and so does a group of padding only (a 64-segment half of a block's
+// last 128); the workgroups after max_groups are one wave per row that
+// zeroes the row's padding slots and, with dbias, sums its dY row. More
+// segments per workgroup stage each X window for more slots: 128 on the
+// 16384^2 layers (95%: 7.79 -> 6.89 ms, 99%: 2.39 -> 2.22; 256 was slower).
+constexpr int kSegWin = 64;                  // floats per window (4 steps)
+constexpr int kSegPieces = kSegWin / 4;      // 16-byte pieces per row
+constexpr int kSegStride = kSegPieces + 4;   // pieces per LDS row (padded)
+static_assert(SLK_SEG_GROUP % 128 == 0, "the list padding holds whole groups of 64 and 128");
+constexpr int64_t kSegGroupMinGroups = 2048;  // 128-segment groups from this many
 
-template <int C, int S, bool LEAN>
-__global__ __launch_bounds__(kSegThreads) void sddmm_seg_kernel(
+template <int C, int S, bool LEAN, int GS>
+__global__ __launch_bounds__(GS * 4) void sddmm_seg_kernel(
     int64_t M, int64_t K, int64_t N, const int32_t* __restrict__ row_start,
     const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ row_cap,
     const int32_t* __restrict__ col, const float* __restrict__ dY, const float* __restrict__ X,
     float* __restrict__ dW, float* __restrict__ dbias, const int32_t* __restrict__ seg_start,
     const int32_t* __restrict__ seg_row, const int32_t* __restrict__ seg_count,
     const int32_t* __restrict__ groups, int64_t max_groups) {
-    constexpr int kLoads = C * kSegPieces / kSegThreads;  // staged pieces per thread
+    constexpr int kSegThreads = GS * 4;                        // one quad per segment
+    constexpr int kSegRowsPerPass = kSegThreads / kSegPieces;  // staged rows per pass
+    constexpr int kLoads = C * kSegPieces / kSegThreads;       // staged pieces per thread
     static_assert(kLoads * kSegThreads == C * kSegPieces, "whole rows per pass");
     __shared__ f32x4 xs[C * kSegStride];
     const int wv = threadIdx.x >> 6;
@@ -446,10 +451,11 @@ __global__ __launch_bounds__(kSegThreads) void sddmm_seg_kernel(
     // in one column block and share its X band in that XCD's L2 (C4 768x3072
     // layer 281 -> 232 us). Ordering the list by row panels to share dY rows
     // instead was slower: the concurrent groups then span many X bands.
-    const int64_t G = groups[0];
+    const int64_t G = static_cast<int64_t>(groups[0]) * (SLK_SEG_GROUP / GS);
     if (grp >= G) return;  // block-uniform
-    const int64_t e0 = xcd_logical_block(grp, G) * SLK_SEG_GROUP;
-    const int32_t c_lo = col[seg_start[e0]] / C * C;  // a group's first segment is never empty
+    const int64_t e0 = xcd_logical_block(grp, G) * GS;
+    if (seg_count[e0] == 0) return;  // padding only: segments precede their block's padding
+    const int32_t c_lo = col[seg_start[e0]] / C * C;
     const int64_t e = e0 + (threadIdx.x >> 2);  // this quad's segment
     const int32_t s0 = seg_start[e];
     const int32_t cnt = seg_count[e];
@@ -621,8 +627,12 @@ int sddmm_impl(const slk_csr* W, const float* dY, int64_t dY_rows, const float* 
     // A segment list: X through LDS, dY rows in registers.
     // (C·N floats of a band addressed with 32-bit byte offsets)
     if (v4 && W->seg_start != nullptr && N >= 16 && W->seg_block * N * 4 < (int64_t{1} << 32)) {
-        const int64_t max_groups = W->n_seg / SLK_SEG_GROUP;
-        const int64_t sblocks = max_groups + ceil_div(W->nrows, int64_t{kSegThreads / kWave});
+        // 128 segments per workgroup on large lists (below, 64: measured on
+        // the 60M-GPT layers); SLK_TUNE_SEG_GROUP = 64|128 overrides
+        int gs = W->n_seg >= int64_t{128} * kSegGroupMinGroups ? 128 : 64;
+        if (const int64_t t = tuning(SLK_TUNE_SEG_GROUP); t == 64 || t == 128) gs = static_cast<int>(t);
+        const int64_t max_groups = W->n_seg / gs;
+        const int64_t sblocks = max_groups + ceil_div(W->nrows, int64_t{gs * 4 / kWave});
         if (sblocks > INT32_MAX) return fail(SLK_EINVAL, std::string(who) + ": problem too large");
 #define SLK_SEG_ARGS                                                                         \
     W->nrows, W->ncols, N, W->row_start, W->row_nnz, W->row_capacity, W->col_indices, dY, X, \
@@ -635,21 +645,27 @@ int sddmm_impl(const slk_csr* W, const float* dY, int64_t dY_rows, const float* 
         // 99%: 2.6 ms against 3.6 lean). SLK_TUNE_SEG_LEAN = 0|1 overrides.
         bool lean = W->seg_slots == 8;
         if (const int64_t t = tuning(SLK_TUNE_SEG_LEAN); t >= 0) lean = t == 1;
-#define SLK_SEG_LAUNCH(CB, SS)                                                                 \
-    do {                                                                                       \
-        if (lean) {                                                                            \
-            hipLaunchKernelGGL((sddmm_seg_kernel<CB, SS, true>), sgrid, dim3(kSegThreads), 0, \
-                               st, SLK_SEG_ARGS);                                              \
-        } else {                                                                               \
-            hipLaunchKernelGGL((sddmm_seg_kernel<CB, SS, false>), sgrid, dim3(kSegThreads), 0, \
-                               st, SLK_SEG_ARGS);                                              \
-        }                                                                                      \
+#define SLK_SEG_LAUNCH_GS(CB, SS, GS)                                                        \
+    do {                                                                                     \
+        if (lean) {                                                                          \
+            hipLaunchKernelGGL((sddmm_seg_kernel<CB, SS, true, GS>), sgrid, dim3(GS * 4), 0, \
+                               st, SLK_SEG_ARGS);                                            \
+        } else {                                                                             \
+            hipLaunchKernelGGL((sddmm_seg_kernel<CB, SS, false, GS>), sgrid, dim3(GS * 4), 0, \
+                               st, SLK_SEG_ARGS);                                            \
+        }                                                                                    \
+    } while (0)
+#define SLK_SEG_LAUNCH(CB, SS)                            \
+    do {                                                  \
+        if (gs == 128) SLK_SEG_LAUNCH_GS(CB, SS, 128);    \
+        else SLK_SEG_LAUNCH_GS(CB, SS, 64);               \
     } while (0)
         if (W->seg_block == 64 && W->seg_slots == 4) SLK_SEG_LAUNCH(64, 4);
         else if (W->seg_block == 64) SLK_SEG_LAUNCH(64, 8);
         else if (W->seg_slots == 4) SLK_SEG_LAUNCH(128, 4);
         else SLK_SEG_LAUNCH(128, 8);
 #undef SLK_SEG_LAUNCH
+#undef SLK_SEG_LAUNCH_GS
 #undef SLK_SEG_ARGS
         return check_launch(who);
     }

@@ -318,7 +318,7 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_group_kernel(
 // 256·H columns of Y: each lane holds 4 adjacent columns of each of H
 // 256-column halves for RW rows in registers (H = 2 halves the readlane,
 // address and loop work per fma; measured 5-17% faster on the denser GPT
-// layers). X is streamed through LDS in chunks of 64/H rows x 256·H columns
+// layers). X is streamed through LDS in chunks of 80/H rows x 256·H columns
 // (1 KB per X row and half), double-buffered: chunk c+1 is loaded into registers while
 // chunk c is read from LDS and is then written to the other buffer, so one
 // barrier per chunk orders both. For each chunk every row consumes its slots
@@ -365,11 +365,11 @@ __global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
     const int32_t* __restrict__ col, const float* __restrict__ val, const float* __restrict__ X,
     const float* __restrict__ bias, float* __restrict__ Y) {
     // H halves of 256 columns per workgroup, each lane 4 columns of each half;
-    // chunks of KC X rows keep the double buffer at 128 KiB
+    // chunks of KC X rows keep the double buffer at 160 KiB, all of a CU's LDS
     constexpr int KC = kLdsK / H;
     constexpr int kStage = KC * H * kWave / kLdsThreads;  // 16-byte loads per thread per chunk
     static_assert(kStage * kLdsWaves == KC * H, "whole X rows per thread group");
-    __shared__ f32x4 xs[2][KC][H][kWave];  // 128 KiB
+    __shared__ f32x4 xs[2][KC][H][kWave];  // 160 KiB
     const int lane = threadIdx.x & (kWave - 1);
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t lb = xcd_logical_block(blockIdx.x, gridDim.x);
@@ -619,7 +619,7 @@ constexpr int64_t kLdsMinN = 1024;
 constexpr double kLdsMinReuse = 4.0;
 constexpr int64_t kCUs = 256;  // MI355X; one LDS-kernel workgroup per CU at a time
 
-// Workgroups of the LDS kernel (one per CU at a time: 128 KiB of LDS each).
+// Workgroups of the LDS kernel (one per CU at a time: 160 KiB of LDS each).
 int64_t lds_blocks(int64_t M, int64_t N, int h, int rw) {
     return ceil_div(M, int64_t{kLdsWaves} * rw) * ceil_div(N, int64_t{kLdsCols} * h);
 }

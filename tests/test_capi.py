@@ -210,7 +210,8 @@ def test_segment_list_fields_are_checked_on_the_host():
         assert rc == _lib.SLK_EINVAL and word in lib.slk_last_error().decode()
     need = lib.slk_seg_list_capacity(ctypes.byref(_lib.CsrView(4, 6, 40, None, None, 1, 1, 1)),
                                      64, 4)
-    assert need == 40 // 4 + min(40, 4 * 1) + 63 + 64
+    G = _lib.SEG_GROUP  # every run's segments, plus each block's padding (< G) and one group
+    assert need == 40 // 4 + min(40, 4 * 1) + (G - 1) + G
     vc = _lib.CsrView(4, 6, 40, 1, 1, 1, 1, 1)
     rc = lib.slk_seg_list_build(ctypes.byref(vc), 64, 4, None, 0, p, p, p, need - 1, p, None)
     assert rc == _lib.SLK_EINVAL and "n_seg" in lib.slk_last_error().decode()
