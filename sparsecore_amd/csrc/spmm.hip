@@ -358,21 +358,23 @@ __device__ __forceinline__ void fma4(float v, const f32x4& x, f32x4& acc) {
     acc[3] = __builtin_fmaf(v, x[3], acc[3]);
 }
 
+// One workgroup's share of the LDS kernel: logical block lb of a launch over
+// positions [0, P) of `order` with nrowblk row blocks per column tile; xs is
+// the workgroup's X double buffer.
 template <int RW, int H>
-__global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
-    int64_t P, int64_t K, int64_t N, int64_t nrowblk, const int32_t* __restrict__ order,
-    const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
-    const int32_t* __restrict__ col, const float* __restrict__ val, const float* __restrict__ X,
-    const float* __restrict__ bias, float* __restrict__ Y) {
+__device__ __forceinline__ void spmm_lds_body(
+    f32x4 (&xs)[2][kLdsK / H][H][kWave], int64_t lb, int64_t P, int64_t K, int64_t N,
+    int64_t nrowblk, const int32_t* __restrict__ order, const int32_t* __restrict__ row_start,
+    const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ col,
+    const float* __restrict__ val, const float* __restrict__ X, const float* __restrict__ bias,
+    float* __restrict__ Y) {
     // H halves of 256 columns per workgroup, each lane 4 columns of each half;
     // chunks of KC X rows keep the double buffer at 160 KiB, all of a CU's LDS
     constexpr int KC = kLdsK / H;
     constexpr int kStage = KC * H * kWave / kLdsThreads;  // 16-byte loads per thread per chunk
     static_assert(kStage * kLdsWaves == KC * H, "whole X rows per thread group");
-    __shared__ f32x4 xs[2][KC][H][kWave];  // 160 KiB
     const int lane = threadIdx.x & (kWave - 1);
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t lb = xcd_logical_block(blockIdx.x, gridDim.x);
     const int64_t tile = lb / nrowblk;  // tile-major: a tile's row blocks share X chunks in L2
     const int64_t rb = lb - tile * nrowblk;
     int64_t n[H];
@@ -535,6 +537,52 @@ __global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
     }
 }
 
+template <int RW, int H>
+__global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
+    int64_t P, int64_t K, int64_t N, int64_t nrowblk, const int32_t* __restrict__ order,
+    const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
+    const int32_t* __restrict__ col, const float* __restrict__ val, const float* __restrict__ X,
+    const float* __restrict__ bias, float* __restrict__ Y) {
+    __shared__ f32x4 xs[2][kLdsK / H][H][kWave];  // 160 KiB
+    spmm_lds_body<RW, H>(xs, xcd_logical_block(blockIdx.x, gridDim.x), P, K, N, nrowblk, order,
+                         row_start, row_nnz, col, val, X, bias, Y);
+}
+
+// A skewed matrix's heavy rows (positions [0, T) of the longest-first order,
+// two rows per wave) and the rest (positions [T, M), RW rows per wave) in one
+// grid: the few workgroups of heavy rows would otherwise leave CUs idle in
+// their launch's last round. Every XCD starts its share of the grid with its
+// share of the heavy workgroups (the longest), then its share of the rest,
+// each in the tile-major order of its own launch.
+template <int RW, int H>
+__global__ __launch_bounds__(kLdsThreads) void spmm_lds_split_kernel(
+    int64_t T, int64_t M, int64_t K, int64_t N, int64_t nblk_a, int64_t nrowblk_a,
+    int64_t nrowblk_b, const int32_t* __restrict__ order, const int32_t* __restrict__ row_start,
+    const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ col,
+    const float* __restrict__ val, const float* __restrict__ X, const float* __restrict__ bias,
+    float* __restrict__ Y) {
+    __shared__ f32x4 xs[2][kLdsK / H][H][kWave];  // 160 KiB
+    const int64_t nb = gridDim.x;
+    const int64_t x = blockIdx.x % kXcds, q = blockIdx.x / kXcds;
+    // blocks of XCD x: q < count_x; heavy ones first: q < ha_x
+    const int64_t ha = nblk_a / kXcds + (x < nblk_a % kXcds ? 1 : 0);
+    const int64_t a0 = x * (nblk_a / kXcds) + (x < nblk_a % kXcds ? x : nblk_a % kXcds);
+    const int64_t nblk_b = nb - nblk_a;
+    // XCD x holds count_x = ceil((nb - x) / 8) blocks, ha of them heavy
+    const int64_t count_x = (nb - x + kXcds - 1) / kXcds;
+    const int64_t hb_lo = x * (nb / kXcds) + (x < nb % kXcds ? x : nb % kXcds) - a0;  // rest before
+    if (q < ha) {
+        spmm_lds_body<2, H>(xs, a0 + q, T, K, N, nrowblk_a, order, row_start, row_nnz, col,
+                            val, X, bias, Y);
+    } else {
+        const int64_t lb = hb_lo + (q - ha);
+        if (lb < nblk_b && q < count_x) {
+            spmm_lds_body<RW, H>(xs, lb, M - T, K, N, nrowblk_b, order + T, row_start,
+                                 row_nnz, col, val, X, bias, Y);
+        }
+    }
+}
+
 int launch_blocks(int64_t waves, int64_t* blocks) {
     *blocks = ceil_div(waves, kSpmmBlock / kWave);
     if (*blocks > INT32_MAX) return fail(SLK_EINVAL, "spmm: problem too large for one launch");
@@ -552,6 +600,24 @@ int launch_lds_rw(const slk_csr* W, const int32_t* order, int64_t P, const float
     hipLaunchKernelGGL((spmm_lds_kernel<RW, H>), dim3(static_cast<unsigned>(blocks)),
                        dim3(kLdsThreads), 0, st, P, W->ncols, N, nrowblk, order, W->row_start,
                        W->row_nnz, W->col_indices, W->values, X, bias, Y);
+    return check_launch("spmm");
+}
+
+// Heavy rows (positions [0, T) of W->row_order, two per wave) and the rest
+// (rw per wave) in one grid (spmm_lds_split_kernel), one column half per lane.
+template <int RW>
+int launch_lds_split_rw(const slk_csr* W, int64_t T, const float* X, int64_t N,
+                        const float* bias, float* Y, hipStream_t st) {
+    const int64_t M = W->nrows;
+    const int64_t tiles = ceil_div(N, int64_t{kLdsCols});
+    const int64_t nrowblk_a = ceil_div(T, int64_t{kLdsWaves} * 2);
+    const int64_t nrowblk_b = ceil_div(M - T, int64_t{kLdsWaves} * RW);
+    const int64_t na = nrowblk_a * tiles, nb = nrowblk_b * tiles;
+    if (na + nb > INT32_MAX) return fail(SLK_EINVAL, "spmm: problem too large for one launch");
+    hipLaunchKernelGGL((spmm_lds_split_kernel<RW, 1>), dim3(static_cast<unsigned>(na + nb)),
+                       dim3(kLdsThreads), 0, st, T, M, W->ncols, N, na, nrowblk_a, nrowblk_b,
+                       W->row_order, W->row_start, W->row_nnz, W->col_indices, W->values, X, bias,
+                       Y);
     return check_launch("spmm");
 }
 
@@ -729,6 +795,17 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
         bool split = T > 0;
         if (const int64_t t = tuning(SLK_TUNE_SPMM_SPLIT); t == 0) split = false;
         if (split) {
+            // one grid when the rest fills at least one workgroup per XCD (the
+            // split kernel's XCD shares need it): 16384^2 Zipf(1.1) at 95%
+            // forward 8.27 -> 8.03 ms against two launches
+            const int64_t nb_rest = ceil_div(M - T, int64_t{kLdsWaves} * rw) * ceil_div(N, int64_t{kLdsCols});
+            if (h == 1 && nb_rest >= kXcds) {
+                switch (rw) {
+                    case 2: return launch_lds_split_rw<2>(W, T, X, N, bias, Y, st);
+                    case 4: return launch_lds_split_rw<4>(W, T, X, N, bias, Y, st);
+                    default: return launch_lds_split_rw<8>(W, T, X, N, bias, Y, st);
+                }
+            }
             if (int rc = launch_lds_rw<2>(W, W->row_order, T, X, N, bias, Y, st)) return rc;
             return launch_lds(h, rw, W, W->row_order + T, M - T, X, N, bias, Y, st);
         }
