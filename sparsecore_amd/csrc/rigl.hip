@@ -376,7 +376,8 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
     int64_t* __restrict__ amb_count) {
     __shared__ uint32_t keep[U * kRowThreads * 4 / 32];
     __shared__ int64_t tmp[kRowThreads];
-    __shared__ uint32_t hist[256];
+    __shared__ uint32_t hist[2048];
+    __shared__ uint32_t lst[U * kRowThreads * 4];  // 64 KiB at U = 16
     __shared__ uint32_t s_digit;
     __shared__ int64_t s_below;
     __shared__ unsigned long long s_best;
@@ -407,72 +408,140 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
     const float ni = nrm_r[i];
     const float* g_row = Gp + i * ldg;
 
-    // the row's |G'| and empty-column mask (bit 4u + e), the largest
-    // candidate norm, and whether every bound exists
-    // (every load is issued before the first use: clamped addresses instead
-    // of branches, the columns past K masked out of `cand`)
-    f32x4 a[U], nr[U];
+    // the row's |G'| and empty-column mask (bit 4u + e) (every load issued
+    // before the first use: clamped addresses instead of branches, the
+    // columns past K masked out of `cand`); the norms are read after the
+    // select, so the two sets of 4U registers are never live together
+    // (held as selection keys, ~bits(|g|), one register per column: |g|
+    // is ~key's float, so the keys and the values are never both live)
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 a[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int64_t c = 4 * (t + int64_t{kRowThreads} * u);
-        const int64_t cl = c < K ? c : K - 4;
-        a[u] = *reinterpret_cast<const f32x4*>(g_row + cl);
-        nr[u] = *reinterpret_cast<const f32x4*>(nrm_c + cl);
+        a[u] = *reinterpret_cast<const u32x4*>(g_row + (c < K ? c : K - 4));
     }
     uint64_t cand = 0;
     int64_t unbounded = 0;
-    uint32_t nmax = 0;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const int64_t c = 4 * (t + int64_t{kRowThreads} * u);
         const uint32_t kw = c < K ? keep[c >> 5] >> (c & 31) : 15u;  // c % 4 == 0: one word
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            a[u][e] = fabsf(a[u][e]);
+            a[u][e] = desc_key(fabsf(__uint_as_float(a[u][e])));
             if ((kw >> e) & 1u) continue;
             cand |= 1ull << (4 * u + e);
-            if (!(nr[u][e] <= kNormCap) || !(a[u][e] <= 0x1p125f)) ++unbounded;
-            else nmax = max(nmax, __float_as_uint(nr[u][e]));
+            if (!(__uint_as_float(~a[u][e]) <= 0x1p125f)) ++unbounded;
         }
     }
-    atomicMax(&s_nmax, nmax);
     block_inclusive_scan(unbounded, tmp);
     unbounded = tmp[kRowThreads - 1];
     if (unbounded > 0 || !(ni <= kNormCap)) return finish_row(kRowExact, n_empty);
-    const float nm = __uint_as_float(s_nmax);
     const int64_t n_grow = n_drop < n_empty ? n_drop : n_empty;
 
-    // T' = the n_grow-th largest |G'| of the empty columns (kth_smallest_key
-    // over the registers)
+    // T' = the n_grow-th largest |G'| of the empty columns: the n_grow-th
+    // smallest key. First the top 11 bits over the registers (2048 bins), then
+    // the keys in that bin, listed in LDS (most rows: a few hundred; the list
+    // holds a whole row), for the remaining 21 bits in passes of 8, 8 and 5
+    // bits. Any exact selection gives the same key.
     uint32_t prefix = 0;
     int64_t need = n_grow;
-    for (int pass = 0; pass < 4; ++pass) {
-        const int shift = 24 - 8 * pass;
-        hist[t] = 0;
-        __syncthreads();
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t key = desc_key(a[u][e]);
-                const bool ok = ((cand >> (4 * u + e)) & 1ull) &&
-                                (pass == 0 || (key >> (shift + 8)) == prefix);
-                hist_add(hist, (key >> shift) & 255u, ok);
+    auto pick = [&](int bins, int64_t h_of_thread_lo, int per) {
+        // thread t holds bins [t*per, t*per + per); finds the bin of the
+        // need-th key and the count below it
+        const int64_t incl = block_inclusive_scan(h_of_thread_lo, tmp);
+        if (incl - h_of_thread_lo < need && need <= incl) {
+            int64_t run = incl - h_of_thread_lo;
+            for (int q = 0; q < per; ++q) {
+                const int64_t hq = hist[t * per + q];
+                if (run + hq >= need) {
+                    s_digit = static_cast<uint32_t>(t * per + q);
+                    s_below = run;
+                    break;
+                }
+                run += hq;
             }
         }
+        (void)bins;
         __syncthreads();
-        const int64_t h = hist[t];
-        const int64_t incl = block_inclusive_scan(h, tmp);
-        if (incl - h < need && need <= incl) {
-            s_digit = static_cast<uint32_t>(t);
-            s_below = incl - h;
-        }
+    };
+    {
+        constexpr int kTopBits = 11, kTopBins = 1 << kTopBits, kPer = kTopBins / kRowThreads;
+        for (int q = 0; q < kPer; ++q) hist[t * kPer + q] = 0;
         __syncthreads();
-        prefix = (prefix << 8) | s_digit;
+        // (one LDS atomic per key: 2048 bins spread a wave's keys enough that
+        // hist_add's folding does not pay for its registers)
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if ((cand >> (4 * u + e)) & 1ull) atomicAdd(&hist[a[u][e] >> (32 - kTopBits)], 1u);
+        __syncthreads();
+        int64_t hs = 0;
+        for (int q = 0; q < kPer; ++q) hs += hist[t * kPer + q];
+        pick(kTopBins, hs, kPer);
+        prefix = s_digit;
         need -= s_below;
+        const int64_t n_bin = hist[prefix];
         __syncthreads();
+        // list the bin's keys: per-thread counts, one scan for the offsets
+        uint64_t in_bin = 0;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if ((a[u][e] >> (32 - kTopBits)) == prefix) in_bin |= 1ull << (4 * u + e);
+        in_bin &= cand;
+        const int64_t mine = __popcll(in_bin);
+        const int32_t at = static_cast<int32_t>(block_inclusive_scan(mine, tmp) - mine);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int bit = 4 * u + e;  // slot: the bin's keys of this thread before it
+                if ((in_bin >> bit) & 1ull)
+                    lst[at + __popcll(in_bin & ((1ull << bit) - 1ull))] = a[u][e];
+            }
+        __syncthreads();
+        int shift = 32 - kTopBits;
+        for (const int width : {8, 8, 5}) {
+            shift -= width;
+            hist[t] = 0;
+            __syncthreads();
+            for (int64_t e = t; e < n_bin; e += kRowThreads) {
+                const uint32_t key = lst[e];
+                if ((key >> (shift + width)) == prefix)
+                    atomicAdd(&hist[(key >> shift) & ((1u << width) - 1u)], 1u);
+            }
+            __syncthreads();
+            pick(1 << width, hist[t], 1);
+            prefix = (prefix << width) | s_digit;
+            need -= s_below;
+            __syncthreads();
+        }
     }
     const float Tp = __uint_as_float(~prefix);
+    // the candidates' norms: the largest, and whether every bound exists
+    f32x4 nr[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int64_t c = 4 * (t + int64_t{kRowThreads} * u);
+        nr[u] = *reinterpret_cast<const f32x4*>(nrm_c + (c < K ? c : K - 4));
+    }
+    uint32_t nmax = 0;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (!((cand >> (4 * u + e)) & 1ull)) continue;
+            if (!(nr[u][e] <= kNormCap)) ++unbounded;
+            else nmax = max(nmax, __float_as_uint(nr[u][e]));
+        }
+    atomicMax(&s_nmax, nmax);
+    block_inclusive_scan(unbounded, tmp);
+    if (tmp[kRowThreads - 1] > 0) return finish_row(kRowExact, n_empty);
+    const float nm = __uint_as_float(s_nmax);
     const float cni = up_(c_bound * ni);
     const float delta = up_(0x1p-100f * up_(1.0f + ni + nm));
     const float e_max = col_err(cni, nm, delta);
@@ -481,17 +550,13 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
     int64_t n_in = 0, n_amb = 0;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int64_t c = 4 * (t + int64_t{kRowThreads} * u);
-        nr[u] = *reinterpret_cast<const f32x4*>(nrm_c + (c < K ? c : K - 4));
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             if (!((cand >> (4 * u + e)) & 1ull)) continue;
             const float ek = col_err(cni, nr[u][e], delta);
-            if (dn_(a[u][e] - ek) > t_in) ++n_in;
-            else if (!(up_(a[u][e] + ek) < t_out)) ++n_amb;
+            const float g = __uint_as_float(~a[u][e]);
+            if (dn_(g - ek) > t_in) ++n_in;
+            else if (!(up_(g + ek) < t_out)) ++n_amb;
         }
     }
     block_inclusive_scan(n_in, tmp);
