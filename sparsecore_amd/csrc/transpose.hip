@@ -213,7 +213,7 @@ __global__ __launch_bounds__(kWave) void tr_scatter_kernel(
 
 // T5 for blocks of at most 32 rows (see above): one 256-thread workgroup per
 // block, LDS holds one mask word per column of the current column chunk.
-constexpr int kParScatterThreads = 256;
+constexpr int kParScatterThreads = 1024;
 constexpr int64_t kParScatterMaxRows = 32;
 
 __global__ __launch_bounds__(kParScatterThreads) void tr_scatter_par_kernel(
