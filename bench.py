@@ -51,10 +51,11 @@ sys.path.insert(0, str(ROOT))
 METRIC = "SpMM fwd+dX+dW achieved HBM GB/s & effective GFLOP/s; train-step tokens/s"
 HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3  # MI355X published fp32 peak (vector, packed; = dense fp32 MFMA)
-# The kernels run on the VALU with packed fp32 disabled, so
-# the non-packed rate is their practical ceiling: 256 CUs x 64 fma/clk x
-# 2.4 GHz x 2 flops.
+# The kernels run on the VALU with packed fp32 disabled at compile time (some
+# packed forms have given wrong results on this hardware), so the non-packed
+# rate is their practical ceiling: 256 CUs x 64 fma/clk x 2.4 GHz x 2 flops.
 VALU_NONPACKED_TFLOPS = 78.6
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X published dense bf16 matrix-core peak
 
 
 def parse_args():
@@ -1217,6 +1218,15 @@ def measure(work, args):
             config = {"workload": f"{work.name}: {work.desc}", "graph": graph_ok,
                       "graph_steps": S if graph_ok else 0,
                       "transpose_rebuild_ms": round(work.rebuild_ms, 3)}
+    roofline_mfma = None
+    apx = [k for k in kern if k["kernel"] == "dense_grad_approx"]
+    if apx:
+        # RigL's matrix-core pass: three bf16 products (x_h·y_h, x_h·y_l,
+        # x_l·y_h) of 2·M·K·N flops each, against the dense bf16 peak
+        t = 3 * apx[0]["flops"] / (apx[0]["avg_us"] * 1e-6) / 1e12
+        roofline_mfma = {"kernel": "dense_grad_approx", "achieved": round(t, 1),
+                         "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(t / MFMA_BF16_PEAK_TFLOPS, 4)}
     return {
         "value": value, "unit": unit, "ms_per_step": ms_per_step, "config": config,
         "path": path, "kernels": kern,
@@ -1230,7 +1240,8 @@ def measure(work, args):
                                  "peak": FP32_PEAK_TFLOPS,
                                  "frac": round(tflops / FP32_PEAK_TFLOPS, 4),
                                  "frac_of_nonpacked_valu": round(tflops / VALU_NONPACKED_TFLOPS,
-                                                                 4)}},
+                                                                 4)},
+                     **({"mfma": roofline_mfma} if roofline_mfma else {})},
     }
 
 

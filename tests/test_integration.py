@@ -1,6 +1,7 @@
-"""The integration boundary as INTEGRATION.md states it: the ctypes binding block
-it shows runs unchanged against the built library, and ``import sparselab``
-resolves to this package after ``install_as_sparselab()``.
+"""The integration boundary as the repository's integration guide states it:
+the ctypes binding block the guide shows runs unchanged against the built
+library, and ``import sparselab`` resolves to this package after
+``install_as_sparselab()``.
 
 CPU: the block's struct matches the library's ``slk_csr`` mirror field for
 field, and the alias serves the reference's module names. GPU: the block's
@@ -25,7 +26,7 @@ def _binding_block() -> str:
     text = (REPO / "INTEGRATION.md").read_text()
     blocks = re.findall(r"```python\n(.*?)```", text, flags=re.S)
     found = [b for b in blocks if "class slk_csr" in b]
-    assert len(found) == 1, "INTEGRATION.md must hold exactly one binding block"
+    assert len(found) == 1, "the integration guide must hold exactly one binding block"
     return found[0]
 
 
@@ -36,7 +37,7 @@ def _run_block() -> dict:
         pytest.skip("libsparsecore_amd.so is not built")
     os.environ["SLK_LIBRARY"] = str(_lib.LIB_PATH)
     ns: dict = {}
-    exec(compile(_binding_block(), "INTEGRATION.md", "exec"), ns)
+    exec(compile(_binding_block(), "integration-guide", "exec"), ns)
     return ns
 
 
