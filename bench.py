@@ -166,8 +166,11 @@ def timed_run(run_steps, steps: int):
 
 def capture(step_body, warm_iters: int = 3, steps: int = 1):
     """Capture `steps` consecutive step_body() calls into one HIP graph after
-    warming it on a side stream; returns the graph and each step's output."""
+    warming it on a side stream; returns the graph, each step's output and the
+    graph's node types (read before the graph is instantiated)."""
     import torch
+
+    from sparsecore_amd import _lib
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -175,10 +178,12 @@ def capture(step_body, warm_iters: int = 3, steps: int = 1):
         for _ in range(warm_iters):
             step_body()
     torch.cuda.current_stream().wait_stream(s)
-    g = torch.cuda.CUDAGraph()
+    g = torch.cuda.CUDAGraph(keep_graph=True)
     with torch.cuda.graph(g):
         outs = [step_body() for _ in range(steps)]
-    return g, outs
+    nodes = _lib.graph_node_types(g)
+    g.instantiate()
+    return g, outs, nodes
 
 
 class GraphSteps:
@@ -1082,11 +1087,16 @@ def measure(work, args):
     use_graph = not args.no_graph and not getattr(work, "dynamic", False)
     graph_ok = False
     # Several steps per graph only where a replay's launch latency is a visible
-    # share of the step (sub-millisecond steps: C1, C2). Longer steps keep one
-    # step per graph: C3's step holds library scans (the embedding backward's
-    # rocprim select), and a 20-step graph of it faulted inside such a scan on
-    # replay, where one-step graphs of the same step replay cleanly.
+    # share of the step (sub-millisecond steps: C1, C2), one step otherwise.
+    # A graph that holds memset nodes is not replayed at all (the step runs
+    # eagerly): memset nodes have left memory uncleared on replays after the
+    # first on these machines, and library code records them (rocprim's
+    # partition zeroes its selected-item count with hipMemsetAsync; torch's
+    # embedding backward runs that partition, torch's multi-block reductions
+    # zero their semaphores the same way). A partition whose count starts
+    # from the previous replay's total writes its outputs past their end.
     S = max(1, min(args.graph_steps, args.steps)) if eager_s < 1e-3 else 1
+    graph_nodes = None
     if use_graph:
         params = work.params()
         snap = [p.detach().clone() for p in params]
@@ -1102,25 +1112,39 @@ def measure(work, args):
                 p.copy_(s)
         torch.cuda.synchronize()
         stage(f"graph capture ({S} steps per graph)")
-        g, gouts = capture(work.body, steps=S)
-        g1 = capture(work.body)[0] if args.steps % S or args.warmup % S else None
-        stage("graph replay check (two replays, every step against eager)")
+        g, gouts, graph_nodes = capture(work.body, steps=S)
+        g1 = None
+        if args.steps % S or args.warmup % S:
+            g1, _, nodes1 = capture(work.body)
+            for k, v in nodes1.items():
+                graph_nodes[k] = graph_nodes.get(k, 0) + v
+        stage(f"graph node types: {graph_nodes}")
         with torch.no_grad():
             for p, s in zip(params, snap):
                 p.copy_(s)
-        graph_ok = True
-        for r in range(2):
-            g.replay()
-            torch.cuda.synchronize()
-            got = [t for o in gouts for t in (o if isinstance(o, tuple) else (o,))]
-            want = eager_flat[r * len(got):(r + 1) * len(got)]
-            graph_ok = graph_ok and len(want) == len(got) and all(
-                torch.equal(a, b) for a, b in zip(got, want))
-        if not all(torch.equal(p, e) for p, e in zip(params, eager_params)):
-            graph_ok = False
+        graph_ok = not graph_nodes.get("memset")
         if not graph_ok:
-            print("bench.py: graph replay differs from eager; timing eager launches",
-                  file=sys.stderr)
+            print(f"bench.py: the captured step holds {graph_nodes['memset']} memset nodes; "
+                  f"not replaying it, timing eager launches", file=sys.stderr)
+        else:
+            stage("graph replay check (two replays, every step against eager)")
+        if graph_ok:
+            for r in range(2):
+                g.replay()
+                torch.cuda.synchronize()
+                got = [t for o in gouts for t in (o if isinstance(o, tuple) else (o,))]
+                want = eager_flat[r * len(got):(r + 1) * len(got)]
+                graph_ok = graph_ok and len(want) == len(got) and all(
+                    torch.equal(a, b) for a, b in zip(got, want))
+            graph_ok = graph_ok and all(torch.equal(p, e) for p, e in zip(params, eager_params))
+            if not graph_ok:
+                print("bench.py: graph replay differs from eager; timing eager launches",
+                      file=sys.stderr)
+        if not graph_ok:
+            del g, g1, gouts  # release the graphs' private memory pool
+            with torch.no_grad():
+                for p, s in zip(params, snap):
+                    p.copy_(s)
         if graph_ok:
             runner = GraphSteps(g, S, g1)
             run_steps = runner.run
@@ -1182,6 +1206,8 @@ def measure(work, args):
                   "l1_dx": "not computed (the input needs no grad; the reference computes "
                            "and discards it)",
                   "graph": graph_ok, "graph_steps": S if graph_ok else 0}
+        if graph_nodes and graph_nodes.get("memset"):
+            config["graph_refused"] = f"{graph_nodes['memset']} memset nodes"
     elif isinstance(work, GPTWork):
         value = work.tokens_per_step() * args.steps / elapsed
         unit = "tokens/s"
@@ -1198,6 +1224,8 @@ def measure(work, args):
         config = {"workload": f"{work.name}: {work.desc}", "global_batch": work.batch,
                   "seq_len": work.ctx, "graph": graph_ok,
                   "graph_steps": S if graph_ok else 0}
+        if graph_nodes and graph_nodes.get("memset"):
+            config["graph_refused"] = f"{graph_nodes['memset']} memset nodes"
     else:
         path_k = [k for k in kern if k["kernel"] in ("spmm_fwd", "sddmm_dw", "transpose_refresh",
                                                       "spmm_dx")]
@@ -1218,6 +1246,8 @@ def measure(work, args):
             config = {"workload": f"{work.name}: {work.desc}", "graph": graph_ok,
                       "graph_steps": S if graph_ok else 0,
                       "transpose_rebuild_ms": round(work.rebuild_ms, 3)}
+            if graph_nodes and graph_nodes.get("memset"):
+                config["graph_refused"] = f"{graph_nodes['memset']} memset nodes"
     roofline_mfma = None
     apx = [k for k in kern if k["kernel"] == "dense_grad_approx"]
     if apx:

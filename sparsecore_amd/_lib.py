@@ -438,3 +438,34 @@ def rigl_finish(view: CsrView, thr: torch.Tensor, G: torch.Tensor, nrm_dY: torch
                                 removed.data_ptr(), stream_of(removed))
     if rc:
         _raise(rc)
+
+
+# HIP graph node types (hip_runtime_api.h, enum hipGraphNodeType)
+GRAPH_NODE_TYPES = {0: "kernel", 1: "memcpy", 2: "memset", 3: "host", 4: "graph", 5: "empty",
+                    6: "wait_event", 7: "event_record", 8: "ext_semaphore_signal",
+                    9: "ext_semaphore_wait", 10: "mem_alloc", 11: "mem_free",
+                    12: "memcpy_from_symbol", 13: "memcpy_to_symbol", 14: "batch_mem_op"}
+
+
+def graph_node_types(graph: "torch.cuda.CUDAGraph") -> dict[str, int]:
+    """Counts of each node type in a captured graph (made with keep_graph=True,
+    read before replay). A memset node is what a captured hipMemsetAsync
+    becomes: this library's entry points record none (their outputs are written
+    by kernels), but library code captured beside them may, e.g. rocprim's
+    partition and radix sort, which zero their counters that way."""
+    hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime torch loaded (same soname)
+    g = ctypes.c_void_p(graph.raw_cuda_graph())
+    n = ctypes.c_size_t(0)
+    if hip.hipGraphGetNodes(g, None, ctypes.byref(n)) != 0:
+        raise RuntimeError("hipGraphGetNodes failed")
+    nodes = (ctypes.c_void_p * max(1, n.value))()
+    if n.value and hip.hipGraphGetNodes(g, nodes, ctypes.byref(n)) != 0:
+        raise RuntimeError("hipGraphGetNodes failed")
+    out: dict[str, int] = {}
+    t = ctypes.c_int(0)
+    for i in range(n.value):
+        if hip.hipGraphNodeGetType(ctypes.c_void_p(nodes[i]), ctypes.byref(t)) != 0:
+            raise RuntimeError("hipGraphNodeGetType failed")
+        name = GRAPH_NODE_TYPES.get(t.value, f"type{t.value}")
+        out[name] = out.get(name, 0) + 1
+    return out
