@@ -418,14 +418,23 @@ __global__ __launch_bounds__(kBlock) void sddmm_scalar_kernel(
 // zeroes the row's padding slots and, with dbias, sums its dY row. More
 // segments per workgroup stage each X window for more slots: 128 on the
 // 16384^2 layers (95%: 7.79 -> 6.89 ms, 99%: 2.39 -> 2.22; 256 was slower).
+// Visiting each segment's slots in an order that keeps the four rows of an
+// LDS pass on different banks (below) took the bank-conflict share of the
+// 95% layer's cycles from 35% to 14% and its time 6.91 -> 6.46 ms. Wider
+// blocks (256 columns, 8 or 16 slots per segment) measured 8.2-8.4 ms: each
+// staged X window then serves fewer slots per byte staged.
 constexpr int kSegWin = 64;                  // floats per window (4 steps)
 constexpr int kSegPieces = kSegWin / 4;      // 16-byte pieces per row
 constexpr int kSegStride = kSegPieces + 4;   // pieces per LDS row (padded)
 static_assert(SLK_SEG_GROUP % 128 == 0, "the list padding holds whole groups of 64 and 128");
 constexpr int64_t kSegGroupMinGroups = 2048;  // 128-segment groups from this many
 
+// (lean kernels are held to 128 VGPRs, 4 waves per SIMD: at 130 a workgroup
+// of 8 waves no longer fits twice per CU; the 128-column, 64-segment one
+// would spill there)
 template <int C, int S, bool LEAN, int GS>
-__global__ __launch_bounds__(GS * 4) void sddmm_seg_kernel(
+__global__ __launch_bounds__(GS * 4)
+__attribute__((amdgpu_waves_per_eu((LEAN && !(C == 128 && GS == 64)) ? 4 : 1))) void sddmm_seg_kernel(
     int64_t M, int64_t K, int64_t N, const int32_t* __restrict__ row_start,
     const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ row_cap,
     const int32_t* __restrict__ col, const float* __restrict__ dY, const float* __restrict__ X,
@@ -460,10 +469,43 @@ __global__ __launch_bounds__(GS * 4) void sddmm_seg_kernel(
     const int32_t s0 = seg_start[e];
     const int32_t cnt = seg_count[e];
     const int64_t row = seg_row[e];
-    int32_t xo[S];
+    // Visiting order of the segment's slots. A 16-lane LDS pass serves four
+    // quads, each reading 16 consecutive floats of its slot's X row; a row
+    // starts 16·(c mod 4) banks into the 64 (stride kSegStride pieces), so the
+    // pass is conflict-free when the four rows differ in c mod 4. Quad j of
+    // the pass takes, at step k, a slot with c ≡ k + j (mod 4) where it has
+    // one (the slots' results are independent: the order changes no bits),
+    // and a step without a slot reads the block row of that residue.
+    const int jq = (threadIdx.x >> 2) & 3;
+    uint32_t byres[4] = {0u, 0u, 0u, 0u};
+    int32_t xo0[S];
 #pragma unroll
-    for (int k = 0; k < S; ++k) xo[k] = ((k < cnt ? col[s0 + k] : c_lo) - c_lo) * kSegStride + q;
-    // X row of slot k (the epilogue's tail), from xo
+    for (int k = 0; k < S; ++k) {
+        const int32_t c = k < cnt ? col[s0 + k] - c_lo : 0;
+        xo0[k] = c * kSegStride + q;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) byres[r] |= (k < cnt && (c & 3) == r) ? (1u << k) : 0u;
+    }
+    static_assert(S <= 8, "slot of each step packed in 4 bits");
+    uint32_t avail = (1u << cnt) - 1u;  // cnt <= S
+    int32_t xo[S];
+    uint32_t slots = 0xFFFFFFFFu;  // 4 bits per step: its slot, 15 = none
+#pragma unroll
+    for (int k = 0; k < S; ++k) {
+        const int want = (k + jq) & 3;
+        const uint32_t bw =
+            (want == 0 ? byres[0] : want == 1 ? byres[1] : want == 2 ? byres[2] : byres[3]) & avail;
+        const uint32_t m = bw != 0u ? bw : avail;
+        const int pick = m != 0u ? __builtin_ctz(m) : -1;
+        avail &= ~(m & (0u - m));
+        if (pick >= 0)
+            slots = (slots & ~(15u << (4 * k))) | (static_cast<uint32_t>(pick) << (4 * k));
+        int32_t v = want * kSegStride + q;
+#pragma unroll
+        for (int i = 0; i < S; ++i) v = pick == i ? xo0[i] : v;
+        xo[k] = v;
+    }
+    // X row of step k (the epilogue's tail), from xo
     auto xrow = [&](int k) { return X + static_cast<int64_t>(c_lo + (xo[k] - q) / kSegStride) * N; };
     const int32_t nC = static_cast<int32_t>(min<int64_t>(C, K - c_lo));
 
@@ -550,7 +592,7 @@ __global__ __launch_bounds__(GS * 4) void sddmm_seg_kernel(
             const f32x4 d = *reinterpret_cast<const f32x4*>(dY + row * N + j);
 #pragma unroll
             for (int k = 0; k < S; ++k) {
-                if (k < cnt) {
+                if (((slots >> (4 * k)) & 15u) != 15u) {
                     fma4x(d, *reinterpret_cast<const f32x4*>(xrow(k) + j), acc[k][0], acc[k][1],
                           acc[k][2], acc[k][3]);
                 }
@@ -567,9 +609,10 @@ __global__ __launch_bounds__(GS * 4) void sddmm_seg_kernel(
     if (q == 0) {
 #pragma unroll
         for (int k = 0; k < S; ++k) {
-            if (k >= cnt) continue;
+            const uint32_t sk = (slots >> (4 * k)) & 15u;
+            if (sk == 15u) continue;
             const float rsum = (acc[k][0] + acc[k][2]) + (acc[k][1] + acc[k][3]);
-            dW[s0 + k] = running_sum(dY + row * N + jt, xrow(k) + jt, N - jt, rsum);
+            dW[s0 + sk] = running_sum(dY + row * N + jt, xrow(k) + jt, N - jt, rsum);
         }
     }
 }
