@@ -548,20 +548,26 @@ __global__ __launch_bounds__(kLdsThreads) void spmm_lds_kernel(
                          row_start, row_nnz, col, val, X, bias, Y);
 }
 
-// A skewed matrix's heavy rows (positions [0, T) of the longest-first order,
-// two rows per wave) and the rest (positions [T, M), RW rows per wave) in one
+// A skewed matrix's heavy rows (positions [0, T) of the longest-first order)
+// and the rest (positions [T, M), RW rows per wave, 4 columns per lane) in one
 // grid: the few workgroups of heavy rows would otherwise leave CUs idle in
-// their launch's last round. Every XCD starts its share of the grid with its
-// share of the heavy workgroups (the longest), then its share of the rest,
-// each in the tile-major order of its own launch.
-template <int RW, int H>
+// their launch's last round. Heavy rows run two per wave with 8 columns per
+// lane (kHeavyH = 2 halves): their long runs of slots amortize a slot's
+// readlane and address work over 8 fmas instead of 4 (16384^2 Zipf(1.1) at
+// 95%: 8.03 -> 7.35 ms; 4 halves or 1 or 4 rows per wave were slower). Every
+// XCD starts its share of the grid with its share of the heavy workgroups (the
+// longest), then its share of the rest, each in the tile-major order of its
+// own part.
+constexpr int kHeavyRW = 2;
+constexpr int kHeavyH = 2;
+template <int RW>
 __global__ __launch_bounds__(kLdsThreads) void spmm_lds_split_kernel(
     int64_t T, int64_t M, int64_t K, int64_t N, int64_t nblk_a, int64_t nrowblk_a,
     int64_t nrowblk_b, const int32_t* __restrict__ order, const int32_t* __restrict__ row_start,
     const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ col,
     const float* __restrict__ val, const float* __restrict__ X, const float* __restrict__ bias,
     float* __restrict__ Y) {
-    __shared__ f32x4 xs[2][kLdsK / H][H][kWave];  // 160 KiB
+    __shared__ f32x4 xraw[2 * kLdsK * kWave];  // 160 KiB, shaped by each part below
     const int64_t nb = gridDim.x;
     const int64_t x = blockIdx.x % kXcds, q = blockIdx.x / kXcds;
     // blocks of XCD x: q < count_x; heavy ones first: q < ha_x
@@ -572,13 +578,15 @@ __global__ __launch_bounds__(kLdsThreads) void spmm_lds_split_kernel(
     const int64_t count_x = (nb - x + kXcds - 1) / kXcds;
     const int64_t hb_lo = x * (nb / kXcds) + (x < nb % kXcds ? x : nb % kXcds) - a0;  // rest before
     if (q < ha) {
-        spmm_lds_body<2, H>(xs, a0 + q, T, K, N, nrowblk_a, order, row_start, row_nnz, col,
-                            val, X, bias, Y);
+        auto& xs = *reinterpret_cast<f32x4(*)[2][kLdsK / kHeavyH][kHeavyH][kWave]>(xraw);
+        spmm_lds_body<kHeavyRW, kHeavyH>(xs, a0 + q, T, K, N, nrowblk_a, order, row_start,
+                                         row_nnz, col, val, X, bias, Y);
     } else {
         const int64_t lb = hb_lo + (q - ha);
         if (lb < nblk_b && q < count_x) {
-            spmm_lds_body<RW, H>(xs, lb, M - T, K, N, nrowblk_b, order + T, row_start,
-                                 row_nnz, col, val, X, bias, Y);
+            auto& xs = *reinterpret_cast<f32x4(*)[2][kLdsK][1][kWave]>(xraw);
+            spmm_lds_body<RW, 1>(xs, lb, M - T, K, N, nrowblk_b, order + T, row_start, row_nnz,
+                                 col, val, X, bias, Y);
         }
     }
 }
@@ -603,18 +611,20 @@ int launch_lds_rw(const slk_csr* W, const int32_t* order, int64_t P, const float
     return check_launch("spmm");
 }
 
-// Heavy rows (positions [0, T) of W->row_order, two per wave) and the rest
-// (rw per wave) in one grid (spmm_lds_split_kernel), one column half per lane.
+// Heavy rows (positions [0, T) of W->row_order, kHeavyRW per wave, kHeavyH
+// halves) and the rest (rw per wave, one half) in one grid
+// (spmm_lds_split_kernel).
 template <int RW>
 int launch_lds_split_rw(const slk_csr* W, int64_t T, const float* X, int64_t N,
                         const float* bias, float* Y, hipStream_t st) {
     const int64_t M = W->nrows;
-    const int64_t tiles = ceil_div(N, int64_t{kLdsCols});
-    const int64_t nrowblk_a = ceil_div(T, int64_t{kLdsWaves} * 2);
+    const int64_t tiles_a = ceil_div(N, int64_t{kLdsCols} * kHeavyH);
+    const int64_t tiles_b = ceil_div(N, int64_t{kLdsCols});
+    const int64_t nrowblk_a = ceil_div(T, int64_t{kLdsWaves} * kHeavyRW);
     const int64_t nrowblk_b = ceil_div(M - T, int64_t{kLdsWaves} * RW);
-    const int64_t na = nrowblk_a * tiles, nb = nrowblk_b * tiles;
+    const int64_t na = nrowblk_a * tiles_a, nb = nrowblk_b * tiles_b;
     if (na + nb > INT32_MAX) return fail(SLK_EINVAL, "spmm: problem too large for one launch");
-    hipLaunchKernelGGL((spmm_lds_split_kernel<RW, 1>), dim3(static_cast<unsigned>(na + nb)),
+    hipLaunchKernelGGL((spmm_lds_split_kernel<RW>), dim3(static_cast<unsigned>(na + nb)),
                        dim3(kLdsThreads), 0, st, T, M, W->ncols, N, na, nrowblk_a, nrowblk_b,
                        W->row_order, W->row_start, W->row_nnz, W->col_indices, W->values, X, bias,
                        Y);
@@ -784,12 +794,13 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
         if (const int64_t t = tuning(SLK_TUNE_SPMM_H); t >= 0) h = t == 2 ? 2 : 1;
         if (const int64_t t = tuning(SLK_TUNE_SPMM_RW); t >= 0) rw = static_cast<int>(t);
         if (rw != 2 && rw != 4 && rw != 8) rw = 8;
-        // Heavy rows (the head of the longest-rows-first order) as a launch of
-        // their own with two rows per wave, then the rest in that order, so
-        // every workgroup holds rows of similar length: on the 16384^2
-        // Zipf(1.1) layer at 95% sparsity 12.6 -> 9.1 ms (heavy rows with the
-        // rest, a long row stalls its workgroup at every chunk; all rows in
-        // one sorted launch, the few workgroups of full rows outlast the rest).
+        // Heavy rows (the head of the longest-rows-first order) in workgroups
+        // of their own with two rows per wave and 8 columns per lane, then the
+        // rest in that order, so every workgroup holds rows of similar length:
+        // on the 16384^2 Zipf(1.1) layer at 95% sparsity 12.6 -> 9.1 ms (heavy
+        // rows with the rest, a long row stalls its workgroup at every chunk;
+        // all rows in one sorted launch, the few workgroups of full rows
+        // outlast the rest).
         // SLK_TUNE_SPMM_SPLIT = 0 runs one launch in natural row order.
         const int64_t T = W->n_heavy_rows;
         bool split = T > 0;
@@ -806,7 +817,8 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
                     default: return launch_lds_split_rw<8>(W, T, X, N, bias, Y, st);
                 }
             }
-            if (int rc = launch_lds_rw<2>(W, W->row_order, T, X, N, bias, Y, st)) return rc;
+            if (int rc = launch_lds_rw<kHeavyRW, kHeavyH>(W, W->row_order, T, X, N, bias, Y, st))
+                return rc;
             return launch_lds(h, rw, W, W->row_order + T, M - T, X, N, bias, Y, st);
         }
         return launch_lds(h, rw, W, nullptr, M, X, N, bias, Y, st);

@@ -187,9 +187,10 @@ def _check_host(nrows, ncols, values, col, rs, nnz, cap) -> str:
 
 # A row is "heavy" for slk_spmm's LDS-staged kernel when it holds more than
 # this many times the mean row's slots (slk_csr.n_heavy_rows). Measured on the
-# 16384^2 Zipf(1.1) layer at 95% sparsity: splitting at 2x, 4x and 8x the mean
-# gave 9.4, 9.1 and 9.8 ms against 12.6 ms unsplit; uniform layers have none.
-HEAVY_ROW_FACTOR = 4.0
+# 16384^2 Zipf(1.1) layer at 95% sparsity, with heavy rows at 8 columns per
+# lane: a bar of 1, 1.5, 2, 3, 4 and 6 x the mean gave 7.37, 7.16, 7.08, 7.11,
+# 7.36 and 7.29 ms (12.6 ms unsplit); uniform layers have none.
+HEAVY_ROW_FACTOR = 2.0
 
 
 def heavy_row_count(row_nnz: np.ndarray) -> int:

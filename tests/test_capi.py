@@ -80,20 +80,20 @@ def test_heavy_row_count_needs_an_order_and_a_valid_range():
 def test_heavy_rows_are_those_far_above_the_mean():
     from sparsecore_amd.layout import HEAVY_ROW_FACTOR, heavy_row_count
 
-    assert HEAVY_ROW_FACTOR == 4.0
+    assert HEAVY_ROW_FACTOR == 2.0
     assert heavy_row_count(np.zeros(0, np.int32)) == 0
     assert heavy_row_count(np.full(100, 7, np.int32)) == 0  # uniform: none
     nnz = np.full(100, 10, np.int32)
-    nnz[[3, 50]] = 200  # mean 13.8: heavy above 55.2
+    nnz[[3, 50]] = 200  # mean 13.8: heavy above 27.6
     assert heavy_row_count(nnz) == 2
-    nnz[7] = 55  # mean 14.25, bar 57: still two
+    nnz[7] = 27  # mean 13.97, bar 27.94: still two
     assert heavy_row_count(nnz) == 2
-    nnz[7] = 58
+    nnz[7] = 29  # mean 13.99, bar 27.98
     assert heavy_row_count(nnz) == 3
     import bench
 
     counts = bench.zipf_row_counts(16384, 16384, 0.05, 1.1, 0)
-    assert heavy_row_count(counts) == int((counts > 4 * counts.mean()).sum()) > 0
+    assert heavy_row_count(counts) == int((counts > 2 * counts.mean()).sum()) > 0
 
 
 @pytest.mark.parametrize("case", ["zipf", "ties", "uniform", "empty-rows", "none"])
