@@ -132,7 +132,11 @@ SLK_API int slk_abi_version(void);
  *   SLK_TUNE_SPMM_KERNEL  0 = per-wave gather kernel, 1 = LDS-staged kernel
  *   SLK_TUNE_SPMM_H       LDS kernel: 1 or 2 column halves per lane
  *   SLK_TUNE_SPMM_RW      LDS kernel: rows per wave (2, 4 or 8)
- *   SLK_TUNE_SPMM_SPLIT   LDS kernel: 0 = no separate launch for heavy rows
+ *   SLK_TUNE_SPMM_SPLIT   LDS kernel: 0 = no separate launch for heavy rows,
+ *                         1 = heavy rows and the rest as LDS launches on the
+ *                         caller's stream only (automatic: with phase bounds
+ *                         the rest runs on the gather kernel on a second
+ *                         stream, see slk_spmm)
  *   SLK_TUNE_SPMM_VEC     gather kernel: floats per lane (1, 2 or 4)
  *   SLK_TUNE_SDDMM_G      windowed dW kernel: groups per wave (1, 2 or 4)
  *   SLK_TUNE_SEG_LEAN     segment dW kernel: 1 = lean variant, 0 = not
@@ -155,7 +159,12 @@ SLK_API int slk_set_tuning(int knob, int64_t value);
  * kernels csrc/kernels/spmm_avx2.cpp:82-263 and spmm.cpp:20-105). Y is fully
  * written (rows without live slots become 0), so it needs no pre-zeroing.
  * Each Y element is the fused multiply-add chain over the row's live slots in
- * slot order, starting from +0.0 — the same arithmetic as the reference.     */
+ * slot order, starting from +0.0 — the same arithmetic as the reference.
+ * For a skewed matrix with phase bounds on the LDS-staged path, the rows
+ * after the heavy ones run concurrently on a second stream of the library's
+ * own, forked from and joined back to `stream` with events (capture-safe:
+ * the second stream joins the caller's capture); it and its two events are
+ * created on the first such call on a device that is not under capture.      */
 SLK_API int slk_spmm(const slk_csr* W, const float* X, int64_t K, int64_t N,
              float* Y, void* stream);
 

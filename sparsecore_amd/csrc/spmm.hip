@@ -33,6 +33,7 @@
 #include "common.hpp"
 
 #include <cstdlib>
+#include <mutex>
 
 namespace slk {
 namespace {
@@ -737,6 +738,96 @@ int launch_wave_t(const slk_csr* W, const float* X, int64_t N, const float* bias
     return check_launch("spmm_t");
 }
 
+// The phased gather sweep with 16-byte lanes: one launch per column phase,
+// stream-ordered, so each phase reads the partial sums its predecessor stored.
+int launch_phased4(const slk_csr* W, const float* X, int64_t N, const float* bias, float* Y,
+                   hipStream_t st) {
+    constexpr int U = 8;
+    const int64_t nitems = W->nrows * ceil_div(N, int64_t{kWave} * 4);
+    int64_t blocks;
+    if (int rc = launch_blocks(nitems, &blocks)) return rc;
+    for (int64_t ph = 0; ph < W->n_phases; ++ph) {
+        const float* b = ph + 1 == W->n_phases ? bias : nullptr;
+        hipLaunchKernelGGL((spmm_wave_kernel<4, U, false, true>),
+                           dim3(static_cast<unsigned>(blocks)), dim3(kSpmmBlock), 0, st,
+                           W->nrows, N, nitems, W->row_order, W->row_start, W->row_nnz,
+                           W->col_indices, W->values, X, b, Y, W->phase_lo, W->n_phases, ph);
+        if (int rc = check_launch("spmm")) return rc;
+    }
+    return SLK_OK;
+}
+
+// A second queue per device for the split forward below: one stream (default
+// priority) and the two events that fork it from and join it back to the
+// caller's stream. Created on the first such call on the device that is not
+// made under graph capture (until then the call keeps to one stream), and
+// kept until the process ends; g_side_mu is held from the fork to the join,
+// so calls from several host threads cannot interleave their event records.
+struct SideQueue {
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+constexpr int kMaxDevices = 64;
+std::mutex g_side_mu;
+SideQueue g_side[kMaxDevices];
+
+SideQueue* side_queue(hipStream_t st) {  // g_side_mu held; nullptr if unavailable
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    SideQueue& q = g_side[dev];
+    if (q.s != nullptr) return &q;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    hipStream_t s = nullptr;
+    hipEvent_t f = nullptr, j = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        if (j != nullptr) (void)hipEventDestroy(j);
+        if (f != nullptr) (void)hipEventDestroy(f);
+        if (s != nullptr) (void)hipStreamDestroy(s);
+        return nullptr;
+    }
+    q.s = s;
+    q.fork = f;
+    q.join = j;
+    return &q;
+}
+
+// Heavy rows (positions [0, T) of W->row_order) on the LDS kernel on the
+// caller's stream, the rest on the phased gather kernel on the side stream,
+// concurrently: the heavy rows' workgroups alone leave CUs idle in their last
+// rounds, which the gather launches fill. Rows are disjoint, so the two write
+// disjoint rows of Y. Returns SLK_OK with *done = false if no side queue.
+int spmm_split_two_queues(const slk_csr* W, int64_t T, const float* X, int64_t N,
+                          const float* bias, float* Y, hipStream_t st, bool* done) {
+    std::lock_guard<std::mutex> lock(g_side_mu);
+    SideQueue* q = side_queue(st);
+    *done = q != nullptr;
+    if (q == nullptr) return SLK_OK;
+    if (hipEventRecord(q->fork, st) != hipSuccess || hipStreamWaitEvent(q->s, q->fork, 0) != hipSuccess)
+        return fail(SLK_EDEVICE, "spmm: fork to the side stream failed");
+    int rc = launch_lds_rw<kHeavyRW, kHeavyH>(W, W->row_order, T, X, N, bias, Y, st);
+    if (rc == SLK_OK) {
+        slk_csr rest = *W;
+        rest.nrows = W->nrows - T;
+        rest.row_order = W->row_order + T;
+        rest.n_heavy_rows = 0;
+        rc = launch_phased4(&rest, X, N, bias, Y, q->s);
+    }
+    // joined back even after a failed launch, so the caller's stream stays ordered
+    if (hipEventRecord(q->join, q->s) != hipSuccess || hipStreamWaitEvent(st, q->join, 0) != hipSuccess)
+        return fail(SLK_EDEVICE, "spmm: join from the side stream failed");
+    return rc;
+}
+
 int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const float* bias,
               float* Y, void* stream, bool transposed_out = false) {
     clear_error();
@@ -803,8 +894,19 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
         // outlast the rest).
         // SLK_TUNE_SPMM_SPLIT = 0 runs one launch in natural row order.
         const int64_t T = W->n_heavy_rows;
-        bool split = T > 0;
-        if (const int64_t t = tuning(SLK_TUNE_SPMM_SPLIT); t == 0) split = false;
+        const int64_t split_t = tuning(SLK_TUNE_SPMM_SPLIT);
+        const bool split = T > 0 && split_t != 0;
+        // With phase bounds (X far beyond the L2s) the rows after the heavy
+        // ones run on the phased gather kernel, concurrently with the heavy
+        // rows' LDS launch (spmm_split_two_queues): 16384^2 Zipf(1.1) at 95%
+        // 7.05 -> 6.0 ms against the one-grid LDS split. SLK_TUNE_SPMM_SPLIT =
+        // 1 keeps the LDS split, 0 runs one launch in natural row order.
+        if (split && split_t < 0 && T < M && W->phase_lo != nullptr && W->n_phases > 1 &&
+            N >= kWave * 4) {
+            bool done = false;
+            const int rc = spmm_split_two_queues(W, T, X, N, bias, Y, st, &done);
+            if (done || rc != SLK_OK) return rc;
+        }
         if (split) {
             // one grid when the rest fills at least one workgroup per XCD (the
             // split kernel's XCD shares need it): 16384^2 Zipf(1.1) at 95%
@@ -839,23 +941,7 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
         if (L < kWave && L >= N) return launch_group_L(L, W, X, N, bias, Y, st);
         vec = 1;
     }
-    if (vec == 4 && W->phase_lo != nullptr && W->n_phases > 1) {
-        // phased sweep: one launch per column phase, stream-ordered, so each
-        // phase reads the partial sums its predecessor stored
-        constexpr int U = 8;
-        const int64_t nitems = M * ceil_div(N, int64_t{kWave} * 4);
-        int64_t blocks;
-        if (int rc = launch_blocks(nitems, &blocks)) return rc;
-        for (int64_t ph = 0; ph < W->n_phases; ++ph) {
-            const float* b = ph + 1 == W->n_phases ? bias : nullptr;
-            hipLaunchKernelGGL((spmm_wave_kernel<4, U, false, true>),
-                               dim3(static_cast<unsigned>(blocks)), dim3(kSpmmBlock), 0, st, M,
-                               N, nitems, W->row_order, W->row_start, W->row_nnz,
-                               W->col_indices, W->values, X, b, Y, W->phase_lo, W->n_phases, ph);
-            if (int rc = check_launch("spmm")) return rc;
-        }
-        return SLK_OK;
-    }
+    if (vec == 4 && W->phase_lo != nullptr && W->n_phases > 1) return launch_phased4(W, X, N, bias, Y, st);
     if (vec == 4) return launch_wave<4>(W, X, N, bias, Y, st);
     if (vec == 2) return launch_wave<2>(W, X, N, bias, Y, st);
     return launch_wave<1>(W, X, N, bias, Y, st);

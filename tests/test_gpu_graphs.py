@@ -63,3 +63,49 @@ def test_sparselinear_step_graph_is_kernels_only_and_replays_exactly(dev, shape)
         eager = step()  # eager work between replays
         torch.cuda.synchronize()
         assert all(torch.equal(a, b) for a, b in zip(eager, want))
+
+
+def test_two_stream_forward_captures_and_replays_exactly(dev, tune):
+    """slk_spmm's split forward on two streams (a skewed matrix with phase
+    bounds on the LDS-staged path) inside a HIP graph: the fork and join
+    become graph edges (kernel nodes only), and every replay gives the eager
+    bits, with eager work and synchronizations between the replays."""
+    import numpy as np
+
+    import oracle
+    from helpers import from_oracle
+
+    tune(spmm_kernel=1)
+    c = oracle.zipf_rows(3000, 700, 0.03, 1.1, seed=92, sigma=0.5)
+    W = from_oracle(c, dev)
+    v = W._view_phased(3)
+    assert v.n_heavy_rows > 0 and v.n_phases == 3
+    g = torch.Generator(device=dev)
+    g.manual_seed(92)
+    X = torch.randn(700, 520, generator=g, device=dev)
+    Y = torch.empty(3000, 520, device=dev)
+    _lib.spmm(v, X, Y)  # eager first: creates the library's side stream
+    torch.cuda.synchronize()
+    want = Y.clone()
+    assert np.array_equal(want.cpu().numpy(), oracle.spmm(c, X.cpu().numpy()))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        _lib.spmm(v, X, Y)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph(keep_graph=True)
+    with torch.cuda.graph(graph):
+        _lib.spmm(v, X, Y)
+    nodes = _lib.graph_node_types(graph)
+    print(f"[graph two streams] node types {nodes}", flush=True)
+    assert nodes.get("kernel", 0) >= 2 and set(nodes) <= {"kernel", "empty"}, nodes
+    graph.instantiate()
+    for r in range(4):
+        Y.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(Y, want), f"replay {r}"
+        _lib.spmm(v, X, Y)  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(Y, want)

@@ -350,6 +350,39 @@ def test_lds_heavy_row_split_bit_exact(dev, tune, h, rw):
         assert_bits_equal(Y.cpu().numpy(), want + b_np[:, None], f"Y+bias (T={T})")
 
 
+@pytest.mark.parametrize("split", [None, 1])
+def test_lds_heavy_rows_with_phase_bounds_on_two_streams_bit_exact(dev, tune, split):
+    """With phase bounds in the view, the rows after the heavy ones run on the
+    phased gather kernel on the library's second stream, concurrently with the
+    heavy rows' LDS launch (split=None, the default), or as the one-grid LDS
+    split (split=1): the oracle's bits either way, for several split points,
+    with and without bias, and again on later calls (the side stream reused)."""
+    tune(spmm_kernel=1)
+    if split is not None:
+        tune(spmm_split=split)
+    print(f"[heavy two streams split={split}]", flush=True)
+    c = oracle.zipf_rows(3000, 700, 0.03, 1.1, seed=91, sigma=0.5)
+    rng = np.random.default_rng(91)
+    N = 520
+    X_np = rng.standard_normal((700, N)).astype(np.float32)
+    b_np = rng.standard_normal(3000).astype(np.float32)
+    W = from_oracle(c, dev)
+    v = W._view_phased(3)
+    assert v.row_order is not None and v.n_heavy_rows > 0 and v.n_phases == 3
+    X, b = _t(X_np, dev), _t(b_np, dev)
+    want = oracle.spmm(c, X_np)
+    for rep in range(2):
+        for T in (1, v.n_heavy_rows, 2999):
+            view = _with_fields(v, n_heavy_rows=T)
+            Y = torch.full((3000, N), float("nan"), device=dev)
+            _lib.spmm(view, X, Y)
+            torch.cuda.synchronize()
+            assert_bits_equal(Y.cpu().numpy(), want, f"Y (T={T}, call {rep})")
+            _lib.spmm(view, X, Y, b)
+            torch.cuda.synchronize()
+            assert_bits_equal(Y.cpu().numpy(), want + b_np[:, None], f"Y+bias (T={T}, call {rep})")
+
+
 def test_transpose_builders_hint_the_heavy_row_count(dev):
     """A transpose's heavy-row count is counted on the device with its capacity
     (no host read of its rows), by both builders; it equals the host rule on
