@@ -88,7 +88,9 @@ typedef struct slk_csr {
      * slk_seg_list_build: segment e covers slots seg_start[e] ..
      * seg_start[e] + seg_count[e] - 1 of row seg_row[e]. Segments go block by
      * block, then by row; each block's list is padded with empty segments
-     * (count 0) to a multiple of SLK_SEG_GROUP, and *seg_groups (a device
+     * (count 0) to a multiple of SLK_SEG_GROUP, each such group of segments
+     * is then stably sorted by count, largest first (so a wave of slk_sddmm
+     * takes segments of close counts), and *seg_groups (a device
      * int32) holds the number of such groups in use; n_seg is the arrays'
      * length. slk_sddmm then gives each group of segments one workgroup that
      * stages the block's X rows in LDS and keeps each segment's dY row in

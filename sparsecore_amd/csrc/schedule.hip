@@ -18,6 +18,10 @@
 //               never straddles two blocks); the number of groups in use is
 //               written to device memory.
 //   S4 scatter  one thread per (row, block): writes its run's segments.
+//   S5 order    one workgroup per group: a stable sort of the group's
+//               segments by count, largest first, so the 16 segments a
+//               wave of slk_sddmm takes have close counts and the wave skips
+//               the steps none of them has (C5 at 95%: 31% fewer steps).
 //
 // The padding is left as empty segments by a fill pass that runs first. The
 // list's length is an upper bound the host can compute without a device read.
@@ -132,6 +136,30 @@ __global__ __launch_bounds__(kSchedThreads) void sg_scatter_kernel(
         seg_row[dst + k] = static_cast<int32_t>(r);
         seg_count[dst + k] = min(S, e - s);
     }
+}
+
+// S5: each group of SLK_SEG_GROUP segments in use, stably sorted by count,
+// largest first (padding, count 0, last). A segment's rank is the number of
+// segments with a larger count plus those before it with the same count.
+__global__ __launch_bounds__(SLK_SEG_GROUP) void sg_order_kernel(
+    const int32_t* __restrict__ groups, int32_t* __restrict__ seg_start,
+    int32_t* __restrict__ seg_row, int32_t* __restrict__ seg_count) {
+    if (static_cast<int64_t>(blockIdx.x) >= groups[0]) return;  // block-uniform
+    __shared__ int32_t cn[SLK_SEG_GROUP];
+    const int64_t e = static_cast<int64_t>(blockIdx.x) * SLK_SEG_GROUP + threadIdx.x;
+    const int32_t s = seg_start[e], r = seg_row[e], c = seg_count[e];
+    cn[threadIdx.x] = c;
+    __syncthreads();
+    int rank = 0;
+    for (int j = 0; j < SLK_SEG_GROUP; ++j) {
+        const int32_t o = cn[j];
+        rank += (o > c || (o == c && j < static_cast<int>(threadIdx.x))) ? 1 : 0;
+    }
+    __syncthreads();  // every entry of the group is read before any is written
+    const int64_t d = static_cast<int64_t>(blockIdx.x) * SLK_SEG_GROUP + rank;
+    seg_start[d] = s;
+    seg_row[d] = r;
+    seg_count[d] = c;
 }
 
 // Every entry an empty segment (row 0, slot 0, count 0): the padding.
@@ -251,7 +279,11 @@ extern "C" int slk_seg_list_build(const slk_csr* W, int64_t block_cols, int64_t 
         hipLaunchKernelGGL(sg_scatter_kernel<8>, sgrid, dim3(kSchedThreads), 0, st, M, p.nb, lo,
                            off, start, seg_start, seg_row, seg_count);
     }
-    return check_launch("seg_list/scatter");
+    if (int rc = check_launch("seg_list/scatter")) return rc;
+    // groups past the ones in use (read on the device) exit at once
+    hipLaunchKernelGGL(sg_order_kernel, dim3(static_cast<unsigned>(n_seg / SLK_SEG_GROUP)),
+                       dim3(SLK_SEG_GROUP), 0, st, seg_groups, seg_start, seg_row, seg_count);
+    return check_launch("seg_list/order");
 }
 
 extern "C" int slk_phase_bounds_build(const slk_csr* W, int64_t n_phases, int32_t* phase_lo,

@@ -487,6 +487,13 @@ __attribute__((amdgpu_waves_per_eu((LEAN && !(C == 128 && GS == 64)) ? 4 : 1))) 
         for (int r = 0; r < 4; ++r) byres[r] |= (k < cnt && (c & 3) == r) ? (1u << k) : 0u;
     }
     static_assert(S <= 8, "slot of each step packed in 4 bits");
+    // Steps at or past every quad's count are empty in the whole wave: the
+    // list sorts each group's segments by count, so a wave's counts are close
+    // and it skips those steps two at a time.
+    int kmax = cnt;
+#pragma unroll
+    for (int o = 32; o >= 4; o >>= 1) kmax = max(kmax, __shfl_xor(kmax, o));
+    kmax = __builtin_amdgcn_readfirstlane(kmax);
     uint32_t avail = (1u << cnt) - 1u;  // cnt <= S
     int32_t xo[S];
     uint32_t slots = 0xFFFFFFFFu;  // 4 bits per step: its slot, 15 = none
@@ -563,14 +570,24 @@ __attribute__((amdgpu_waves_per_eu((LEAN && !(C == 128 && GS == 64)) ? 4 : 1))) 
         for (int t = 0; t < kSegWin / 16; ++t) {
 #pragma unroll
             for (int k0 = 0; k0 < S; k0 += SH) {
-                if (t < tn) {  // block-uniform
+                if (t < tn && k0 < kmax) {  // block-uniform, wave-uniform
                     f32x4 x[SH];
 #pragma unroll
-                    for (int k = 0; k < SH; ++k) x[k] = xs[xo[k0 + k] + 4 * t];
+                    for (int k = 0; k < SH; k += 2) {
+                        if (k == 0 || k0 + k < kmax) {
+                            x[k] = xs[xo[k0 + k] + 4 * t];
+                            x[k + 1] = xs[xo[k0 + k + 1] + 4 * t];
+                        }
+                    }
 #pragma unroll
-                    for (int k = 0; k < SH; ++k)
-                        fma4x(dcur[t], x[k], acc[k0 + k][0], acc[k0 + k][1], acc[k0 + k][2],
-                              acc[k0 + k][3]);
+                    for (int k = 0; k < SH; k += 2) {
+                        if (k == 0 || k0 + k < kmax) {
+                            fma4x(dcur[t], x[k], acc[k0 + k][0], acc[k0 + k][1],
+                                  acc[k0 + k][2], acc[k0 + k][3]);
+                            fma4x(dcur[t], x[k + 1], acc[k0 + k + 1][0], acc[k0 + k + 1][1],
+                                  acc[k0 + k + 1][2], acc[k0 + k + 1][3]);
+                        }
+                    }
                 }
                 // SH reads in flight at a time: hoisting the next reads ahead
                 // of these fmas would take 16 registers per read

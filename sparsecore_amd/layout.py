@@ -393,7 +393,7 @@ class PaddedCSR:
         """The view plus W's live slots cut into segments of at most seg_slots
         consecutive slots of one row inside one column block (slk_csr.seg_start):
         a schedule for slk_sddmm that keeps each segment's dY row in registers.
-        Built on the device (slk_seg_list_build, five launches, no host read)
+        Built on the device (slk_seg_list_build, six launches, no host read)
         once per topology. The cached view is rebuilt whenever the base view
         is (a values rebind, a row-schedule change), so it never carries a
         stale pointer; the segment arrays survive that as long as the

@@ -131,14 +131,16 @@ _SEG_WIDE_MIN_X_BYTES = 128 << 20
 
 def _seg_shape(W: PaddedCSR, K: int, N: int) -> tuple[int, int]:
     """(block columns, slots per segment) of the segment list: 128-column
-    blocks where X is far beyond the L2s and a row holds at least 4 live slots
-    per 128 columns (each dY row is then fetched once per 128 columns instead
-    of 64: 16384^2 at 95% 7.9 ms against 8.3), else 64 (at 99%: 2.33 ms
-    against 2.60); 8 slots per segment where a row holds at least 4 live slots
-    per block on average, else 4 (fewer empty slots in short runs)."""
+    blocks of 8-slot segments where X is far beyond the L2s (each dY row is
+    then fetched once per 128 columns instead of 64; waves skip the slots
+    their segments lack, so short runs cost little: 16384^2 at 95% 5.65 ms
+    against 6.53 for 64x8, at 99% 1.92 against 2.21 for 64x4); else 64
+    columns, with 8 slots per segment where a row holds at least 4 live slots
+    per block on average, else 4."""
+    if 4 * K * N >= _SEG_WIDE_MIN_X_BYTES:
+        return 128, 8
     density = W.nnz / max(1, W.nrows * W.ncols)
-    cols = 128 if 4 * K * N >= _SEG_WIDE_MIN_X_BYTES and density * 128 >= 4 else 64
-    return cols, 8 if density * cols >= 4 else 4
+    return 64, 8 if density * 64 >= 4 else 4
 
 
 def _sddmm_view(W: PaddedCSR, X: torch.Tensor):

@@ -691,7 +691,8 @@ def _expected_seg_list(c, block, S, n):
     """The padded segment list, restated in numpy: for every column block, for
     every row, the row's run of live slots in the block cut into segments of at
     most S slots; each block padded with empty segments (row 0, slot 0, count 0)
-    to a multiple of SEG_GROUP; n entries in all."""
+    to a multiple of SEG_GROUP; each group of SEG_GROUP segments then stably
+    sorted by count, largest first; n entries in all."""
     G = _lib.SEG_GROUP
     start, row, cnt = [], [], []
     nb = -(-c.ncols // block)
@@ -711,6 +712,10 @@ def _expected_seg_list(c, block, S, n):
         row += [0] * pad
         cnt += [0] * pad
     groups = len(start) // G
+    for g in range(groups):
+        sl = slice(g * G, (g + 1) * G)
+        order = np.argsort(-np.asarray(cnt[sl]), kind="stable")
+        start[sl], row[sl], cnt[sl] = ([v[sl][i] for i in order] for v in (start, row, cnt))
     assert len(start) <= n
     fill = n - len(start)
     as32 = lambda v: np.asarray(v + [0] * fill, dtype=np.int32)
@@ -728,8 +733,8 @@ def _expected_seg_list(c, block, S, n):
 def test_seg_list_build_matches_the_restatement(dev, S, shape, density, block):
     """slk_seg_list_build writes exactly the numpy restatement's padded list
     (segments block by block and row by row, runs cut every S slots, blocks
-    padded to whole groups, the rest of the arrays empty) and the group count,
-    for skewed rows including an empty one."""
+    padded to whole groups, each group sorted by count, the rest of the arrays
+    empty) and the group count, for skewed rows including an empty one."""
     M, K = shape
     print(f"[seg list] S={S} shape={shape} d={density} block={block}", flush=True)
     c = oracle.zipf_rows(M, K, density, 1.1, seed=M + K + block + S, sigma=0.5)
