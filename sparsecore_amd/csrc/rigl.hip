@@ -13,10 +13,10 @@
 //   approx   G' = dY·X^T on the matrix cores: every fp32 operand is split into
 //            bf16 parts, x = x_h + x_l + r (|r| <= 2^-16 |x|, round to nearest
 //            even), and G' = Σ x_h y_h + Σ (x_h y_l + x_l y_h), three
-//            bf16 MFMA products per term in fp32. The x_h y_h products are
-//            summed in chunks of 512 j on the matrix cores and the chunk sums
-//            added on the VALU, so no product passes through more than
-//            511 + N/512 additions.
+//            bf16 MFMA products per term in fp32. All three are summed in
+//            chunks of 128 j on the matrix cores and the chunk sums added on
+//            the VALU, so no product passes through more than 3·128 + N/128
+//            additions.
 //   bound    |G'[i,k] - G[i,k]| <= E[i,k] = c_N·n_i·n_k + δ, where
 //            c_N covers the reference's own rounding (γ_N), the matrix-core
 //            sums (≤ 2u per addition, to cover any rounding mode), the dropped
@@ -72,10 +72,11 @@ __global__ __launch_bounds__(256) void rigl_norm_kernel(const float* __restrict_
 
 // ───────────────────────────── approximate G ───────────────────────────────
 
-constexpr int kAT = 128;        // output tile edge (rows of dY, rows of X)
+constexpr int kATI = 128;       // output tile rows (rows of dY)
+constexpr int kATK = 128;       // output tile columns (rows of X)
 constexpr int kAJ = 32;         // j per LDS stage: two MFMA k-steps of 16
-constexpr int kAChunk = 512;    // j per matrix-core partial sum of x_h·y_h
-constexpr int kAThreads = 512;  // 8 waves, 4 x 2, each 32 x 64 of the tile
+constexpr int kAChunk = 128;    // j per matrix-core partial sum
+constexpr int kAThreads = 256;  // 4 waves, 2 x 2, each 64 x 64 of the tile
 constexpr int kAGroup = 8;      // tile rows per group of the tile order
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -131,133 +132,165 @@ __global__ __launch_bounds__(256) void rigl_split_kernel(const float* __restrict
 
 constexpr int kALdsRow = kAStageBytes + 16;  // bytes per staged row (padded)
 
-// G'[i0 + 128 tile] = x_h·y_h (fp32 matrix-core sums over chunks of kAChunk
-// j, the chunk sums added on the VALU) + (x_h·y_l + x_l·y_h) (one fp32
-// matrix-core sum), where x = dY row i, y = X row k. Eight waves in a 4 x 2
-// grid, each 32 rows x 64 columns (two 32 x 32 MFMA blocks): two waves per
-// SIMD, so one wave's LDS waits and barrier are covered by the other's MFMAs.
+// Stages per row: N rounded up to whole chunks (zero beyond N).
+inline int64_t approx_stages(int64_t N) { return ceil_div(N, kAChunk) * (kAChunk / kAJ); }
+
+// G'[i0 + 128, k0 + 128 tile] = Σ (x_h·y_h + x_h·y_l + x_l·y_h), where
+// x = dY row i, y = X row k: the three products of each term go to one fp32
+// matrix-core sum per chunk of kAChunk j, and the chunk sums are added on the
+// VALU, so no term passes through more than 3·kAChunk + N/kAChunk additions.
+// Four waves in a 2 x 2 grid, each 64 rows x 64 columns (2 x 2 blocks of
+// 32 x 32): per k-step of 16 j a wave reads four A and four B fragments from
+// LDS for twelve MFMAs (waves of 32 x 64 read six for six). Two workgroups
+// per CU (72 KiB of LDS each), so one workgroup's barrier waits are covered
+// by the other's MFMAs. (A 256 x 128 tile of eight such waves, one workgroup
+// per CU, measured the same: 6.75 against 6.70 ms at 16384^2 x 4096.)
 __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64_t K, int64_t nst,
                                                                 const uint16_t* __restrict__ PA,
                                                                 const uint16_t* __restrict__ PB,
                                                                 float* __restrict__ G) {
-    __shared__ __align__(16) unsigned char sA[2][kAT * kALdsRow];
-    __shared__ __align__(16) unsigned char sB[2][kAT * kALdsRow];
+    __shared__ __align__(16) unsigned char sA[2][kATI * kALdsRow];
+    __shared__ __align__(16) unsigned char sB[2][kATK * kALdsRow];
 
     // grouped, XCD-contiguous tile order: consecutive tiles share dY and X rows
-    const int64_t nTi = ceil_div(M, kAT), nTk = ceil_div(K, kAT);
+    const int64_t nTi = ceil_div(M, kATI), nTk = ceil_div(K, kATK);
     const int64_t L = xcd_logical_block(blockIdx.x, gridDim.x);
     const int64_t grp = L / (kAGroup * nTk);
     const int64_t first = grp * kAGroup;
     const int64_t gsize = nTi - first < kAGroup ? nTi - first : kAGroup;
     const int64_t in_grp = L - grp * kAGroup * nTk;
-    const int64_t i0 = (first + in_grp % gsize) * kAT;
-    const int64_t k0 = (in_grp / gsize) * kAT;
+    const int64_t i0 = (first + in_grp % gsize) * kATI;
+    const int64_t k0 = (in_grp / gsize) * kATK;
 
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wv = t >> 6;
-    const int wm = wv >> 1, wn = wv & 1;  // rows wm*32 .. +32, columns wn*64 .. +64
-    // staging: thread t moves bytes [32h, 32h + 32) of staged row t/4, of A and of B
-    constexpr int kPieces = kAStageBytes / 16 * kAT / kAThreads;  // 16-byte pieces per thread
-    static_assert(kPieces * kAThreads * 16 == kAT * kAStageBytes, "whole rows per stage");
-    const int lr = t >> 2, lh = (t & 3) * (16 * kPieces);
+    const int wm = wv >> 1, wn = wv & 1;  // rows wm*64 .. +64, columns wn*64 .. +64
+    // staging: thread t moves bytes [64(t&1), +64) of staged row t/2 of A and of B
+    constexpr int kPA = kAStageBytes / 16 * kATI / kAThreads;  // 16-byte pieces per thread
+    constexpr int kPB = kAStageBytes / 16 * kATK / kAThreads;
+    static_assert(kPA == 4 && kPB == 4, "staging map below");
+    const int lra = t >> 1, lha = (t & 1) * 64;
+    const int lrb = t >> 1, lhb = (t & 1) * 64;
     const unsigned char* ga = reinterpret_cast<const unsigned char*>(
-        PA + (i0 + lr < M ? i0 + lr : M - 1) * nst * (2 * kAJ)) + lh;
+        PA + (i0 + lra < M ? i0 + lra : M - 1) * nst * (2 * kAJ)) + lha;
     const unsigned char* gb = reinterpret_cast<const unsigned char*>(
-        PB + (k0 + lr < K ? k0 + lr : K - 1) * nst * (2 * kAJ)) + lh;
+        PB + (k0 + lrb < K ? k0 + lrb : K - 1) * nst * (2 * kAJ)) + lhb;
 
-    f32x16 cm[2], mm[2], cx[2];  // [column block]
+    f32x16 cs[2][2], tot[2][2];  // [row block][column block]: chunk sums, totals
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) cm[b][r] = mm[b][r] = cx[b][r] = 0.0f;
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) tot[a][b][r] = 0.0f;
 
     // Pipeline: stage st+2's loads are issued while stage st is computed from
     // LDS buffer st&1; stage st+1 (loaded during stage st-1) is written into
-    // the other buffer after this stage's MFMAs; one barrier per stage.
-    f32x4 ra[2][kPieces], rb[2][kPieces];
+    // the other buffer after this stage's MFMAs; one barrier per stage. nst is
+    // a whole number of chunks (the split pads with zero stages), so every
+    // load and LDS write is unconditional: past the end a stage reloads the
+    // last one, unused. (A conditional load would leave the wait before the
+    // LDS write covering the newer loads as well.)
+    f32x4 ra[2][kPA], rb[2][kPB];
     auto fetch = [&](int reg, int64_t st) {
         const unsigned char* pa = ga + st * kAStageBytes;
         const unsigned char* pb = gb + st * kAStageBytes;
 #pragma unroll
-        for (int q = 0; q < kPieces; ++q) {
-            ra[reg][q] = *reinterpret_cast<const f32x4*>(pa + 16 * q);
-            rb[reg][q] = *reinterpret_cast<const f32x4*>(pb + 16 * q);
-        }
+        for (int q = 0; q < kPA; ++q) ra[reg][q] = *reinterpret_cast<const f32x4*>(pa + 16 * q);
+#pragma unroll
+        for (int q = 0; q < kPB; ++q) rb[reg][q] = *reinterpret_cast<const f32x4*>(pb + 16 * q);
     };
-    const int st_off = lr * kALdsRow + lh;
+    const int sta = lra * kALdsRow + lha, stb = lrb * kALdsRow + lhb;
     auto stage_to_lds = [&](int reg, int b) {
 #pragma unroll
-        for (int q = 0; q < kPieces; ++q) {
-            *reinterpret_cast<f32x4*>(&sA[b][st_off + 16 * q]) = ra[reg][q];
-            *reinterpret_cast<f32x4*>(&sB[b][st_off + 16 * q]) = rb[reg][q];
-        }
+        for (int q = 0; q < kPA; ++q)
+            *reinterpret_cast<f32x4*>(&sA[b][sta + 16 * q]) = ra[reg][q];
+#pragma unroll
+        for (int q = 0; q < kPB; ++q)
+            *reinterpret_cast<f32x4*>(&sB[b][stb + 16 * q]) = rb[reg][q];
     };
-    if (nst > 0) fetch(0, 0);
-    if (nst > 1) fetch(1, 1);
-    if (nst > 0) stage_to_lds(0, 0);
-    __syncthreads();
     const int half = 16 * (lane >> 5);
-    const int ra0 = (wm * 32 + (lane & 31)) * kALdsRow + half;
+    const int ra0 = (wm * 64 + (lane & 31)) * kALdsRow + half;
     const int rb0 = (wn * 64 + (lane & 31)) * kALdsRow + half;
     // stage st lives in register set st & 1 and LDS buffer st & 1; the two
-    // parities are unrolled so both indexes are compile-time constants
-    auto stage = [&](auto R, int64_t st) {
+    // parities are unrolled so both indexes are compile-time constants. The
+    // first stage of a chunk starts its sums from zero.
+    auto stage = [&](auto R, auto F, int64_t st) {
         constexpr int reg = decltype(R)::value;
-        if (st + 2 < nst) fetch(reg, st + 2);  // register set of stage st: already in LDS
+        constexpr bool first = decltype(F)::value;
+        fetch(reg, st + 2 < nst ? st + 2 : nst - 1);  // set of stage st: already in LDS
         const unsigned char* la = sA[reg];
         const unsigned char* lb = sB[reg];
 #pragma unroll
         for (int s = 0; s < kAJ / 16; ++s) {
-            bf16x8 af[2], bf[2][2];  // [high, low], [block][high, low]
+            bf16x8 af[2][2], bf[2][2];  // [block][high, low]
 #pragma unroll
             for (int p = 0; p < 2; ++p) {
                 const int o = p * (kAStageBytes / 2) + 32 * s;
-                af[p] = *reinterpret_cast<const bf16x8*>(la + ra0 + o);
 #pragma unroll
-                for (int b = 0; b < 2; ++b)
+                for (int b = 0; b < 2; ++b) {
+                    af[b][p] = *reinterpret_cast<const bf16x8*>(la + ra0 + b * 32 * kALdsRow + o);
                     bf[b][p] = *reinterpret_cast<const bf16x8*>(lb + rb0 + b * 32 * kALdsRow + o);
+                }
             }
 #pragma unroll
-            for (int b = 0; b < 2; ++b)
-                cm[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0], bf[b][0], cm[b], 0, 0, 0);
+            for (int a = 0; a < 2; ++a)
 #pragma unroll
-            for (int b = 0; b < 2; ++b)
-                cx[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0], bf[b][1], cx[b], 0, 0, 0);
+                for (int b = 0; b < 2; ++b)
+                    cs[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        af[a][0], bf[b][0], (first && s == 0) ? f32x16{} : cs[a][b], 0, 0, 0);
 #pragma unroll
-            for (int b = 0; b < 2; ++b)
-                cx[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[1], bf[b][0], cx[b], 0, 0, 0);
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+                    cs[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a][0], bf[b][1], cs[a][b], 0, 0, 0);
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+                    cs[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a][1], bf[b][0], cs[a][b], 0, 0, 0);
         }
         // stage st+1 into the other buffer (its last readers, stage st-1,
         // passed the previous barrier)
-        if (st + 1 < nst) stage_to_lds(reg ^ 1, reg ^ 1);
+        stage_to_lds(reg ^ 1, reg ^ 1);
         __syncthreads();
     };
-    static_assert((kAChunk / kAJ) % 2 == 0, "chunks hold whole stage pairs");
-    for (int64_t c0 = 0; c0 < nst; c0 += kAChunk / kAJ) {
-        const int64_t c1 = c0 + kAChunk / kAJ < nst ? c0 + kAChunk / kAJ : nst;
-        for (int64_t st = c0; st < c1; st += 2) {
-            stage(std::integral_constant<int, 0>{}, st);
-            if (st + 1 < c1) stage(std::integral_constant<int, 1>{}, st + 1);
+    static_assert(kAChunk / kAJ == 4, "four stages per chunk below");
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using T = std::true_type;
+    using F = std::false_type;
+    if (nst > 0) {  // workgroup-uniform
+        fetch(0, 0);
+        fetch(1, 1);
+        stage_to_lds(0, 0);
+        __syncthreads();
+        for (int64_t c0 = 0; c0 < nst; c0 += kAChunk / kAJ) {
+            stage(I0{}, T{}, c0);
+            stage(I1{}, F{}, c0 + 1);
+            stage(I0{}, F{}, c0 + 2);
+            stage(I1{}, F{}, c0 + 3);
+            // a chunk done: add its sums on the VALU
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) tot[a][b][r] = tot[a][b][r] + cs[a][b][r];
         }
-        // a chunk of x_h·y_h done: add its sums on the VALU
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                mm[b][r] = mm[b][r] + cm[b][r];
-                cm[b][r] = 0.0f;
-            }
     }
     // lane l, register 4g + q of a 32x32 block: row 8g + 4(l/32) + q, column l % 32
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
         const int64_t col = k0 + wn * 64 + b * 32 + (lane & 31);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t row = i0 + wm * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (row < M && col < K) G[row * K + col] = mm[b][r] + cx[b][r];
-        }
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = i0 + wm * 64 + a * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (row < M && col < K) G[row * K + col] = tot[a][b][r];
+            }
     }
 }
 
@@ -876,21 +909,22 @@ __global__ __launch_bounds__(kRowThreads) void rigl_finish_kernel(
 
 __global__ void rigl_clear_kernel(unsigned long long* __restrict__ c) { *c = 0; }
 
-// c_N of the bound (see the file comment): the reference's γ_N, the matrix
-// cores' sums at <= 2u per addition (chunks of kAChunk, chunk sums added on
-// the VALU at <= u), the cross products' sums, the dropped parts, the final
-// add; times 1.01.
+// c_N of the bound (see the file comment): the reference's γ_N; the matrix
+// cores' chunk sums of 3·kAChunk terms at <= 2u per addition, and the N/kAChunk
+// chunk sums added on the VALU at <= u, over Σ|x_h y_h| + |x_h y_l| + |x_l y_h|
+// <= (1 + 2^-7 + 2^-14)·Σ|x y| (taken as 1 + 2^-6); the dropped parts; the
+// final add; times 1.01.
 double certified_c(int64_t N) {
     const double u = 0x1p-24;
     auto gam = [&](double n, double uu) { return n * uu / (1.0 - n * uu); };
     const double n = static_cast<double>(N > 0 ? N : 1);
     const double chunks = ceil(n / kAChunk) + 1.0;
     const double g_ref = gam(n, u);
-    const double g_main = (gam(kAChunk, 2 * u) + gam(chunks, u)) * (1.0 + 0x1p-7);
-    const double g_cross = gam(2 * n, 2 * u) * 2 * 0x1p-8 * (1.0 + 0x1p-7);
+    const double g_chunk = gam(3.0 * kAChunk, 2 * u);
+    const double g_mc = (g_chunk + gam(chunks, u) * (1.0 + g_chunk)) * (1.0 + 0x1p-6);
     const double dropped = 3.1 * 0x1p-16;
     const double fin = 1.01 * u;
-    return (g_ref + g_main + g_cross + dropped + fin) * 1.01;
+    return (g_ref + g_mc + dropped + fin) * 1.01;
 }
 
 }  // namespace
@@ -918,7 +952,7 @@ extern "C" int slk_rigl_norms(const float* dY, int64_t M, const float* X, int64_
 
 extern "C" int64_t slk_dense_grad_approx_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     if (M < 0 || K < 0 || N < 0) return 0;
-    return (M + K) * slk::ceil_div(N, slk::kAJ) * slk::kAStageBytes;
+    return (M + K) * slk::approx_stages(N) * slk::kAStageBytes;
 }
 
 extern "C" int slk_dense_grad_approx(const float* dY, const float* X, int64_t M, int64_t K,
@@ -931,12 +965,12 @@ extern "C" int slk_dense_grad_approx(const float* dY, const float* X, int64_t M,
     if (M == 0 || K == 0) return SLK_OK;
     if (G == nullptr || (N > 0 && (dY == nullptr || X == nullptr)))
         return fail(SLK_EINVAL, "dense_grad_approx: NULL pointer");
-    const int64_t nst = ceil_div(N, kAJ);
+    const int64_t nst = approx_stages(N);
     const int64_t need = (M + K) * nst * kAStageBytes;
     if (need > 0 && (workspace == nullptr || workspace_bytes < need))
         return fail(SLK_EINVAL, "dense_grad_approx: workspace smaller than "
                                 "slk_dense_grad_approx_workspace_bytes");
-    const int64_t tiles = ceil_div(M, kAT) * ceil_div(K, kAT);
+    const int64_t tiles = ceil_div(M, kATI) * ceil_div(K, kATK);
     if (tiles > INT32_MAX || ceil_div((M + K) * nst * (kAJ / 4), 256) > INT32_MAX)
         return fail(SLK_EINVAL, "dense_grad_approx: problem too large");
     hipStream_t st = as_stream(stream);
