@@ -29,11 +29,12 @@
 //            largest lower / upper. A column with lower > T_hi is certainly
 //            grown (|G| > T_hi >= the exact n_grow-th largest |G|), one with
 //            upper < T_lo certainly not; the rest are undecided. Counts them.
-//   finish   per row: lists the undecided columns (ascending), computes their
-//            exact G with the reference's arithmetic (dY_i staged in LDS, X_k
-//            streamed), takes the n_grow - (certain) smallest exact keys
-//            ~bits(|G|) among them (ties to the lower column), and rewrites
-//            the row exactly as the exact drop/grow kernel does.
+//   finish   per row, the undecided columns listed (ascending); over all
+//            undecided (row, column) pairs, their exact G with the reference's
+//            arithmetic (a wave per 64 pairs, both rows streamed through LDS);
+//            per row, the n_grow - (certain) smallest exact keys ~bits(|G|)
+//            among them (ties to the lower column) grown, and the row
+//            rewritten exactly as the exact drop/grow kernel does.
 //
 // A row whose norms are not finite or too large (n_i·n_k beyond 2^120, where
 // G could overflow) is an exact row: every empty column is undecided, and NaN
@@ -794,22 +795,207 @@ __device__ __forceinline__ float exact_dot(const float* y, const float* __restri
     return acc;
 }
 
-template <bool V4, bool VG>
-__global__ __launch_bounds__(kRowThreads) void rigl_finish_kernel(
-    int64_t K, int64_t Kw, int64_t N, const int32_t* __restrict__ row_start,
-    int32_t* __restrict__ row_nnz, float* __restrict__ values, int32_t* __restrict__ cols,
-    const float* __restrict__ thr_ptr, const float* __restrict__ Gp, int64_t ldg,
-    const float* __restrict__ nrm_c, const RowInfo* __restrict__ info,
-    const int64_t* __restrict__ amb_off,
-    int32_t* __restrict__ amb_col, uint32_t* __restrict__ amb_key,
-    const float* __restrict__ dY, const float* __restrict__ X,
+// Lists the set columns of the bitmap bm (Kw words) in ascending order:
+// emit(position, column) for every one, positions from 0. One workgroup.
+template <class Emit>
+__device__ void list_bitmap(const uint32_t* bm, int64_t Kw, int64_t* tmp, Emit emit) {
+    const int t = threadIdx.x;
+    const int64_t per = ceil_div(Kw, kRowThreads);
+    const int64_t w0 = t * per < Kw ? t * per : Kw, w1 = w0 + per < Kw ? w0 + per : Kw;
+    int64_t cnt = 0;
+    for (int64_t w = w0; w < w1; ++w) cnt += __popc(bm[w]);
+    int64_t pos = block_inclusive_scan(cnt, tmp) - cnt;
+    for (int64_t w = w0; w < w1; ++w) {
+        uint32_t bits = bm[w];
+        while (bits) {
+            const int b = __builtin_ctz(bits);
+            bits &= bits - 1;
+            emit(pos, w * 32 + b);
+            ++pos;
+        }
+    }
+}
+
+// Finish, step 1, per row: the undecided columns in ascending order into
+// amb_col[amb_off[i] ..] with the row index in amb_key (the exact step turns
+// it into the key), and the columns certainly grown into the row's own
+// staging slots stage_col[row_start ..] (there are n_in < row_nnz of them;
+// the select step reads them before it stages the new row there).
+template <bool VG>
+__global__ __launch_bounds__(kRowThreads) void rigl_list_kernel(
+    int64_t K, int64_t Kw, const int32_t* __restrict__ row_start,
+    const int32_t* __restrict__ row_nnz, const float* __restrict__ values,
+    const int32_t* __restrict__ cols, const float* __restrict__ thr_ptr,
+    const float* __restrict__ Gp, int64_t ldg, const float* __restrict__ nrm_c,
+    const RowInfo* __restrict__ info, const int64_t* __restrict__ amb_off,
+    int32_t* __restrict__ amb_col, uint32_t* __restrict__ amb_key, int64_t amb_cap,
+    int32_t* __restrict__ stage_col) {
+    extern __shared__ uint32_t lds[];
+    uint32_t* keep = lds;
+    uint32_t* grow = lds + Kw;
+    uint32_t* ambm = lds + 2 * Kw;
+    __shared__ int64_t tmp[kRowThreads];
+    __shared__ unsigned long long s_best;
+
+    const int64_t i = blockIdx.x;
+    const int t = threadIdx.x;
+    const RowInfo ri = info[i];
+    if (ri.flags & kRowKeep) return;
+    const int32_t n_live = row_nnz[i];
+    const int32_t start = row_start[i];
+    for (int64_t w = t; w < Kw; w += kRowThreads) keep[w] = grow[w] = ambm[w] = 0;
+    __syncthreads();
+    mark_survivors(values, cols, start, n_live, thr_ptr[0], keep, tmp, &s_best);
+    const int64_t off = amb_off[i];
+    const int64_t n_amb = amb_off[i + 1] - off;
+    if (ri.flags & kRowExact) {
+        for (int64_t c = t; c < K; c += kRowThreads)
+            if (!bit_of(keep, c)) atomicOr(&ambm[c >> 5], 1u << (c & 31));
+    } else {
+        for_each_col<VG>(Gp + i * ldg, nrm_c, K, [&](int64_t c, float g, float nk) {
+            if (bit_of(keep, c)) return;
+            const float a = fabsf(g);
+            const float e = col_err(ri.cni, nk, ri.delta);
+            if (dn_(a - e) > ri.t_in) atomicOr(&grow[c >> 5], 1u << (c & 31));
+            else if (!(up_(a + e) < ri.t_out)) atomicOr(&ambm[c >> 5], 1u << (c & 31));
+        });
+    }
+    __syncthreads();
+    // (the count pass classified the same columns the same way, so every
+    // position is below n_amb and n_in; the guards keep a mismatch inside the row)
+    list_bitmap(ambm, Kw, tmp, [&](int64_t pos, int64_t c) {
+        if (pos < n_amb && off + pos < amb_cap) {
+            amb_col[off + pos] = static_cast<int32_t>(c);
+            amb_key[off + pos] = static_cast<uint32_t>(i);
+        }
+    });
+    __syncthreads();
+    const int64_t n_in = (ri.flags & kRowExact) ? 0 : ri.n_in;
+    list_bitmap(grow, Kw, tmp, [&](int64_t pos, int64_t c) {
+        if (pos < n_in && pos < n_live) stage_col[start + pos] = static_cast<int32_t>(c);
+    });
+}
+
+// Finish, step 2, over all P undecided (row, column) pairs: the exact G with
+// the reference's arithmetic (exact_dot), as the key ~bits(|G|) (0 for NaN).
+// amb_key holds the row on entry. A wave takes 64 consecutive pairs, one per
+// lane; the dY and X rows of its pairs are streamed through the wave's own
+// LDS rows in chunks of kExJ floats, eight lanes loading one 128-byte piece
+// of a row (so a pair's 16 KB X row is 128 coalesced loads of the wave, two
+// chunks ahead in registers, instead of one thread's dependent stream). Each
+// lane then runs its pair's sum over the chunk from LDS. N % 4 == 0 and
+// 16-byte aligned rows; the four waves of a workgroup run in step (barriers).
+constexpr int kExJ = 32;               // floats per chunk
+constexpr int kExRow = kExJ / 4 + 1;   // 16-byte pieces per LDS row (one padding)
+constexpr int kExThreads = 256;
+__global__ __launch_bounds__(kExThreads) void rigl_exact_kernel(
+    const int64_t* __restrict__ total, int64_t cap, int64_t M, int64_t K, int64_t N,
+    const int32_t* __restrict__ amb_col, uint32_t* __restrict__ amb_key,
+    const float* __restrict__ dY, const float* __restrict__ X) {
+    __shared__ f32x4 xs[kExThreads / kWave][kWave][kExRow];
+    __shared__ f32x4 ys[kExThreads / kWave][kWave][kExRow];
+    const int64_t P = *total < cap ? *total : cap;  // the grid covers the capacity
+    if (static_cast<int64_t>(blockIdx.x) * kExThreads >= P) return;  // workgroup-uniform
+    const int w = threadIdx.x >> 6;
+    const int l = threadIdx.x & 63;
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * kExThreads + threadIdx.x;
+    const int64_t pc = p < P ? p : P - 1;
+    // (rows and columns clamped into the matrices: a list that disagreed
+    // with the count would give wrong keys, never an out-of-bounds read)
+    const int32_t my_col = min(max(amb_col[pc], 0), static_cast<int32_t>(K - 1));
+    const int32_t my_row = static_cast<int32_t>(min<uint32_t>(amb_key[pc], static_cast<uint32_t>(M - 1)));
+    // staging: load u of lane l is piece l % 8 of pair 8u + l / 8's rows
+    constexpr int kU = kWave * (kExJ / 4) / kWave;  // loads per lane per chunk and matrix
+    static_assert(kU == 8, "eight lanes per 128-byte piece of a row");
+    const int pe = l & 7;
+    const float* xsrc[kU];
+    const float* ysrc[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+        const int src = 8 * u + (l >> 3);
+        xsrc[u] = X + static_cast<int64_t>(__shfl(my_col, src)) * N;
+        ysrc[u] = dY + static_cast<int64_t>(__shfl(my_row, src)) * N;
+    }
+    const int64_t nch = ceil_div(N, kExJ);
+    f32x4 rx[2][kU], ry[2][kU];
+    // chunks past the last reload the last one, and a piece past N loads
+    // the row's last piece: every load is in bounds and unconditional
+    auto load = [&](int set, int64_t ch) {
+        const int64_t c = ch < nch ? ch : nch - 1;
+        const int64_t j0 = c * kExJ + 4 * pe;
+        const int64_t j = j0 + 4 <= N ? j0 : N - 4;
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            rx[set][u] = *reinterpret_cast<const f32x4*>(xsrc[u] + j);
+            ry[set][u] = *reinterpret_cast<const f32x4*>(ysrc[u] + j);
+        }
+    };
+    float acc = 0.0f;
+    auto chunk = [&](auto S, int64_t ch) {
+        constexpr int set = decltype(S)::value;
+        __syncthreads();  // every lane has read the previous chunk
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            xs[w][8 * u + (l >> 3)][pe] = rx[set][u];
+            ys[w][8 * u + (l >> 3)][pe] = ry[set][u];
+        }
+        __syncthreads();
+        load(set, ch + 2);
+        const int64_t left = N - ch * kExJ;  // workgroup-uniform
+        const int terms = left <= 0 ? 0 : left < kExJ ? static_cast<int>(left) : kExJ;
+#pragma unroll
+        for (int q = 0; q < kExJ / 4; ++q) {
+            if (4 * q < terms) {
+                const f32x4 a = ys[w][l][q];
+                const f32x4 b = xs[w][l][q];
+                acc = acc + a[0] * b[0];
+                acc = acc + a[1] * b[1];
+                acc = acc + a[2] * b[2];
+                acc = acc + a[3] * b[3];
+            }
+        }
+    };
+    load(0, 0);
+    load(1, 1);
+    for (int64_t ch = 0; ch < nch; ch += 2) {
+        chunk(std::integral_constant<int, 0>{}, ch);
+        chunk(std::integral_constant<int, 1>{}, ch + 1);
+    }
+    if (p < P) {
+        const float a = fabsf(acc);
+        amb_key[p] = a == a ? desc_key(a) : 0u;
+    }
+}
+
+// The same for any N and alignment: one thread per pair, from global memory.
+__global__ __launch_bounds__(256) void rigl_exact_simple_kernel(
+    const int64_t* __restrict__ total, int64_t cap, int64_t M, int64_t K, int64_t N,
+    const int32_t* __restrict__ amb_col, uint32_t* __restrict__ amb_key,
+    const float* __restrict__ dY, const float* __restrict__ X) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (p >= *total || p >= cap) return;
+    const int64_t c = min(max(amb_col[p], 0), static_cast<int32_t>(K - 1));
+    const int64_t r = min<uint32_t>(amb_key[p], static_cast<uint32_t>(M - 1));
+    const float a = fabsf(exact_dot<false>(dY + r * N, X + c * N, N));
+    amb_key[p] = a == a ? desc_key(a) : 0u;
+}
+
+// Finish, step 3, per row: survivors, the certain grows (from the row's
+// staging slots), the need = n_grow - n_in smallest exact keys among the
+// undecided (ties to the lower column; for an exact row n_grow counts only
+// non-NaN columns), and the row rewritten as the exact drop/grow kernel
+// writes it.
+__global__ __launch_bounds__(kRowThreads) void rigl_select_kernel(
+    int64_t Kw, const int32_t* __restrict__ row_start, int32_t* __restrict__ row_nnz,
+    float* __restrict__ values, int32_t* __restrict__ cols, const float* __restrict__ thr_ptr,
+    const RowInfo* __restrict__ info, const int64_t* __restrict__ amb_off,
+    const int32_t* __restrict__ amb_col, const uint32_t* __restrict__ amb_key, int64_t amb_cap,
     int32_t* __restrict__ stage_col, float* __restrict__ stage_val,
     unsigned long long* __restrict__ removed) {
     extern __shared__ uint32_t lds[];
     uint32_t* keep = lds;
     uint32_t* grow = lds + Kw;
     uint32_t* wpre = lds + 2 * Kw;
-    float* ys = reinterpret_cast<float*>(lds + ((3 * Kw + 3) & ~int64_t{3}));  // 16-byte aligned
     __shared__ int64_t tmp[kRowThreads];
     __shared__ uint32_t hist[256];
     __shared__ uint32_t s_digit;
@@ -828,67 +1014,16 @@ __global__ __launch_bounds__(kRowThreads) void rigl_finish_kernel(
                                           &s_best);
     const int64_t n_drop = n_live - n_keep;
     const bool exact_row = (ri.flags & kRowExact) != 0;
-    const float* g_row = Gp + i * ldg;
+    const int64_t n_in = exact_row ? 0 : ri.n_in;
+    for (int64_t e = t; e < n_in && e < n_live; e += kRowThreads) {
+        const int32_t c = stage_col[start + e];
+        atomicOr(&grow[c >> 5], 1u << (c & 31));
+    }
+    __syncthreads();
     const int64_t off = amb_off[i];
-    const int64_t n_amb = amb_off[i + 1] - off;
-
-    // undecided columns into a bitmap (in wpre, free until the write-back),
-    // certainly grown ones straight into `grow`; then listed in ascending
-    // order with one scan over the bitmap's words
-    uint32_t* ambm = wpre;
-    for (int64_t w = t; w < Kw; w += kRowThreads) ambm[w] = 0;
-    __syncthreads();
-    if (exact_row) {
-        for (int64_t c = t; c < K; c += kRowThreads)
-            if (!bit_of(keep, c)) atomicOr(&ambm[c >> 5], 1u << (c & 31));
-    } else {
-        for_each_col<VG>(g_row, nrm_c, K, [&](int64_t c, float g, float nk) {
-            if (bit_of(keep, c)) return;
-            const float a = fabsf(g);
-            const float e = col_err(ri.cni, nk, ri.delta);
-            if (dn_(a - e) > ri.t_in) atomicOr(&grow[c >> 5], 1u << (c & 31));
-            else if (!(up_(a + e) < ri.t_out)) atomicOr(&ambm[c >> 5], 1u << (c & 31));
-        });
-    }
-    __syncthreads();
-    {
-        const int64_t per = ceil_div(Kw, kRowThreads);
-        const int64_t w0 = t * per < Kw ? t * per : Kw, w1 = w0 + per < Kw ? w0 + per : Kw;
-        int64_t cnt = 0;
-        for (int64_t w = w0; w < w1; ++w) cnt += __popc(ambm[w]);
-        int64_t pos = block_inclusive_scan(cnt, tmp) - cnt;
-        // (the count pass classified the same columns the same way, so every
-        // position is below n_amb; the guard keeps a mismatch inside the row)
-        for (int64_t w = w0; w < w1; ++w) {
-            uint32_t bits = ambm[w];
-            while (bits) {
-                const int b = __builtin_ctz(bits);
-                bits &= bits - 1;
-                if (pos < n_amb) amb_col[off + pos] = static_cast<int32_t>(w * 32 + b);
-                ++pos;
-            }
-        }
-    }
-    __syncthreads();
-
-    // exact keys of the undecided columns (0 marks a NaN |G|)
-    const float* y = dY + i * N;
-    const bool staged = V4 && N <= kStageMaxN;
-    if (staged) {
-        for (int64_t j = 4 * t; j < N; j += 4 * kRowThreads)
-            *reinterpret_cast<f32x4*>(ys + j) = *reinterpret_cast<const f32x4*>(y + j);
-        __syncthreads();
-    }
-    for (int64_t e = t; e < n_amb; e += kRowThreads) {
-        const int64_t c = amb_col[off + e];
-        const float g = staged ? exact_dot<true>(ys, X + c * N, N)
-                               : exact_dot<V4>(y, X + c * N, N);
-        const float a = fabsf(g);
-        amb_key[off + e] = a == a ? desc_key(a) : 0u;
-    }
-    __syncthreads();
-
-    int64_t n_grow = ri.n_grow, need = ri.n_grow - ri.n_in;
+    const int64_t n_amb = min(amb_off[i + 1], amb_cap) - min(off, amb_cap);  // (a workspace
+    // smaller than the contract asks leaves columns out, never reads past it)
+    int64_t n_grow = ri.n_grow, need = ri.n_grow - n_in;
     if (exact_row) {  // NaN columns are not growable
         int64_t ok = 0;
         for (int64_t e = t; e < n_amb; e += kRowThreads) ok += amb_key[off + e] != 0u;
@@ -1092,32 +1227,40 @@ extern "C" int slk_rigl_finish(const slk_csr* W, float* values, int32_t* col_ind
     int32_t* amb_col = static_cast<int32_t*>(amb_ws);
     uint32_t* amb_key = reinterpret_cast<uint32_t*>(amb_col + n_amb_max);
     const int64_t Kw = ceil_div(K, 32) > 0 ? ceil_div(K, 32) : 1;
-    const bool v4 = N % 4 == 0 && reinterpret_cast<uintptr_t>(dY) % 16 == 0 &&
-                    reinterpret_cast<uintptr_t>(X) % 16 == 0;
-    const int64_t words = ((3 * Kw + 3) & ~int64_t{3}) + (v4 && N <= kStageMaxN ? N : 0);
-    const size_t lds = static_cast<size_t>(words) * 4;
+    // the exact step's grid covers the workspace's capacity; the pairs in
+    // use are amb_off[M] (slk_rigl_count's total), read on the device
+    const int64_t P = n_amb_max;
+    const size_t lds = static_cast<size_t>(3 * Kw) * 4;
     int32_t* stage_col = static_cast<int32_t*>(workspace);
     float* stage_val = reinterpret_cast<float*>(stage_col + W->total_capacity);
     const bool vg = K % 4 == 0 && ldg % 4 == 0 && reinterpret_cast<uintptr_t>(G_approx) % 16 == 0 &&
                     reinterpret_cast<uintptr_t>(nrm_X) % 16 == 0;
     const dim3 grid(static_cast<unsigned>(M));
-#define SLK_FINISH_ARGS                                                                      \
-    K, Kw, N, W->row_start, row_nnz, values, col_indices, thr_dev, G_approx, ldg, nrm_X,     \
-        static_cast<const RowInfo*>(info), amb_off, amb_col, amb_key, dY, X, stage_col, stage_val, \
-        removed_u
-    if (v4 && vg) {
-        hipLaunchKernelGGL((rigl_finish_kernel<true, true>), grid, dim3(kRowThreads), lds, st,
-                           SLK_FINISH_ARGS);
-    } else if (v4) {
-        hipLaunchKernelGGL((rigl_finish_kernel<true, false>), grid, dim3(kRowThreads), lds, st,
-                           SLK_FINISH_ARGS);
-    } else if (vg) {
-        hipLaunchKernelGGL((rigl_finish_kernel<false, true>), grid, dim3(kRowThreads), lds, st,
-                           SLK_FINISH_ARGS);
+#define SLK_LIST_ARGS                                                                      \
+    K, Kw, W->row_start, row_nnz, values, col_indices, thr_dev, G_approx, ldg, nrm_X,       \
+        static_cast<const RowInfo*>(info), amb_off, amb_col, amb_key, n_amb_max, stage_col
+    if (vg) {
+        hipLaunchKernelGGL(rigl_list_kernel<true>, grid, dim3(kRowThreads), lds, st, SLK_LIST_ARGS);
     } else {
-        hipLaunchKernelGGL((rigl_finish_kernel<false, false>), grid, dim3(kRowThreads), lds, st,
-                           SLK_FINISH_ARGS);
+        hipLaunchKernelGGL(rigl_list_kernel<false>, grid, dim3(kRowThreads), lds, st, SLK_LIST_ARGS);
     }
-#undef SLK_FINISH_ARGS
+#undef SLK_LIST_ARGS
+    if (int rc = check_launch("rigl_finish/list")) return rc;
+    if (P > 0) {
+        if (ceil_div(P, 256) > INT32_MAX) return fail(SLK_EINVAL, "rigl_finish: too many undecided columns");
+        const bool v4 = N > 0 && N % 4 == 0 && reinterpret_cast<uintptr_t>(dY) % 16 == 0 &&
+                        reinterpret_cast<uintptr_t>(X) % 16 == 0;
+        if (v4) {
+            hipLaunchKernelGGL(rigl_exact_kernel, dim3(static_cast<unsigned>(ceil_div(P, kExThreads))),
+                               dim3(kExThreads), 0, st, amb_off + M, P, M, K, N, amb_col, amb_key, dY, X);
+        } else {  // any N (N = 0: every G is +0.0)
+            hipLaunchKernelGGL(rigl_exact_simple_kernel, dim3(static_cast<unsigned>(ceil_div(P, 256))),
+                               dim3(256), 0, st, amb_off + M, P, M, K, N, amb_col, amb_key, dY, X);
+        }
+        if (int rc = check_launch("rigl_finish/exact")) return rc;
+    }
+    hipLaunchKernelGGL(rigl_select_kernel, grid, dim3(kRowThreads), lds, st, Kw, W->row_start,
+                       row_nnz, values, col_indices, thr_dev, static_cast<const RowInfo*>(info),
+                       amb_off, amb_col, amb_key, n_amb_max, stage_col, stage_val, removed_u);
     return check_launch("rigl_finish");
 }
