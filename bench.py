@@ -652,6 +652,7 @@ class LayerWork:
         W = self.W
         M, K, N = self.M, self.K, self.N
         G = torch.empty(M, K, device=self.dev)
+        Gc = torch.empty(M, K, dtype=torch.uint8, device=self.dev)
         nd = torch.empty(M, device=self.dev)
         nx = torch.empty(K, device=self.dev)
         k = max(1, int(0.3 * W.nnz))
@@ -663,8 +664,8 @@ class LayerWork:
         return [
             ("rigl_norms", lambda: _lib.rigl_norms(self.dY, self.X, nd, nx),
              4 * (M * N + K * N + M + K), 0),
-            ("dense_grad_approx", lambda: _lib.dense_grad_approx(self.dY, self.X, G),
-             4 * (M * N + K * N + M * K), 2 * M * K * N),
+            ("dense_grad_approx", lambda: _lib.dense_grad_approx(self.dY, self.X, G, Gc),
+             4 * (M * N + K * N + M * K) + M * K, 2 * M * K * N),
             ("rigl_update", lambda: W._rigl_update(k, self.dY, self.X), 0, 0),
             ("transpose_rebuild", rebuild,
              8 * M + 8 * W.nnz + 16 * int(1.2 * W.nnz + K) + 12 * K, 0),

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define SLK_ABI_VERSION 10
+#define SLK_ABI_VERSION 11
 
 #if defined(__GNUC__)
 #define SLK_API __attribute__((visibility("default")))
@@ -340,9 +340,13 @@ SLK_API int slk_dense_grad(const float* dY, const float* X, int64_t M, int64_t K
  *                          grow choice, the rewrite (as slk_drop_grow).
  * The caller reads *amb_total after slk_rigl_count to size the finish
  * workspace (8 bytes per undecided column). |G'[i,k] - G[i,k]| <=
- * slk_rigl_bound_factor(N)·nrm_dY[i]·nrm_X[k] + 2^-100·(1 + nrm_dY[i] +
- * nrm_X[k]) for norms up to 2^60 (larger or non-finite norms make the row
- * exact: every empty column is computed exactly).                           */
+ * slk_rigl_bound_factor(N)·nrm_dY[i]·nrm_X[k] + slk_rigl_partial_factor(N)·
+ * 2^(G_code[i,k] - 127) + 2^-100·(1 + nrm_dY[i] + nrm_X[k]) for norms up to
+ * 2^60 (larger or non-finite norms make the row exact: every empty column is
+ * computed exactly). G_code (one byte per element of G', row-major M x K) is
+ * written by slk_dense_grad_approx: 2^(G_code - 127) bounds the element's sum
+ * of |partial sums of G'| at the ends of its 128-term chunks, which bounds
+ * the reference's own rounding far tighter than a multiple of n_i·n_k.      */
 
 /* nrm_dY[i] >= ||dY_i||_2, nrm_X[k] >= ||X_k||_2 (+inf where not finite). */
 SLK_API int slk_rigl_norms(const float* dY, int64_t M, const float* X, int64_t K, int64_t N,
@@ -352,13 +356,15 @@ SLK_API int slk_rigl_norms(const float* dY, int64_t M, const float* X, int64_t K
  * into bf16 parts, (M + K) * ceil(N / 32) * 128.                            */
 SLK_API int64_t slk_dense_grad_approx_workspace_bytes(int64_t M, int64_t K, int64_t N);
 
-/* G' = dY·X^T within the bound above; dY is M x N and X is K x N, row-major. */
+/* G' = dY·X^T within the bound above, and its partial-sum codes G_code (M x K
+ * bytes); dY is M x N and X is K x N, row-major. */
 SLK_API int slk_dense_grad_approx(const float* dY, const float* X, int64_t M, int64_t K,
-                                  int64_t N, float* G, void* workspace,
+                                  int64_t N, float* G, uint8_t* G_code, void* workspace,
                                   int64_t workspace_bytes, void* stream);
 
-/* The factor c_N of the bound above (host function, no device work). */
+/* The factors of the bound above (host functions, no device work). */
 SLK_API double slk_rigl_bound_factor(int64_t N);
+SLK_API double slk_rigl_partial_factor(int64_t N);
 
 /* Per row of W: survivors of *thr_dev (the global drop threshold, as for
  * slk_drop_grow) and the empty columns the bound leaves undecided. info:
@@ -367,8 +373,9 @@ SLK_API double slk_rigl_bound_factor(int64_t N);
  * counts, the rest is scratch; *amb_total = amb_off[nrows] (device int64).
  * ncols at most 131072.                                                     */
 SLK_API int slk_rigl_count(const slk_csr* W, const float* thr_dev, const float* G_approx,
-                           int64_t ldg, const float* nrm_dY, const float* nrm_X, int64_t N,
-                           void* info, int64_t* amb_off, int64_t* amb_total, void* stream);
+                           int64_t ldg, const uint8_t* G_code, const float* nrm_dY,
+                           const float* nrm_X, int64_t N, void* info, int64_t* amb_off,
+                           int64_t* amb_total, void* stream);
 
 /* Finishes the RigL pass slk_rigl_count began: values, col_indices and
  * row_nnz must be W's own arrays (rewritten as slk_drop_grow rewrites them);
@@ -376,7 +383,8 @@ SLK_API int slk_rigl_count(const slk_csr* W, const float* thr_dev, const float* 
  * workspace as slk_drop_grow's; *removed as slk_drop_grow's.                */
 SLK_API int slk_rigl_finish(const slk_csr* W, float* values, int32_t* col_indices,
                             int32_t* row_nnz, const float* thr_dev, const float* G_approx,
-                            int64_t ldg, const float* nrm_dY, const float* nrm_X,
+                            int64_t ldg, const uint8_t* G_code, const float* nrm_dY,
+                            const float* nrm_X,
                             const float* dY, const float* X, int64_t N, const void* info,
                             const int64_t* amb_off, void* amb_ws, int64_t amb_ws_bytes,
                             void* workspace, int64_t workspace_bytes, int64_t* removed,

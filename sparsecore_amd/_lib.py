@@ -21,7 +21,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libsparsecore_amd.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 SLK_OK, SLK_EINVAL, SLK_EDEVICE = 0, 1, 2
 SLK_DW_SIMD, SLK_DW_SCALAR = 0, 1
@@ -59,6 +59,7 @@ EXPORTS = (
     "slk_dense_grad_approx_workspace_bytes",
     "slk_dense_grad_approx",
     "slk_rigl_bound_factor",
+    "slk_rigl_partial_factor",
     "slk_rigl_count",
     "slk_rigl_finish",
 )
@@ -147,16 +148,19 @@ def _declare(lib) -> None:
     lib.slk_rigl_norms.argtypes = [_vp, _i64, _vp, _i64, _i64, _vp, _vp, _vp]
     lib.slk_dense_grad_approx_workspace_bytes.restype = _i64
     lib.slk_dense_grad_approx_workspace_bytes.argtypes = [_i64, _i64, _i64]
-    lib.slk_dense_grad_approx.argtypes = [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp]
+    lib.slk_dense_grad_approx.argtypes = [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp]
     lib.slk_rigl_bound_factor.restype = ctypes.c_double
     lib.slk_rigl_bound_factor.argtypes = [_i64]
-    lib.slk_rigl_count.argtypes = [_csrp, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp]
+    lib.slk_rigl_partial_factor.restype = ctypes.c_double
+    lib.slk_rigl_partial_factor.argtypes = [_i64]
+    lib.slk_rigl_count.argtypes = [_csrp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
+                                   _vp]
     lib.slk_rigl_finish.argtypes = [_csrp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
-                                    _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp]
+                                    _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp]
     lib.slk_drop_grow_noalloc.argtypes = [_csrp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _i64,
                                           ctypes.c_uint64, _vp, _vp]
     sized = ("slk_last_error", "slk_abi_version", "slk_transpose_workspace_bytes",
-             "slk_drop_grow_workspace_bytes", "slk_rigl_bound_factor",
+             "slk_drop_grow_workspace_bytes", "slk_rigl_bound_factor", "slk_rigl_partial_factor",
              "slk_dense_grad_approx_workspace_bytes",
              "slk_seg_list_capacity", "slk_seg_list_workspace_bytes")
     for name in EXPORTS:
@@ -399,16 +403,20 @@ def rigl_norms(dY: torch.Tensor, X: torch.Tensor, nrm_dY: torch.Tensor,
         _raise(rc)
 
 
-def dense_grad_approx(dY: torch.Tensor, X: torch.Tensor, G: torch.Tensor) -> None:
-    """G' = dY·Xᵀ on the matrix cores within the certified bound
-    (slk_dense_grad_approx); dY (M x N), X (K x N) row-major."""
+def dense_grad_approx(dY: torch.Tensor, X: torch.Tensor, G: torch.Tensor,
+                      G_code: torch.Tensor) -> None:
+    """G' = dY·Xᵀ on the matrix cores within the certified bound, and its
+    partial-sum codes (uint8, M x K) (slk_dense_grad_approx); dY (M x N),
+    X (K x N) row-major."""
     lib = load()
     M, N = dY.shape
     K = X.shape[0]
+    if G_code.dtype != torch.uint8 or G_code.numel() != M * K or not G_code.is_contiguous():
+        raise ValueError("dense_grad_approx: G_code must be a contiguous uint8 M x K tensor")
     nbytes = int(lib.slk_dense_grad_approx_workspace_bytes(M, K, N))
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=G.device)
-    rc = lib.slk_dense_grad_approx(ptr(dY), ptr(X), M, K, N, ptr(G), ptr(ws), nbytes,
-                                   stream_of(G))
+    rc = lib.slk_dense_grad_approx(ptr(dY), ptr(X), M, K, N, ptr(G), ptr(G_code), ptr(ws),
+                                   nbytes, stream_of(G))
     if rc:
         _raise(rc)
 
@@ -417,22 +425,28 @@ def rigl_bound_factor(N: int) -> float:
     return float(load().slk_rigl_bound_factor(int(N)))
 
 
-def rigl_count(view: CsrView, thr: torch.Tensor, G: torch.Tensor, nrm_dY: torch.Tensor,
-               nrm_X: torch.Tensor, N: int, info: torch.Tensor, amb_off: torch.Tensor,
-               amb_total: torch.Tensor) -> None:
+def rigl_partial_factor(N: int) -> float:
+    return float(load().slk_rigl_partial_factor(int(N)))
+
+
+def rigl_count(view: CsrView, thr: torch.Tensor, G: torch.Tensor, G_code: torch.Tensor,
+               nrm_dY: torch.Tensor, nrm_X: torch.Tensor, N: int, info: torch.Tensor,
+               amb_off: torch.Tensor, amb_total: torch.Tensor) -> None:
     rc = load().slk_rigl_count(ctypes.byref(view), thr.data_ptr(), ptr(G), G.stride(0),
-                               ptr(nrm_dY), ptr(nrm_X), int(N), ptr(info), amb_off.data_ptr(),
+                               ptr(G_code), ptr(nrm_dY), ptr(nrm_X), int(N), ptr(info),
+                               amb_off.data_ptr(),
                                amb_total.data_ptr(), stream_of(amb_total))
     if rc:
         _raise(rc)
 
 
-def rigl_finish(view: CsrView, thr: torch.Tensor, G: torch.Tensor, nrm_dY: torch.Tensor,
-                nrm_X: torch.Tensor, dY: torch.Tensor, X: torch.Tensor, info: torch.Tensor,
-                amb_off: torch.Tensor, amb_ws: torch.Tensor, ws: torch.Tensor,
-                removed: torch.Tensor) -> None:
+def rigl_finish(view: CsrView, thr: torch.Tensor, G: torch.Tensor, G_code: torch.Tensor,
+                nrm_dY: torch.Tensor, nrm_X: torch.Tensor, dY: torch.Tensor, X: torch.Tensor,
+                info: torch.Tensor, amb_off: torch.Tensor, amb_ws: torch.Tensor,
+                ws: torch.Tensor, removed: torch.Tensor) -> None:
     rc = load().slk_rigl_finish(ctypes.byref(view), view.values, view.col_indices, view.row_nnz,
-                                thr.data_ptr(), ptr(G), G.stride(0), ptr(nrm_dY), ptr(nrm_X),
+                                thr.data_ptr(), ptr(G), G.stride(0), ptr(G_code), ptr(nrm_dY),
+                                ptr(nrm_X),
                                 ptr(dY), ptr(X), dY.shape[1], ptr(info), amb_off.data_ptr(),
                                 ptr(amb_ws), amb_ws.numel(), ptr(ws), ws.numel(),
                                 removed.data_ptr(), stream_of(removed))

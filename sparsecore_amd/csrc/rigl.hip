@@ -17,18 +17,20 @@
 //            chunks of 128 j on the matrix cores and the chunk sums added on
 //            the VALU, so no product passes through more than 3·128 + N/128
 //            additions.
-//   bound    |G'[i,k] - G[i,k]| <= E[i,k] = c_N·n_i·n_k + δ, where
-//            c_N covers the reference's own rounding (γ_N), the matrix-core
-//            sums (≤ 2u per addition, to cover any rounding mode), the dropped
-//            x_l y_l and r terms, the final add, plus a 1% margin; and δ the
+//   bound    |G'[i,k] - G[i,k]| <= E[i,k] = c1·n_i·n_k + c2·pm[i,k] + δ
+//            (certified_factors below): the matrix cores' rounding (≤ 2u per
+//            addition, any order and rounding mode) and the reference's own
+//            are both relative to running sums, bounded through pm = the sum of
+//            |partial sums| at the 128-term chunk ends (a byte code per
+//            element); the dropped x_l y_l and r terms; a 1% margin; and δ the
 //            flushing of subnormal bf16 parts and products (2^-100·(1+n_i+n_k)).
 //            Σ_j |x_j y_j| <= n_i·n_k by Cauchy-Schwarz.
 //   count    per row: survivors as in the exact kernel; n_grow = min(dropped,
-//            empty columns); among the empty columns, lower = |G'| - E and
-//            upper = |G'| + E (rounded outward); T_lo / T_hi = the n_grow-th
-//            largest lower / upper. A column with lower > T_hi is certainly
-//            grown (|G| > T_hi >= the exact n_grow-th largest |G|), one with
-//            upper < T_lo certainly not; the rest are undecided. Counts them.
+//            empty columns); T' = the n_grow-th largest |G'| of the empty
+//            columns and E_max = the row's largest E_k, so the exact n_grow-th
+//            largest |G| lies in [T' - E_max, T' + E_max]. A column with
+//            |G'| - E_k above that is certainly grown, one with |G'| + E_k
+//            below it certainly not; the rest are undecided. Counts them.
 //   finish   per row, the undecided columns listed (ascending); over all
 //            undecided (row, column) pairs, their exact G with the reference's
 //            arithmetic (a wave per 64 pairs, both rows streamed through LDS);
@@ -133,13 +135,24 @@ __global__ __launch_bounds__(256) void rigl_split_kernel(const float* __restrict
 
 constexpr int kALdsRow = kAStageBytes + 16;  // bytes per staged row (padded)
 
+// The partial-sum code of an element: pm = the sum of |G' partial sums| at
+// the chunk ends, stored as the exponent code c with pm < 2^(c - 127)
+// (c = biased exponent + 1, at most 255 = +inf for a non-finite pm).
+__device__ __forceinline__ uint32_t partial_code(float pm) {
+    return min(((__float_as_uint(pm) >> 23) & 0xffu) + 1u, 255u);
+}
+// 2^(c - 127) for c in [1, 255] (255: +inf)
+__device__ __forceinline__ float partial_bound(uint32_t c) { return __uint_as_float(c << 23); }
+
 // Stages per row: N rounded up to whole chunks (zero beyond N).
 inline int64_t approx_stages(int64_t N) { return ceil_div(N, kAChunk) * (kAChunk / kAJ); }
 
 // G'[i0 + 128, k0 + 128 tile] = Σ (x_h·y_h + x_h·y_l + x_l·y_h), where
-// x = dY row i, y = X row k: the three products of each term go to one fp32
-// matrix-core sum per chunk of kAChunk j, and the chunk sums are added on the
-// VALU, so no term passes through more than 3·kAChunk + N/kAChunk additions.
+// x = dY row i, y = X row k: one fp32 matrix-core sum of the three products
+// of every term, and beside it pm = the sum of the running sum's magnitudes
+// at the ends of its chunks of kAChunk j, written as the element's partial-sum
+// code. The bound uses pm twice: each MFMA's rounding is relative to its
+// running sum, and so is each addition of the reference's own sum.
 // Four waves in a 2 x 2 grid, each 64 rows x 64 columns (2 x 2 blocks of
 // 32 x 32): per k-step of 16 j a wave reads four A and four B fragments from
 // LDS for twelve MFMAs (waves of 32 x 64 read six for six). Two workgroups
@@ -149,7 +162,8 @@ inline int64_t approx_stages(int64_t N) { return ceil_div(N, kAChunk) * (kAChunk
 __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64_t K, int64_t nst,
                                                                 const uint16_t* __restrict__ PA,
                                                                 const uint16_t* __restrict__ PB,
-                                                                float* __restrict__ G) {
+                                                                float* __restrict__ G,
+                                                                uint8_t* __restrict__ Gc) {
     __shared__ __align__(16) unsigned char sA[2][kATI * kALdsRow];
     __shared__ __align__(16) unsigned char sB[2][kATK * kALdsRow];
 
@@ -178,13 +192,15 @@ __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64
     const unsigned char* gb = reinterpret_cast<const unsigned char*>(
         PB + (k0 + lrb < K ? k0 + lrb : K - 1) * nst * (2 * kAJ)) + lhb;
 
-    f32x16 cs[2][2], tot[2][2];  // [row block][column block]: chunk sums, totals
+    // [row block][column block]: the running sums, and the sum of their
+    // magnitudes at the chunk ends (the partial sums the bound uses)
+    f32x16 acc[2][2], pm[2][2];
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) tot[a][b][r] = 0.0f;
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = pm[a][b][r] = 0.0f;
 
     // Pipeline: stage st+2's loads are issued while stage st is computed from
     // LDS buffer st&1; stage st+1 (loaded during stage st-1) is written into
@@ -215,11 +231,9 @@ __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64
     const int ra0 = (wm * 64 + (lane & 31)) * kALdsRow + half;
     const int rb0 = (wn * 64 + (lane & 31)) * kALdsRow + half;
     // stage st lives in register set st & 1 and LDS buffer st & 1; the two
-    // parities are unrolled so both indexes are compile-time constants. The
-    // first stage of a chunk starts its sums from zero.
-    auto stage = [&](auto R, auto F, int64_t st) {
+    // parities are unrolled so both indexes are compile-time constants.
+    auto stage = [&](auto R, int64_t st) {
         constexpr int reg = decltype(R)::value;
-        constexpr bool first = decltype(F)::value;
         fetch(reg, st + 2 < nst ? st + 2 : nst - 1);  // set of stage st: already in LDS
         const unsigned char* la = sA[reg];
         const unsigned char* lb = sB[reg];
@@ -239,18 +253,17 @@ __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64
             for (int a = 0; a < 2; ++a)
 #pragma unroll
                 for (int b = 0; b < 2; ++b)
-                    cs[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                        af[a][0], bf[b][0], (first && s == 0) ? f32x16{} : cs[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a][0], bf[b][0], acc[a][b], 0, 0, 0);
 #pragma unroll
             for (int a = 0; a < 2; ++a)
 #pragma unroll
                 for (int b = 0; b < 2; ++b)
-                    cs[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a][0], bf[b][1], cs[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a][0], bf[b][1], acc[a][b], 0, 0, 0);
 #pragma unroll
             for (int a = 0; a < 2; ++a)
 #pragma unroll
                 for (int b = 0; b < 2; ++b)
-                    cs[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a][1], bf[b][0], cs[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a][1], bf[b][0], acc[a][b], 0, 0, 0);
         }
         // stage st+1 into the other buffer (its last readers, stage st-1,
         // passed the previous barrier)
@@ -260,25 +273,23 @@ __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64
     static_assert(kAChunk / kAJ == 4, "four stages per chunk below");
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
-    using T = std::true_type;
-    using F = std::false_type;
     if (nst > 0) {  // workgroup-uniform
         fetch(0, 0);
         fetch(1, 1);
         stage_to_lds(0, 0);
         __syncthreads();
         for (int64_t c0 = 0; c0 < nst; c0 += kAChunk / kAJ) {
-            stage(I0{}, T{}, c0);
-            stage(I1{}, F{}, c0 + 1);
-            stage(I0{}, F{}, c0 + 2);
-            stage(I1{}, F{}, c0 + 3);
-            // a chunk done: add its sums on the VALU
+            stage(I0{}, c0);
+            stage(I1{}, c0 + 1);
+            stage(I0{}, c0 + 2);
+            stage(I1{}, c0 + 3);
+            // a chunk done: the running sum's magnitude to pm
 #pragma unroll
             for (int a = 0; a < 2; ++a)
 #pragma unroll
                 for (int b = 0; b < 2; ++b)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) tot[a][b][r] = tot[a][b][r] + cs[a][b][r];
+                    for (int r = 0; r < 16; ++r) pm[a][b][r] = pm[a][b][r] + fabsf(acc[a][b][r]);
         }
     }
     // lane l, register 4g + q of a 32x32 block: row 8g + 4(l/32) + q, column l % 32
@@ -290,7 +301,10 @@ __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int64_t row = i0 + wm * 64 + a * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (row < M && col < K) G[row * K + col] = tot[a][b][r];
+                if (row < M && col < K) {
+                    G[row * K + col] = acc[a][b][r];
+                    Gc[row * K + col] = static_cast<uint8_t>(partial_code(pm[a][b][r]));
+                }
             }
     }
 }
@@ -317,10 +331,12 @@ __device__ __forceinline__ float up_(float x) { return x * (1.0f + 0x1p-20f) + 0
 __device__ __forceinline__ float dn_(float x) { return x * (1.0f - 0x1p-20f) - 0x1p-120f; }
 constexpr float kNormCap = 0x1p60f;  // norms above this make the row exact
 
-// The per-column error E_k = up(cni·n_k) + delta >= c_N·n_i·n_k + the
-// absolute part (delta = up(2^-100·(1 + n_i + max n_k))).
-__device__ __forceinline__ float col_err(float cni, float nk, float delta) {
-    return up_(cni * nk) + delta;
+// The per-column error E_k = up(cni·n_k) + delta + up(c2·2^(code - 127))
+// >= c_N·n_i·n_k + the absolute part (delta = up(2^-100·(1 + n_i + max n_k)))
+// + c2·(the element's sum of |partial sums|).
+__device__ __forceinline__ float col_err(float cni, float nk, float delta, float c2,
+                                         uint32_t code) {
+    return up_(up_(cni * nk) + delta + up_(c2 * partial_bound(code)));
 }
 
 // Largest-first selection key of a non-negative float.
@@ -361,52 +377,57 @@ __device__ uint32_t kth_smallest_key(Cand cand, int64_t n, int64_t need, uint32_
 constexpr int64_t kStageMaxK = 16384;  // G' rows up to this length are staged in LDS
 constexpr int kColBlock = 8;            // float4 loads per thread in flight per block
 
-// Calls f(c, g, nk) for every column c < K of a row: g = G'[c] of the row,
-// nk = nrm_c[c]. V4 (K % 4 == 0, 16-byte aligned rows): each thread issues
-// kColBlock float4 loads of both before using any, so a row streams with one
-// memory latency per block instead of one per column.
+// Calls f(c, g, nk, code) for every column c < K of a row: g = G'[c] of the
+// row, nk = nrm_c[c], code = the row's partial-sum code of c. V4 (K % 4 == 0,
+// 16-byte aligned rows, 4-byte aligned codes): each thread issues kColBlock
+// loads of each before using any, so a row streams with one memory latency
+// per block instead of one per column.
 template <bool V4, class F>
 __device__ __forceinline__ void for_each_col(const float* __restrict__ g_row,
-                                             const float* __restrict__ nrm_c, int64_t K, F f) {
+                                             const float* __restrict__ nrm_c,
+                                             const uint8_t* __restrict__ code_row, int64_t K,
+                                             F f) {
     const int t = threadIdx.x;
     if (V4) {
         constexpr int64_t step = int64_t{kRowThreads} * 4 * kColBlock;
         for (int64_t base = 0; base < K; base += step) {
             f32x4 g[kColBlock], n[kColBlock];
+            uint32_t cw[kColBlock];
 #pragma unroll
             for (int u = 0; u < kColBlock; ++u) {  // no branch: all loads issued at once
                 const int64_t c = base + 4 * (t + int64_t{kRowThreads} * u);
                 const int64_t cl = c < K ? c : K - 4;  // in bounds, unused past K
                 g[u] = *reinterpret_cast<const f32x4*>(g_row + cl);
                 n[u] = *reinterpret_cast<const f32x4*>(nrm_c + cl);
+                cw[u] = *reinterpret_cast<const uint32_t*>(code_row + cl);
             }
 #pragma unroll
             for (int u = 0; u < kColBlock; ++u) {
                 const int64_t c = base + 4 * (t + int64_t{kRowThreads} * u);
                 if (c < K) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) f(c + e, g[u][e], n[u][e]);
+                    for (int e = 0; e < 4; ++e) f(c + e, g[u][e], n[u][e], (cw[u] >> (8 * e)) & 255u);
                 }
             }
         }
     } else {
-        for (int64_t c = t; c < K; c += kRowThreads) f(c, g_row[c], nrm_c[c]);
+        for (int64_t c = t; c < K; c += kRowThreads) f(c, g_row[c], nrm_c[c], uint32_t{code_row[c]});
     }
 }
 
 // rigl_count_kernel with the row's |G'| in registers: thread t owns columns
-// 4(t + 256u) + e (u < U, e < 4), so the radix passes read no memory and the
-// kernel needs 2 KiB of LDS instead of 4K + K/8 bytes (five workgroups per
-// CU instead of two). For K <= 1024·U, K % 4 == 0 and 16-byte aligned rows of
-// G' and nrm_c. Same counts, thresholds and flags as rigl_count_kernel: the
-// select visits the same candidates with the same keys.
+// 16(t + 256v) + e (v < U/4, e < 16), so the radix passes read no memory. For
+// K <= 1024·U, K % 16 == 0, 16-byte aligned rows of G', codes and nrm_c. Same
+// counts, thresholds and flags as rigl_count_kernel: the select visits the
+// same candidates with the same keys.
 template <int U>
 __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
     int64_t K, int64_t Kw, const int32_t* __restrict__ row_start,
     const int32_t* __restrict__ row_nnz, const float* __restrict__ values,
     const int32_t* __restrict__ cols, const float* __restrict__ thr_ptr,
-    const float* __restrict__ Gp, int64_t ldg, const float* __restrict__ nrm_r,
-    const float* __restrict__ nrm_c, float c_bound, RowInfo* __restrict__ info,
+    const float* __restrict__ Gp, int64_t ldg, const uint8_t* __restrict__ Gc,
+    const float* __restrict__ nrm_r, const float* __restrict__ nrm_c, float c_bound, float c2,
+    RowInfo* __restrict__ info,
     int64_t* __restrict__ amb_count) {
     __shared__ uint32_t keep[U * kRowThreads * 4 / 32];
     __shared__ int64_t tmp[kRowThreads];
@@ -415,10 +436,15 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
     __shared__ uint32_t s_digit;
     __shared__ int64_t s_below;
     __shared__ unsigned long long s_best;
-    __shared__ uint32_t s_nmax;
+    __shared__ uint32_t s_nmax, s_cmax;
 
     const int64_t i = blockIdx.x;
     const int t = threadIdx.x;
+    // thread t owns the 16 consecutive columns 16(t + 256v) .. + 15 for each
+    // v < U/4: register u holds the four columns col_of(u) .. + 3
+    auto col_of = [&](int u) -> int64_t {
+        return 16 * (t + int64_t{kRowThreads} * (u / 4)) + 4 * (u % 4);
+    };
     RowInfo ri{};
     const int32_t n_live = row_nnz[i];
     auto finish_row = [&](int32_t flags, int64_t n_amb) {
@@ -431,7 +457,7 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
     if (n_live <= 0) return finish_row(kRowKeep, 0);  // the reference skips empty rows
     const int32_t start = row_start[i];
     for (int64_t w = t; w < Kw; w += kRowThreads) keep[w] = 0;
-    if (t == 0) s_nmax = 0;
+    if (t == 0) s_nmax = s_cmax = 0;
     __syncthreads();
     const int64_t n_keep = mark_survivors(values, cols, start, n_live, thr_ptr[0], keep, tmp,
                                           &s_best);
@@ -452,14 +478,14 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
     u32x4 a[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int64_t c = 4 * (t + int64_t{kRowThreads} * u);
+        const int64_t c = col_of(u);
         a[u] = *reinterpret_cast<const u32x4*>(g_row + (c < K ? c : K - 4));
     }
     uint64_t cand = 0;
     int64_t unbounded = 0;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int64_t c = 4 * (t + int64_t{kRowThreads} * u);
+        const int64_t c = col_of(u);
         const uint32_t kw = c < K ? keep[c >> 5] >> (c & 31) : 15u;  // c % 4 == 0: one word
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -560,34 +586,47 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
     f32x4 nr[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const int64_t c = 4 * (t + int64_t{kRowThreads} * u);
+        const int64_t c = col_of(u);
         nr[u] = *reinterpret_cast<const f32x4*>(nrm_c + (c < K ? c : K - 4));
     }
-    uint32_t nmax = 0;
+    // the partial-sum codes of thread t's columns: one 16-byte load per 16
+    // columns (K % 16 == 0 for this kernel)
+    const uint8_t* c_row = Gc + i * K;
+    typedef uint32_t u32x4c __attribute__((ext_vector_type(4)));
+    auto codes16 = [&](int v) -> u32x4c {  // past K: a clamped load, its columns not candidates
+        const int64_t c = 16 * (t + int64_t{kRowThreads} * v);
+        return *reinterpret_cast<const u32x4c*>(c_row + (c < K ? c : K - 16));
+    };
+    uint32_t nmax = 0, cmax = 0;
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+    for (int u = 0; u < U; ++u) {
+        const uint32_t cw = codes16(u / 4)[u % 4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             if (!((cand >> (4 * u + e)) & 1ull)) continue;
             if (!(nr[u][e] <= kNormCap)) ++unbounded;
             else nmax = max(nmax, __float_as_uint(nr[u][e]));
+            cmax = max(cmax, (cw >> (8 * e)) & 255u);
         }
+    }
     atomicMax(&s_nmax, nmax);
+    atomicMax(&s_cmax, cmax);
     block_inclusive_scan(unbounded, tmp);
     if (tmp[kRowThreads - 1] > 0) return finish_row(kRowExact, n_empty);
     const float nm = __uint_as_float(s_nmax);
     const float cni = up_(c_bound * ni);
     const float delta = up_(0x1p-100f * up_(1.0f + ni + nm));
-    const float e_max = col_err(cni, nm, delta);
+    const float e_max = col_err(cni, nm, delta, c2, s_cmax);
     const float t_in = up_(Tp + e_max);
     const float t_out = dn_(Tp - e_max);
     int64_t n_in = 0, n_amb = 0;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+        const uint32_t cw = codes16(u / 4)[u % 4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             if (!((cand >> (4 * u + e)) & 1ull)) continue;
-            const float ek = col_err(cni, nr[u][e], delta);
+            const float ek = col_err(cni, nr[u][e], delta, c2, (cw >> (8 * e)) & 255u);
             const float g = __uint_as_float(~a[u][e]);
             if (dn_(g - ek) > t_in) ++n_in;
             else if (!(up_(g + ek) < t_out)) ++n_amb;
@@ -619,8 +658,9 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_kernel(
     int64_t K, int64_t Kw, const int32_t* __restrict__ row_start,
     const int32_t* __restrict__ row_nnz, const float* __restrict__ values,
     const int32_t* __restrict__ cols, const float* __restrict__ thr_ptr,
-    const float* __restrict__ Gp, int64_t ldg, const float* __restrict__ nrm_r,
-    const float* __restrict__ nrm_c, float c_bound, RowInfo* __restrict__ info,
+    const float* __restrict__ Gp, int64_t ldg, const uint8_t* __restrict__ Gc,
+    const float* __restrict__ nrm_r, const float* __restrict__ nrm_c, float c_bound, float c2,
+    RowInfo* __restrict__ info,
     int64_t* __restrict__ amb_count) {
     extern __shared__ uint32_t lds[];
     uint32_t* keep = lds;
@@ -630,7 +670,7 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_kernel(
     __shared__ uint32_t s_digit;
     __shared__ int64_t s_below;
     __shared__ unsigned long long s_best;
-    __shared__ uint32_t s_nmax;
+    __shared__ uint32_t s_nmax, s_cmax;
 
     const int64_t i = blockIdx.x;
     const int t = threadIdx.x;
@@ -646,7 +686,7 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_kernel(
     if (n_live <= 0) return finish_row(kRowKeep, 0);  // the reference skips empty rows
     const int32_t start = row_start[i];
     for (int64_t w = t; w < Kw; w += kRowThreads) keep[w] = 0;
-    if (t == 0) s_nmax = 0;
+    if (t == 0) s_nmax = s_cmax = 0;
     __syncthreads();
     const int64_t n_keep = mark_survivors(values, cols, start, n_live, thr_ptr[0], keep, tmp,
                                           &s_best);
@@ -659,15 +699,18 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_kernel(
 
     // stage |G'|, the largest candidate norm, and whether every bound exists
     int64_t unbounded = 0;
-    uint32_t nmax = 0;
-    for_each_col<V4>(g_row, nrm_c, K, [&](int64_t c, float g, float nk) {
+    uint32_t nmax = 0, cmax = 0;
+    const uint8_t* c_row = Gc + i * K;
+    for_each_col<V4>(g_row, nrm_c, c_row, K, [&](int64_t c, float g, float nk, uint32_t code) {
         const float a = fabsf(g);
         if (STAGED) ag[c] = a;
         if (bit_of(keep, c)) return;
         if (!(nk <= kNormCap) || !(a <= 0x1p125f)) ++unbounded;
         else nmax = max(nmax, __float_as_uint(nk));
+        cmax = max(cmax, code);
     });
     atomicMax(&s_nmax, nmax);
+    atomicMax(&s_cmax, cmax);
     block_inclusive_scan(unbounded, tmp);
     unbounded = tmp[kRowThreads - 1];
     if (unbounded > 0 || !(ni <= kNormCap)) return finish_row(kRowExact, n_empty);
@@ -683,14 +726,14 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_kernel(
                                                        &s_below, tmp));
     const float cni = up_(c_bound * ni);
     const float delta = up_(0x1p-100f * up_(1.0f + ni + nm));
-    const float e_max = col_err(cni, nm, delta);
+    const float e_max = col_err(cni, nm, delta, c2, s_cmax);
     const float t_in = up_(Tp + e_max);
     const float t_out = dn_(Tp - e_max);
     int64_t n_in = 0, n_amb = 0;
-    for_each_col<V4>(g_row, nrm_c, K, [&](int64_t c, float g, float nk) {
+    for_each_col<V4>(g_row, nrm_c, c_row, K, [&](int64_t c, float g, float nk, uint32_t code) {
         if (bit_of(keep, c)) return;
         const float a = fabsf(g);
-        const float e = col_err(cni, nk, delta);
+        const float e = col_err(cni, nk, delta, c2, code);
         if (dn_(a - e) > t_in) ++n_in;
         else if (!(up_(a + e) < t_out)) ++n_amb;
     });
@@ -826,9 +869,10 @@ __global__ __launch_bounds__(kRowThreads) void rigl_list_kernel(
     int64_t K, int64_t Kw, const int32_t* __restrict__ row_start,
     const int32_t* __restrict__ row_nnz, const float* __restrict__ values,
     const int32_t* __restrict__ cols, const float* __restrict__ thr_ptr,
-    const float* __restrict__ Gp, int64_t ldg, const float* __restrict__ nrm_c,
-    const RowInfo* __restrict__ info, const int64_t* __restrict__ amb_off,
-    int32_t* __restrict__ amb_col, uint32_t* __restrict__ amb_key, int64_t amb_cap,
+    const float* __restrict__ Gp, int64_t ldg, const uint8_t* __restrict__ Gc, float c2,
+    const float* __restrict__ nrm_c, const RowInfo* __restrict__ info,
+    const int64_t* __restrict__ amb_off, int32_t* __restrict__ amb_col,
+    uint32_t* __restrict__ amb_key, int64_t amb_cap,
     int32_t* __restrict__ stage_col) {
     extern __shared__ uint32_t lds[];
     uint32_t* keep = lds;
@@ -852,10 +896,11 @@ __global__ __launch_bounds__(kRowThreads) void rigl_list_kernel(
         for (int64_t c = t; c < K; c += kRowThreads)
             if (!bit_of(keep, c)) atomicOr(&ambm[c >> 5], 1u << (c & 31));
     } else {
-        for_each_col<VG>(Gp + i * ldg, nrm_c, K, [&](int64_t c, float g, float nk) {
+        for_each_col<VG>(Gp + i * ldg, nrm_c, Gc + i * K, K,
+                         [&](int64_t c, float g, float nk, uint32_t code) {
             if (bit_of(keep, c)) return;
             const float a = fabsf(g);
-            const float e = col_err(ri.cni, nk, ri.delta);
+            const float e = col_err(ri.cni, nk, ri.delta, c2, code);
             if (dn_(a - e) > ri.t_in) atomicOr(&grow[c >> 5], 1u << (c & 31));
             else if (!(up_(a + e) < ri.t_out)) atomicOr(&ambm[c >> 5], 1u << (c & 31));
         });
@@ -1044,22 +1089,51 @@ __global__ __launch_bounds__(kRowThreads) void rigl_select_kernel(
 
 __global__ void rigl_clear_kernel(unsigned long long* __restrict__ c) { *c = 0; }
 
-// c_N of the bound (see the file comment): the reference's γ_N; the matrix
-// cores' chunk sums of 3·kAChunk terms at <= 2u per addition, and the N/kAChunk
-// chunk sums added on the VALU at <= u, over Σ|x_h y_h| + |x_h y_l| + |x_l y_h|
-// <= (1 + 2^-7 + 2^-14)·Σ|x y| (taken as 1 + 2^-6); the dropped parts; the
-// final add; times 1.01.
-double certified_c(int64_t N) {
-    const double u = 0x1p-24;
+// The bound's factors: |G'[i,k] - G[i,k]| <= c1·n_i·n_k + c2·pm[i,k] + δ,
+// pm = the element's sum of |running sums of G'| at the chunk ends (its
+// code's power of two bounds it). u = 2^-24, u' = u / (1 - u), L = kAChunk,
+// C = ceil(N / L) chunks, I = 3L/16 MFMAs per chunk, g = γ_16(2u).
+//  * G' against the exact sum S_N = Σ x_j y_j: each MFMA adds 16 exact bf16
+//    products to its running sum R, at <= 2u per addition in any order and
+//    rounding mode: error <= g·(|R| + Σ|t|). Inside chunk c, |R| <= |S_{a_c}| +
+//    Σ_{chunk c}|t| + (the error so far <= c_run·Σ|x y|), so the matrix-core
+//    error is <= g·I·Σ_c |S_{a_c}| + g·(I + 1 + (3N/16)·c_run)·Σ|t|, with
+//    Σ|t| = Σ|x_h y_h| + |x_h y_l| + |x_l y_h| <= (1 + 2^-6)·Σ|x y|; plus the
+//    dropped x_l y_l and r terms, 3.1·2^-16·Σ|x y|.
+//  * The reference's sum G = ŝ_N (products rounded, then added in order)
+//    against S_N: |ŝ_N - S_N| <= u·Σ|p| + u'·Σ_j |ŝ_j|, Σ_j |ŝ_j| <=
+//    Σ_j |S_j| + N·γ_N·Σ|p|, and inside chunk c |S_j| <= |S_{a_c}| +
+//    Σ_{chunk c}|p|: Σ_j |S_j| <= L·Σ_c |S_{a_c}| + L·Σ|p|.
+//  * Σ_c |S_{a_c}| <= (1 + 2Cu)·pm + C·c_run·Σ|x y| (pm: C positive terms
+//    summed in fp32, over running sums within c_run·Σ|x y| of the exact
+//    partial sums; c_run = g·(3N/16)·2·(1 + 2^-6) + 3.1·2^-16, a crude bound
+//    that only ever multiplies small factors).
+//  * Σ|x y| <= n_i·n_k (Cauchy-Schwarz); everything times 1.01.
+// Against γ_N·Σ|x y| for the reference's rounding alone this is L instead of
+// N per unit of Σ|x y|, plus the partial sums' magnitudes, which grow like a
+// random walk, not like Σ|x y| (16384^2 x 4096: c1 = 1.14e-4 against the
+// 3.43e-4 of a bound without pm, and c2·pm is about a tenth of the bound).
+struct BoundFactors {
+    double c1, c2;
+};
+BoundFactors certified_factors(int64_t N) {
+    const double u = 0x1p-24, u1 = u / (1.0 - u);
     auto gam = [&](double n, double uu) { return n * uu / (1.0 - n * uu); };
     const double n = static_cast<double>(N > 0 ? N : 1);
-    const double chunks = ceil(n / kAChunk) + 1.0;
-    const double g_ref = gam(n, u);
-    const double g_chunk = gam(3.0 * kAChunk, 2 * u);
-    const double g_mc = (g_chunk + gam(chunks, u) * (1.0 + g_chunk)) * (1.0 + 0x1p-6);
+    const double L = kAChunk;
+    const double C = ceil(n / L);
+    const double I = 3.0 * L / 16.0;
+    const double ninstr = 3.0 * C * L / 16.0;  // MFMAs per element, padded chunks included
+    const double g = gam(16.0, 2 * u);
+    const double sums = 1.0 + 0x1p-6;
     const double dropped = 3.1 * 0x1p-16;
-    const double fin = 1.01 * u;
-    return (g_ref + g_mc + dropped + fin) * 1.01;
+    const double c_run = g * ninstr * 2.0 * sums + dropped;
+    const double c_mc = g * (I + 1.0 + ninstr * c_run) * sums + dropped;
+    const double c_ref = u + u1 * (L + n * gam(n, u));
+    const double part = g * I + u1 * L;  // per unit of Σ_c |S_{a_c}|
+    const double c1 = (c_mc + c_ref + part * C * c_run + 1.01 * u) * 1.01;
+    const double c2 = part * (1.0 + 2.0 * C * u) * 1.01;
+    return {c1, c2};
 }
 
 }  // namespace
@@ -1091,14 +1165,14 @@ extern "C" int64_t slk_dense_grad_approx_workspace_bytes(int64_t M, int64_t K, i
 }
 
 extern "C" int slk_dense_grad_approx(const float* dY, const float* X, int64_t M, int64_t K,
-                                     int64_t N, float* G, void* workspace,
+                                     int64_t N, float* G, uint8_t* G_code, void* workspace,
                                      int64_t workspace_bytes, void* stream) {
     using namespace slk;
     clear_error();
     if (M < 0 || K < 0 || N < 0)
         return fail(SLK_EINVAL, "dense_grad_approx: shape params must be non-negative");
     if (M == 0 || K == 0) return SLK_OK;
-    if (G == nullptr || (N > 0 && (dY == nullptr || X == nullptr)))
+    if (G == nullptr || G_code == nullptr || (N > 0 && (dY == nullptr || X == nullptr)))
         return fail(SLK_EINVAL, "dense_grad_approx: NULL pointer");
     const int64_t nst = approx_stages(N);
     const int64_t need = (M + K) * nst * kAStageBytes;
@@ -1121,15 +1195,18 @@ extern "C" int slk_dense_grad_approx(const float* dY, const float* X, int64_t M,
         if (int rc = check_launch("dense_grad_approx/split")) return rc;
     }
     hipLaunchKernelGGL(rigl_approx_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kAThreads), 0,
-                       st, M, K, nst, PA, PB, G);
+                       st, M, K, nst, PA, PB, G, G_code);
     return check_launch("dense_grad_approx");
 }
 
-extern "C" double slk_rigl_bound_factor(int64_t N) { return slk::certified_c(N); }
+extern "C" double slk_rigl_bound_factor(int64_t N) { return slk::certified_factors(N).c1; }
+
+extern "C" double slk_rigl_partial_factor(int64_t N) { return slk::certified_factors(N).c2; }
 
 extern "C" int slk_rigl_count(const slk_csr* W, const float* thr_dev, const float* G_approx,
-                              int64_t ldg, const float* nrm_dY, const float* nrm_X, int64_t N,
-                              void* info, int64_t* amb_off, int64_t* amb_total, void* stream) {
+                              int64_t ldg, const uint8_t* G_code, const float* nrm_dY,
+                              const float* nrm_X, int64_t N, void* info, int64_t* amb_off,
+                              int64_t* amb_total, void* stream) {
     using namespace slk;
     clear_error();
     if (int rc = validate_csr(W, "rigl_count")) return rc;
@@ -1141,31 +1218,36 @@ extern "C" int slk_rigl_count(const slk_csr* W, const float* thr_dev, const floa
     if (N < 0) return fail(SLK_EINVAL, "rigl_count: negative N");
     if (amb_off == nullptr || amb_total == nullptr)
         return fail(SLK_EINVAL, "rigl_count: NULL output");
-    if (W->nrows > 0 && (thr_dev == nullptr || G_approx == nullptr || ldg < W->ncols ||
-                         nrm_dY == nullptr || nrm_X == nullptr || info == nullptr))
+    if (W->nrows > 0 && (thr_dev == nullptr || G_approx == nullptr || G_code == nullptr ||
+                         ldg < W->ncols || nrm_dY == nullptr || nrm_X == nullptr ||
+                         info == nullptr))
         return fail(SLK_EINVAL, "rigl_count: NULL input or ldg < ncols");
     hipStream_t st = as_stream(stream);
     const int64_t M = W->nrows, K = W->ncols;
     const int64_t Kw = ceil_div(K, 32) > 0 ? ceil_div(K, 32) : 1;
     // amb_off doubles as the per-row counts before the scan
     if (M > 0) {
-        // c_N rounded up to a float
-        const float c_f = std::nextafter(static_cast<float>(certified_c(N)), INFINITY);
+        // the factors rounded up to floats
+        const BoundFactors bf = certified_factors(N);
+        const float c_f = std::nextafter(static_cast<float>(bf.c1), INFINITY);
+        const float c2_f = std::nextafter(static_cast<float>(bf.c2), INFINITY);
         const bool vg = K % 4 == 0 && ldg % 4 == 0 &&
                         reinterpret_cast<uintptr_t>(G_approx) % 16 == 0 &&
+                        reinterpret_cast<uintptr_t>(G_code) % 4 == 0 &&
                         reinterpret_cast<uintptr_t>(nrm_X) % 16 == 0;
         const dim3 grid(static_cast<unsigned>(M));
         const size_t lds_st = static_cast<size_t>(Kw + K) * 4, lds_un = static_cast<size_t>(Kw) * 4;
 #define SLK_COUNT_ARGS                                                                       \
-    K, Kw, W->row_start, W->row_nnz, W->values, W->col_indices, thr_dev, G_approx, ldg, nrm_dY, \
-        nrm_X, c_f, static_cast<RowInfo*>(info), amb_off + M + 1
-        if (vg && K <= 4 * kRowThreads * 4) {
+    K, Kw, W->row_start, W->row_nnz, W->values, W->col_indices, thr_dev, G_approx, ldg, G_code, \
+        nrm_dY, nrm_X, c_f, c2_f, static_cast<RowInfo*>(info), amb_off + M + 1
+        const bool vr = vg && K % 16 == 0 && reinterpret_cast<uintptr_t>(G_code) % 16 == 0;
+        if (vr && K <= 4 * kRowThreads * 4) {
             hipLaunchKernelGGL(rigl_count_reg_kernel<4>, grid, dim3(kRowThreads), 0, st,
                                SLK_COUNT_ARGS);
-        } else if (vg && K <= 4 * kRowThreads * 8) {
+        } else if (vr && K <= 4 * kRowThreads * 8) {
             hipLaunchKernelGGL(rigl_count_reg_kernel<8>, grid, dim3(kRowThreads), 0, st,
                                SLK_COUNT_ARGS);
-        } else if (vg && K <= 4 * kRowThreads * 16) {
+        } else if (vr && K <= 4 * kRowThreads * 16) {
             hipLaunchKernelGGL(rigl_count_reg_kernel<16>, grid, dim3(kRowThreads), 0, st,
                                SLK_COUNT_ARGS);
         } else if (K <= kStageMaxK && vg) {
@@ -1191,7 +1273,8 @@ extern "C" int slk_rigl_count(const slk_csr* W, const float* thr_dev, const floa
 
 extern "C" int slk_rigl_finish(const slk_csr* W, float* values, int32_t* col_indices,
                                int32_t* row_nnz, const float* thr_dev, const float* G_approx,
-                               int64_t ldg, const float* nrm_dY, const float* nrm_X,
+                               int64_t ldg, const uint8_t* G_code, const float* nrm_dY,
+                               const float* nrm_X,
                                const float* dY, const float* X, int64_t N, const void* info,
                                const int64_t* amb_off, void* amb_ws, int64_t amb_ws_bytes,
                                void* workspace, int64_t workspace_bytes, int64_t* removed,
@@ -1207,7 +1290,8 @@ extern "C" int slk_rigl_finish(const slk_csr* W, float* values, int32_t* col_ind
                                     std::to_string(kRiglMaxCols));
     if (removed == nullptr) return fail(SLK_EINVAL, "rigl_finish: NULL removed-slot counter");
     const int64_t M = W->nrows, K = W->ncols;
-    if (M > 0 && (thr_dev == nullptr || G_approx == nullptr || ldg < K || nrm_dY == nullptr ||
+    if (M > 0 && (thr_dev == nullptr || G_approx == nullptr || G_code == nullptr || ldg < K ||
+                  nrm_dY == nullptr ||
                   nrm_X == nullptr || info == nullptr || amb_off == nullptr ||
                   (N > 0 && (dY == nullptr || X == nullptr))))
         return fail(SLK_EINVAL, "rigl_finish: NULL input or ldg < ncols");
@@ -1234,11 +1318,13 @@ extern "C" int slk_rigl_finish(const slk_csr* W, float* values, int32_t* col_ind
     int32_t* stage_col = static_cast<int32_t*>(workspace);
     float* stage_val = reinterpret_cast<float*>(stage_col + W->total_capacity);
     const bool vg = K % 4 == 0 && ldg % 4 == 0 && reinterpret_cast<uintptr_t>(G_approx) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(G_code) % 4 == 0 &&
                     reinterpret_cast<uintptr_t>(nrm_X) % 16 == 0;
+    const float c2_f = std::nextafter(static_cast<float>(certified_factors(N).c2), INFINITY);
     const dim3 grid(static_cast<unsigned>(M));
 #define SLK_LIST_ARGS                                                                      \
-    K, Kw, W->row_start, row_nnz, values, col_indices, thr_dev, G_approx, ldg, nrm_X,       \
-        static_cast<const RowInfo*>(info), amb_off, amb_col, amb_key, n_amb_max, stage_col
+    K, Kw, W->row_start, row_nnz, values, col_indices, thr_dev, G_approx, ldg, G_code, c2_f, \
+        nrm_X, static_cast<const RowInfo*>(info), amb_off, amb_col, amb_key, n_amb_max, stage_col
     if (vg) {
         hipLaunchKernelGGL(rigl_list_kernel<true>, grid, dim3(kRowThreads), lds, st, SLK_LIST_ARGS);
     } else {

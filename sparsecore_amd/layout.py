@@ -605,21 +605,23 @@ class PaddedCSR:
         nrm_X = torch.empty(K, dtype=_F32, device=dev)
         _lib.rigl_norms(dY, X, nrm_dY, nrm_X)
         Gp = torch.empty(M, K, dtype=_F32, device=dev)
-        _lib.dense_grad_approx(dY, X, Gp)
+        Gc = torch.empty(M, K, dtype=torch.uint8, device=dev)
+        _lib.dense_grad_approx(dY, X, Gp, Gc)
         info = torch.empty(M * _lib.RIGL_INFO_BYTES, dtype=torch.uint8, device=dev)
         amb_off = torch.empty(2 * M + 1, dtype=torch.int64, device=dev)
         total = torch.empty(1, dtype=torch.int64, device=dev)
-        _lib.rigl_count(view, thr, Gp, nrm_dY, nrm_X, dY.shape[1], info, amb_off, total)
+        _lib.rigl_count(view, thr, Gp, Gc, nrm_dY, nrm_X, dY.shape[1], info, amb_off, total)
         n_amb = int(total.item())
         if n_amb > self._RIGL_EXACT_SHARE * max(1, M * K - self._nnz):
-            del Gp
+            del Gp, Gc
             from .ops import dense_grad
             self._drop_grow(k_drop, _lib.SLK_GROW_GRADIENT, dense_grad(dY, X))
             return
         amb = torch.empty(max(8, 8 * n_amb), dtype=torch.uint8, device=dev)
         stage = torch.empty(_lib.drop_grow_workspace_bytes(view), dtype=torch.uint8, device=dev)
         removed = torch.empty(1, dtype=torch.int64, device=dev)
-        _lib.rigl_finish(view, thr, Gp, nrm_dY, nrm_X, dY, X, info, amb_off, amb, stage, removed)
+        _lib.rigl_finish(view, thr, Gp, Gc, nrm_dY, nrm_X, dY, X, info, amb_off, amb, stage,
+                         removed)
         self._after_topology_pass(int(removed.item()))
 
     def _after_topology_pass(self, lost: int) -> None:

@@ -437,9 +437,11 @@ def _rigl_inputs(M, K, N, seed, kind="normal"):
     (256, 384, 4096, "normal"), (130, 257, 1000, "normal"), (64, 64, 7, "normal"),
     (300, 200, 513, "scaled"), (128, 128, 1, "normal"), (200, 300, 96, "ties")])
 def test_dense_grad_approx_within_certified_bound(dev, M, K, N, kind):
-    """|G' - G| <= c_N·n_i·n_k + 2^-100·(1 + n_i + n_k) for every element, G
-    the reference-arithmetic dense gradient (itself pinned to the reference
-    build); the norms bound the true row norms."""
+    """|G' - G| <= c1·n_i·n_k + c2·2^(code - 127) + 2^-100·(1 + n_i + n_k) for
+    every element, G the reference-arithmetic dense gradient (itself pinned to
+    the reference build); the norms bound the true row norms, and each code
+    bounds the element's sum of |partial sums| at the 128-term chunk ends
+    (checked against float64 partial sums)."""
     print(f"[rigl bound] {M}x{K} N={N} {kind}", flush=True)
     dY_np, X_np = _rigl_inputs(M, K, N, M + K + N, kind)
     dY, X = torch.from_numpy(dY_np).to(dev), torch.from_numpy(X_np).to(dev)
@@ -451,11 +453,27 @@ def test_dense_grad_approx_within_certified_bound(dev, M, K, N, kind):
     assert np.all(nd.cpu().numpy().astype(np.float64) >= nd64)
     assert np.all(nx.cpu().numpy().astype(np.float64) >= nx64)
     Gp = torch.empty(M, K, device=dev)
-    _lib.dense_grad_approx(dY, X, Gp)
+    Gc = torch.empty(M, K, dtype=torch.uint8, device=dev)
+    _lib.dense_grad_approx(dY, X, Gp, Gc)
     G = ops.dense_grad(dY, X).cpu().numpy().astype(np.float64)
-    c = _lib.rigl_bound_factor(N)
-    E = (c * nd.cpu().numpy().astype(np.float64)[:, None] * nx.cpu().numpy().astype(np.float64)[None, :]
-         + 2.0 ** -100 * (1 + nd.cpu().numpy()[:, None] + nx.cpu().numpy()[None, :]))
+    c1, c2 = _lib.rigl_bound_factor(N), _lib.rigl_partial_factor(N)
+    code = Gc.cpu().numpy().astype(np.float64)
+    assert np.all((code >= 1) & (code <= 255))
+    pbound = np.exp2(code - 127.0)
+    # the codes bound the exact partial sums' magnitudes, up to the
+    # approximation's own error (C·c_approx·n_i·n_k, c_approx < 1e-4, which the
+    # bound's c1 carries)
+    x64, y64 = dY_np.astype(np.float64), X_np.astype(np.float64)
+    if np.all(np.isfinite(x64)) and np.all(np.isfinite(y64)) and np.max(np.abs(x64)) < 1e15:
+        pm = np.zeros((M, K))
+        for j0 in range(0, N, 128):
+            part = x64[:, :min(N, j0 + 128)] @ y64[:, :min(N, j0 + 128)].T
+            pm += np.abs(part)
+        nn = (np.linalg.norm(x64, axis=1)[:, None] * np.linalg.norm(y64, axis=1)[None, :])
+        slack = -(-N // 128) * 1e-4 * nn + 2.0 ** -90
+        assert np.all(pm <= pbound * (1 + 1e-5) + slack), float(np.max(pm / (pbound + slack)))
+    E = (c1 * nd.cpu().numpy().astype(np.float64)[:, None] * nx.cpu().numpy().astype(np.float64)[None, :]
+         + c2 * pbound + 2.0 ** -100 * (1 + nd.cpu().numpy()[:, None] + nx.cpu().numpy()[None, :]))
     err = np.abs(Gp.cpu().numpy().astype(np.float64) - G)
     assert np.all(err <= E), float(np.max(err / E))
     # the bound is a bound, not noise: the approximation is far inside it
