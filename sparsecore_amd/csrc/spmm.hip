@@ -637,13 +637,17 @@ int launch_lds(int h, int rw, const slk_csr* W, const int32_t* order, int64_t P,
     if (h == 2) {
         switch (rw) {
             case 2: return launch_lds_rw<2, 2>(W, order, P, X, N, bias, Y, st);
+            case 3: return launch_lds_rw<3, 2>(W, order, P, X, N, bias, Y, st);
             case 4: return launch_lds_rw<4, 2>(W, order, P, X, N, bias, Y, st);
+            case 6: return launch_lds_rw<6, 2>(W, order, P, X, N, bias, Y, st);
             default: return launch_lds_rw<8, 2>(W, order, P, X, N, bias, Y, st);
         }
     }
     switch (rw) {
         case 2: return launch_lds_rw<2>(W, order, P, X, N, bias, Y, st);
+        case 3: return launch_lds_rw<3>(W, order, P, X, N, bias, Y, st);
         case 4: return launch_lds_rw<4>(W, order, P, X, N, bias, Y, st);
+        case 6: return launch_lds_rw<6>(W, order, P, X, N, bias, Y, st);
         default: return launch_lds_rw<8>(W, order, P, X, N, bias, Y, st);
     }
 }
@@ -860,7 +864,11 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
         const double density =
             K > 0 ? static_cast<double>(W->total_capacity) / (1.2 * M * K) : 0.0;
         double best = 0.0;
-        for (const int cfg : {18, 14, 12, 28, 24, 22}) {  // h * 10 + rw
+        // (3 and 6 rows per wave fit row counts such as 768 and 2304 to whole
+        // rounds of 256 workgroups: the 60M-GPT QKV input gradient, 768 rows,
+        // is 192 workgroups at 4 rows and 256 at 3; 6 rows with 8 columns per
+        // lane would spill registers, so it is not offered)
+        for (const int cfg : {18, 16, 14, 13, 12, 28, 24, 23, 22}) {  // h * 10 + rw
             const int ch = cfg / 10, crw = cfg % 10;
             // 8 rows x 8 columns per lane: rows of uniform length only (the
             // light rows of a skewed matrix run slower with it: 16384^2
@@ -884,7 +892,7 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
     if (rw != 0) {
         if (const int64_t t = tuning(SLK_TUNE_SPMM_H); t >= 0) h = t == 2 ? 2 : 1;
         if (const int64_t t = tuning(SLK_TUNE_SPMM_RW); t >= 0) rw = static_cast<int>(t);
-        if (rw != 2 && rw != 4 && rw != 8) rw = 8;
+        if (rw != 2 && rw != 3 && rw != 4 && rw != 6 && rw != 8) rw = 8;
         // Heavy rows (the head of the longest-rows-first order) in workgroups
         // of their own with two rows per wave and 8 columns per lane, then the
         // rest in that order, so every workgroup holds rows of similar length:
