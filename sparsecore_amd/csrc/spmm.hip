@@ -320,9 +320,9 @@ __global__ __launch_bounds__(kSpmmBlock) void spmm_group_kernel(
 // 256-column halves for RW rows in registers (H = 2 halves the readlane,
 // address and loop work per fma; measured 5-17% faster on the denser GPT
 // layers). X is streamed through LDS in chunks of 80/H rows x 256·H columns
-// (1 KB per X row and half), double-buffered: chunk c+1 is loaded into registers while
-// chunk c is read from LDS and is then written to the other buffer, so one
-// barrier per chunk orders both. For each chunk every row consumes its slots
+// (1 KB per X row and half), double-buffered: chunk c+1 is loaded straight
+// into the other buffer (direct global-to-LDS loads) while chunk c is read,
+// so one barrier per chunk orders both. For each chunk every row consumes its slots
 // whose column falls in the chunk; columns ascend within a row, so walking
 // the chunks in order visits each row's slots in slot order and every
 // element's fma chain is exactly the reference's. Each X element is fetched
@@ -350,6 +350,13 @@ __device__ __forceinline__ void lds_window(const int32_t* __restrict__ col,
     const int32_t s = at + lane;
     c = s < end ? col[s] : INT32_MAX;  // past the row: never below a chunk end
     v = s < end ? val[s] : 0.0f;
+}
+
+// One wave's direct load of 64 x 16 bytes into LDS (global_load_lds_dwordx4):
+// lane l's 16 bytes from src go to row + l (row: the wave's common LDS
+// address, 1 KB).
+__device__ __forceinline__ void lds_load_row(const void* src, f32x4* row) {
+    __builtin_amdgcn_global_load_lds(src, row, 16, 0, 0);
 }
 
 __device__ __forceinline__ void fma4(float v, const f32x4& x, f32x4& acc) {
@@ -411,9 +418,11 @@ __device__ __forceinline__ void spmm_lds_body(
         for (int h = 0; h < H; ++h) acc[j][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    // thread t stages piece t + 1024i (i < kStage) of the chunk: X row
-    // p / (64H), half (p / 64) mod H, lane p mod 64
-    f32x4 pre[kStage];
+    // The chunk is staged by direct loads into LDS (global_load_lds_dwordx4:
+    // lane l of a wave writes its 16 bytes at the instruction's LDS base +
+    // 16 l), one 1 KB row-half per wave instruction: wave w's load i fills
+    // row-half w + 16i, i.e. X row (w + 16i) / H, half (w + 16i) mod H, so no
+    // registers hold the next chunk and no LDS stores copy it.
     // Piece i's byte offset from the chunk's first X row (KC·N·4 < 2^32: the
     // launcher's bar), its columns clamped into the row where they pass N
     // (lanes whose columns pass N never store theirs): a full chunk is a
@@ -426,36 +435,29 @@ __device__ __forceinline__ void spmm_lds_body(
         const int64_t nn = tile * (H * kLdsCols) + ((p / kWave) % H) * kLdsCols + 4 * (p % kWave);
         poff[i] = static_cast<uint32_t>(((p / (H * kWave)) * N + (nn < N ? nn : N - 4)) * 4);
     }
-    auto prefetch = [&](int64_t k0) {
+    auto prefetch = [&](int buf, int64_t k0) {  // chunk at X row k0 into xs[buf]
         const char* xb = reinterpret_cast<const char*>(X + k0 * N);
-        if (k0 + KC <= K) {  // workgroup-uniform
-#pragma unroll
-            for (int i = 0; i < kStage; ++i)
-                pre[i] = *reinterpret_cast<const f32x4*>(xb + poff[i]);
-        } else {
-#pragma unroll
-            for (int i = 0; i < kStage; ++i) {
-                const int64_t kr = (threadIdx.x + i * kLdsThreads) / (H * kWave);
-                const int64_t back = k0 + kr < K ? 0 : (k0 + kr - (K - 1)) * N * 4;
-                pre[i] = *reinterpret_cast<const f32x4*>(xb + poff[i] - back);
-            }
-        }
-    };
-    auto stage = [&](int b) {
+        const bool full = k0 + KC <= K;  // workgroup-uniform
 #pragma unroll
         for (int i = 0; i < kStage; ++i) {
-            const int p = threadIdx.x + i * kLdsThreads;
-            xs[b][p / (H * kWave)][(p / kWave) % H][p % kWave] = pre[i];
+            const int q = w + i * kLdsWaves;  // the wave's row-half: wave-uniform
+            int64_t back = 0;
+            if (!full) {
+                const int64_t kr = q / H;
+                back = k0 + kr < K ? 0 : (k0 + kr - (K - 1)) * N * 4;
+            }
+            lds_load_row(xb + poff[i] - back, &xs[buf][q / H][q % H][0]);
         }
     };
     const int64_t nchunks = ceil_div(K, KC);
-    prefetch(0);
-    stage(0);
+    prefetch(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's direct loads have landed
     __syncthreads();
     for (int64_t ch = 0; ch < nchunks; ++ch) {
         const int b = static_cast<int>(ch & 1);
         const bool more = ch + 1 < nchunks;
-        if (more) prefetch((ch + 1) * KC);
+        // the other buffer's last readers (chunk ch - 1) passed the barrier
+        if (more) prefetch(b ^ 1, (ch + 1) * KC);
         const int32_t k0 = static_cast<int32_t>(ch * KC);
         const int32_t k1 = k0 + KC;
 #pragma unroll
@@ -515,7 +517,7 @@ __device__ __forceinline__ void spmm_lds_body(
                 first = 0;
             }
         }
-        if (more) stage(b ^ 1);
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of chunk ch + 1 have landed
         __syncthreads();
     }
 #pragma unroll
@@ -866,9 +868,8 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
         double best = 0.0;
         // (3 and 6 rows per wave fit row counts such as 768 and 2304 to whole
         // rounds of 256 workgroups: the 60M-GPT QKV input gradient, 768 rows,
-        // is 192 workgroups at 4 rows and 256 at 3; 6 rows with 8 columns per
-        // lane would spill registers, so it is not offered)
-        for (const int cfg : {18, 16, 14, 13, 12, 28, 24, 23, 22}) {  // h * 10 + rw
+        // is 192 workgroups at 4 rows and 256 at 3)
+        for (const int cfg : {18, 16, 14, 13, 12, 28, 26, 24, 23, 22}) {  // h * 10 + rw
             const int ch = cfg / 10, crw = cfg % 10;
             // 8 rows x 8 columns per lane: rows of uniform length only (the
             // light rows of a skewed matrix run slower with it: 16384^2

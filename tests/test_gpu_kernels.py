@@ -126,7 +126,7 @@ def test_spmm_every_vector_width(dev, tune, vec, N, per_row):
     assert_bits_equal(_spmm(W, _t(X_np, dev)).cpu().numpy(), oracle.spmm(c, X_np), "Y")
 
 
-@pytest.mark.parametrize("h,rw", [(1, 2), (1, 3), (1, 4), (1, 6), (1, 8), (2, 2), (2, 3), (2, 4), (2, 8)])
+@pytest.mark.parametrize("h,rw", [(1, 2), (1, 3), (1, 4), (1, 6), (1, 8), (2, 2), (2, 3), (2, 4), (2, 6), (2, 8)])
 @pytest.mark.parametrize("M,K,N,per_row", [
     (1, 1, 4, 1), (63, 127, 64, 40), (64, 128, 256, 128), (65, 129, 260, 100),
     (200, 300, 1000, 37), (130, 1000, 200, 700), (70, 5000, 96, 3000), (33, 260, 132, 0),
@@ -289,7 +289,7 @@ def test_gather_path_skewed_rows_wide_N_bit_exact(dev):
     assert_bits_equal(Y.cpu().numpy(), want + b_np[:, None], "Y+bias")
 
 
-@pytest.mark.parametrize("h,rw", [(1, 2), (1, 3), (1, 4), (1, 6), (1, 8), (2, 2), (2, 3), (2, 4), (2, 8)])
+@pytest.mark.parametrize("h,rw", [(1, 2), (1, 3), (1, 4), (1, 6), (1, 8), (2, 2), (2, 3), (2, 4), (2, 6), (2, 8)])
 def test_row_order_lds_kernel_bit_exact(dev, tune, h, rw):
     """Every LDS-staged kernel variant gives the natural order's bits whatever
     row schedule the view carries (the longest-first one, a random
@@ -319,7 +319,7 @@ def test_row_order_lds_kernel_bit_exact(dev, tune, h, rw):
         assert_bits_equal(Y.cpu().numpy(), want + b_np[:, None], f"Y+bias ({name} order)")
 
 
-@pytest.mark.parametrize("h,rw", [(1, 2), (1, 3), (1, 4), (1, 6), (1, 8), (2, 2), (2, 3), (2, 4), (2, 8)])
+@pytest.mark.parametrize("h,rw", [(1, 2), (1, 3), (1, 4), (1, 6), (1, 8), (2, 2), (2, 3), (2, 4), (2, 6), (2, 8)])
 def test_lds_heavy_row_split_bit_exact(dev, tune, h, rw):
     """A skewed matrix's heavy rows (the head of the longest-first order) run
     as their own LDS launch and the rest as a second one: the bits are the
