@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define SLK_ABI_VERSION 11
+#define SLK_ABI_VERSION 12
 
 #if defined(__GNUC__)
 #define SLK_API __attribute__((visibility("default")))
@@ -143,6 +143,8 @@ SLK_API int slk_abi_version(void);
  *   SLK_TUNE_SDDMM_G      windowed dW kernel: groups per wave (1, 2 or 4)
  *   SLK_TUNE_SEG_LEAN     segment dW kernel: 1 = lean variant, 0 = not
  *   SLK_TUNE_SEG_GROUP    segment dW kernel: segments per workgroup (64 or 128)
+ *   SLK_TUNE_TRANSPOSE_TILE transpose fill: 0 = one workgroup per row block over
+ *                         all columns instead of row x column tiles
  * Returns SLK_EINVAL for an unknown knob.                                   */
 enum slk_tune_knob {
     SLK_TUNE_SPMM_KERNEL = 0,
@@ -153,7 +155,8 @@ enum slk_tune_knob {
     SLK_TUNE_SDDMM_G = 5,
     SLK_TUNE_SEG_LEAN = 6,
     SLK_TUNE_SEG_GROUP = 7,
-    SLK_TUNE_COUNT = 8
+    SLK_TUNE_TRANSPOSE_TILE = 8,
+    SLK_TUNE_COUNT = 9
 };
 SLK_API int slk_set_tuning(int knob, int64_t value);
 

@@ -21,7 +21,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libsparsecore_amd.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 SLK_OK, SLK_EINVAL, SLK_EDEVICE = 0, 1, 2
 SLK_DW_SIMD, SLK_DW_SCALAR = 0, 1
@@ -70,7 +70,7 @@ DROP_GROW_NOALLOC_MAX_SLOTS = 1 << 21  # SLK_DROP_GROW_NOALLOC_MAX_SLOTS
 
 # Kernel-choice overrides (slk_set_tuning): knob numbers of enum slk_tune_knob.
 TUNE_KNOBS = {"spmm_kernel": 0, "spmm_h": 1, "spmm_rw": 2, "spmm_split": 3, "spmm_vec": 4,
-              "sddmm_g": 5, "seg_lean": 6, "seg_group": 7}
+              "sddmm_g": 5, "seg_lean": 6, "seg_group": 7, "transpose_tile": 8}
 
 SEG_GROUP = 128  # SLK_SEG_GROUP
 

@@ -7,11 +7,19 @@ namespace slk {
 
 namespace {
 thread_local std::string g_last_error;
-// Kernel-choice overrides, process-wide; -1 = the launcher's own choice.
-std::atomic<int64_t> g_tuning[SLK_TUNE_COUNT] = {-1, -1, -1, -1, -1, -1, -1};
+// Kernel-choice overrides, process-wide; -1 = the launcher's own choice
+// (every knob, whatever their number: a braced list shorter than the array
+// would leave the rest at 0).
+struct Tuning {
+    std::atomic<int64_t> v[SLK_TUNE_COUNT];
+    Tuning() {
+        for (auto& x : v) x.store(-1, std::memory_order_relaxed);
+    }
+};
+Tuning g_tuning;
 }
 
-int64_t tuning(int knob) { return g_tuning[knob].load(std::memory_order_relaxed); }
+int64_t tuning(int knob) { return g_tuning.v[knob].load(std::memory_order_relaxed); }
 
 int fail(int code, const std::string& msg) {
     g_last_error = msg;
@@ -79,6 +87,6 @@ extern "C" int slk_set_tuning(int knob, int64_t value) {
     if (knob < 0 || knob >= SLK_TUNE_COUNT) {
         return slk::fail(SLK_EINVAL, "set_tuning: unknown knob " + std::to_string(knob));
     }
-    slk::g_tuning[knob].store(value < 0 ? -1 : value, std::memory_order_relaxed);
+    slk::g_tuning.v[knob].store(value < 0 ? -1 : value, std::memory_order_relaxed);
     return SLK_OK;
 }

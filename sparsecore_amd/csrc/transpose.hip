@@ -262,6 +262,106 @@ __global__ __launch_bounds__(kParScatterThreads) void tr_scatter_par_kernel(
     }
 }
 
+// T5 by tiles of kTileSub blocks (of B <= 32 rows) x kTileCols columns, one
+// 1024-thread workgroup each: the same positions as tr_scatter_par_kernel
+// (start of WT row c + the block's start in it + the earlier rows of the
+// block marked at c), but a workgroup's writes now fall into kTileCols WT
+// rows, a run of about B·kTileSub·density consecutive slots in each, which
+// the L2 merges into whole lines before they reach HBM. (A workgroup per
+// block over all columns writes one or two slots per WT row: every write a
+// partial line.) Each row's slots of the tile are found by binary search on
+// its columns; the tile's slots are then visited flat, a slot's row found by
+// binary search over the rows' run offsets in LDS.
+constexpr int kTileSub = 32;
+constexpr int kTileCols = 512;
+constexpr int kTileThreads = 1024;
+static_assert(kTileSub * kParScatterMaxRows <= kTileThreads, "one boundary per thread and row");
+
+__global__ __launch_bounds__(kTileThreads) void tr_scatter_tile_kernel(
+    int64_t M, int64_t K, int64_t B, int64_t nblk, int64_t ntc,
+    const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
+    const int32_t* __restrict__ col, const float* __restrict__ val,
+    const int32_t* __restrict__ bh, const int32_t* __restrict__ start_t,
+    float* __restrict__ val_t, int32_t* __restrict__ col_t, int64_t* __restrict__ perm) {
+    __shared__ uint32_t mask[kTileSub][kTileCols];  // 64 KiB
+    __shared__ int32_t lo[kTileThreads], hi[kTileThreads];
+    __shared__ int32_t pre[kTileThreads];  // exclusive offsets of the rows' runs
+    __shared__ int32_t wsum[kTileThreads / kWave];
+    __shared__ int32_t s_total;
+    const int t = threadIdx.x;
+    const int64_t tr = blockIdx.x / ntc, tc = blockIdx.x % ntc;
+    const int64_t b0 = tr * kTileSub;
+    const int64_t nsub = nblk - b0 < kTileSub ? nblk - b0 : kTileSub;
+    const int64_t r0 = b0 * B;
+    const int64_t r1 = (b0 + nsub) * B < M ? (b0 + nsub) * B : M;
+    const int R = static_cast<int>(r1 - r0);  // <= kTileSub * B <= 1024
+    const int32_t c0 = static_cast<int32_t>(tc * kTileCols);
+    const int32_t c1 = static_cast<int32_t>(c0 + kTileCols < K ? c0 + kTileCols : K);
+    for (int u = t; u < kTileSub * kTileCols; u += kTileThreads) (&mask[0][0])[u] = 0;
+    // each row's run of columns in [c0, c1): lo = first slot with col >= c0,
+    // hi = first with col >= c1 (live columns ascend within a row)
+    for (int i = t; i < 2 * R; i += kTileThreads) {
+        const int rl = i < R ? i : i - R;
+        const int32_t bound = i < R ? c0 : c1;
+        const int64_t s0 = row_start[r0 + rl];
+        int32_t a = 0, e = row_nnz[r0 + rl];
+        while (a < e) {
+            const int32_t m = (a + e) >> 1;
+            if (col[s0 + m] < bound) a = m + 1;
+            else e = m;
+        }
+        if (i < R) lo[rl] = a;
+        else hi[rl] = a;
+    }
+    __syncthreads();
+    {  // exclusive scan of the run lengths (rows past R: 0)
+        const int len = t < R ? hi[t] - lo[t] : 0;
+        const int lane = t & (kWave - 1), w = t / kWave;
+        int v = len;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int up = __shfl_up(v, off);
+            if (lane >= off) v += up;
+        }
+        if (lane == kWave - 1) wsum[w] = v;
+        __syncthreads();
+        int base = 0;
+        for (int q = 0; q < w; ++q) base += wsum[q];
+        pre[t] = base + v - len;
+        if (t == kTileThreads - 1) s_total = base + v;
+        __syncthreads();
+    }
+    const int total = s_total;
+    auto row_of = [&](int e) -> int {  // the last row whose run starts at or before e
+        int a = 0, b = R - 1;
+        while (a < b) {
+            const int m = (a + b + 1) >> 1;
+            if (pre[m] <= e) a = m;
+            else b = m - 1;
+        }
+        return a;
+    };
+    for (int e = t; e < total; e += kTileThreads) {
+        const int rl = row_of(e);
+        const int64_t s = row_start[r0 + rl] + lo[rl] + (e - pre[rl]);
+        const int32_t c = col[s];
+        atomicOr(&mask[rl / B][c - c0], 1u << (rl % B));
+    }
+    __syncthreads();
+    for (int e = t; e < total; e += kTileThreads) {
+        const int rl = row_of(e);
+        const int64_t s = row_start[r0 + rl] + lo[rl] + (e - pre[rl]);
+        const int32_t c = col[s];
+        const int64_t sb = rl / B;
+        const uint32_t below = (1u << (rl % B)) - 1u;
+        const int64_t pos = static_cast<int64_t>(start_t[c]) + bh[(b0 + sb) * K + c] +
+                            __popc(mask[sb][c - c0] & below);
+        perm[pos] = s;
+        col_t[pos] = static_cast<int32_t>(r0 + rl);
+        val_t[pos] = val[s];
+    }
+}
+
 __global__ __launch_bounds__(256) void tr_refresh_kernel(const float* __restrict__ w_val,
                                                          int64_t w_cap,
                                                          const int64_t* __restrict__ perm,
@@ -358,6 +458,20 @@ extern "C" int slk_transpose_fill(const slk_csr* W, const void* workspace, int64
     if (int rc = check_launch("transpose_fill/pad")) return rc;
     if (p.nblk == 0) return SLK_OK;
     const size_t lds = static_cast<size_t>(K < kColChunk ? K : kColChunk) * sizeof(int32_t);
+    // tiles where a row block spans many columns' worth of WT rows
+    if (p.rows_per_block <= kParScatterMaxRows && K >= kTileCols &&
+        tuning(SLK_TUNE_TRANSPOSE_TILE) != 0) {
+        const int64_t ntc = ceil_div(K, int64_t{kTileCols});
+        const int64_t tiles = ceil_div(p.nblk, int64_t{kTileSub}) * ntc;
+        if (tiles <= INT32_MAX) {
+            hipLaunchKernelGGL(tr_scatter_tile_kernel, dim3(static_cast<unsigned>(tiles)),
+                               dim3(kTileThreads), 0, st, M, K, p.rows_per_block, p.nblk, ntc,
+                               W->row_start, W->row_nnz, W->col_indices, W->values,
+                               static_cast<const int32_t*>(workspace), WT_row_start, WT_values,
+                               WT_col_indices, perm);
+            return check_launch("transpose_fill/scatter");
+        }
+    }
     if (p.rows_per_block <= kParScatterMaxRows) {
         hipLaunchKernelGGL(tr_scatter_par_kernel, dim3(static_cast<unsigned>(p.nblk)),
                            dim3(kParScatterThreads), lds, st, M, K, p.rows_per_block,

@@ -478,6 +478,26 @@ def test_transpose_bit_exact(dev, M, K, sparsity, pr):
     WT.assert_invariants()
 
 
+@pytest.mark.parametrize("M,K,kind", [
+    (2000, 1000, "uniform"), (1300, 3000, "zipf"), (777, 5000, "uniform"), (4100, 700, "zipf"),
+    (70, 20000, "uniform")])
+def test_transpose_tiles_bit_exact(dev, tune, M, K, kind):
+    """The row x column tiled scatter (the default where a row block is at most
+    32 rows and ncols >= 512) gives the oracle's WT and perm, as does the
+    one-workgroup-per-row-block scatter it replaces: partial row and column
+    tiles, skewed rows."""
+    print(f"[transpose tiles] {M}x{K} {kind}", flush=True)
+    c = (oracle.zipf_rows(M, K, 0.03, 1.1, seed=M, sigma=1.0) if kind == "zipf"
+         else oracle.uniform_rows(M, K, max(1, K // 40), seed=M))
+    W = from_oracle(c, dev)
+    WT_o, perm_o = oracle.transpose_with_perm(c)
+    for tile in (None, 0):
+        tune(transpose_tile=tile)
+        WT, perm = layout.transpose_with_perm(W)
+        csr_arrays_equal(to_oracle(WT), WT_o, f"WT tile={tile}")
+        assert_bits_equal(perm.cpu().numpy(), perm_o, f"perm tile={tile}")
+
+
 def test_transpose_wide_matrix_uses_column_chunks(dev):
     """ncols > 16384 exercises the multi-pass (column-chunked) LDS counters."""
     c = oracle.uniform_rows(40, 40000, 300, seed=4)
