@@ -331,12 +331,26 @@ __device__ __forceinline__ float up_(float x) { return x * (1.0f + 0x1p-20f) + 0
 __device__ __forceinline__ float dn_(float x) { return x * (1.0f - 0x1p-20f) - 0x1p-120f; }
 constexpr float kNormCap = 0x1p60f;  // norms above this make the row exact
 
-// The per-column error E_k = up(cni·n_k) + delta + up(c2·2^(code - 127))
-// >= c_N·n_i·n_k + the absolute part (delta = up(2^-100·(1 + n_i + max n_k)))
-// + c2·(the element's sum of |partial sums|).
+// The per-column error E_k >= c_N·n_i·n_k + the absolute part (delta =
+// up(2^-100·(1 + n_i + max n_k))) + c2·(the element's sum of |partial
+// sums|): two fmas (c2·2^(code - 127) is exact), each rounding by at most u,
+// then raised by 2^-20 relative (> 2u) and 2^-120 absolute.
 __device__ __forceinline__ float col_err(float cni, float nk, float delta, float c2,
                                          uint32_t code) {
-    return up_(up_(cni * nk) + delta + up_(c2 * partial_bound(code)));
+    return fmaf(fmaf(cni, nk, fmaf(c2, partial_bound(code), delta)), 1.0f + 0x1p-20f, 0x1p-120f);
+}
+
+// A column's class for the row's thresholds t_in / t_out (kGrowIn: |G| is
+// certainly above the n_grow-th largest; kGrowOut: certainly below;
+// otherwise undecided; a NaN |G'| is undecided). E_k as in col_err but
+// unraised; each sum with it is raised by 2^-20 relative (covering its own
+// rounding and E_k's two) and 2^-120 absolute before the compare.
+constexpr int kGrowOut = 0, kGrowIn = 1, kGrowUndecided = 2;
+__device__ __forceinline__ int classify_col(float a, float cni, float nk, float delta, float c2,
+                                            uint32_t code, float t_in, float t_out) {
+    const float ek = fmaf(cni, nk, fmaf(c2, partial_bound(code), delta));
+    if (a > fmaf(t_in + ek, 1.0f + 0x1p-20f, 0x1p-120f)) return kGrowIn;
+    return fmaf(a + ek, 1.0f + 0x1p-20f, 0x1p-120f) < t_out ? kGrowOut : kGrowUndecided;
 }
 
 // Largest-first selection key of a non-negative float.
@@ -626,10 +640,10 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             if (!((cand >> (4 * u + e)) & 1ull)) continue;
-            const float ek = col_err(cni, nr[u][e], delta, c2, (cw >> (8 * e)) & 255u);
-            const float g = __uint_as_float(~a[u][e]);
-            if (dn_(g - ek) > t_in) ++n_in;
-            else if (!(up_(g + ek) < t_out)) ++n_amb;
+            const int cls = classify_col(__uint_as_float(~a[u][e]), cni, nr[u][e], delta, c2,
+                                         (cw >> (8 * e)) & 255u, t_in, t_out);
+            n_in += cls == kGrowIn;
+            n_amb += cls == kGrowUndecided;
         }
     }
     block_inclusive_scan(n_in, tmp);
@@ -732,10 +746,9 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_kernel(
     int64_t n_in = 0, n_amb = 0;
     for_each_col<V4>(g_row, nrm_c, c_row, K, [&](int64_t c, float g, float nk, uint32_t code) {
         if (bit_of(keep, c)) return;
-        const float a = fabsf(g);
-        const float e = col_err(cni, nk, delta, c2, code);
-        if (dn_(a - e) > t_in) ++n_in;
-        else if (!(up_(a + e) < t_out)) ++n_amb;
+        const int cls = classify_col(fabsf(g), cni, nk, delta, c2, code, t_in, t_out);
+        n_in += cls == kGrowIn;
+        n_amb += cls == kGrowUndecided;
     });
     block_inclusive_scan(n_in, tmp);
     n_in = tmp[kRowThreads - 1];
@@ -899,10 +912,9 @@ __global__ __launch_bounds__(kRowThreads) void rigl_list_kernel(
         for_each_col<VG>(Gp + i * ldg, nrm_c, Gc + i * K, K,
                          [&](int64_t c, float g, float nk, uint32_t code) {
             if (bit_of(keep, c)) return;
-            const float a = fabsf(g);
-            const float e = col_err(ri.cni, nk, ri.delta, c2, code);
-            if (dn_(a - e) > ri.t_in) atomicOr(&grow[c >> 5], 1u << (c & 31));
-            else if (!(up_(a + e) < ri.t_out)) atomicOr(&ambm[c >> 5], 1u << (c & 31));
+            const int cls = classify_col(fabsf(g), ri.cni, nk, ri.delta, c2, code, ri.t_in, ri.t_out);
+            if (cls == kGrowIn) atomicOr(&grow[c >> 5], 1u << (c & 31));
+            else if (cls == kGrowUndecided) atomicOr(&ambm[c >> 5], 1u << (c & 31));
         });
     }
     __syncthreads();
