@@ -394,14 +394,14 @@ __device__ __forceinline__ void spmm_lds_body(
     }
     const int64_t r0 = rb * (kLdsWaves * RW) + w;
 
-    // PREF: the next window is requested as soon as a window is entered; the
-    // 8-row, 8-column-per-lane variant loads it when needed instead (its
-    // registers are spent on the wider accumulators; its rows are the light ones)
-    constexpr bool PREF = !(RW == 8 && H == 2);
-    constexpr int G = PREF ? 4 : 2;  // slots per group of LDS reads
-    constexpr int RN = PREF ? RW : 1;
-    int32_t rows[RW], pos[RW], end[RW], base[RW], mc[RW], nmc[RN];  // rows[j] < 0: none
-    float mv[RW], nmv[RN];
+    // The next window is requested as soon as a window is entered, so a row
+    // never waits on its stream inside a chunk (a wait there holds all 16
+    // waves at the next barrier). The 8-row, 8-column-per-lane variant keeps
+    // two slots' reads in flight instead of four to stay within 128 VGPRs
+    // (four spill).
+    constexpr int G = (RW == 8 && H == 2) ? 2 : 4;  // slots per group of LDS reads
+    int32_t rows[RW], pos[RW], end[RW], base[RW], mc[RW], nmc[RW];  // rows[j] < 0: none
+    float mv[RW], nmv[RW];
     f32x4 acc[RW][H];
 #pragma unroll
     for (int j = 0; j < RW; ++j) {
@@ -413,7 +413,7 @@ __device__ __forceinline__ void spmm_lds_body(
         pos[j] = base[j] = s;
         end[j] = e;
         lds_window(col, val, s, e, lane, mc[j], mv[j]);
-        if constexpr (PREF) lds_window(col, val, s + kWave, e, lane, nmc[j], nmv[j]);
+        lds_window(col, val, s + kWave, e, lane, nmc[j], nmv[j]);
 #pragma unroll
         for (int h = 0; h < H; ++h) acc[j][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
@@ -507,13 +507,9 @@ __device__ __forceinline__ void spmm_lds_body(
                 if (first + cnt < kWave) break;  // the run ended inside this window
                 // window used up: shift the next one in and request the one after
                 base[j] += kWave;
-                if constexpr (PREF) {
-                    mc[j] = nmc[j];
-                    mv[j] = nmv[j];
-                    lds_window(col, val, base[j] + kWave, end[j], lane, nmc[j], nmv[j]);
-                } else {
-                    lds_window(col, val, base[j], end[j], lane, mc[j], mv[j]);
-                }
+                mc[j] = nmc[j];
+                mv[j] = nmv[j];
+                lds_window(col, val, base[j] + kWave, end[j], lane, nmc[j], nmv[j]);
                 first = 0;
             }
         }
@@ -873,8 +869,9 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
             const int ch = cfg / 10, crw = cfg % 10;
             // 8 rows x 8 columns per lane: rows of uniform length only (the
             // light rows of a skewed matrix run slower with it: 16384^2
-            // Zipf(1.1) forward 8.24 -> 8.51 ms, while its transpose runs
-            // 7.05 -> 6.60 ms)
+            // Zipf(1.1) at 95%, forward as one split grid 6.97 -> 7.94 ms
+            // against 8 rows x 4 columns, while its transpose runs 6.91 ->
+            // 5.69 ms)
             if (cfg == 28 && W->n_heavy_rows > 0) continue;
             if (density * kLdsWaves * crw < kLdsMinReuse) continue;
             if (lds_blocks(M, N, ch, crw) < kLdsMinBlocks) continue;
