@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define SLK_ABI_VERSION 12
+#define SLK_ABI_VERSION 13
 
 #if defined(__GNUC__)
 #define SLK_API __attribute__((visibility("default")))
@@ -112,6 +112,32 @@ typedef struct slk_csr {
      * bit, is the same. A schedule the caller caches per topology. */
     const int32_t* phase_lo;
     int64_t n_phases;
+    /* Optional (may be NULL): the binned slot stream of slk_spmm's
+     * LDS-staged kernel, as built by slk_bin_build for bin_rw rows per wave
+     * and bin_h column halves (X staged in chunks of 80 / bin_h rows). It
+     * covers positions p in [bin_first, nrows): rows row_order[p] when
+     * bin_first > 0 (the rows after the heavy ones), else rows p. Position
+     * p goes to unit u = (q / (16 bin_rw)) * 16 + q % 16 as its row j =
+     * (q / 16) % bin_rw, q = p - bin_first (a unit is one wave's rows).
+     * For unit u and chunk ch, the bytes of bin_cnt[(u * nchunks + ch) * 2]
+     * and [.. + 1] (byte j at bits 8 (j mod 4) of word j / 4) count row j's
+     * live slots whose column lies in the chunk, and the unit's slots are
+     * listed from bin_start[u] on (bin_start[units] = n_bin), chunk by chunk,
+     * row by row, in slot order: bin_off = the byte offset of the slot's X
+     * row inside the staged chunk, bin_slot = the slot's index into values
+     * (read through it, so the stream stays valid when values change). With
+     * it, slk_spmm runs those rows on the binned kernel, which reads each
+     * chunk's work of a wave as one run with its row counts known, and the
+     * rows before bin_first on the LDS-staged kernel; results are the same.
+     * A schedule the caller caches per topology. */
+    const int32_t* bin_off;
+    const int32_t* bin_slot;
+    const uint32_t* bin_cnt;
+    const int32_t* bin_start;
+    int64_t bin_first;
+    int64_t bin_rw;
+    int64_t bin_h;
+    int64_t n_bin;
 } slk_csr;
 
 /* Padding unit of a segment list: each column block's segments are padded
@@ -145,6 +171,8 @@ SLK_API int slk_abi_version(void);
  *   SLK_TUNE_SEG_GROUP    segment dW kernel: segments per workgroup (64 or 128)
  *   SLK_TUNE_TRANSPOSE_TILE transpose fill: 0 = one workgroup per row block over
  *                         all columns instead of row x column tiles
+ *   SLK_TUNE_SPMM_BIN     0 = ignore a binned slot stream (slk_csr.bin_off)
+ *   SLK_TUNE_SPMM_G       binned kernel: slots of a row read ahead (1, 2 or 4)
  * Returns SLK_EINVAL for an unknown knob.                                   */
 enum slk_tune_knob {
     SLK_TUNE_SPMM_KERNEL = 0,
@@ -156,7 +184,9 @@ enum slk_tune_knob {
     SLK_TUNE_SEG_LEAN = 6,
     SLK_TUNE_SEG_GROUP = 7,
     SLK_TUNE_TRANSPOSE_TILE = 8,
-    SLK_TUNE_COUNT = 9
+    SLK_TUNE_SPMM_BIN = 9,
+    SLK_TUNE_SPMM_G = 10,
+    SLK_TUNE_COUNT = 11
 };
 SLK_API int slk_set_tuning(int knob, int64_t value);
 
@@ -460,6 +490,38 @@ SLK_API int slk_seg_list_build(const slk_csr* W, int64_t block_cols, int64_t seg
  * every output bit unchanged.                                               */
 SLK_API int slk_phase_bounds_build(const slk_csr* W, int64_t n_phases, int32_t* phase_lo,
                                    void* stream);
+
+/* Sizes of the binned slot stream of slk_csr (see bin_off there) for W's
+ * positions [first, nrows), rw rows per wave (1, 2, 4 or 8) and h column
+ * halves (1 or 2): *units (wave units; bin_start has units + 1 entries,
+ * bin_cnt 2 * units * *nchunks words) and *nchunks (X chunks of 80 / h
+ * rows). SLK_EINVAL where the stream is not supported: bad arguments, or
+ * more than SLK_BIN_MAX_CHUNKS chunks (ncols beyond 80 * that / h).       */
+#define SLK_BIN_MAX_CHUNKS 960
+SLK_API int slk_bin_sizes(const slk_csr* W, int64_t first, int64_t rw, int64_t h,
+                          int64_t* units, int64_t* nchunks);
+
+/* Builds the binned slot stream (see bin_off in slk_csr) on the device: two
+ * launches, deterministic, no host read. n_bin (the length of bin_off and
+ * bin_slot) must be at least the live slots of the covered rows; bin_start
+ * receives units + 1 entries, bin_cnt 2 * units * nchunks words. Rows before
+ * `first` are W->row_order's first `first` (first > 0 needs row_order). No
+ * counterpart in the reference (csrc/kernels/spmm_avx2.cpp walks each row's
+ * slots in one pass): a visiting schedule for slk_spmm that leaves every
+ * output bit unchanged.                                                     */
+SLK_API int slk_bin_build(const slk_csr* W, int64_t first, int64_t rw, int64_t h,
+                          int32_t* bin_off, int32_t* bin_slot, int64_t n_bin,
+                          uint32_t* bin_cnt, int32_t* bin_start, void* stream);
+
+/* Diagnostic with no counterpart in the reference: n independent
+ * 32 x 32 x 16 bf16 matrix-core products with an fp32 accumulator, the
+ * instruction slk_dense_grad_approx accumulates G' with:
+ * D[t] = C[t] + A[t]·B[t]^T, A[t] and B[t] 32 x 16 bf16 (raw bits,
+ * row-major), C[t] and D[t] 32 x 32 float row-major. For checking the
+ * rounding model the certified RigL bound assumes (each accumulation step
+ * within 2u of its exact value relative to the magnitudes summed).          */
+SLK_API int slk_rigl_mfma_probe(const uint16_t* A, const uint16_t* B, const float* C, float* D,
+                                int64_t n, void* stream);
 
 #ifdef __cplusplus
 }

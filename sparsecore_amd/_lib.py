@@ -21,7 +21,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libsparsecore_amd.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 SLK_OK, SLK_EINVAL, SLK_EDEVICE = 0, 1, 2
 SLK_DW_SIMD, SLK_DW_SCALAR = 0, 1
@@ -62,6 +62,9 @@ EXPORTS = (
     "slk_rigl_partial_factor",
     "slk_rigl_count",
     "slk_rigl_finish",
+    "slk_bin_sizes",
+    "slk_bin_build",
+    "slk_rigl_mfma_probe",
 )
 
 RIGL_INFO_BYTES = 32  # per row, slk_rigl_count's info
@@ -70,7 +73,10 @@ DROP_GROW_NOALLOC_MAX_SLOTS = 1 << 21  # SLK_DROP_GROW_NOALLOC_MAX_SLOTS
 
 # Kernel-choice overrides (slk_set_tuning): knob numbers of enum slk_tune_knob.
 TUNE_KNOBS = {"spmm_kernel": 0, "spmm_h": 1, "spmm_rw": 2, "spmm_split": 3, "spmm_vec": 4,
-              "sddmm_g": 5, "seg_lean": 6, "seg_group": 7, "transpose_tile": 8}
+              "sddmm_g": 5, "seg_lean": 6, "seg_group": 7, "transpose_tile": 8, "spmm_bin": 9,
+              "spmm_g": 10}
+
+BIN_MAX_CHUNKS = 960  # SLK_BIN_MAX_CHUNKS
 
 SEG_GROUP = 128  # SLK_SEG_GROUP
 
@@ -101,6 +107,14 @@ class CsrView(ctypes.Structure):
         ("seg_slots", ctypes.c_int64),
         ("phase_lo", ctypes.c_void_p),
         ("n_phases", ctypes.c_int64),
+        ("bin_off", ctypes.c_void_p),
+        ("bin_slot", ctypes.c_void_p),
+        ("bin_cnt", ctypes.c_void_p),
+        ("bin_start", ctypes.c_void_p),
+        ("bin_first", ctypes.c_int64),
+        ("bin_rw", ctypes.c_int64),
+        ("bin_h", ctypes.c_int64),
+        ("n_bin", ctypes.c_int64),
     ]
 
 
@@ -159,6 +173,10 @@ def _declare(lib) -> None:
                                     _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp]
     lib.slk_drop_grow_noalloc.argtypes = [_csrp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _i64,
                                           ctypes.c_uint64, _vp, _vp]
+    lib.slk_bin_sizes.argtypes = [_csrp, _i64, _i64, _i64, ctypes.POINTER(_i64),
+                                  ctypes.POINTER(_i64)]
+    lib.slk_bin_build.argtypes = [_csrp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp]
+    lib.slk_rigl_mfma_probe.argtypes = [_vp, _vp, _vp, _vp, _i64, _vp]
     sized = ("slk_last_error", "slk_abi_version", "slk_transpose_workspace_bytes",
              "slk_drop_grow_workspace_bytes", "slk_rigl_bound_factor", "slk_rigl_partial_factor",
              "slk_dense_grad_approx_workspace_bytes",
@@ -372,6 +390,48 @@ def phase_bounds_build(view: CsrView, n_phases: int, device) -> torch.Tensor:
     if rc:
         _raise(rc)
     return lo
+
+
+def bin_sizes(view: CsrView, first: int, rw: int, h: int) -> tuple[int, int]:
+    """(units, chunks) of the binned slot stream (slk_bin_sizes); ValueError
+    where the stream is not supported (e.g. more than BIN_MAX_CHUNKS chunks)."""
+    units, nch = ctypes.c_int64(0), ctypes.c_int64(0)
+    rc = load().slk_bin_sizes(ctypes.byref(view), int(first), int(rw), int(h),
+                              ctypes.byref(units), ctypes.byref(nch))
+    if rc:
+        _raise(rc)
+    return units.value, nch.value
+
+
+def bin_build(view: CsrView, first: int, rw: int, h: int, n_bin: int, device):
+    """(bin_off, bin_slot, bin_cnt, bin_start) device arrays of the binned slot
+    stream of view's positions [first, nrows) (slk_bin_build); n_bin >= the
+    covered live slots."""
+    lib = load()
+    units, nch = bin_sizes(view, first, rw, h)
+    n = max(1, int(n_bin))
+    off = torch.empty(n, dtype=torch.int32, device=device)
+    slot = torch.empty(n, dtype=torch.int32, device=device)
+    cnt = torch.empty(max(1, 2 * units * nch), dtype=torch.int32, device=device)
+    start = torch.empty(units + 1, dtype=torch.int32, device=device)
+    rc = lib.slk_bin_build(ctypes.byref(view), int(first), int(rw), int(h), ptr(off), ptr(slot),
+                           int(n_bin), ptr(cnt), ptr(start), stream_of(start))
+    if rc:
+        _raise(rc)
+    return off, slot, cnt, start
+
+
+def rigl_mfma_probe(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, D: torch.Tensor) -> None:
+    """D[t] = C[t] + A[t]·B[t]ᵀ on the matrix cores, one 32x32x16 bf16 MFMA per
+    t (slk_rigl_mfma_probe): A, B int16 (bf16 bits) n x 32 x 16, C, D float32
+    n x 32 x 32, all contiguous."""
+    n = A.shape[0]
+    if (A.shape != (n, 32, 16) or B.shape != (n, 32, 16) or C.shape != (n, 32, 32)
+            or D.shape != (n, 32, 32)):
+        raise ValueError("rigl_mfma_probe: A, B must be n x 32 x 16 and C, D n x 32 x 32")
+    rc = load().slk_rigl_mfma_probe(ptr(A), ptr(B), ptr(C), ptr(D), n, stream_of(D))
+    if rc:
+        _raise(rc)
 
 
 def transpose_dense(src: torch.Tensor, dst: torch.Tensor) -> None:

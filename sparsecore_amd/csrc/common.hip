@@ -73,6 +73,17 @@ int validate_csr(const slk_csr* W, const char* who) {
         return fail(SLK_EINVAL, std::string(who) + ": phase_lo needs n_phases >= 1, got " +
                                     std::to_string(W->n_phases));
     }
+    if (W->bin_off != nullptr &&
+        (W->bin_slot == nullptr || W->bin_cnt == nullptr || W->bin_start == nullptr ||
+         W->n_bin < 0 || W->bin_first < 0 || W->bin_first > W->nrows ||
+         (W->bin_first > 0 && W->row_order == nullptr) ||
+         (W->bin_rw != 1 && W->bin_rw != 2 && W->bin_rw != 4 && W->bin_rw != 8) ||
+         (W->bin_h != 1 && W->bin_h != 2))) {
+        return fail(SLK_EINVAL, std::string(who) +
+                                    ": a binned stream needs bin_slot, bin_cnt, bin_start, "
+                                    "n_bin >= 0, bin_first in [0, nrows] (row_order if > 0), "
+                                    "bin_rw 1, 2, 4 or 8 and bin_h 1 or 2");
+    }
     return SLK_OK;
 }
 

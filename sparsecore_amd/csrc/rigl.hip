@@ -13,18 +13,23 @@
 //   approx   G' = dY·X^T on the matrix cores: every fp32 operand is split into
 //            bf16 parts, x = x_h + x_l + r (|r| <= 2^-16 |x|, round to nearest
 //            even), and G' = Σ x_h y_h + Σ (x_h y_l + x_l y_h), three
-//            bf16 MFMA products per term in fp32. All three are summed in
-//            chunks of 128 j on the matrix cores and the chunk sums added on
-//            the VALU, so no product passes through more than 3·128 + N/128
-//            additions.
+//            bf16 MFMA products per term, all accumulated into one running
+//            fp32 sum per element over the whole of N (each MFMA adds 16
+//            exact products to it). Beside it the kernel samples the running
+//            sum's magnitude at the end of every chunk of 128 j and keeps
+//            pm = the sum of those magnitudes, written as a byte code per
+//            element.
 //   bound    |G'[i,k] - G[i,k]| <= E[i,k] = c1·n_i·n_k + c2·pm[i,k] + δ
-//            (certified_factors below): the matrix cores' rounding (≤ 2u per
-//            addition, any order and rounding mode) and the reference's own
-//            are both relative to running sums, bounded through pm = the sum of
-//            |partial sums| at the 128-term chunk ends (a byte code per
-//            element); the dropped x_l y_l and r terms; a 1% margin; and δ the
-//            flushing of subnormal bf16 parts and products (2^-100·(1+n_i+n_k)).
-//            Σ_j |x_j y_j| <= n_i·n_k by Cauchy-Schwarz.
+//            (certified_factors below, which derives each term): the matrix
+//            cores' rounding (<= 2u per addition, any order and rounding
+//            mode, relative to the running sum and the products added) and
+//            the reference's own rounding (relative to its running sums) are
+//            both bounded through the partial sums at the chunk ends, so pm
+//            carries them; the dropped x_l y_l and r terms; a 1% margin; and
+//            δ the flushing of subnormal bf16 parts and products
+//            (2^-100·(1+n_i+n_k)). Σ_j |x_j y_j| <= n_i·n_k by Cauchy-Schwarz.
+//            slk_rigl_mfma_probe runs the instruction on chosen operands, so
+//            a test can check the 2u-per-addition model against exact sums.
 //   count    per row: survivors as in the exact kernel; n_grow = min(dropped,
 //            empty columns); T' = the n_grow-th largest |G'| of the empty
 //            columns and E_max = the row's largest E_k, so the exact n_grow-th
@@ -1099,6 +1104,35 @@ __global__ __launch_bounds__(kRowThreads) void rigl_select_kernel(
                    stage_col, stage_val, removed, tmp);
 }
 
+// One 32 x 32 x 16 bf16 MFMA per wave on given operands
+// (slk_rigl_mfma_probe), with the operand and accumulator layout
+// rigl_approx_kernel uses: lane l holds row l % 32 of A and of B at k = 8 (l /
+// 32) .. + 8, and accumulator register 4 g + q holds row 8 g + 4 (l / 32) + q,
+// column l % 32.
+__global__ __launch_bounds__(64) void rigl_mfma_probe_kernel(const uint16_t* __restrict__ A,
+                                                             const uint16_t* __restrict__ B,
+                                                             const float* __restrict__ C,
+                                                             float* __restrict__ D, int64_t n) {
+    const int64_t t = blockIdx.x;
+    if (t >= n) return;
+    const int lane = threadIdx.x;
+    const int r = lane & 31, k0 = 8 * (lane >> 5);
+    const bf16x8 a = *reinterpret_cast<const bf16x8*>(A + (t * 32 + r) * 16 + k0);
+    const bf16x8 b = *reinterpret_cast<const bf16x8*>(B + (t * 32 + r) * 16 + k0);
+    f32x16 acc;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            acc[4 * g + q] = C[(t * 32 + 8 * g + 4 * (lane >> 5) + q) * 32 + r];
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            D[(t * 32 + 8 * g + 4 * (lane >> 5) + q) * 32 + r] = acc[4 * g + q];
+}
+
 __global__ void rigl_clear_kernel(unsigned long long* __restrict__ c) { *c = 0; }
 
 // The bound's factors: |G'[i,k] - G[i,k]| <= c1·n_i·n_k + c2·pm[i,k] + δ,
@@ -1361,4 +1395,17 @@ extern "C" int slk_rigl_finish(const slk_csr* W, float* values, int32_t* col_ind
                        row_nnz, values, col_indices, thr_dev, static_cast<const RowInfo*>(info),
                        amb_off, amb_col, amb_key, n_amb_max, stage_col, stage_val, removed_u);
     return check_launch("rigl_finish");
+}
+
+extern "C" int slk_rigl_mfma_probe(const uint16_t* A, const uint16_t* B, const float* C, float* D,
+                                   int64_t n, void* stream) {
+    using namespace slk;
+    clear_error();
+    if (n < 0 || n > INT32_MAX) return fail(SLK_EINVAL, "rigl_mfma_probe: n outside [0, 2^31)");
+    if (n == 0) return SLK_OK;
+    if (A == nullptr || B == nullptr || C == nullptr || D == nullptr)
+        return fail(SLK_EINVAL, "rigl_mfma_probe: NULL pointer");
+    hipLaunchKernelGGL(rigl_mfma_probe_kernel, dim3(static_cast<unsigned>(n)), dim3(64), 0,
+                       as_stream(stream), A, B, C, D, n);
+    return check_launch("rigl_mfma_probe");
 }

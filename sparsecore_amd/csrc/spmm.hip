@@ -34,6 +34,8 @@
 
 #include <cstdlib>
 #include <mutex>
+#include <type_traits>
+#include <utility>
 
 namespace slk {
 namespace {
@@ -366,6 +368,43 @@ __device__ __forceinline__ void fma4(float v, const f32x4& x, f32x4& acc) {
     acc[3] = __builtin_fmaf(v, x[3], acc[3]);
 }
 
+// X chunk staging of the LDS kernels. A chunk is KC = kLdsK / H X rows x
+// 256·H columns of column tile `tile`, 1 KiB per X row and half; it goes
+// straight from global memory into LDS (global_load_lds_dwordx4: lane l of
+// a wave writes its 16 bytes at the instruction's LDS base + 16 l), so wave
+// w's load i fills row-half w + 16 i, i.e. X row (w + 16 i) / H, half
+// (w + 16 i) mod H: no registers hold the next chunk and no LDS stores copy
+// it. Each load is a scalar X row address (64-bit, computed per chunk; rows
+// past K, in the last chunk, are clamped to row K - 1: no slot has a column
+// >= K) plus the lane's 32-bit byte offset inside the row, clamped to the
+// row's last 16 bytes where the lane's columns pass N (those lanes never
+// store theirs); the offset is below 4N < 2^31 (the launcher's bound on N).
+template <int H>
+struct ChunkStager {
+    static constexpr int KC = kLdsK / H;
+    static constexpr int kStage = KC * H * kWave / kLdsThreads;  // 16-byte loads per thread
+    static_assert(kStage * kLdsWaves == KC * H, "whole X rows per thread group");
+    // 16 i is a multiple of H, so every load of wave w stages half w mod H:
+    // cb is the lane's byte offset inside the X row for that half
+    uint32_t cb;
+    __device__ __forceinline__ ChunkStager(int64_t tile, int64_t N, int lane, int w) {
+        const int64_t nn = tile * (H * kLdsCols) + (w % H) * kLdsCols + 4 * lane;
+        cb = static_cast<uint32_t>((nn < N ? nn : N - 4) * 4);
+    }
+    // The chunk at X row k0 into xs[buf], by wave w.
+    __device__ __forceinline__ void load(f32x4 (&xs)[2][KC][H][kWave], int buf,
+                                         const float* __restrict__ X, int64_t k0, int64_t K,
+                                         int64_t N, int w) const {
+#pragma unroll
+        for (int i = 0; i < kStage; ++i) {
+            const int q = w + i * kLdsWaves;  // the wave's row-half: wave-uniform
+            const int64_t kr = k0 + q / H;
+            const char* row = reinterpret_cast<const char*>(X + (kr < K ? kr : K - 1) * N);
+            lds_load_row(row + cb, &xs[buf][q / H][q % H][0]);
+        }
+    }
+};
+
 // One workgroup's share of the LDS kernel: logical block lb of a launch over
 // positions [0, P) of `order` with nrowblk row blocks per column tile; xs is
 // the workgroup's X double buffer.
@@ -379,8 +418,6 @@ __device__ __forceinline__ void spmm_lds_body(
     // H halves of 256 columns per workgroup, each lane 4 columns of each half;
     // chunks of KC X rows keep the double buffer at 160 KiB, all of a CU's LDS
     constexpr int KC = kLdsK / H;
-    constexpr int kStage = KC * H * kWave / kLdsThreads;  // 16-byte loads per thread per chunk
-    static_assert(kStage * kLdsWaves == KC * H, "whole X rows per thread group");
     const int lane = threadIdx.x & (kWave - 1);
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t tile = lb / nrowblk;  // tile-major: a tile's row blocks share X chunks in L2
@@ -418,37 +455,8 @@ __device__ __forceinline__ void spmm_lds_body(
         for (int h = 0; h < H; ++h) acc[j][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    // The chunk is staged by direct loads into LDS (global_load_lds_dwordx4:
-    // lane l of a wave writes its 16 bytes at the instruction's LDS base +
-    // 16 l), one 1 KB row-half per wave instruction: wave w's load i fills
-    // row-half w + 16i, i.e. X row (w + 16i) / H, half (w + 16i) mod H, so no
-    // registers hold the next chunk and no LDS stores copy it.
-    // Piece i's byte offset from the chunk's first X row (KC·N·4 < 2^32: the
-    // launcher's bar), its columns clamped into the row where they pass N
-    // (lanes whose columns pass N never store theirs): a full chunk is a
-    // scalar base plus one 32-bit offset per load. Rows past K (the last
-    // chunk) are clamped to row K - 1: no slot has a column >= K.
-    uint32_t poff[kStage];
-#pragma unroll
-    for (int i = 0; i < kStage; ++i) {
-        const int p = threadIdx.x + i * kLdsThreads;
-        const int64_t nn = tile * (H * kLdsCols) + ((p / kWave) % H) * kLdsCols + 4 * (p % kWave);
-        poff[i] = static_cast<uint32_t>(((p / (H * kWave)) * N + (nn < N ? nn : N - 4)) * 4);
-    }
-    auto prefetch = [&](int buf, int64_t k0) {  // chunk at X row k0 into xs[buf]
-        const char* xb = reinterpret_cast<const char*>(X + k0 * N);
-        const bool full = k0 + KC <= K;  // workgroup-uniform
-#pragma unroll
-        for (int i = 0; i < kStage; ++i) {
-            const int q = w + i * kLdsWaves;  // the wave's row-half: wave-uniform
-            int64_t back = 0;
-            if (!full) {
-                const int64_t kr = q / H;
-                back = k0 + kr < K ? 0 : (k0 + kr - (K - 1)) * N * 4;
-            }
-            lds_load_row(xb + poff[i] - back, &xs[buf][q / H][q % H][0]);
-        }
-    };
+    const ChunkStager<H> stager(tile, N, lane, w);
+    auto prefetch = [&](int buf, int64_t k0) { stager.load(xs, buf, X, k0, K, N, w); };
     const int64_t nchunks = ceil_div(K, KC);
     prefetch(0, 0);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's direct loads have landed
@@ -590,6 +598,284 @@ __global__ __launch_bounds__(kLdsThreads) void spmm_lds_split_kernel(
     }
 }
 
+// ───────────────────────── binned-stream kernel ─────────────────────────────
+//
+// The LDS kernel above finds, per row and chunk, the run of the row's slots
+// that falls in the chunk (a ballot over the row's window of columns) and
+// keeps two windows of (column, value) per row. With a binned slot stream
+// (slk_csr.bin_*, built per topology) each wave's work for a chunk is one
+// contiguous run of the stream, row by row, with the rows' counts known:
+//   * per wave and chunk, one 64-entry window of (LDS offset, value): the
+//     chunk's entries, loaded during the previous chunk (values read through
+//     the slot index then, so they are never stale), and the per-row counts
+//     from a window of 32 chunks' count records;
+//   * each slot costs a readlane of its offset, one address add, H LDS
+//     reads, a readlane of its value and 4·H fmas; no per-row search;
+//   * the first G slots of row j+1 are read from LDS before row j's fmas,
+//     so one row's reads are in flight while the previous row computes (the
+//     reads are issued unconditionally — a slot past the row's count reads a
+//     valid offset and is not used — so the wait counts are static).
+// A chunk whose entries pass the window (more than 64 for the wave: dense
+// rows) takes them one by one from the stream.
+
+template <class F, int... J>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, J...>) {
+    (f(std::integral_constant<int, J>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// One wave's share of workgroup lb of a binned launch over positions [0, P)
+// (rows order[p], or p when order is NULL), nrowblk row blocks per column
+// tile; the stream's unit u = (row block) * 16 + wave.
+template <int RW, int H, int G>
+__device__ __forceinline__ void spmm_bin_body(
+    f32x4 (&xs)[2][kLdsK / H][H][kWave], int64_t lb, int64_t P, int64_t K, int64_t N,
+    int64_t nrowblk, const int32_t* __restrict__ order, const float* __restrict__ val,
+    const int32_t* __restrict__ bin_off, const int32_t* __restrict__ bin_slot,
+    const uint32_t* __restrict__ bin_cnt, const int32_t* __restrict__ bin_start, int64_t n_bin,
+    const float* __restrict__ X, const float* __restrict__ bias, float* __restrict__ Y) {
+    constexpr int KC = kLdsK / H;
+    constexpr int kHalfBytes = kWave * 16;  // one staged X row half
+    const int lane = threadIdx.x & (kWave - 1);
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t tile = lb / nrowblk;
+    const int64_t rb = lb - tile * nrowblk;
+    const int64_t u = rb * kLdsWaves + w;
+    const int64_t nch = ceil_div(K, KC);
+    f32x4 acc[RW][H];
+#pragma unroll
+    for (int j = 0; j < RW; ++j)
+#pragma unroll
+        for (int h = 0; h < H; ++h) acc[j][h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const uint32_t* cnt = bin_cnt + u * nch * 2;
+    const int64_t e_lim = bin_start[u + 1] < n_bin ? bin_start[u + 1] : n_bin;
+    // chunk c's count record (wave-uniform address: scalar loads, issued a
+    // chunk ahead and first read after the barrier's wait)
+    auto rec = [&](int64_t c, uint32_t& a, uint32_t& b) {
+        a = cnt[2 * c];
+        b = cnt[2 * c + 1];
+    };
+    auto load_idx = [&](int64_t at, int32_t& o, int32_t& s) {
+        const int64_t i = at + lane;
+        o = 0;
+        s = -1;
+        if (i < e_lim) {
+            o = bin_off[i];
+            s = bin_slot[i];
+        }
+    };
+    auto gather = [&](int32_t s) -> float { return s >= 0 ? val[s] : 0.0f; };
+    auto rec_total = [](uint32_t a, uint32_t b) -> int32_t {
+        return static_cast<int32_t>((a & 0xff) + ((a >> 8) & 0xff) + ((a >> 16) & 0xff) + (a >> 24) +
+                                    (b & 0xff) + ((b >> 8) & 0xff) + ((b >> 16) & 0xff) + (b >> 24));
+    };
+    // chunk ch's entries (cur_*) and counts (rc*), chunk ch+1's indices
+    // (nxt_*) and counts (rn*); e_cur / e_nxt their first entries
+    int64_t e_cur = bin_start[u];
+    uint32_t rc0, rc1, rn0 = 0, rn1 = 0;
+    rec(0, rc0, rc1);
+    int64_t e_nxt = e_cur + rec_total(rc0, rc1);
+    int32_t cur_off, cur_slot, nxt_off = 0, nxt_slot = -1;
+    load_idx(e_cur, cur_off, cur_slot);
+    float cur_val = gather(cur_slot);
+    if (nch > 1) {
+        rec(1, rn0, rn1);
+        load_idx(e_nxt, nxt_off, nxt_slot);
+    }
+
+    const ChunkStager<H> stager(tile, N, lane, w);
+    stager.load(xs, 0, X, 0, K, N, w);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's direct loads have landed
+    __syncthreads();
+    for (int64_t ch = 0; ch < nch; ++ch) {
+        const int b = static_cast<int>(ch & 1);
+        const bool more = ch + 1 < nch;
+        // the other buffer's last readers (chunk ch - 1) passed the barrier
+        if (more) stager.load(xs, b ^ 1, X, (ch + 1) * KC, K, N, w);
+        // chunk ch+1's values, chunk ch+2's indices and counts
+        float nxt_val = 0.0f;
+        int32_t nn_off = 0, nn_slot = -1;
+        uint32_t rnn0 = 0, rnn1 = 0;
+        int64_t e_nn = e_nxt;
+        if (more) {
+            nxt_val = gather(nxt_slot);
+            e_nn = e_nxt + rec_total(rn0, rn1);
+            if (ch + 2 < nch) {
+                rec(ch + 2, rnn0, rnn1);
+                load_idx(e_nn, nn_off, nn_slot);
+            }
+        }
+
+        const char* lbase = reinterpret_cast<const char*>(&xs[b][0][0][lane]);
+        const int32_t tot = rec_total(rc0, rc1);
+        int32_t nr[RW];
+#pragma unroll
+        for (int j = 0; j < RW; ++j)
+            nr[j] = static_cast<int32_t>(((j < 4 ? rc0 : rc1) >> (8 * (j & 3))) & 0xff);
+        // One pass per 64 entries of the chunk (one pass unless the wave's
+        // rows are dense): each row's part of its run inside the pass's
+        // window, rows in order, each row's slots in order.
+        auto pass = [&](int32_t wb) {
+            f32x4 xa[G][H], xb[G][H];
+            // the X rows of the G slots from window position r0 (positions
+            // past 63 wrap: their reads are valid and unused)
+            auto issue = [&](f32x4 (&x)[G][H], int32_t r0) {
+#pragma unroll
+                for (int k = 0; k < G; ++k) {
+                    const int32_t o = bcast_i(cur_off, (r0 + k) & (kWave - 1));
+#pragma unroll
+                    for (int h = 0; h < H; ++h)
+                        x[k][h] = *reinterpret_cast<const f32x4*>(lbase + o + h * kHalfBytes);
+                }
+                // keep the reads here: the compiler would otherwise sink each
+                // into the branch that uses it, after the previous row's fmas
+                asm volatile("" ::: "memory");
+            };
+            // row j's run [rs, rs + nr) clipped to the window [wb, wb + 64)
+            // (no clipping in the usual single window)
+            int32_t pj[RW], nj[RW];
+            {
+                const bool whole = wb == 0 && tot <= kWave;
+                int32_t rs = 0;
+#pragma unroll
+                for (int j = 0; j < RW; ++j) {
+                    if (whole) {
+                        pj[j] = rs;
+                        nj[j] = nr[j];
+                    } else {
+                        const int32_t lo = rs > wb ? rs : wb;
+                        const int32_t hi = rs + nr[j] < wb + kWave ? rs + nr[j] : wb + kWave;
+                        pj[j] = lo - wb;
+                        nj[j] = max(hi - lo, 0);
+                    }
+                    rs += nr[j];
+                }
+            }
+            auto consume = [&](const f32x4 (&x)[G][H], f32x4 (&a)[H], int32_t p0, int32_t n) {
+#pragma unroll
+                for (int k = 0; k < G; ++k) {
+                    if (k < n) {
+                        const float v = bcast_f(cur_val, p0 + k);
+#pragma unroll
+                        for (int h = 0; h < H; ++h) fma4(v, x[k][h], a[h]);
+                    }
+                }
+            };
+            // pass 1, straight-line: each row's first G slots, row j+1's
+            // reads issued before row j's fmas
+            issue(xa, pj[0]);
+            static_for<RW>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                f32x4(&xj)[G][H] = (j & 1) ? xb : xa;
+                f32x4(&xo)[G][H] = (j & 1) ? xa : xb;
+                if constexpr (j + 1 < RW) issue(xo, pj[j + 1]);
+                consume(xj, acc[j], pj[j], nj[j]);
+            });
+            // pass 2: the rest of the rows with more than G slots here
+            static_for<RW>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                for (int32_t t = G; t < nj[j]; t += G) {
+                    issue(xa, pj[j] + t);
+                    consume(xa, acc[j], pj[j] + t, nj[j] - t);
+                }
+            });
+        };
+        // the first window outside any loop, so its reads wait only on LDS
+        // (a loop with the reload below would make them wait for the next
+        // chunk's loads too)
+        pass(0);
+        for (int32_t wb = kWave; wb < tot; wb += kWave) {
+            int32_t sl;  // the next 64 entries into the current window
+            load_idx(e_cur + wb, cur_off, sl);
+            cur_val = gather(sl);
+            pass(wb);
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // chunk ch+1 and the next windows have landed
+        __syncthreads();
+        cur_off = nxt_off;
+        cur_val = nxt_val;
+        nxt_off = nn_off;
+        nxt_slot = nn_slot;
+        rc0 = rn0;
+        rc1 = rn1;
+        rn0 = rnn0;
+        rn1 = rnn1;
+        e_cur = e_nxt;
+        e_nxt = e_nn;
+    }
+#pragma unroll
+    for (int j = 0; j < RW; ++j) {
+        const int64_t q = rb * (kLdsWaves * RW) + w + kLdsWaves * j;
+        if (q >= P) continue;
+        const int64_t row = order != nullptr ? order[q] : q;
+        const float bb = bias != nullptr ? bias[row] : 0.0f;
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+            const int64_t nn = tile * (H * kLdsCols) + h * kLdsCols + 4 * lane;
+            if (nn >= N) continue;  // N % 4 == 0 for this kernel
+            f32x4 a = acc[j][h];
+            if (bias != nullptr) {
+                a[0] = a[0] + bb;
+                a[1] = a[1] + bb;
+                a[2] = a[2] + bb;
+                a[3] = a[3] + bb;
+            }
+            *reinterpret_cast<f32x4*>(Y + row * N + nn) = a;
+        }
+    }
+}
+
+template <int RW, int H, int G>
+__global__ __launch_bounds__(kLdsThreads) void spmm_bin_kernel(
+    int64_t P, int64_t K, int64_t N, int64_t nrowblk, const int32_t* __restrict__ order,
+    const float* __restrict__ val, const int32_t* __restrict__ bin_off,
+    const int32_t* __restrict__ bin_slot, const uint32_t* __restrict__ bin_cnt,
+    const int32_t* __restrict__ bin_start, int64_t n_bin, const float* __restrict__ X,
+    const float* __restrict__ bias, float* __restrict__ Y) {
+    __shared__ f32x4 xs[2][kLdsK / H][H][kWave];  // 160 KiB
+    spmm_bin_body<RW, H, G>(xs, xcd_logical_block(blockIdx.x, gridDim.x), P, K, N, nrowblk, order,
+                            val, bin_off, bin_slot, bin_cnt, bin_start, n_bin, X, bias, Y);
+}
+
+// The heavy rows (positions [0, T) of the longest-first order, two per wave,
+// 8 columns per lane, on the LDS kernel) and the binned rest in one grid,
+// each XCD starting its share with its share of the heavy workgroups (as
+// spmm_lds_split_kernel).
+template <int RW, int H, int G>
+__global__ __launch_bounds__(kLdsThreads) void spmm_bin_split_kernel(
+    int64_t T, int64_t M, int64_t K, int64_t N, int64_t nblk_a, int64_t nrowblk_a,
+    int64_t nrowblk_b, const int32_t* __restrict__ order, const int32_t* __restrict__ row_start,
+    const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ col,
+    const float* __restrict__ val, const int32_t* __restrict__ bin_off,
+    const int32_t* __restrict__ bin_slot, const uint32_t* __restrict__ bin_cnt,
+    const int32_t* __restrict__ bin_start, int64_t n_bin, const float* __restrict__ X,
+    const float* __restrict__ bias, float* __restrict__ Y) {
+    __shared__ f32x4 xraw[2 * kLdsK * kWave];  // 160 KiB, shaped by each part below
+    const int64_t nb = gridDim.x;
+    const int64_t x = blockIdx.x % kXcds, q = blockIdx.x / kXcds;
+    const int64_t ha = nblk_a / kXcds + (x < nblk_a % kXcds ? 1 : 0);
+    const int64_t a0 = x * (nblk_a / kXcds) + (x < nblk_a % kXcds ? x : nblk_a % kXcds);
+    const int64_t nblk_b = nb - nblk_a;
+    const int64_t count_x = (nb - x + kXcds - 1) / kXcds;
+    const int64_t hb_lo = x * (nb / kXcds) + (x < nb % kXcds ? x : nb % kXcds) - a0;
+    if (q < ha) {
+        auto& xs = *reinterpret_cast<f32x4(*)[2][kLdsK / kHeavyH][kHeavyH][kWave]>(xraw);
+        spmm_lds_body<kHeavyRW, kHeavyH>(xs, a0 + q, T, K, N, nrowblk_a, order, row_start,
+                                         row_nnz, col, val, X, bias, Y);
+    } else {
+        const int64_t lb = hb_lo + (q - ha);
+        if (lb < nblk_b && q < count_x) {
+            auto& xs = *reinterpret_cast<f32x4(*)[2][kLdsK / H][H][kWave]>(xraw);
+            spmm_bin_body<RW, H, G>(xs, lb, M - T, K, N, nrowblk_b, order + T, val, bin_off,
+                                    bin_slot, bin_cnt, bin_start, n_bin, X, bias, Y);
+        }
+    }
+}
+
 int launch_blocks(int64_t waves, int64_t* blocks) {
     *blocks = ceil_div(waves, kSpmmBlock / kWave);
     if (*blocks > INT32_MAX) return fail(SLK_EINVAL, "spmm: problem too large for one launch");
@@ -686,6 +972,88 @@ int launch_group_L(int L, const slk_csr* W, const float* X, int64_t N, const flo
         case 8: return launch_group<8, 1>(W, X, N, bias, Y, st);
         case 16: return launch_group<16, 1>(W, X, N, bias, Y, st);
         default: return launch_group<32, 1>(W, X, N, bias, Y, st);
+    }
+}
+
+// The binned rows (positions [T, M), T = W->bin_first) on the binned
+// kernel, with the heavy rows before them on the LDS kernel in the same grid
+// when T > 0 (one grid needs the rest to fill a workgroup per XCD; else two
+// launches).
+template <int RW, int H, int G>
+int launch_bin_cfg(const slk_csr* W, const float* X, int64_t N, const float* bias, float* Y,
+                   hipStream_t st) {
+    const int64_t M = W->nrows, K = W->ncols, T = W->bin_first;
+    const int64_t nrowblk_b = ceil_div(M - T, int64_t{kLdsWaves} * RW);
+    const int64_t nb = nrowblk_b * ceil_div(N, int64_t{kLdsCols} * H);
+    const int32_t* order = T > 0 ? W->row_order + T : nullptr;
+    if (T > 0) {
+        const int64_t nrowblk_a = ceil_div(T, int64_t{kLdsWaves} * kHeavyRW);
+        const int64_t na = nrowblk_a * ceil_div(N, int64_t{kLdsCols} * kHeavyH);
+        if (na + nb > INT32_MAX) return fail(SLK_EINVAL, "spmm: problem too large for one launch");
+        if (nb >= kXcds) {
+            hipLaunchKernelGGL((spmm_bin_split_kernel<RW, H, G>), dim3(static_cast<unsigned>(na + nb)),
+                               dim3(kLdsThreads), 0, st, T, M, K, N, na, nrowblk_a, nrowblk_b,
+                               W->row_order, W->row_start, W->row_nnz, W->col_indices, W->values,
+                               W->bin_off, W->bin_slot, W->bin_cnt, W->bin_start, W->n_bin, X, bias,
+                               Y);
+            return check_launch("spmm");
+        }
+        if (int rc = launch_lds_rw<kHeavyRW, kHeavyH>(W, W->row_order, T, X, N, bias, Y, st))
+            return rc;
+    }
+    if (nb == 0) return SLK_OK;
+    if (nb > INT32_MAX) return fail(SLK_EINVAL, "spmm: problem too large for one launch");
+    hipLaunchKernelGGL((spmm_bin_kernel<RW, H, G>), dim3(static_cast<unsigned>(nb)),
+                       dim3(kLdsThreads), 0, st, M - T, K, N, nrowblk_b, order, W->values,
+                       W->bin_off, W->bin_slot, W->bin_cnt, W->bin_start, W->n_bin, X, bias, Y);
+    return check_launch("spmm");
+}
+
+// Slots of a binned row read ahead (G): about one per expected slot of a row
+// in a chunk, so few reads go unused.
+int bin_group(const slk_csr* W) {
+    if (const int64_t t = tuning(SLK_TUNE_SPMM_G); t == 1 || t == 2 || t == 4)
+        return static_cast<int>(t);
+    const int64_t rows = W->nrows - W->bin_first;
+    const double per_chunk = rows > 0 && W->ncols > 0
+                                 ? static_cast<double>(W->n_bin) / (static_cast<double>(rows) *
+                                                                    W->ncols) *
+                                       (kLdsK / W->bin_h)
+                                 : 0.0;
+    return per_chunk < 1.5 ? 1 : per_chunk < 3.0 ? 2 : 4;
+}
+
+// (8 rows x 2 halves reads at most 2 slots ahead: 4 would not fit 128 VGPRs)
+template <int RW, int H>
+int launch_bin_g(int g, const slk_csr* W, const float* X, int64_t N, const float* bias, float* Y,
+                 hipStream_t st) {
+    if constexpr (RW * H >= 16) {
+        if (g == 1) return launch_bin_cfg<RW, H, 1>(W, X, N, bias, Y, st);
+        return launch_bin_cfg<RW, H, 2>(W, X, N, bias, Y, st);
+    } else {
+        switch (g) {
+            case 1: return launch_bin_cfg<RW, H, 1>(W, X, N, bias, Y, st);
+            case 2: return launch_bin_cfg<RW, H, 2>(W, X, N, bias, Y, st);
+            default: return launch_bin_cfg<RW, H, 4>(W, X, N, bias, Y, st);
+        }
+    }
+}
+
+int launch_bin(const slk_csr* W, const float* X, int64_t N, const float* bias, float* Y,
+               hipStream_t st) {
+    const int g = bin_group(W);
+    const int64_t cfg = W->bin_h * 10 + W->bin_rw;
+    switch (cfg) {
+        case 28: return launch_bin_g<8, 2>(g, W, X, N, bias, Y, st);
+        case 24: return launch_bin_g<4, 2>(g, W, X, N, bias, Y, st);
+        case 22: return launch_bin_g<2, 2>(g, W, X, N, bias, Y, st);
+        case 21: return launch_bin_g<1, 2>(g, W, X, N, bias, Y, st);
+        case 18: return launch_bin_g<8, 1>(g, W, X, N, bias, Y, st);
+        case 14: return launch_bin_g<4, 1>(g, W, X, N, bias, Y, st);
+        default:
+            return fail(SLK_EINVAL, "spmm: binned stream of " + std::to_string(W->bin_rw) +
+                                        " rows per wave and " + std::to_string(W->bin_h) +
+                                        " halves has no kernel");
     }
 }
 
@@ -847,6 +1215,15 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
     if (transposed_out) return launch_wave_t(W, X, N, bias, Y, st);
     const uintptr_t align = reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(Y);
     const int64_t M = W->nrows;
+    // A binned slot stream (built by the caller where it pays) takes the LDS
+    // path with its own kernel. SLK_TUNE_SPMM_BIN = 0 ignores it, and so does
+    // a forced choice of the other kernels unless SLK_TUNE_SPMM_BIN = 1.
+    const int64_t tb = tuning(SLK_TUNE_SPMM_BIN);
+    const bool forced = tuning(SLK_TUNE_SPMM_KERNEL) >= 0 || tuning(SLK_TUNE_SPMM_H) >= 0 ||
+                        tuning(SLK_TUNE_SPMM_RW) >= 0 || tuning(SLK_TUNE_SPMM_VEC) >= 0;
+    if (W->bin_off != nullptr && (tb > 0 || (tb < 0 && !forced)) && K > 0 && N % 4 == 0 &&
+        align % 16 == 0 && ceil_div(K, kLdsK / W->bin_h) <= SLK_BIN_MAX_CHUNKS)
+        return launch_bin(W, X, N, bias, Y, st);
 
     // Kernel choice. The LDS-staged kernel needs 16-byte lanes (N % 4 == 0,
     // aligned X and Y) and pays off when each staged X element feeds several
@@ -855,8 +1232,7 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
     // configurations that pass both bars, lds_cost picks one. The per-wave
     // gather kernels cover everything else (small N is latency-bound).
     // SLK_TUNE_SPMM_KERNEL, SLK_TUNE_SPMM_H and SLK_TUNE_SPMM_RW override.
-    // (N < 2^24: a chunk of X rows is addressed with 32-bit byte offsets)
-    const bool lds_ok = N % 4 == 0 && align % 16 == 0 && N < (int64_t{1} << 24);
+    const bool lds_ok = N % 4 == 0 && align % 16 == 0;
     int rw = 0, h = 1;
     if (lds_ok && N >= kLdsMinN) {
         const double density =

@@ -273,6 +273,7 @@ class PaddedCSR:
         # derived views: (key, the base view they copy, view, schedule arrays)
         self._seglist = None    # key (topology_version, block_cols, seg_slots)
         self._phased = None     # key (topology_version, n_phases)
+        self._binned = None     # key (topology_version, first, rw, h)
         # True when a few columns hold many of the slots (a transpose of a
         # matrix with heavy rows): its gathers already stay in cache
         self._cols_skewed = False
@@ -429,6 +430,43 @@ class PaddedCSR:
             view = self._derived(base, phase_lo=_lib.ptr(c[3]), n_phases=int(n_phases))
             c = (key, base, view, c[3])
         self._phased = c
+        return c[2]
+
+    def _bin_coverage(self) -> tuple[int, int]:
+        """(first, slots): the positions a binned stream covers start at
+        `first` (after the heavy rows, which the LDS kernel runs; 0 without
+        them), and `slots` bounds their live slots (exact where the host row
+        mirror is at hand, else nnz)."""
+        base = self._view()
+        first = int(base.n_heavy_rows)
+        if first == 0:
+            return 0, self._nnz
+        if self._host_rows is None:
+            return first, self._nnz
+        nz = np.sort(self._host_rows[1])[::-1]
+        return first, self._nnz - int(nz[:first].sum())
+
+    def _view_binned(self, rw: int, h: int) -> _lib.CsrView:
+        """The view plus the binned slot stream of slk_spmm's LDS-staged kernel
+        (slk_csr.bin_*) for rw rows per wave and h column halves: the rows after
+        the heavy ones (all rows without heavy ones), each wave's slots listed
+        chunk by chunk and row by row. Built on the device (slk_bin_build, two
+        launches, no host read) once per topology; the cached view follows the
+        base view as the other schedules do."""
+        base = self._view()
+        first, n_bin = self._bin_coverage()
+        key = (self._topology_version, first, int(rw), int(h))
+        c = self._binned
+        if c is None or c[0] != key:
+            c = (key, None, None,
+                 _lib.bin_build(base, first, int(rw), int(h), n_bin, self.device), n_bin)
+        if c[1] is not base:
+            off, slot, cnt, start = c[3]
+            view = self._derived(base, bin_off=_lib.ptr(off), bin_slot=_lib.ptr(slot),
+                                 bin_cnt=_lib.ptr(cnt), bin_start=_lib.ptr(start),
+                                 bin_first=first, bin_rw=int(rw), bin_h=int(h), n_bin=c[4])
+            c = (key, base, view, c[3], c[4])
+        self._binned = c
         return c[2]
 
     def _rows_host(self):

@@ -94,17 +94,67 @@ _PHASE_MIN_X_BYTES = 128 << 20
 _PHASE_X_ROWS = 4096
 
 
+# Binned slot stream for slk_spmm's LDS-staged kernel (slk_csr.bin_*): for
+# matrices without heavy rows where N is large, each staged X element is
+# expected to serve at least _BIN_MIN_REUSE rows of a workgroup (density x
+# rows per workgroup; fewer, and gathering X rows directly is faster), and a
+# wave's rows are expected to hold at most _BIN_MAX_PER_CHUNK slots per
+# staged chunk (its window holds 64; a chunk with more takes extra passes).
+# Rows per wave and halves are the first of _BIN_SHAPES that qualifies (more
+# rows per workgroup stage each X chunk for more rows; two halves halve the
+# per-slot overhead per fma). Measured on 16384^2 x 4096 (same bits): the
+# 95% layer's input gradient 5.80 -> 5.53 ms at 8 x 2; its forward, whose
+# heavy rows run beside the light ones, 6.0 ms on the two-stream path against
+# 6.43 binned; at 99% the gather kernel (1.79 ms) beats any binned shape
+# (3.5 ms and up: staging all of X per workgroup dominates).
+_BIN_MIN_N = 1024
+_BIN_MIN_REUSE = 4.0
+_BIN_MAX_PER_CHUNK = 48
+_BIN_MIN_BLOCKS = 192
+_BIN_SHAPES = ((8, 2), (4, 2), (2, 2), (8, 1), (4, 1), (1, 2))
+
+
+def _bin_shape(W: PaddedCSR, K: int, N: int):
+    """(rows per wave, halves) of the binned stream slk_spmm should get for W
+    and an N-column X, or None."""
+    if N < _BIN_MIN_N or N % 4 or K == 0:
+        return None
+    first, slots = W._bin_coverage()
+    rows = W.nrows - first
+    if first > 0 or rows <= 0 or slots <= 0:
+        return None
+    density = slots / (rows * K)
+    for rw, h in _BIN_SHAPES:
+        kc = 80 // h
+        if -(-K // kc) > _lib.BIN_MAX_CHUNKS:
+            continue
+        if rw * kc * density > _BIN_MAX_PER_CHUNK or density * 16 * rw < _BIN_MIN_REUSE:
+            continue
+        if -(-rows // (16 * rw)) * -(-N // (256 * h)) < _BIN_MIN_BLOCKS:
+            continue
+        return rw, h
+    return None
+
+
 # Schedule overrides for tests and measurement (the launchers' own choices
 # otherwise; results keep their bits either way): "spmm_phases" = n forces
 # n column phases on slk_spmm's gather path (<= 1: none); "seg" = (block
-# columns, slots per segment) forces that segment list on slk_sddmm, () none.
+# columns, slots per segment) forces that segment list on slk_sddmm, () none;
+# "bin_shape" = (rows per wave, halves) forces that binned stream on
+# slk_spmm, False none.
 _overrides: dict[str, object] = {}
 
 
 def _spmm_view(W: PaddedCSR, X: torch.Tensor):
-    """W's view for slk_spmm: with phase bounds where X is far beyond the L2s
-    and W's columns are not skewed."""
+    """W's view for slk_spmm: with a binned slot stream where it pays (see
+    above), else with phase bounds where X is far beyond the L2s and W's
+    columns are not skewed."""
     K, N = X.shape
+    binned = _overrides.get("bin_shape")
+    if binned is None:
+        binned = _bin_shape(W, K, N)
+    if binned:
+        return W._view_binned(*binned)
     forced = _overrides.get("spmm_phases")
     if forced is not None:
         return W._view_phased(int(forced)) if int(forced) > 1 else W._view()

@@ -53,10 +53,11 @@ def tune():
     """Forces kernel / schedule choices for one test and restores the
     launchers' own choices afterwards: tune(spmm_kernel=1, spmm_rw=4, ...)
     for the library's knobs (slk_set_tuning), tune(spmm_phases=3) or
-    tune(seg=(64, 8)) for the host-side schedule overrides of ops."""
+    tune(seg=(64, 8)) or tune(bin_shape=(8, 2)) for the host-side schedule
+    overrides of ops."""
     from sparsecore_amd import _lib, ops
 
-    host_keys = ("spmm_phases", "seg")
+    host_keys = ("spmm_phases", "seg", "bin_shape")
     touched = []
 
     def set_(**kw):
