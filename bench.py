@@ -45,6 +45,13 @@ import sys
 import time
 from pathlib import Path
 
+# The CPU baseline's OpenMP threads are bound to consecutive physical cores,
+# as the reference's published OpenMP numbers were measured; libgomp reads
+# these when it loads, so they are set before anything imports it. A
+# caller's own setting wins.
+os.environ.setdefault("OMP_PROC_BIND", "close")
+os.environ.setdefault("OMP_PLACES", "cores")
+
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
@@ -79,8 +86,9 @@ def parse_args():
                     help="build the workload, then time only this kernel label (e.g. spmm_fwd, "
                          "sddmm_dw, 'spmm_dx[qkv 768x2304]') and print its timing: a short "
                          "run for profiler counter passes")
-    ap.add_argument("--kernel-reps", type=int, default=200,
-                    help="most launches per kernel in the kernel-timing phase")
+    ap.add_argument("--kernel-reps", type=int, default=30,
+                    help="timed calls per kernel label in the kernel-timing phase (after 3 "
+                         "warm-up calls; the median is reported)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after the run, copy a buffer of this many MiB three times (a "
                          "known-size reference dispatch for HBM byte counters)")
@@ -108,33 +116,33 @@ def flops(nnz, N):
 
 # ───────────────────────────── timing helpers ────────────────────────────────
 
-KERNEL_REPS = 200
+KERNEL_WARMUP = 3
+KERNEL_REPS = 30
 
 
-def kernel_avg_ms(fn, reps: int | None = None, with_reps: bool = False):
-    """Average device time of `fn` (one kernel launch) over back-to-back launches
-    (and, with_reps, how many launches were timed)."""
+def kernel_time_ms(fn, reps: int | None = None):
+    """Per-call device time of `fn` (one kernel label) as the reference's
+    profiler measures it (examples/profile_dw_baseline.py:94-128): KERNEL_WARMUP
+    untimed calls, then `reps` calls, each between two HIP events on the
+    current stream, queued behind a GPU sleep so no host launch gap enters an
+    interval. Returns (median ms, mean ms, reps)."""
     import torch
 
-    fn()
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    fn()
-    end.record()
-    torch.cuda.synchronize()
-    one = start.elapsed_time(end)
-    reps = KERNEL_REPS if reps is None else reps
-    reps = max(min(5, reps), min(reps, int(100.0 / max(one, 1e-3))))  # ~0.1 s at most
-    torch.cuda._sleep(int(2e7))  # keeps the GPU busy while the launches queue up
-    start.record()
-    for _ in range(reps):
+    for _ in range(KERNEL_WARMUP):
         fn()
-    end.record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / reps
-    return (ms, reps) if with_reps else ms
+    reps = KERNEL_REPS if reps is None else max(1, int(reps))
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    torch.cuda._sleep(int(2e7))  # keeps the GPU busy while the launches queue up
+    ev[0].record()
+    for i in range(reps):
+        fn()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    ts = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(reps))
+    mid = reps // 2
+    median = ts[mid] if reps % 2 else 0.5 * (ts[mid - 1] + ts[mid])
+    return median, sum(ts) / reps, reps
 
 
 def stage(msg: str) -> None:
@@ -778,9 +786,24 @@ def cpu_baseline(work, seconds: float):
         _set_threads(threads)
         out["one_thread"] = {k: one.get(k) for k in ("value", "unit", "cores", "sample")}
     out["host"] = _host_info()
-    out["threads_note"] = ("cores = OpenMP/torch threads used; OMP_PROC_BIND/OMP_PLACES left "
-                           "at their defaults")
+    out["threads_note"] = ("cores = OpenMP/torch threads used; binding: " + _omp_binding())
     return out
+
+
+def _omp_binding() -> str:
+    """The OpenMP binding libgomp applies (OMP_PROC_BIND / OMP_PLACES, set by
+    this script before anything loads libgomp)."""
+    import ctypes
+
+    names = {0: "false", 1: "true", 2: "primary", 3: "close", 4: "spread"}
+    try:
+        gomp = ctypes.CDLL("libgomp.so.1")
+        bind = names.get(gomp.omp_get_proc_bind(), "?")
+        places = gomp.omp_get_num_places()
+    except (OSError, AttributeError):
+        return "libgomp not found"
+    return (f"OMP_PROC_BIND={os.environ.get('OMP_PROC_BIND')} (libgomp: {bind}), "
+            f"OMP_PLACES={os.environ.get('OMP_PLACES')} (libgomp: {places} places)")
 
 
 def _cpu_run(work, seconds: float, threads: int):
@@ -971,22 +994,29 @@ def _cpu_run(work, seconds: float, threads: int):
         unit = "GB/s"
         sample = f"{work.name} fwd+dW+dX steps ({work.M}x{work.K}, N={work.N})"
 
+    # 3 warm-up steps (1 where a step takes more than a twentieth of the
+    # budget), then up to 30 steps timed one by one within the budget; the
+    # median step is reported
     t0 = time.perf_counter()
     step()
     if time.perf_counter() - t0 < seconds / 20:
         for _ in range(2):
             step()
-    t0 = time.perf_counter()
-    n = 0
-    while True:
+    times = []
+    t_all = time.perf_counter()
+    while len(times) < 30:
+        t0 = time.perf_counter()
         step()
-        n += 1
-        if time.perf_counter() - t0 > seconds:
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_all > seconds:
             break
-    dt = time.perf_counter() - t0
-    return {"value": unit_per_step * n / dt, "unit": unit, "cores": threads, "kind": kind,
-            "sample": f"{n} {sample} in {dt:.1f} s, OpenMP/torch threads={threads}, "
-                      f"ms/step={1e3 * dt / n:.3f}"}
+    times.sort()
+    n = len(times)
+    med = times[n // 2] if n % 2 else 0.5 * (times[n // 2 - 1] + times[n // 2])
+    return {"value": unit_per_step / med, "unit": unit, "cores": threads, "kind": kind,
+            "sample": f"median of {n} timed {sample} (after warm-up), OpenMP/torch "
+                      f"threads={threads}, ms/step median={1e3 * med:.3f} "
+                      f"mean={1e3 * sum(times) / n:.3f}"}
 
 
 def _cpu_rigl_sample(work, HostLayer, kind, threads, seconds, row_div=16):
@@ -1172,15 +1202,16 @@ def measure(work, args):
     kern = []
     for name, fn, nbytes, nflops in work.kernels():
         stage(f"kernel timing: {name}")
-        ms, reps = kernel_avg_ms(fn, with_reps=True)
-        kern.append({"kernel": name, "avg_us": round(ms * 1e3, 3), "bytes": nbytes,
+        ms, mean_ms, reps = kernel_time_ms(fn)
+        kern.append({"kernel": name, "median_us": round(ms * 1e3, 3),
+                     "mean_us": round(mean_ms * 1e3, 3), "bytes": nbytes,
                      "flops": nflops, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                     "timed_calls": reps})
+                     "timed_calls": reps, "warmup_calls": KERNEL_WARMUP})
     # roofline on the path's dominant kernel (forward SpMM, dX SpMM or dW SDDMM)
     dom = max((k for k in kern if k["kernel"].startswith(("spmm", "sddmm", "backward_narrow"))),
-              key=lambda k: k["avg_us"])
-    achieved = dom["bytes"] / (dom["avg_us"] * 1e-6) / 1e9
-    tflops = dom["flops"] / (dom["avg_us"] * 1e-6) / 1e12
+              key=lambda k: k["median_us"])
+    achieved = dom["bytes"] / (dom["median_us"] * 1e-6) / 1e9
+    tflops = dom["flops"] / (dom["median_us"] * 1e-6) / 1e12
     # HBM bytes per launch of the dominant kernel, from the committed
     # rocprofv3 FETCH_SIZE/WRITE_SIZE summary of this workload (if any)
     traffic = None
@@ -1196,12 +1227,12 @@ def measure(work, args):
         unit = "tokens/s"
         W = work.spmm_layer()
         l1 = [k for k in kern if "[l1" in k["kernel"]]
-        spmm_us = sum(k["avg_us"] for k in kern)
+        spmm_us = sum(k["median_us"] for k in kern)
         path = {"spmm_kernels_us_per_step": round(spmm_us, 2),
                 "layer1_fwd_dw_GBps": round(sum(k["bytes"] for k in l1) /
-                                            (sum(k["avg_us"] for k in l1) * 1e-6) / 1e9, 1),
+                                            (sum(k["median_us"] for k in l1) * 1e-6) / 1e9, 1),
                 "layer1_fwd_dw_GFLOPs": round(sum(k["flops"] for k in l1) /
-                                              (sum(k["avg_us"] for k in l1) * 1e-6) / 1e9, 1),
+                                              (sum(k["median_us"] for k in l1) * 1e-6) / 1e9, 1),
                 "layer1_nnz": W.nnz}
         config = {"workload": "c2: " + work.desc, "global_batch": work.batch,
                   "l1_dx": "not computed (the input needs no grad; the reference computes "
@@ -1212,7 +1243,8 @@ def measure(work, args):
     elif isinstance(work, GPTWork):
         value = work.tokens_per_step() * args.steps / elapsed
         unit = "tokens/s"
-        per_block_us = sum(k["avg_us"] for k in kern if k["kernel"].startswith(("spmm", "sddmm")))
+        per_block_us = sum(k["median_us"] for k in kern
+                           if k["kernel"].startswith(("spmm", "sddmm")))
         path = {"block0_sparse_kernels_us": round(per_block_us, 1),
                 "block0_sparse_GBps": round(sum(k["bytes"] for k in kern) /
                                             (per_block_us * 1e-6) / 1e9, 1),
@@ -1230,7 +1262,7 @@ def measure(work, args):
     else:
         path_k = [k for k in kern if k["kernel"] in ("spmm_fwd", "sddmm_dw", "transpose_refresh",
                                                       "spmm_dx")]
-        path_us = sum(k["avg_us"] for k in path_k)
+        path_us = sum(k["median_us"] for k in path_k)
         path = {"fwd_dw_dx_us": round(path_us, 1),
                 "fwd_dw_dx_GBps": round(work.step_bytes() / (path_us * 1e-6) / 1e9, 1),
                 "fwd_dw_dx_GFLOPs": round(work.step_flops() / (path_us * 1e-6) / 1e9, 1),
@@ -1254,7 +1286,7 @@ def measure(work, args):
     if apx:
         # RigL's matrix-core pass: three bf16 products (x_h·y_h, x_h·y_l,
         # x_l·y_h) of 2·M·K·N flops each, against the dense bf16 peak
-        t = 3 * apx[0]["flops"] / (apx[0]["avg_us"] * 1e-6) / 1e12
+        t = 3 * apx[0]["flops"] / (apx[0]["median_us"] * 1e-6) / 1e12
         roofline_mfma = {"kernel": "dense_grad_approx", "achieved": round(t, 1),
                          "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(t / MFMA_BF16_PEAK_TFLOPS, 4)}
@@ -1302,10 +1334,11 @@ def main():
                      f"{[k[0] for k in work.kernels()]}")
         name, fn, nbytes, nflops = got[0]
         stage(f"kernel timing: {name}")
-        ms = kernel_avg_ms(fn)
+        ms, mean_ms, reps = kernel_time_ms(fn)
         calibrate_copy(args, dev)
-        print(json.dumps({"workload": args.workload, "kernel": name, "avg_us": round(ms * 1e3, 3),
-                          "bytes": nbytes, "flops": nflops, "reps": KERNEL_REPS}), flush=True)
+        print(json.dumps({"workload": args.workload, "kernel": name,
+                          "median_us": round(ms * 1e3, 3), "mean_us": round(mean_ms * 1e3, 3),
+                          "bytes": nbytes, "flops": nflops, "reps": reps}), flush=True)
         return
     m = measure(work, args)
     line = {

@@ -172,6 +172,57 @@ def test_c4_sparse_linear_step_and_set_rewrite(dev):
     assert_bits_equal(ops._transpose_cache[id(W)][3].cpu().numpy(), perm_o2, "perm after SET")
 
 
+def _device_copy(W):
+    """A device copy of W's arrays (no host round trip, no re-validation)."""
+    from sparsecore_amd import PaddedCSR
+
+    return PaddedCSR._from_parts(W.nrows, W.ncols, W.values.detach().clone(),
+                                 W.col_indices.clone(), W.row_start.clone(), W.row_nnz.clone(),
+                                 W.row_capacity.clone(), W.nnz, W.topology_version)
+
+
+def _device_rows_equal(A, B, what):
+    """Every row of two device PaddedCSRs: the same row_nnz, and the same
+    column and value bits over each row's capacity (live slots and padding)."""
+    assert A.nnz == B.nnz, what
+    for name in ("row_nnz", "row_start", "row_capacity", "col_indices"):
+        a, b = getattr(A, name), getattr(B, name)
+        bad = torch.nonzero(a != b)
+        assert bad.numel() == 0, f"{what}: {name} differs at {bad[:8].flatten().tolist()}"
+    va, vb = A.values.detach().view(torch.int32), B.values.detach().view(torch.int32)
+    bad = torch.nonzero(va != vb)
+    assert bad.numel() == 0, f"{what}: value bits differ at slots {bad[:8].flatten().tolist()}"
+
+
+def test_c4_ffn_rigl_certified_every_row(dev):
+    """The C4 FFN-up layer (3072 x 768 at 90%, N = 8192) through one RigL
+    update: the certified path (matrix-core G', exact G only where undecided)
+    rewrites every row exactly as the exact-G drop/grow does; the exact path is
+    checked against the oracle's row rule on sampled rows."""
+    W = _uniform_layer(3072, 768, 0.9, 405, dev)
+    X, dY = _dense_inputs(3072, 768, 8192, 406, dev)
+    c = to_oracle(W)
+    W_exact = _device_copy(W)
+    k = max(1, int(0.3 * W.nnz))
+    print("[config c4 RigL] certified update", flush=True)
+    W._rigl_update(k, dY, X)
+    G = ops.dense_grad(dY, X)
+    W_exact._drop_grow(k, _lib.SLK_GROW_GRADIENT, G)
+    _device_rows_equal(W, W_exact, "c4 ffn certified vs exact, every row")
+    thr = np.float32(oracle.live_abs_kth(c, k))
+    after = to_oracle(W_exact)
+    rows = _sample(c.row_nnz, 7)
+    G_rows = G[torch.from_numpy(rows).to(dev)].cpu().numpy()
+    for r, g_row in zip(rows, G_rows):
+        s, n = int(c.row_start[r]), int(c.row_nnz[r])
+        wc, wv = oracle.drop_grow_row(c.col_indices[s:s + n], c.values[s:s + n], thr, "gradient",
+                                      c.ncols, g_row, row=int(r))
+        m = int(after.row_nnz[r])
+        assert m == wc.size, r
+        assert_bits_equal(after.col_indices[s:s + m], wc, f"exact RigL cols row {r}")
+        assert_bits_equal(after.values[s:s + m], wv, f"exact RigL vals row {r}")
+
+
 # ───────────────────────────── C5 ───────────────────────────────────────
 
 @pytest.fixture(scope="module")
@@ -214,6 +265,7 @@ def test_c5_rigl_rewrite_at_full_size(dev, c5_layers, density):
     topology (sampled rows)."""
     W, X, dY = c5_layers(density)
     c = to_oracle(W)
+    W_exact = _device_copy(W)  # the exact-G drop/grow, pinned to the oracle below
     print(f"[config c5 RigL] density={density} dense_grad", flush=True)
     G = ops.dense_grad(dY, X)
     torch.cuda.synchronize()
@@ -231,6 +283,11 @@ def test_c5_rigl_rewrite_at_full_size(dev, c5_layers, density):
     assert thr.view(np.uint32) == np.float32(oracle.live_abs_kth(c, k)).view(np.uint32)
     print(f"[config c5 RigL] density={density} certified RigL update", flush=True)
     W._rigl_update(k, dY, X)
+    # every row: the certified update against the exact-G drop/grow on a copy
+    print(f"[config c5 RigL] density={density} every row against exact G", flush=True)
+    W_exact._drop_grow(k, _lib.SLK_GROW_GRADIENT, G)
+    _device_rows_equal(W, W_exact, f"c5 {density} certified vs exact, every row")
+    del W_exact
     after = to_oracle(W)
     rows = _sample(c.row_nnz, 13)
     G_rows = G[torch.from_numpy(rows).to(dev)].cpu().numpy()

@@ -430,12 +430,22 @@ def _rigl_inputs(M, K, N, seed, kind="normal"):
     elif kind == "nonfinite-cols":  # a NaN column leaves no row certifiable
         X[2, 5] = np.nan
         X[7, 1] = -np.inf
+    elif kind == "cancel":
+        # partial sums climb to ~|a_i|·N/2 and cancel back down: dY_i = a_i on
+        # the first half of j and -a_i on the second, X_k = 1 + noise/2, so
+        # |G| ~ |a_i|·sqrt(N)/2 while the running sums peak 2^5 x higher and
+        # the bound's c2·pm term outweighs its c1·n_i·n_k term
+        a = rng.standard_normal((M, 1)).astype(np.float32)
+        sign = np.where(np.arange(N) < N // 2, 1.0, -1.0).astype(np.float32)
+        dY = a * sign[None, :]
+        X = (1.0 + 0.5 * rng.standard_normal((K, N))).astype(np.float32)
     return dY, X
 
 
 @pytest.mark.parametrize("M,K,N,kind", [
     (256, 384, 4096, "normal"), (130, 257, 1000, "normal"), (64, 64, 7, "normal"),
-    (300, 200, 513, "scaled"), (128, 128, 1, "normal"), (200, 300, 96, "ties")])
+    (300, 200, 513, "scaled"), (128, 128, 1, "normal"), (200, 300, 96, "ties"),
+    (192, 320, 4096, "cancel")])
 def test_dense_grad_approx_within_certified_bound(dev, M, K, N, kind):
     """|G' - G| <= c1·n_i·n_k + c2·2^(code - 127) + 2^-100·(1 + n_i + n_k) for
     every element, G the reference-arithmetic dense gradient (itself pinned to
@@ -478,6 +488,13 @@ def test_dense_grad_approx_within_certified_bound(dev, M, K, N, kind):
     assert np.all(err <= E), float(np.max(err / E))
     # the bound is a bound, not noise: the approximation is far inside it
     assert float(np.max(err / E)) < 0.5
+    if kind == "cancel":
+        # the partial-sum term decides the bound here: it is the larger term
+        # for nearly every element, and |G| sits far below the running sums
+        nn_b = c1 * nd.cpu().numpy().astype(np.float64)[:, None] * \
+            nx.cpu().numpy().astype(np.float64)[None, :]
+        assert np.mean(c2 * pbound > nn_b) > 0.95
+        assert np.median(pm / (-(-N // 128)) / np.maximum(np.abs(G), 1e-30)) > 8
 
 
 def _rigl_case(name):
@@ -495,6 +512,8 @@ def _rigl_case(name):
         return oracle.uniform_rows(40, 90, 20, seed=39, sigma=1.0), 64, "nonfinite-cols"
     if name == "n-odd":
         return oracle.zipf_rows(150, 129, 0.2, 1.1, seed=36, sigma=1.0), 37, "normal"
+    if name == "cancel":
+        return oracle.uniform_rows(96, 300, 40, seed=41, sigma=1.0), 4096, "cancel"
     if name == "dense-rows":
         W = np.random.default_rng(37).standard_normal((30, 50)).astype(np.float32)
         W[::3, :] *= (np.random.default_rng(38).random((10, 50)) < 0.1)  # some sparse rows
@@ -504,7 +523,7 @@ def _rigl_case(name):
 
 @pytest.mark.parametrize("df", [0.3, 0.9])
 @pytest.mark.parametrize("name", ["uniform", "zipf", "ties", "scaled", "nonfinite-rows",
-                                  "nonfinite-cols", "n-odd", "dense-rows"])
+                                  "nonfinite-cols", "n-odd", "dense-rows", "cancel"])
 def test_rigl_certified_matches_exact_drop_grow(dev, name, df):
     """The certified path (matrix-core G', exact G only where the bound cannot
     decide) rewrites every row exactly as the exact-G drop/grow does, and as
@@ -523,3 +542,104 @@ def test_rigl_certified_matches_exact_drop_grow(dev, name, df):
     csr_arrays_equal(to_oracle(W_cert), want, f"{name} certified vs oracle")
     if name == "nonfinite-rows":
         assert want.nnz < c.nnz  # the NaN row shrank
+    if name == "cancel":
+        # the certified path decided this case (not the exact fallback), with
+        # undecided columns left for the exact finish
+        W = from_oracle(c, dev)
+        view = W._view()
+        thr = torch.empty(1, device=dev)
+        _lib.live_abs_kth(view, k, torch.empty(_lib.SLK_KTH_WORKSPACE_BYTES, dtype=torch.uint8,
+                                               device=dev), thr)
+        nd, nx = torch.empty(c.nrows, device=dev), torch.empty(c.ncols, device=dev)
+        _lib.rigl_norms(dY, X, nd, nx)
+        Gp = torch.empty(c.nrows, c.ncols, device=dev)
+        Gc = torch.empty(c.nrows, c.ncols, dtype=torch.uint8, device=dev)
+        _lib.dense_grad_approx(dY, X, Gp, Gc)
+        info = torch.empty(c.nrows * _lib.RIGL_INFO_BYTES, dtype=torch.uint8, device=dev)
+        off = torch.empty(2 * c.nrows + 1, dtype=torch.int64, device=dev)
+        total = torch.empty(1, dtype=torch.int64, device=dev)
+        _lib.rigl_count(view, thr, Gp, Gc, nd, nx, N, info, off, total)
+        n_amb = int(total.item())
+        assert 0 < n_amb <= W._RIGL_EXACT_SHARE * (c.nrows * c.ncols - c.nnz), n_amb
+
+
+def _bf16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bits, round to nearest even (finite inputs)."""
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    b = (b + 0x7FFF + ((b >> 16) & 1)) >> 16
+    return b.astype(np.uint16)
+
+
+def _bf16_value(bits: np.ndarray) -> np.ndarray:
+    return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+def test_rigl_mfma_accumulation_model(dev):
+    """The matrix-core instruction the certified RigL bound models
+    (v_mfma_f32_32x32x16_bf16, run by slk_rigl_mfma_probe with the operand
+    layout of slk_dense_grad_approx): D = C + sum of 16 exact bf16 products.
+    Small integers (every sum exact) must come out exact, which pins the lane
+    layout; on random, wide-range, cancelling and tie-breaking operands the
+    error against the exact sum stays within gamma_16(2u)·(|C| + sum|a b|),
+    the per-step allowance the bound's c1 and c2 are built on."""
+    rng = np.random.default_rng(2024)
+    n_per = 16
+    cases = []
+    # exact: small integers
+    A = rng.integers(-3, 4, (n_per, 32, 16)).astype(np.float32)
+    B = rng.integers(-3, 4, (n_per, 32, 16)).astype(np.float32)
+    C = rng.integers(-50, 51, (n_per, 32, 32)).astype(np.float32)
+    cases.append(("integers", A, B, C, True))
+    # random normal operands, accumulators over several magnitudes
+    A = rng.standard_normal((n_per, 32, 16)).astype(np.float32)
+    B = rng.standard_normal((n_per, 32, 16)).astype(np.float32)
+    C = (rng.standard_normal((n_per, 32, 32)) * 10.0 ** rng.integers(-3, 4, (n_per, 32, 32))
+         ).astype(np.float32)
+    cases.append(("normal", A, B, C, False))
+    # products over 2^-20 .. 2^20 against a unit accumulator
+    A = (rng.standard_normal((n_per, 32, 16)) * 2.0 ** rng.integers(-10, 11, (n_per, 32, 16))
+         ).astype(np.float32)
+    B = (rng.standard_normal((n_per, 32, 16)) * 2.0 ** rng.integers(-10, 11, (n_per, 32, 16))
+         ).astype(np.float32)
+    C = rng.standard_normal((n_per, 32, 32)).astype(np.float32)
+    cases.append(("wide", A, B, C, False))
+    # cancellation: C = -(the products' sum)·(1 + tiny)
+    A = rng.standard_normal((n_per, 32, 16)).astype(np.float32)
+    B = rng.standard_normal((n_per, 32, 16)).astype(np.float32)
+    Av, Bv = _bf16_value(_bf16_bits(A)), _bf16_value(_bf16_bits(B))
+    S = np.einsum("tik,tjk->tij", Av.astype(np.float64), Bv.astype(np.float64))
+    C = (-S * (1 + 1e-6 * rng.standard_normal(S.shape))).astype(np.float32)
+    cases.append(("cancel", A, B, C, False))
+    # ties: 1 + 2^-24 exactly halfway between two floats, and 1 + 3·2^-25
+    A = np.zeros((n_per, 32, 16), np.float32)
+    B = np.zeros((n_per, 32, 16), np.float32)
+    A[:, :, 0] = 2.0 ** -12
+    B[:, :, 0] = 2.0 ** -12
+    A[:, ::2, 1] = 2.0 ** -13
+    B[:, :, 1] = 2.0 ** -12
+    C = np.ones((n_per, 32, 32), np.float32)
+    cases.append(("ties", A, B, C, False))
+
+    u = 2.0 ** -24
+    gamma = 16 * 2 * u / (1 - 16 * 2 * u)
+    worst = 0.0
+    for name, A, B, C, exact in cases:
+        Ab, Bb = _bf16_bits(A), _bf16_bits(B)
+        Av = _bf16_value(Ab).astype(np.float64)
+        Bv = _bf16_value(Bb).astype(np.float64)
+        P = Av[:, :, None, :] * Bv[:, None, :, :]          # t, i, j, k: exact products
+        want = C.astype(np.float64) + P.sum(axis=3)
+        mag = np.abs(C.astype(np.float64)) + np.abs(P).sum(axis=3)
+        D = torch.empty(C.shape, device=dev)
+        _lib.rigl_mfma_probe(torch.from_numpy(Ab.view(np.int16)).to(dev),
+                             torch.from_numpy(Bb.view(np.int16)).to(dev),
+                             torch.from_numpy(C).to(dev), D)
+        got = D.cpu().numpy().astype(np.float64)
+        err = np.abs(got - want)
+        print(f"[mfma probe] {name}: max err / (u·mag) = {float(np.max(err / (u * mag))):.3f}",
+              flush=True)
+        if exact:
+            assert_bits_equal(got.astype(np.float32), want.astype(np.float32), f"{name} exact")
+        assert np.all(err <= gamma * mag + 2.0 ** -126), name
+        worst = max(worst, float(np.max(err / (u * mag))))
+    assert worst <= 32.0
