@@ -173,6 +173,8 @@ SLK_API int slk_abi_version(void);
  *                         all columns instead of row x column tiles
  *   SLK_TUNE_SPMM_BIN     0 = ignore a binned slot stream (slk_csr.bin_off)
  *   SLK_TUNE_SPMM_G       binned kernel: slots of a row read ahead (1, 2 or 4)
+ *   SLK_TUNE_RIGL_TILE    slk_dense_grad_approx: 128 = 128 x 128 tiles staged
+ *                         through registers (else 256 x 128 tiles, direct loads)
  * Returns SLK_EINVAL for an unknown knob.                                   */
 enum slk_tune_knob {
     SLK_TUNE_SPMM_KERNEL = 0,
@@ -186,7 +188,8 @@ enum slk_tune_knob {
     SLK_TUNE_TRANSPOSE_TILE = 8,
     SLK_TUNE_SPMM_BIN = 9,
     SLK_TUNE_SPMM_G = 10,
-    SLK_TUNE_COUNT = 11
+    SLK_TUNE_RIGL_TILE = 11,
+    SLK_TUNE_COUNT = 12
 };
 SLK_API int slk_set_tuning(int knob, int64_t value);
 

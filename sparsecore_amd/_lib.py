@@ -74,7 +74,7 @@ DROP_GROW_NOALLOC_MAX_SLOTS = 1 << 21  # SLK_DROP_GROW_NOALLOC_MAX_SLOTS
 # Kernel-choice overrides (slk_set_tuning): knob numbers of enum slk_tune_knob.
 TUNE_KNOBS = {"spmm_kernel": 0, "spmm_h": 1, "spmm_rw": 2, "spmm_split": 3, "spmm_vec": 4,
               "sddmm_g": 5, "seg_lean": 6, "seg_group": 7, "transpose_tile": 8, "spmm_bin": 9,
-              "spmm_g": 10}
+              "spmm_g": 10, "rigl_tile": 11}
 
 BIN_MAX_CHUNKS = 960  # SLK_BIN_MAX_CHUNKS
 

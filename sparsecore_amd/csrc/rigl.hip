@@ -88,6 +88,11 @@ constexpr int kAThreads = 256;  // 4 waves, 2 x 2, each 64 x 64 of the tile
 constexpr int kAGroup = 8;      // tile rows per group of the tile order
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// s_waitcnt operand: vector-memory count <= n and no LDS or scalar access
+// outstanding (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt
+// 11:8)
+constexpr int kVmcntLe(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // bf16 bits of x rounded to nearest even (x finite; non-finite x keeps its
@@ -296,6 +301,194 @@ __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64
 #pragma unroll
                     for (int r = 0; r < 16; ++r) pm[a][b][r] = pm[a][b][r] + fabsf(acc[a][b][r]);
         }
+    }
+    // lane l, register 4g + q of a 32x32 block: row 8g + 4(l/32) + q, column l % 32
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+        const int64_t col = k0 + wn * 64 + b * 32 + (lane & 31);
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = i0 + wm * 64 + a * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (row < M && col < K) {
+                    G[row * K + col] = acc[a][b][r];
+                    Gc[row * K + col] = static_cast<uint8_t>(partial_code(pm[a][b][r]));
+                }
+            }
+    }
+}
+
+// The same G' and codes from larger tiles fed by direct loads into LDS.
+// A workgroup of 8 waves (4 x 2, each 64 x 64 as above) takes a 256 x 128
+// tile, so every staged B row serves twice the rows of A. Stages reach LDS by
+// global_load_lds_dwordx4 (no registers, no LDS stores) in a ring of three,
+// issued two stages ahead, with one barrier per stage. A staged row is its
+// 128 bytes unpadded: piece c (16 bytes) of row r sits at slot r·8 + (c ^
+// ((r >> 1) & 7)), so the 16 lanes of an LDS pass, reading one piece of 16
+// consecutive rows, hit 16 distinct slot columns (all 64 banks once). Each
+// element's MFMA sequence (per k-step: hi·hi, hi·lo, lo·hi; k-steps in j
+// order; |running sum| added to pm at every chunk end) is the 128 x 128
+// kernel's, so G' and the codes are bit for bit the same.
+constexpr int kGTI = 256;                      // output tile rows (rows of dY)
+constexpr int kGTK = 128;                      // output tile columns (rows of X)
+constexpr int kGThreads = 512;                 // 8 waves
+constexpr int kGBufs = 3;                      // LDS ring of stages
+constexpr int kGPerA = kGTI * 8 / 64 / 8;      // A loads per wave and stage (64 pieces each)
+constexpr int kGPerB = kGTK * 8 / 64 / 8;      // B loads per wave and stage
+static_assert(kAStageBytes == 128, "eight 16-byte pieces per staged row");
+
+__device__ __forceinline__ int g_slot(int r, int c) { return r * 8 + (c ^ ((r >> 1) & 7)); }
+
+__global__ __launch_bounds__(kGThreads) void rigl_approx_dma_kernel(
+    int64_t M, int64_t K, int64_t nst, const uint16_t* __restrict__ PA,
+    const uint16_t* __restrict__ PB, float* __restrict__ G, uint8_t* __restrict__ Gc) {
+    // one LDS array (A rows, then B rows, per ring buffer): 3 x 48 KiB
+    __shared__ __align__(16) unsigned char sAB[kGBufs][(kGTI + kGTK) * kAStageBytes];
+
+    const int64_t nTi = ceil_div(M, kGTI), nTk = ceil_div(K, kGTK);
+    const int64_t L = xcd_logical_block(blockIdx.x, gridDim.x);
+    const int64_t grp = L / (kAGroup * nTk);
+    const int64_t first = grp * kAGroup;
+    const int64_t gsize = nTi - first < kAGroup ? nTi - first : kAGroup;
+    const int64_t in_grp = L - grp * kAGroup * nTk;
+    const int64_t i0 = (first + in_grp % gsize) * kGTI;
+    const int64_t k0 = (in_grp / gsize) * kGTK;
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wm = wv >> 1, wn = wv & 1;  // rows wm*64 .. +64, columns wn*64 .. +64
+
+    // Staging. Load i of a stage fills slots [64 i, 64 i + 64) of its matrix's
+    // buffer: rows 8 i .. 8 i + 7; lane l fetches piece (l mod 8) ^ swizzle of
+    // row 8 i + l / 8, so it lands at its swizzled slot. Wave wv issues loads
+    // wv, wv + 8, ...: per lane a fixed 32-bit offset from a scalar row base
+    // (rows past the matrix clamped to its last row), plus 128 bytes a stage.
+    const char* baseA[kGPerA];
+    const char* baseB[kGPerB];
+    uint32_t offA[kGPerA], offB[kGPerB];
+    auto plan = [&](const uint16_t* P, int64_t R, int64_t r0, int i, const char*& base,
+                    uint32_t& off) {
+        const int64_t rb = min(r0 + 8 * i, R - 1);
+        const int64_t r = min(r0 + 8 * i + lane / 8, R - 1);
+        const int rr = 8 * i + lane / 8;  // the row inside the tile
+        const int c = (lane & 7) ^ ((rr >> 1) & 7);
+        base = reinterpret_cast<const char*>(P) + rb * nst * kAStageBytes;
+        off = static_cast<uint32_t>((r - rb) * nst * kAStageBytes + 16 * c);
+    };
+#pragma unroll
+    for (int q = 0; q < kGPerA; ++q) plan(PA, M, i0, wv + 8 * q, baseA[q], offA[q]);
+#pragma unroll
+    for (int q = 0; q < kGPerB; ++q) plan(PB, K, k0, wv + 8 * q, baseB[q], offB[q]);
+    auto issue = [&](int buf, int64_t st) {
+        const int64_t so = st * kAStageBytes;
+#pragma unroll
+        for (int q = 0; q < kGPerA; ++q)
+            __builtin_amdgcn_global_load_lds(baseA[q] + so + offA[q],
+                                             &sAB[buf][64 * 16 * (wv + 8 * q)], 16, 0, 0);
+#pragma unroll
+        for (int q = 0; q < kGPerB; ++q)
+            __builtin_amdgcn_global_load_lds(baseB[q] + so + offB[q],
+                                             &sAB[buf][kGTI * kAStageBytes + 64 * 16 * (wv + 8 * q)],
+                                             16, 0, 0);
+    };
+
+    f32x16 acc[2][2], pm[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[a][b][r] = pm[a][b][r] = 0.0f;
+
+    const int half = lane >> 5;
+    const int rA = wm * 64 + (lane & 31), rB = wn * 64 + (lane & 31);
+    auto frag = [&](const unsigned char* lds, int r, int c) {
+        return *reinterpret_cast<const bf16x8*>(lds + 16 * g_slot(r, c));
+    };
+    constexpr int kLoads = kGPerA + kGPerB;  // this wave's direct loads per stage
+    // Stage st reads ring buffer st mod 3 and loads stage st + 2 into buffer
+    // (st + 2) mod 3. The loop is unrolled by three so both indexes are
+    // compile-time constants: the compiler then sees that the reads and the
+    // direct loads touch different buffers (with run-time indexes it makes
+    // every read wait for the loads just issued).
+    auto stage = [&](auto I, int64_t st) {
+        constexpr int buf = decltype(I)::value;
+        // This wave's loads of stage st have landed (loads complete in order;
+        // stage st+1's may still be in flight) and its reads of stage st-1
+        // have returned; then the barrier: every wave's loads of stage st are
+        // in LDS and stage st-1's buffer is free. A bare s_barrier: the
+        // workgroup fence of __syncthreads() would also wait for stage st+1's
+        // loads; the memory clobber keeps the compiler from moving LDS
+        // accesses across it.
+        if (st + 1 < nst) __builtin_amdgcn_s_waitcnt(kVmcntLe(kLoads));
+        else __builtin_amdgcn_s_waitcnt(0);
+        asm volatile("s_barrier" ::: "memory");
+        const unsigned char* la = sAB[buf];
+        const unsigned char* lb = sAB[buf] + kGTI * kAStageBytes;
+        // Reads and MFMAs interleaved so that reads are in flight while MFMAs
+        // run, at most 12 LDS reads outstanding (the wait counter tracks 15):
+        // k-step 0's reads (high parts first), its high x high MFMAs, k-step
+        // 1's reads (and stage st+2's direct loads), the rest of k-step 0,
+        // then k-step 1. Scheduling barriers keep the compiler from sinking
+        // the reads to their uses.
+        bf16x8 af[kAJ / 16][2][2], bf[kAJ / 16][2][2];  // [k-step][block][high, low]
+        auto reads = [&](int ks) {
+#pragma unroll
+            for (int p = 0; p < 2; ++p)
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    const int c = 4 * p + 2 * ks + half;
+                    af[ks][b][p] = frag(la, rA + 32 * b, c);
+                    bf[ks][b][p] = frag(lb, rB + 32 * b, c);
+                }
+        };
+        auto mfmas = [&](int ks, int pa, int pb) {
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks][a][pa], bf[ks][b][pb],
+                                                                         acc[a][b], 0, 0, 0);
+        };
+        static_assert(kAJ / 16 == 2, "two k-steps per stage below");
+        reads(0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        reads(1);
+        // then stage st+2's loads (its buffer was read in stage st-1)
+        if (st + 2 < nst) issue((buf + 2) % kGBufs, st + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(0, 0, 1);
+        mfmas(0, 1, 0);
+        mfmas(1, 0, 0);
+        mfmas(1, 0, 1);
+        mfmas(1, 1, 0);
+        if ((st + 1) % (kAChunk / kAJ) == 0) {  // a chunk done: |running sum| to pm
+#pragma unroll
+            for (int a = 0; a < 2; ++a)
+#pragma unroll
+                for (int b = 0; b < 2; ++b)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) pm[a][b][r] = pm[a][b][r] + fabsf(acc[a][b][r]);
+        }
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    using B2 = std::integral_constant<int, 2>;
+    if (nst > 0) {
+        issue(0, 0);
+        if (nst > 1) issue(1, 1);
+        int64_t st = 0;
+        for (; st + 3 <= nst; st += 3) {
+            stage(B0{}, st);
+            stage(B1{}, st + 1);
+            stage(B2{}, st + 2);
+        }
+        if (st < nst) stage(B0{}, st);
+        if (st + 1 < nst) stage(B1{}, st + 1);
     }
     // lane l, register 4g + q of a 32x32 block: row 8g + 4(l/32) + q, column l % 32
 #pragma unroll
@@ -1240,8 +1433,14 @@ extern "C" int slk_dense_grad_approx(const float* dY, const float* X, int64_t M,
                            dim3(256), 0, st, X, K, N, nst, PB);
         if (int rc = check_launch("dense_grad_approx/split")) return rc;
     }
-    hipLaunchKernelGGL(rigl_approx_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kAThreads), 0,
-                       st, M, K, nst, PA, PB, G, G_code);
+    if (tuning(SLK_TUNE_RIGL_TILE) == 128) {
+        hipLaunchKernelGGL(rigl_approx_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kAThreads),
+                           0, st, M, K, nst, PA, PB, G, G_code);
+    } else {
+        const int64_t big = ceil_div(M, kGTI) * ceil_div(K, kGTK);
+        hipLaunchKernelGGL(rigl_approx_dma_kernel, dim3(static_cast<unsigned>(big)),
+                           dim3(kGThreads), 0, st, M, K, nst, PA, PB, G, G_code);
+    }
     return check_launch("dense_grad_approx");
 }
 

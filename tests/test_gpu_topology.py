@@ -497,6 +497,28 @@ def test_dense_grad_approx_within_certified_bound(dev, M, K, N, kind):
         assert np.median(pm / (-(-N // 128)) / np.maximum(np.abs(G), 1e-30)) > 8
 
 
+@pytest.mark.parametrize("M,K,N,kind", [
+    (256, 384, 4096, "normal"), (130, 257, 1000, "normal"), (300, 200, 513, "scaled"),
+    (64, 64, 7, "normal"), (520, 136, 260, "ties"), (1, 1, 1, "normal"),
+    (192, 320, 4096, "cancel")])
+def test_dense_grad_approx_tilings_agree(dev, tune, M, K, N, kind):
+    """The 256 x 128 direct-load kernel and the 128 x 128 register-staged one
+    run each element's matrix-core sequence in the same order: identical G'
+    and codes, bit for bit (partial tiles, N not a multiple of the stage)."""
+    print(f"[G' tilings] {M}x{K} N={N} {kind}", flush=True)
+    dY_np, X_np = _rigl_inputs(M, K, N, M * 3 + K + N, kind)
+    dY, X = torch.from_numpy(dY_np).to(dev), torch.from_numpy(X_np).to(dev)
+    out = []
+    for tile in (None, 128):
+        tune(rigl_tile=tile)
+        Gp = torch.full((M, K), float("nan"), device=dev)
+        Gc = torch.zeros(M, K, dtype=torch.uint8, device=dev)
+        _lib.dense_grad_approx(dY, X, Gp, Gc)
+        out.append((Gp.cpu().numpy(), Gc.cpu().numpy()))
+    assert_bits_equal(out[0][0], out[1][0], "G'")
+    assert_bits_equal(out[0][1], out[1][1], "G' codes")
+
+
 def _rigl_case(name):
     if name == "uniform":
         return oracle.uniform_rows(96, 300, 40, seed=31, sigma=1.0), 512, "normal"
