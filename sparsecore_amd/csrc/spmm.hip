@@ -1295,9 +1295,11 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
             // forward 8.27 -> 8.03 ms against two launches
             const int64_t nb_rest = ceil_div(M - T, int64_t{kLdsWaves} * rw) * ceil_div(N, int64_t{kLdsCols});
             if (h == 1 && nb_rest >= kXcds) {
-                switch (rw) {
+                switch (rw) {  // every rw the checks above admit
                     case 2: return launch_lds_split_rw<2>(W, T, X, N, bias, Y, st);
+                    case 3: return launch_lds_split_rw<3>(W, T, X, N, bias, Y, st);
                     case 4: return launch_lds_split_rw<4>(W, T, X, N, bias, Y, st);
+                    case 6: return launch_lds_split_rw<6>(W, T, X, N, bias, Y, st);
                     default: return launch_lds_split_rw<8>(W, T, X, N, bias, Y, st);
                 }
             }

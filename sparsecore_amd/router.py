@@ -20,9 +20,12 @@ uniform random subset of the row's empty columns, as the reference does, but
 from its own counter-based generator (splitmix64 keys) seeded from the
 algorithm's ``seed``: the reference's numpy ``Generator.choice`` stream
 cannot be reproduced on the device, so SET topologies match the reference's
-in distribution, not draw for draw. Row nnz never changes (a row regrows
-exactly what it dropped), so the cached row schedule survives; the topology
-version is bumped and the transpose cache rebuilds on the next backward.
+in distribution, not draw for draw. A row regrows as many columns as it
+dropped, except under RigL's NaN rule: a column whose G is NaN is never
+grown, so a row with fewer non-NaN empty columns than drops ends shorter
+(its capacity is unchanged). Every update bumps the topology version, and
+every cached schedule (row order, segment list, phase bounds, binned stream,
+the transpose) is keyed by it, so each rebuilds on its next use.
 """
 
 from __future__ import annotations
