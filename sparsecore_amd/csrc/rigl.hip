@@ -408,61 +408,67 @@ __global__ __launch_bounds__(kGThreads) void rigl_approx_dma_kernel(
         return *reinterpret_cast<const bf16x8*>(lds + 16 * g_slot(r, c));
     };
     constexpr int kLoads = kGPerA + kGPerB;  // this wave's direct loads per stage
+    bf16x8 af[kAJ / 16][2][2], bf[kAJ / 16][2][2];  // [k-step][block][high, low]
+    auto reads = [&](const unsigned char* buf, int ks) {
+        const unsigned char* lb = buf + kGTI * kAStageBytes;
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const int c = 4 * p + 2 * ks + half;
+                af[ks][b][p] = frag(buf, rA + 32 * b, c);
+                bf[ks][b][p] = frag(lb, rB + 32 * b, c);
+            }
+    };
+    auto mfmas = [&](int ks, int pa, int pb) {
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks][a][pa], bf[ks][b][pb],
+                                                                     acc[a][b], 0, 0, 0);
+    };
+    static_assert(kAJ / 16 == 2, "two k-steps per stage below");
     // Stage st reads ring buffer st mod 3 and loads stage st + 2 into buffer
     // (st + 2) mod 3. The loop is unrolled by three so both indexes are
     // compile-time constants: the compiler then sees that the reads and the
     // direct loads touch different buffers (with run-time indexes it makes
     // every read wait for the loads just issued).
+    //
+    // The workgroup barrier sits in the middle of a stage, after its last
+    // reads, so that the next stage's first reads go out right after it and
+    // land while this stage's last twelve MFMAs run: per stage, k-step 0's
+    // fragments (read in the previous stage) feed its high x high MFMAs;
+    // k-step 1's reads and stage st+2's direct loads go out; the rest of
+    // k-step 0; then this wave's loads of stage st+1 have landed (loads
+    // complete in order; stage st+2's may still be in flight) and its reads
+    // of stage st have returned, and the barrier: every wave's loads of stage
+    // st+1 are in LDS and buffer st is free for stage st+3's loads; stage
+    // st+1's k-step 0 reads; k-step 1's MFMAs. A bare s_barrier: the
+    // workgroup fence of __syncthreads() would also wait for stage st+2's
+    // loads; the memory clobber keeps the compiler from moving LDS accesses
+    // across it, and scheduling barriers keep it from sinking the reads to
+    // their uses. At most 12 LDS reads are outstanding (the wait counter
+    // tracks 15). The last two stages load the last stage again (into the
+    // buffer that is free), so every stage waits for the same count and
+    // passes the barrier, with no branch for the compiler's wait tracking to
+    // merge (at a branch join it waits for every outstanding read). Each
+    // element's MFMA order is unchanged: per k-step hi·hi, hi·lo, lo·hi,
+    // k-steps in j order.
     auto stage = [&](auto I, int64_t st) {
         constexpr int buf = decltype(I)::value;
-        // This wave's loads of stage st have landed (loads complete in order;
-        // stage st+1's may still be in flight) and its reads of stage st-1
-        // have returned; then the barrier: every wave's loads of stage st are
-        // in LDS and stage st-1's buffer is free. A bare s_barrier: the
-        // workgroup fence of __syncthreads() would also wait for stage st+1's
-        // loads; the memory clobber keeps the compiler from moving LDS
-        // accesses across it.
-        if (st + 1 < nst) __builtin_amdgcn_s_waitcnt(kVmcntLe(kLoads));
-        else __builtin_amdgcn_s_waitcnt(0);
-        asm volatile("s_barrier" ::: "memory");
-        const unsigned char* la = sAB[buf];
-        const unsigned char* lb = sAB[buf] + kGTI * kAStageBytes;
-        // Reads and MFMAs interleaved so that reads are in flight while MFMAs
-        // run, at most 12 LDS reads outstanding (the wait counter tracks 15):
-        // k-step 0's reads (high parts first), its high x high MFMAs, k-step
-        // 1's reads (and stage st+2's direct loads), the rest of k-step 0,
-        // then k-step 1. Scheduling barriers keep the compiler from sinking
-        // the reads to their uses.
-        bf16x8 af[kAJ / 16][2][2], bf[kAJ / 16][2][2];  // [k-step][block][high, low]
-        auto reads = [&](int ks) {
-#pragma unroll
-            for (int p = 0; p < 2; ++p)
-#pragma unroll
-                for (int b = 0; b < 2; ++b) {
-                    const int c = 4 * p + 2 * ks + half;
-                    af[ks][b][p] = frag(la, rA + 32 * b, c);
-                    bf[ks][b][p] = frag(lb, rB + 32 * b, c);
-                }
-        };
-        auto mfmas = [&](int ks, int pa, int pb) {
-#pragma unroll
-            for (int a = 0; a < 2; ++a)
-#pragma unroll
-                for (int b = 0; b < 2; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks][a][pa], bf[ks][b][pb],
-                                                                         acc[a][b], 0, 0, 0);
-        };
-        static_assert(kAJ / 16 == 2, "two k-steps per stage below");
-        reads(0);
-        __builtin_amdgcn_sched_barrier(0);
         mfmas(0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
-        reads(1);
-        // then stage st+2's loads (its buffer was read in stage st-1)
-        if (st + 2 < nst) issue((buf + 2) % kGBufs, st + 2);
+        reads(sAB[buf], 1);
+        issue((buf + 2) % kGBufs, st + 2 < nst ? st + 2 : nst - 1);
         __builtin_amdgcn_sched_barrier(0);
         mfmas(0, 0, 1);
         mfmas(0, 1, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(kVmcntLe(kLoads));
+        asm volatile("s_barrier" ::: "memory");
+        reads(sAB[(buf + 1) % kGBufs], 0);
+        __builtin_amdgcn_sched_barrier(0);
         mfmas(1, 0, 0);
         mfmas(1, 0, 1);
         mfmas(1, 1, 0);
@@ -480,7 +486,11 @@ __global__ __launch_bounds__(kGThreads) void rigl_approx_dma_kernel(
     using B2 = std::integral_constant<int, 2>;
     if (nst > 0) {
         issue(0, 0);
-        if (nst > 1) issue(1, 1);
+        issue(1, nst > 1 ? 1 : 0);
+        // stage 0's loads landed (stage 1's may be in flight), then its k-step 0 reads
+        __builtin_amdgcn_s_waitcnt(kVmcntLe(kLoads));
+        asm volatile("s_barrier" ::: "memory");
+        reads(sAB[0], 0);
         int64_t st = 0;
         for (; st + 3 <= nst; st += 3) {
             stage(B0{}, st);
@@ -489,6 +499,7 @@ __global__ __launch_bounds__(kGThreads) void rigl_approx_dma_kernel(
         }
         if (st < nst) stage(B0{}, st);
         if (st + 1 < nst) stage(B1{}, st + 1);
+        __builtin_amdgcn_s_waitcnt(0);  // no direct load still writing LDS when the waves end
     }
     // lane l, register 4g + q of a 32x32 block: row 8g + 4(l/32) + q, column l % 32
 #pragma unroll

@@ -25,7 +25,8 @@ dropped, except under RigL's NaN rule: a column whose G is NaN is never
 grown, so a row with fewer non-NaN empty columns than drops ends shorter
 (its capacity is unchanged). Every update bumps the topology version, and
 every cached schedule (row order, segment list, phase bounds, binned stream,
-the transpose) is keyed by it, so each rebuilds on its next use.
+the transpose) is keyed by it, so each rebuilds on its next use; only the
+longest-first row order is carried over, when no row shrank.
 """
 
 from __future__ import annotations
