@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define SLK_ABI_VERSION 13
+#define SLK_ABI_VERSION 14
 
 #if defined(__GNUC__)
 #define SLK_API __attribute__((visibility("default")))
@@ -370,12 +370,16 @@ SLK_API int slk_dense_grad(const float* dY, const float* X, int64_t M, int64_t K
  *   slk_rigl_norms         row norms of dY (M x N) and X (K x N), row-major;
  *   slk_dense_grad_approx  G' = dY·X^T on the matrix cores (fp32 split into
  *                          bf16 parts), M x K row-major;
- *   slk_rigl_count         per row: survivors, and the empty columns whose
- *                          rank |G'| cannot certify; their exclusive scan;
+ *   slk_rigl_count         per row: survivors, the empty columns whose rank
+ *                          |G'| certifies, and those it cannot (undecided);
+ *                          their counts, and (for rows of up to 16384
+ *                          columns, K % 16 == 0) their lists;
  *   slk_rigl_finish        per row: exact G of the undecided columns, the
  *                          grow choice, the rewrite (as slk_drop_grow).
- * The caller reads *amb_total after slk_rigl_count to size the finish
- * workspace (8 bytes per undecided column). |G'[i,k] - G[i,k]| <=
+ * The caller sizes amb_ws before slk_rigl_count (8 bytes per undecided
+ * column it accepts) and reads *amb_total after it: a total above that
+ * capacity means the lists are incomplete and the finish must not run (the
+ * caller computes G exactly instead). |G'[i,k] - G[i,k]| <=
  * slk_rigl_bound_factor(N)·nrm_dY[i]·nrm_X[k] + slk_rigl_partial_factor(N)·
  * 2^(G_code[i,k] - 127) + 2^-100·(1 + nrm_dY[i] + nrm_X[k]) for norms up to
  * 2^60 (larger or non-finite norms make the row exact: every empty column is
@@ -405,18 +409,22 @@ SLK_API double slk_rigl_partial_factor(int64_t N);
 /* Per row of W: survivors of *thr_dev (the global drop threshold, as for
  * slk_drop_grow) and the empty columns the bound leaves undecided. info:
  * 32 bytes per row (opaque to the caller, read by slk_rigl_finish); amb_off:
- * 2*nrows + 1 int64: [0, nrows] receive the exclusive scan of the undecided
- * counts, the rest is scratch; *amb_total = amb_off[nrows] (device int64).
- * ncols at most 131072.                                                     */
+ * 2*nrows + 1 int64: row i's undecided columns are pairs
+ * [amb_off[i], amb_off[i] + amb_off[nrows + 1 + i]) of the list, and
+ * *amb_total = amb_off[nrows] (device int64) their total. amb_ws (8 bytes per
+ * pair, amb_ws_bytes of them) and workspace (as slk_drop_grow's) are the
+ * ones slk_rigl_finish then receives: the lists go there. ncols at most
+ * 131072.                                                                   */
 SLK_API int slk_rigl_count(const slk_csr* W, const float* thr_dev, const float* G_approx,
                            int64_t ldg, const uint8_t* G_code, const float* nrm_dY,
                            const float* nrm_X, int64_t N, void* info, int64_t* amb_off,
-                           int64_t* amb_total, void* stream);
+                           int64_t* amb_total, void* amb_ws, int64_t amb_ws_bytes,
+                           void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Finishes the RigL pass slk_rigl_count began: values, col_indices and
  * row_nnz must be W's own arrays (rewritten as slk_drop_grow rewrites them);
- * amb_ws holds 8 bytes per undecided column (amb_ws_bytes >= 8 * *amb_total);
- * workspace as slk_drop_grow's; *removed as slk_drop_grow's.                */
+ * amb_ws and workspace the ones slk_rigl_count received, with
+ * amb_ws_bytes >= 8 * *amb_total; *removed as slk_drop_grow's.             */
 SLK_API int slk_rigl_finish(const slk_csr* W, float* values, int32_t* col_indices,
                             int32_t* row_nnz, const float* thr_dev, const float* G_approx,
                             int64_t ldg, const uint8_t* G_code, const float* nrm_dY,

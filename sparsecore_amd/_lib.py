@@ -21,7 +21,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libsparsecore_amd.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 SLK_OK, SLK_EINVAL, SLK_EDEVICE = 0, 1, 2
 SLK_DW_SIMD, SLK_DW_SCALAR = 0, 1
@@ -168,7 +168,7 @@ def _declare(lib) -> None:
     lib.slk_rigl_partial_factor.restype = ctypes.c_double
     lib.slk_rigl_partial_factor.argtypes = [_i64]
     lib.slk_rigl_count.argtypes = [_csrp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp,
-                                   _vp]
+                                   _vp, _i64, _vp, _i64, _vp]
     lib.slk_rigl_finish.argtypes = [_csrp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp,
                                     _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp]
     lib.slk_drop_grow_noalloc.argtypes = [_csrp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _i64,
@@ -491,11 +491,15 @@ def rigl_partial_factor(N: int) -> float:
 
 def rigl_count(view: CsrView, thr: torch.Tensor, G: torch.Tensor, G_code: torch.Tensor,
                nrm_dY: torch.Tensor, nrm_X: torch.Tensor, N: int, info: torch.Tensor,
-               amb_off: torch.Tensor, amb_total: torch.Tensor) -> None:
+               amb_off: torch.Tensor, amb_total: torch.Tensor, amb_ws: torch.Tensor,
+               ws: torch.Tensor) -> None:
+    """Per-row survivors and undecided columns (slk_rigl_count); the lists go
+    to amb_ws (8 bytes per undecided column) and ws (slk_drop_grow's
+    workspace), which slk_rigl_finish then receives."""
     rc = load().slk_rigl_count(ctypes.byref(view), thr.data_ptr(), ptr(G), G.stride(0),
                                ptr(G_code), ptr(nrm_dY), ptr(nrm_X), int(N), ptr(info),
-                               amb_off.data_ptr(),
-                               amb_total.data_ptr(), stream_of(amb_total))
+                               amb_off.data_ptr(), amb_total.data_ptr(), ptr(amb_ws),
+                               amb_ws.numel(), ptr(ws), ws.numel(), stream_of(amb_total))
     if rc:
         _raise(rc)
 

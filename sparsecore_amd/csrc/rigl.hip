@@ -638,28 +638,37 @@ __device__ __forceinline__ void for_each_col(const float* __restrict__ g_row,
     }
 }
 
-// rigl_count_kernel with the row's |G'| in registers: thread t owns columns
-// 16(t + 256v) + e (v < U/4, e < 16), so the radix passes read no memory. For
-// K <= 1024·U, K % 16 == 0, 16-byte aligned rows of G', codes and nrm_c. Same
-// counts, thresholds and flags as rigl_count_kernel: the select visits the
-// same candidates with the same keys.
+// rigl_count_kernel with the row's |G'| in registers, and the list pass
+// (rigl_list_kernel) folded in: thread t owns columns 16(t + 256v) + e
+// (v < U/4, e < 16), so the radix passes read no memory, and the classes
+// found for the counts are the ones listed, with no second pass over G'. For
+// K <= 1024·U, K % 16 == 0, 16-byte aligned rows of G', codes and nrm_c.
+// Same counts, thresholds and flags as rigl_count_kernel (the select visits
+// the same candidates with the same keys), and the same lists as
+// rigl_list_kernel: the row's undecided columns ascending at its range of the
+// pair list (reserved with one atomic add on the running total amb_off[M],
+// which the caller zeroes; amb_off[i] = the row's start, amb_off[M + 1 + i]
+// its count; pairs past amb_cap are not written), its certain grows
+// ascending in its staging slots.
 template <int U>
 __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
-    int64_t K, int64_t Kw, const int32_t* __restrict__ row_start,
+    int64_t K, int64_t M, const int32_t* __restrict__ row_start,
     const int32_t* __restrict__ row_nnz, const float* __restrict__ values,
     const int32_t* __restrict__ cols, const float* __restrict__ thr_ptr,
     const float* __restrict__ Gp, int64_t ldg, const uint8_t* __restrict__ Gc,
     const float* __restrict__ nrm_r, const float* __restrict__ nrm_c, float c_bound, float c2,
-    RowInfo* __restrict__ info,
-    int64_t* __restrict__ amb_count) {
+    RowInfo* __restrict__ info, int64_t* __restrict__ amb_off, int32_t* __restrict__ amb_col,
+    uint32_t* __restrict__ amb_key, int64_t amb_cap, int32_t* __restrict__ stage_col) {
+    constexpr int kGroups = U / 4;  // groups of 16 consecutive columns per thread
+    static_assert(kGroups >= 1 && kGroups <= 4, "four 16-bit counts per int64");
     __shared__ uint32_t keep[U * kRowThreads * 4 / 32];
     __shared__ int64_t tmp[kRowThreads];
     __shared__ uint32_t hist[2048];
-    __shared__ uint32_t lst[U * kRowThreads * 4];  // 64 KiB at U = 16
     __shared__ uint32_t s_digit;
     __shared__ int64_t s_below;
     __shared__ unsigned long long s_best;
     __shared__ uint32_t s_nmax, s_cmax;
+    __shared__ int64_t s_base;
 
     const int64_t i = blockIdx.x;
     const int t = threadIdx.x;
@@ -670,26 +679,90 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
     };
     RowInfo ri{};
     const int32_t n_live = row_nnz[i];
-    auto finish_row = [&](int32_t flags, int64_t n_amb) {
+    auto keep_row = [&]() {  // nothing to grow: nothing listed
         if (t == 0) {
-            ri.flags = flags;
+            ri.flags = kRowKeep;
             info[i] = ri;
-            amb_count[i] = n_amb;
+            amb_off[i] = 0;
+            amb_off[M + 1 + i] = 0;
         }
     };
-    if (n_live <= 0) return finish_row(kRowKeep, 0);  // the reference skips empty rows
+    if (n_live <= 0) return keep_row();  // the reference skips empty rows
     const int32_t start = row_start[i];
-    for (int64_t w = t; w < Kw; w += kRowThreads) keep[w] = 0;
+    for (int w = t; w < U * kRowThreads * 4 / 32; w += kRowThreads) keep[w] = 0;
     if (t == 0) s_nmax = s_cmax = 0;
     __syncthreads();
     const int64_t n_keep = mark_survivors(values, cols, start, n_live, thr_ptr[0], keep, tmp,
                                           &s_best);
     const int64_t n_drop = n_live - n_keep;
     ri.n_keep = static_cast<int32_t>(n_keep);
-    if (n_drop == 0) return finish_row(kRowKeep, 0);
+    if (n_drop == 0) return keep_row();
     const int64_t n_empty = K - n_keep;
     const float ni = nrm_r[i];
     const float* g_row = Gp + i * ldg;
+
+    // Lists the row (bit 4u + e of a mask is column col_of(u) + e): the
+    // undecided columns `amb` and, for a certified row, the certain grows
+    // `in`, in ascending column order, i.e. in the order (v, t, u % 4, e).
+    // Per-thread counts of each group v, 16 bits apiece in one int64, go
+    // through one workgroup scan per list, which gives every thread its start
+    // in every group.
+    auto emit = [&](int32_t flags, uint64_t amb, uint64_t in) {
+        int64_t pa = 0, pi = 0;
+#pragma unroll
+        for (int v = 0; v < kGroups; ++v) {
+            pa |= static_cast<int64_t>(__popcll((amb >> (16 * v)) & 0xFFFFull)) << (16 * v);
+            pi |= static_cast<int64_t>(__popcll((in >> (16 * v)) & 0xFFFFull)) << (16 * v);
+        }
+        const int64_t xa = block_inclusive_scan(pa, tmp) - pa;
+        const int64_t ta = tmp[kRowThreads - 1];
+        const int64_t xi = block_inclusive_scan(pi, tmp) - pi;
+        const int64_t ti = tmp[kRowThreads - 1];
+        int64_t n_amb = 0, n_in = 0;
+#pragma unroll
+        for (int v = 0; v < kGroups; ++v) {
+            n_amb += (ta >> (16 * v)) & 0xFFFF;
+            n_in += (ti >> (16 * v)) & 0xFFFF;
+        }
+        if (t == 0) {
+            const int64_t base =
+                n_amb > 0 ? static_cast<int64_t>(atomicAdd(
+                                reinterpret_cast<unsigned long long*>(amb_off + M),
+                                static_cast<unsigned long long>(n_amb)))
+                          : 0;
+            s_base = base;
+            ri.flags = flags;
+            ri.n_in = static_cast<int32_t>(n_in);
+            info[i] = ri;
+            amb_off[i] = base;
+            amb_off[M + 1 + i] = n_amb;
+        }
+        __syncthreads();
+        int64_t pos_a = s_base, pos_i = 0;  // this thread's next positions, group by group
+#pragma unroll
+        for (int v = 0; v < kGroups; ++v) {
+            int64_t a = pos_a + ((xa >> (16 * v)) & 0xFFFF);
+            int64_t g = pos_i + ((xi >> (16 * v)) & 0xFFFF);
+#pragma unroll
+            for (int b = 0; b < 16; ++b) {
+                const int bit = 16 * v + b;
+                const int64_t c = col_of(bit / 4) + (bit % 4);
+                if ((amb >> bit) & 1ull) {
+                    if (a < amb_cap) {
+                        amb_col[a] = static_cast<int32_t>(c);
+                        amb_key[a] = static_cast<uint32_t>(i);
+                    }
+                    ++a;
+                }
+                if ((in >> bit) & 1ull) {
+                    if (g < n_live) stage_col[start + g] = static_cast<int32_t>(c);
+                    ++g;
+                }
+            }
+            pos_a += (ta >> (16 * v)) & 0xFFFF;
+            pos_i += (ti >> (16 * v)) & 0xFFFF;
+        }
+    };
 
     // the row's |G'| and empty-column mask (bit 4u + e) (every load issued
     // before the first use: clamped addresses instead of branches, the
@@ -720,17 +793,17 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
     }
     block_inclusive_scan(unbounded, tmp);
     unbounded = tmp[kRowThreads - 1];
-    if (unbounded > 0 || !(ni <= kNormCap)) return finish_row(kRowExact, n_empty);
+    if (unbounded > 0 || !(ni <= kNormCap)) return emit(kRowExact, cand, 0);
     const int64_t n_grow = n_drop < n_empty ? n_drop : n_empty;
 
     // T' = the n_grow-th largest |G'| of the empty columns: the n_grow-th
-    // smallest key. First the top 11 bits over the registers (2048 bins), then
-    // the keys in that bin, listed in LDS (most rows: a few hundred; the list
-    // holds a whole row), for the remaining 21 bits in passes of 8, 8 and 5
-    // bits. Any exact selection gives the same key.
+    // smallest key, by a radix select over the registers: the top 11 bits
+    // (2048 bins), then the remaining 21 in passes of 8, 8 and 5 bits over
+    // the keys that share the prefix found so far. Any exact selection gives
+    // the same key.
     uint32_t prefix = 0;
     int64_t need = n_grow;
-    auto pick = [&](int bins, int64_t h_of_thread_lo, int per) {
+    auto pick = [&](int64_t h_of_thread_lo, int per) {
         // thread t holds bins [t*per, t*per + per); finds the bin of the
         // need-th key and the count below it
         const int64_t incl = block_inclusive_scan(h_of_thread_lo, tmp);
@@ -746,7 +819,6 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
                 run += hq;
             }
         }
-        (void)bins;
         __syncthreads();
     };
     {
@@ -763,42 +835,23 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
         __syncthreads();
         int64_t hs = 0;
         for (int q = 0; q < kPer; ++q) hs += hist[t * kPer + q];
-        pick(kTopBins, hs, kPer);
+        pick(hs, kPer);
         prefix = s_digit;
         need -= s_below;
-        const int64_t n_bin = hist[prefix];
-        __syncthreads();
-        // list the bin's keys: per-thread counts, one scan for the offsets
-        uint64_t in_bin = 0;
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if ((a[u][e] >> (32 - kTopBits)) == prefix) in_bin |= 1ull << (4 * u + e);
-        in_bin &= cand;
-        const int64_t mine = __popcll(in_bin);
-        const int32_t at = static_cast<int32_t>(block_inclusive_scan(mine, tmp) - mine);
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int bit = 4 * u + e;  // slot: the bin's keys of this thread before it
-                if ((in_bin >> bit) & 1ull)
-                    lst[at + __popcll(in_bin & ((1ull << bit) - 1ull))] = a[u][e];
-            }
         __syncthreads();
         int shift = 32 - kTopBits;
         for (const int width : {8, 8, 5}) {
-            shift -= width;
             hist[t] = 0;
             __syncthreads();
-            for (int64_t e = t; e < n_bin; e += kRowThreads) {
-                const uint32_t key = lst[e];
-                if ((key >> (shift + width)) == prefix)
-                    atomicAdd(&hist[(key >> shift) & ((1u << width) - 1u)], 1u);
-            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (((cand >> (4 * u + e)) & 1ull) && (a[u][e] >> shift) == prefix)
+                        atomicAdd(&hist[(a[u][e] >> (shift - width)) & ((1u << width) - 1u)], 1u);
+            shift -= width;
             __syncthreads();
-            pick(1 << width, hist[t], 1);
+            pick(hist[t], 1);
             prefix = (prefix << width) | s_digit;
             need -= s_below;
             __syncthreads();
@@ -835,14 +888,14 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
     atomicMax(&s_nmax, nmax);
     atomicMax(&s_cmax, cmax);
     block_inclusive_scan(unbounded, tmp);
-    if (tmp[kRowThreads - 1] > 0) return finish_row(kRowExact, n_empty);
+    if (tmp[kRowThreads - 1] > 0) return emit(kRowExact, cand, 0);
     const float nm = __uint_as_float(s_nmax);
     const float cni = up_(c_bound * ni);
     const float delta = up_(0x1p-100f * up_(1.0f + ni + nm));
     const float e_max = col_err(cni, nm, delta, c2, s_cmax);
     const float t_in = up_(Tp + e_max);
     const float t_out = dn_(Tp - e_max);
-    int64_t n_in = 0, n_amb = 0;
+    uint64_t amb = 0, in = 0;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const uint32_t cw = codes16(u / 4)[u % 4];
@@ -851,21 +904,16 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
             if (!((cand >> (4 * u + e)) & 1ull)) continue;
             const int cls = classify_col(__uint_as_float(~a[u][e]), cni, nr[u][e], delta, c2,
                                          (cw >> (8 * e)) & 255u, t_in, t_out);
-            n_in += cls == kGrowIn;
-            n_amb += cls == kGrowUndecided;
+            if (cls == kGrowIn) in |= 1ull << (4 * u + e);
+            if (cls == kGrowUndecided) amb |= 1ull << (4 * u + e);
         }
     }
-    block_inclusive_scan(n_in, tmp);
-    n_in = tmp[kRowThreads - 1];
-    block_inclusive_scan(n_amb, tmp);
-    n_amb = tmp[kRowThreads - 1];
     ri.n_grow = static_cast<int32_t>(n_grow);
-    ri.n_in = static_cast<int32_t>(n_in);
     ri.t_in = t_in;
     ri.t_out = t_out;
     ri.cni = cni;
     ri.delta = delta;
-    finish_row(0, n_amb);
+    emit(0, amb, in);
 }
 
 // Per row: survivors (as the exact kernel), then, over the empty columns,
@@ -1113,7 +1161,7 @@ __global__ __launch_bounds__(kRowThreads) void rigl_list_kernel(
     __syncthreads();
     mark_survivors(values, cols, start, n_live, thr_ptr[0], keep, tmp, &s_best);
     const int64_t off = amb_off[i];
-    const int64_t n_amb = amb_off[i + 1] - off;
+    const int64_t n_amb = amb_off[gridDim.x + 1 + i];
     if (ri.flags & kRowExact) {
         for (int64_t c = t; c < K; c += kRowThreads)
             if (!bit_of(keep, c)) atomicOr(&ambm[c >> 5], 1u << (c & 31));
@@ -1287,8 +1335,9 @@ __global__ __launch_bounds__(kRowThreads) void rigl_select_kernel(
     }
     __syncthreads();
     const int64_t off = amb_off[i];
-    const int64_t n_amb = min(amb_off[i + 1], amb_cap) - min(off, amb_cap);  // (a workspace
-    // smaller than the contract asks leaves columns out, never reads past it)
+    const int64_t n_amb = min(off + amb_off[gridDim.x + 1 + i], amb_cap) - min(off, amb_cap);
+    // (a workspace smaller than the contract asks leaves columns out, never
+    // reads past it)
     int64_t n_grow = ri.n_grow, need = ri.n_grow - n_in;
     if (exact_row) {  // NaN columns are not growable
         int64_t ok = 0;
@@ -1338,6 +1387,21 @@ __global__ __launch_bounds__(64) void rigl_mfma_probe_kernel(const uint16_t* __r
 }
 
 __global__ void rigl_clear_kernel(unsigned long long* __restrict__ c) { *c = 0; }
+__global__ void rigl_copy_kernel(const int64_t* __restrict__ s, int64_t* __restrict__ d) { *d = *s; }
+
+// U of the row-in-registers count kernel for this problem, or 0 for the
+// generic count kernel (whose lists the finish's list pass writes). Both
+// slk_rigl_count and slk_rigl_finish decide with it.
+int count_reg_units(int64_t K, int64_t ldg, const float* G, const uint8_t* Gc, const float* nrm_X) {
+    const bool vr = K % 16 == 0 && ldg % 4 == 0 && reinterpret_cast<uintptr_t>(G) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(Gc) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(nrm_X) % 16 == 0;
+    if (!vr) return 0;
+    if (K <= 4 * kRowThreads * 4) return 4;
+    if (K <= 4 * kRowThreads * 8) return 8;
+    if (K <= 4 * kRowThreads * 16) return 16;
+    return 0;
+}
 
 // The bound's factors: |G'[i,k] - G[i,k]| <= c1·n_i·n_k + c2·pm[i,k] + δ,
 // pm = the element's sum of |running sums of G'| at the chunk ends (its
@@ -1462,7 +1526,8 @@ extern "C" double slk_rigl_partial_factor(int64_t N) { return slk::certified_fac
 extern "C" int slk_rigl_count(const slk_csr* W, const float* thr_dev, const float* G_approx,
                               int64_t ldg, const uint8_t* G_code, const float* nrm_dY,
                               const float* nrm_X, int64_t N, void* info, int64_t* amb_off,
-                              int64_t* amb_total, void* stream) {
+                              int64_t* amb_total, void* amb_ws, int64_t amb_ws_bytes,
+                              void* workspace, int64_t workspace_bytes, void* stream) {
     using namespace slk;
     clear_error();
     if (int rc = validate_csr(W, "rigl_count")) return rc;
@@ -1478,10 +1543,21 @@ extern "C" int slk_rigl_count(const slk_csr* W, const float* thr_dev, const floa
                          ldg < W->ncols || nrm_dY == nullptr || nrm_X == nullptr ||
                          info == nullptr))
         return fail(SLK_EINVAL, "rigl_count: NULL input or ldg < ncols");
+    if (amb_ws_bytes < 0 || (amb_ws_bytes > 0 && amb_ws == nullptr))
+        return fail(SLK_EINVAL, "rigl_count: bad undecided-column workspace");
+    if (W->nrows > 0 && W->total_capacity > 0 &&
+        (workspace == nullptr || workspace_bytes < W->total_capacity * 8))
+        return fail(SLK_EINVAL, "rigl_count: workspace smaller than slk_drop_grow_workspace_bytes");
     hipStream_t st = as_stream(stream);
     const int64_t M = W->nrows, K = W->ncols;
     const int64_t Kw = ceil_div(K, 32) > 0 ? ceil_div(K, 32) : 1;
-    // amb_off doubles as the per-row counts before the scan
+    const int U = M > 0 ? count_reg_units(K, ldg, G_approx, G_code, nrm_X) : 0;
+    if (U > 0) {
+        // the lists written here: the running total amb_off[M] from zero
+        hipLaunchKernelGGL(rigl_clear_kernel, dim3(1), dim3(1), 0, st,
+                           reinterpret_cast<unsigned long long*>(amb_off + M));
+        if (int rc = check_launch("rigl_count")) return rc;
+    }
     if (M > 0) {
         // the factors rounded up to floats
         const BoundFactors bf = certified_factors(N);
@@ -1493,19 +1569,22 @@ extern "C" int slk_rigl_count(const slk_csr* W, const float* thr_dev, const floa
                         reinterpret_cast<uintptr_t>(nrm_X) % 16 == 0;
         const dim3 grid(static_cast<unsigned>(M));
         const size_t lds_st = static_cast<size_t>(Kw + K) * 4, lds_un = static_cast<size_t>(Kw) * 4;
-#define SLK_COUNT_ARGS                                                                       \
-    K, Kw, W->row_start, W->row_nnz, W->values, W->col_indices, thr_dev, G_approx, ldg, G_code, \
-        nrm_dY, nrm_X, c_f, c2_f, static_cast<RowInfo*>(info), amb_off + M + 1
-        const bool vr = vg && K % 16 == 0 && reinterpret_cast<uintptr_t>(G_code) % 16 == 0;
-        if (vr && K <= 4 * kRowThreads * 4) {
+        const int64_t n_amb_max = amb_ws_bytes / 8;
+        int32_t* amb_col = static_cast<int32_t*>(amb_ws);
+        uint32_t* amb_key = reinterpret_cast<uint32_t*>(amb_col + n_amb_max);
+        int32_t* stage_col = static_cast<int32_t*>(workspace);
+#define SLK_COUNT_REG_ARGS                                                                      K, M, W->row_start, W->row_nnz, W->values, W->col_indices, thr_dev, G_approx, ldg, G_code,         nrm_dY, nrm_X, c_f, c2_f, static_cast<RowInfo*>(info), amb_off, amb_col, amb_key,            n_amb_max, stage_col
+        // (amb_off + M + 1: the per-row counts, which the scan turns into offsets)
+#define SLK_COUNT_ARGS                                                                           K, Kw, W->row_start, W->row_nnz, W->values, W->col_indices, thr_dev, G_approx, ldg, G_code,         nrm_dY, nrm_X, c_f, c2_f, static_cast<RowInfo*>(info), amb_off + M + 1
+        if (U == 4) {
             hipLaunchKernelGGL(rigl_count_reg_kernel<4>, grid, dim3(kRowThreads), 0, st,
-                               SLK_COUNT_ARGS);
-        } else if (vr && K <= 4 * kRowThreads * 8) {
+                               SLK_COUNT_REG_ARGS);
+        } else if (U == 8) {
             hipLaunchKernelGGL(rigl_count_reg_kernel<8>, grid, dim3(kRowThreads), 0, st,
-                               SLK_COUNT_ARGS);
-        } else if (vr && K <= 4 * kRowThreads * 16) {
+                               SLK_COUNT_REG_ARGS);
+        } else if (U == 16) {
             hipLaunchKernelGGL(rigl_count_reg_kernel<16>, grid, dim3(kRowThreads), 0, st,
-                               SLK_COUNT_ARGS);
+                               SLK_COUNT_REG_ARGS);
         } else if (K <= kStageMaxK && vg) {
             hipLaunchKernelGGL((rigl_count_kernel<true, true>), grid, dim3(kRowThreads), lds_st, st,
                                SLK_COUNT_ARGS);
@@ -1520,10 +1599,15 @@ extern "C" int slk_rigl_count(const slk_csr* W, const float* thr_dev, const floa
                                st, SLK_COUNT_ARGS);
         }
 #undef SLK_COUNT_ARGS
+#undef SLK_COUNT_REG_ARGS
         if (int rc = check_launch("rigl_count")) return rc;
     }
-    hipLaunchKernelGGL(rigl_scan_kernel, dim3(1), dim3(1024), 0, st, M, amb_off + M + 1, amb_off,
-                       amb_total);
+    if (U > 0) {
+        hipLaunchKernelGGL(rigl_copy_kernel, dim3(1), dim3(1), 0, st, amb_off + M, amb_total);
+    } else {
+        hipLaunchKernelGGL(rigl_scan_kernel, dim3(1), dim3(1024), 0, st, M, amb_off + M + 1,
+                           amb_off, amb_total);
+    }
     return check_launch("rigl_count/scan");
 }
 
@@ -1578,16 +1662,22 @@ extern "C" int slk_rigl_finish(const slk_csr* W, float* values, int32_t* col_ind
                     reinterpret_cast<uintptr_t>(nrm_X) % 16 == 0;
     const float c2_f = std::nextafter(static_cast<float>(certified_factors(N).c2), INFINITY);
     const dim3 grid(static_cast<unsigned>(M));
+    // the lists: written by the count kernel where it held the row in
+    // registers, else by the list pass
 #define SLK_LIST_ARGS                                                                      \
     K, Kw, W->row_start, row_nnz, values, col_indices, thr_dev, G_approx, ldg, G_code, c2_f, \
         nrm_X, static_cast<const RowInfo*>(info), amb_off, amb_col, amb_key, n_amb_max, stage_col
-    if (vg) {
-        hipLaunchKernelGGL(rigl_list_kernel<true>, grid, dim3(kRowThreads), lds, st, SLK_LIST_ARGS);
-    } else {
-        hipLaunchKernelGGL(rigl_list_kernel<false>, grid, dim3(kRowThreads), lds, st, SLK_LIST_ARGS);
+    if (count_reg_units(K, ldg, G_approx, G_code, nrm_X) == 0) {
+        if (vg) {
+            hipLaunchKernelGGL(rigl_list_kernel<true>, grid, dim3(kRowThreads), lds, st,
+                               SLK_LIST_ARGS);
+        } else {
+            hipLaunchKernelGGL(rigl_list_kernel<false>, grid, dim3(kRowThreads), lds, st,
+                               SLK_LIST_ARGS);
+        }
+        if (int rc = check_launch("rigl_finish/list")) return rc;
     }
 #undef SLK_LIST_ARGS
-    if (int rc = check_launch("rigl_finish/list")) return rc;
     if (P > 0) {
         if (ceil_div(P, 256) > INT32_MAX) return fail(SLK_EINVAL, "rigl_finish: too many undecided columns");
         const bool v4 = N > 0 && N % 4 == 0 && reinterpret_cast<uintptr_t>(dY) % 16 == 0 &&

@@ -648,15 +648,19 @@ class PaddedCSR:
         info = torch.empty(M * _lib.RIGL_INFO_BYTES, dtype=torch.uint8, device=dev)
         amb_off = torch.empty(2 * M + 1, dtype=torch.int64, device=dev)
         total = torch.empty(1, dtype=torch.int64, device=dev)
-        _lib.rigl_count(view, thr, Gp, Gc, nrm_dY, nrm_X, dY.shape[1], info, amb_off, total)
+        # the undecided-column lists, sized for the most the certified path
+        # takes (the count writes them where it holds rows in registers)
+        cap = max(1, int(self._RIGL_EXACT_SHARE * max(1, M * K - self._nnz)))
+        amb = torch.empty(8 * cap, dtype=torch.uint8, device=dev)
+        stage = torch.empty(_lib.drop_grow_workspace_bytes(view), dtype=torch.uint8, device=dev)
+        _lib.rigl_count(view, thr, Gp, Gc, nrm_dY, nrm_X, dY.shape[1], info, amb_off, total,
+                        amb, stage)
         n_amb = int(total.item())
-        if n_amb > self._RIGL_EXACT_SHARE * max(1, M * K - self._nnz):
-            del Gp, Gc
+        if n_amb > cap:
+            del Gp, Gc, amb, stage
             from .ops import dense_grad
             self._drop_grow(k_drop, _lib.SLK_GROW_GRADIENT, dense_grad(dY, X))
             return
-        amb = torch.empty(max(8, 8 * n_amb), dtype=torch.uint8, device=dev)
-        stage = torch.empty(_lib.drop_grow_workspace_bytes(view), dtype=torch.uint8, device=dev)
         removed = torch.empty(1, dtype=torch.int64, device=dev)
         _lib.rigl_finish(view, thr, Gp, Gc, nrm_dY, nrm_X, dY, X, info, amb_off, amb, stage,
                          removed)

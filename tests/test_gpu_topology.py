@@ -540,12 +540,32 @@ def _rigl_case(name):
         W = np.random.default_rng(37).standard_normal((30, 50)).astype(np.float32)
         W[::3, :] *= (np.random.default_rng(38).random((10, 50)) < 0.1)  # some sparse rows
         return oracle.from_dense(W), 256, "normal"
+    # ncols % 16 == 0: the count kernel that holds a row in registers and
+    # lists the columns itself (4, 8 and 16 registers of keys per thread)
+    if name == "uniform-k16":
+        return oracle.uniform_rows(96, 320, 40, seed=51, sigma=1.0), 512, "normal"
+    if name == "zipf-k16":
+        return oracle.zipf_rows(400, 704, 0.06, 1.1, seed=52, sigma=1.0), 1024, "normal"
+    if name == "ties-k16":
+        return oracle.uniform_rows(64, 208, 30, seed=53, sigma=1.0), 96, "ties"
+    if name == "nonfinite-rows-k16":
+        return oracle.uniform_rows(200, 96, 20, seed=54, sigma=1.0), 64, "nonfinite-rows"
+    if name == "nonfinite-cols-k16":
+        return oracle.uniform_rows(40, 96, 20, seed=55, sigma=1.0), 64, "nonfinite-cols"
+    if name == "cancel-k16":
+        return oracle.uniform_rows(96, 320, 40, seed=56, sigma=1.0), 4096, "cancel"
+    if name == "wide-u8":
+        return oracle.zipf_rows(48, 6144, 0.05, 1.1, seed=57, sigma=1.0), 64, "normal"
+    if name == "wide-u16":
+        return oracle.uniform_rows(32, 12288, 600, seed=58, sigma=1.0), 48, "normal"
     raise KeyError(name)
 
 
 @pytest.mark.parametrize("df", [0.3, 0.9])
 @pytest.mark.parametrize("name", ["uniform", "zipf", "ties", "scaled", "nonfinite-rows",
-                                  "nonfinite-cols", "n-odd", "dense-rows", "cancel"])
+                                  "nonfinite-cols", "n-odd", "dense-rows", "cancel",
+                                  "uniform-k16", "zipf-k16", "ties-k16", "nonfinite-rows-k16",
+                                  "nonfinite-cols-k16", "cancel-k16", "wide-u8", "wide-u16"])
 def test_rigl_certified_matches_exact_drop_grow(dev, name, df):
     """The certified path (matrix-core G', exact G only where the bound cannot
     decide) rewrites every row exactly as the exact-G drop/grow does, and as
@@ -562,9 +582,9 @@ def test_rigl_certified_matches_exact_drop_grow(dev, name, df):
     assert W_cert.nnz == W_exact.nnz and W_cert.topology_version == 1
     want = oracle.drop_grow(c, k, "gradient", oracle.dense_grad(dY_np, X_np))
     csr_arrays_equal(to_oracle(W_cert), want, f"{name} certified vs oracle")
-    if name == "nonfinite-rows":
+    if name.startswith("nonfinite-rows"):
         assert want.nnz < c.nnz  # the NaN row shrank
-    if name == "cancel":
+    if name.startswith("cancel"):
         # the certified path decided this case (not the exact fallback), with
         # undecided columns left for the exact finish
         W = from_oracle(c, dev)
@@ -580,7 +600,9 @@ def test_rigl_certified_matches_exact_drop_grow(dev, name, df):
         info = torch.empty(c.nrows * _lib.RIGL_INFO_BYTES, dtype=torch.uint8, device=dev)
         off = torch.empty(2 * c.nrows + 1, dtype=torch.int64, device=dev)
         total = torch.empty(1, dtype=torch.int64, device=dev)
-        _lib.rigl_count(view, thr, Gp, Gc, nd, nx, N, info, off, total)
+        amb = torch.empty(8 * c.nrows * c.ncols, dtype=torch.uint8, device=dev)
+        stage = torch.empty(_lib.drop_grow_workspace_bytes(view), dtype=torch.uint8, device=dev)
+        _lib.rigl_count(view, thr, Gp, Gc, nd, nx, N, info, off, total, amb, stage)
         n_amb = int(total.item())
         assert 0 < n_amb <= W._RIGL_EXACT_SHARE * (c.nrows * c.ncols - c.nnz), n_amb
 
