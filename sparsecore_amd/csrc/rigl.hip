@@ -638,6 +638,8 @@ __device__ __forceinline__ void for_each_col(const float* __restrict__ g_row,
     }
 }
 
+constexpr int kCountList = 2048;  // keys of the selected top bin listed in LDS (8 KiB)
+
 // rigl_count_kernel with the row's |G'| in registers, and the list pass
 // (rigl_list_kernel) folded in: thread t owns columns 16(t + 256v) + e
 // (v < U/4, e < 16), so the radix passes read no memory, and the classes
@@ -664,6 +666,7 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
     __shared__ uint32_t keep[U * kRowThreads * 4 / 32];
     __shared__ int64_t tmp[kRowThreads];
     __shared__ uint32_t hist[2048];
+    __shared__ uint32_t lst[kCountList];
     __shared__ uint32_t s_digit;
     __shared__ int64_t s_below;
     __shared__ unsigned long long s_best;
@@ -738,30 +741,33 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
             amb_off[M + 1 + i] = n_amb;
         }
         __syncthreads();
-        int64_t pos_a = s_base, pos_i = 0;  // this thread's next positions, group by group
-#pragma unroll
-        for (int v = 0; v < kGroups; ++v) {
-            int64_t a = pos_a + ((xa >> (16 * v)) & 0xFFFF);
-            int64_t g = pos_i + ((xi >> (16 * v)) & 0xFFFF);
-#pragma unroll
-            for (int b = 0; b < 16; ++b) {
-                const int bit = 16 * v + b;
-                const int64_t c = col_of(bit / 4) + (bit % 4);
-                if ((amb >> bit) & 1ull) {
-                    if (a < amb_cap) {
-                        amb_col[a] = static_cast<int32_t>(c);
-                        amb_key[a] = static_cast<uint32_t>(i);
-                    }
-                    ++a;
-                }
-                if ((in >> bit) & 1ull) {
-                    if (g < n_live) stage_col[start + g] = static_cast<int32_t>(c);
-                    ++g;
-                }
+        // field v of cum(x) << 16: the counts of the groups before v (each
+        // field sum stays below 2^16: at most 16384 columns a row)
+        auto cum = [](int64_t x) { return x + (x << 16) + (x << 32) + (x << 48); };
+        const int64_t sa = (cum(ta) << 16) + xa, si = (cum(ti) << 16) + xi;
+        // column of bit q: 16(t + 256(q / 16)) + q % 16; its position: its
+        // group's start for this thread + the earlier bits of its group
+        auto place = [&](uint64_t m, int64_t starts, auto put) {
+            const uint64_t all = m;
+            while (m) {
+                const int q = __builtin_ctzll(m);
+                m &= m - 1;
+                const int v = q >> 4;
+                const uint64_t below = all & ((1ull << q) - 1ull) & (0xFFFFull << (16 * v));
+                put(((starts >> (16 * v)) & 0xFFFF) + __popcll(below),
+                    16 * (t + int64_t{kRowThreads} * v) + (q & 15));
             }
-            pos_a += (ta >> (16 * v)) & 0xFFFF;
-            pos_i += (ti >> (16 * v)) & 0xFFFF;
-        }
+        };
+        place(amb, sa, [&](int64_t pos, int64_t c) {
+            const int64_t at = s_base + pos;
+            if (at < amb_cap) {
+                amb_col[at] = static_cast<int32_t>(c);
+                amb_key[at] = static_cast<uint32_t>(i);
+            }
+        });
+        place(in, si, [&](int64_t pos, int64_t c) {
+            if (pos < n_live) stage_col[start + pos] = static_cast<int32_t>(c);
+        });
     };
 
     // the row's |G'| and empty-column mask (bit 4u + e) (every load issued
@@ -777,6 +783,7 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
         const int64_t c = col_of(u);
         a[u] = *reinterpret_cast<const u32x4*>(g_row + (c < K ? c : K - 4));
     }
+    asm volatile("" ::: "memory");  // all U loads in flight before the first use
     uint64_t cand = 0;
     int64_t unbounded = 0;
 #pragma unroll
@@ -838,23 +845,69 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
         pick(hs, kPer);
         prefix = s_digit;
         need -= s_below;
+        const int64_t n_bin = hist[prefix];
         __syncthreads();
         int shift = 32 - kTopBits;
-        for (const int width : {8, 8, 5}) {
-            hist[t] = 0;
-            __syncthreads();
+        if (n_bin <= kCountList) {
+            // the bin's keys listed in LDS (per-thread counts, one scan for
+            // the offsets); the passes then read only them
+            uint64_t in_bin = 0;
 #pragma unroll
             for (int u = 0; u < U; ++u)
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    if (((cand >> (4 * u + e)) & 1ull) && (a[u][e] >> shift) == prefix)
-                        atomicAdd(&hist[(a[u][e] >> (shift - width)) & ((1u << width) - 1u)], 1u);
-            shift -= width;
+                    if ((a[u][e] >> shift) == prefix) in_bin |= 1ull << (4 * u + e);
+            in_bin &= cand;
+            const int64_t mine = __popcll(in_bin);
+            const int32_t at = static_cast<int32_t>(block_inclusive_scan(mine, tmp) - mine);
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int bit = 4 * u + e;
+                    if ((in_bin >> bit) & 1ull)
+                        lst[at + __popcll(in_bin & ((1ull << bit) - 1ull))] = a[u][e];
+                }
             __syncthreads();
-            pick(hist[t], 1);
-            prefix = (prefix << width) | s_digit;
-            need -= s_below;
-            __syncthreads();
+            auto pass = [&](int width) {
+                hist[t] = 0;
+                __syncthreads();
+                for (int64_t e = t; e < n_bin; e += kRowThreads) {
+                    const uint32_t key = lst[e];
+                    if ((key >> shift) == prefix)
+                        atomicAdd(&hist[(key >> (shift - width)) & ((1u << width) - 1u)], 1u);
+                }
+                shift -= width;
+                __syncthreads();
+                pick(hist[t], 1);
+                prefix = (prefix << width) | s_digit;
+                need -= s_below;
+                __syncthreads();
+            };
+            pass(8);
+            pass(8);
+            pass(5);
+        } else {  // a crowded bin: the passes over the registers
+            auto pass = [&](int width) {
+                hist[t] = 0;
+                __syncthreads();
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (((cand >> (4 * u + e)) & 1ull) && (a[u][e] >> shift) == prefix)
+                            atomicAdd(&hist[(a[u][e] >> (shift - width)) & ((1u << width) - 1u)],
+                                      1u);
+                shift -= width;
+                __syncthreads();
+                pick(hist[t], 1);
+                prefix = (prefix << width) | s_digit;
+                need -= s_below;
+                __syncthreads();
+            };
+            pass(8);
+            pass(8);
+            pass(5);
         }
     }
     const float Tp = __uint_as_float(~prefix);
@@ -866,17 +919,21 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
         nr[u] = *reinterpret_cast<const f32x4*>(nrm_c + (c < K ? c : K - 4));
     }
     // the partial-sum codes of thread t's columns: one 16-byte load per 16
-    // columns (K % 16 == 0 for this kernel)
+    // columns (K % 16 == 0 for this kernel); past K a clamped load, its
+    // columns not candidates
     const uint8_t* c_row = Gc + i * K;
     typedef uint32_t u32x4c __attribute__((ext_vector_type(4)));
-    auto codes16 = [&](int v) -> u32x4c {  // past K: a clamped load, its columns not candidates
+    u32x4c cw4[kGroups];
+#pragma unroll
+    for (int v = 0; v < kGroups; ++v) {
         const int64_t c = 16 * (t + int64_t{kRowThreads} * v);
-        return *reinterpret_cast<const u32x4c*>(c_row + (c < K ? c : K - 16));
-    };
+        cw4[v] = *reinterpret_cast<const u32x4c*>(c_row + (c < K ? c : K - 16));
+    }
+    asm volatile("" ::: "memory");  // norms and codes in flight before the first use
     uint32_t nmax = 0, cmax = 0;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const uint32_t cw = codes16(u / 4)[u % 4];
+        const uint32_t cw = cw4[u / 4][u % 4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             if (!((cand >> (4 * u + e)) & 1ull)) continue;
@@ -898,7 +955,7 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
     uint64_t amb = 0, in = 0;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const uint32_t cw = codes16(u / 4)[u % 4];
+        const uint32_t cw = cw4[u / 4][u % 4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             if (!((cand >> (4 * u + e)) & 1ull)) continue;

@@ -54,16 +54,31 @@ __device__ int64_t mark_survivors(const float* __restrict__ values,
     __syncthreads();
     int64_t kept = 0;
     unsigned long long best = 0;
-    for (int32_t s = t; s < n_live; s += kRowThreads) {
-        const uint32_t u = __float_as_uint(fabsf(values[start + s]));
-        if (__uint_as_float(u) > thr) {
-            ++kept;
-            const int32_t c = cols[start + s];
-            atomicOr(&keep[c >> 5], 1u << (c & 31));
+    // four slots per thread per pass, their loads issued before any use (a
+    // long row then costs one memory latency per 1024 slots, not per 256)
+    constexpr int kU = 4;
+    for (int32_t s0 = t; s0 < n_live; s0 += kU * kRowThreads) {
+        uint32_t u[kU];
+        int32_t c[kU];
+#pragma unroll
+        for (int q = 0; q < kU; ++q) {
+            const int32_t s = s0 + q * kRowThreads;
+            const int32_t sc = s < n_live ? s : n_live - 1;  // in the row, unused past it
+            u[q] = __float_as_uint(fabsf(values[start + sc]));
+            c[q] = cols[start + sc];
         }
-        const unsigned long long key =
-            (static_cast<unsigned long long>(u) << 32) | (0xFFFFFFFFull - static_cast<uint32_t>(s));
-        if (key > best) best = key;
+#pragma unroll
+        for (int q = 0; q < kU; ++q) {
+            const int32_t s = s0 + q * kRowThreads;
+            if (s >= n_live) continue;
+            if (__uint_as_float(u[q]) > thr) {
+                ++kept;
+                atomicOr(&keep[c[q] >> 5], 1u << (c[q] & 31));
+            }
+            const unsigned long long key = (static_cast<unsigned long long>(u[q]) << 32) |
+                                           (0xFFFFFFFFull - static_cast<uint32_t>(s));
+            if (key > best) best = key;
+        }
     }
     block_inclusive_scan(kept, tmp);
     int64_t n_keep = tmp[kRowThreads - 1];
