@@ -783,7 +783,18 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
         const int64_t c = col_of(u);
         a[u] = *reinterpret_cast<const u32x4*>(g_row + (c < K ? c : K - 4));
     }
-    asm volatile("" ::: "memory");  // all U loads in flight before the first use
+    // the columns' partial-sum codes (one 16-byte load per 16 columns: K %
+    // 16 == 0 for this kernel; past K a clamped load, its columns not
+    // candidates), requested now so that they arrive while the select runs
+    const uint8_t* c_row = Gc + i * K;
+    typedef uint32_t u32x4c __attribute__((ext_vector_type(4)));
+    u32x4c cw4[kGroups];
+#pragma unroll
+    for (int v = 0; v < kGroups; ++v) {
+        const int64_t c = 16 * (t + int64_t{kRowThreads} * v);
+        cw4[v] = *reinterpret_cast<const u32x4c*>(c_row + (c < K ? c : K - 16));
+    }
+    asm volatile("" ::: "memory");  // all these loads in flight before the first use
     uint64_t cand = 0;
     int64_t unbounded = 0;
 #pragma unroll
@@ -918,18 +929,7 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
         const int64_t c = col_of(u);
         nr[u] = *reinterpret_cast<const f32x4*>(nrm_c + (c < K ? c : K - 4));
     }
-    // the partial-sum codes of thread t's columns: one 16-byte load per 16
-    // columns (K % 16 == 0 for this kernel); past K a clamped load, its
-    // columns not candidates
-    const uint8_t* c_row = Gc + i * K;
-    typedef uint32_t u32x4c __attribute__((ext_vector_type(4)));
-    u32x4c cw4[kGroups];
-#pragma unroll
-    for (int v = 0; v < kGroups; ++v) {
-        const int64_t c = 16 * (t + int64_t{kRowThreads} * v);
-        cw4[v] = *reinterpret_cast<const u32x4c*>(c_row + (c < K ? c : K - 16));
-    }
-    asm volatile("" ::: "memory");  // norms and codes in flight before the first use
+    asm volatile("" ::: "memory");  // all U loads in flight before the first use
     uint32_t nmax = 0, cmax = 0;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -1250,12 +1250,14 @@ __global__ __launch_bounds__(kRowThreads) void rigl_list_kernel(
 // Finish, step 2, over all P undecided (row, column) pairs: the exact G with
 // the reference's arithmetic (exact_dot), as the key ~bits(|G|) (0 for NaN).
 // amb_key holds the row on entry. A wave takes 64 consecutive pairs, one per
-// lane; the dY and X rows of its pairs are streamed through the wave's own
-// LDS rows in chunks of kExJ floats, eight lanes loading one 128-byte piece
-// of a row (so a pair's 16 KB X row is 128 coalesced loads of the wave, two
-// chunks ahead in registers, instead of one thread's dependent stream). Each
-// lane then runs its pair's sum over the chunk from LDS. N % 4 == 0 and
-// 16-byte aligned rows; the four waves of a workgroup run in step (barriers).
+// lane; the X rows of its pairs and its distinct dY rows (a row's pairs are
+// consecutive, so a wave's 64 pairs usually span a few rows) are streamed
+// through the wave's own LDS rows in chunks of kExJ floats, eight lanes
+// loading one 128-byte piece of a row (so a pair's 16 KB X row is 128
+// coalesced loads of the wave, two chunks ahead in registers, instead of one
+// thread's dependent stream). Each lane then runs its pair's sum over the
+// chunk from LDS. N % 4 == 0 and 16-byte aligned rows; the four waves of a
+// workgroup run in step (barriers).
 constexpr int kExJ = 32;               // floats per chunk
 constexpr int kExRow = kExJ / 4 + 1;   // 16-byte pieces per LDS row (one padding)
 constexpr int kExThreads = 256;
@@ -1265,6 +1267,7 @@ __global__ __launch_bounds__(kExThreads) void rigl_exact_kernel(
     const float* __restrict__ dY, const float* __restrict__ X) {
     __shared__ f32x4 xs[kExThreads / kWave][kWave][kExRow];
     __shared__ f32x4 ys[kExThreads / kWave][kWave][kExRow];
+    __shared__ int32_t drow[kExThreads / kWave][kWave];
     const int64_t P = *total < cap ? *total : cap;  // the grid covers the capacity
     if (static_cast<int64_t>(blockIdx.x) * kExThreads >= P) return;  // workgroup-uniform
     const int w = threadIdx.x >> 6;
@@ -1275,9 +1278,20 @@ __global__ __launch_bounds__(kExThreads) void rigl_exact_kernel(
     // with the count would give wrong keys, never an out-of-bounds read)
     const int32_t my_col = min(max(amb_col[pc], 0), static_cast<int32_t>(K - 1));
     const int32_t my_row = static_cast<int32_t>(min<uint32_t>(amb_key[pc], static_cast<uint32_t>(M - 1)));
-    // staging: load u of lane l is piece l % 8 of pair 8u + l / 8's rows
+    // the wave's distinct rows: a lane whose row differs from its left
+    // neighbour's starts one; its rank among them indexes the LDS rows of dY
+    const int32_t left = __shfl_up(my_row, 1);
+    const bool first = l == 0 || left != my_row;
+    const uint64_t starts = __ballot(first);
+    const int rank = __popcll(starts & ((2ull << l) - 1ull)) - 1;
+    const int nd = __popcll(starts);  // wave-uniform
+    if (first) drow[w][rank] = my_row;
+    __syncthreads();
+    // staging: load u of lane l is piece l % 8 of pair 8u + l / 8's X row
+    // and, for the first ceil(nd / 8) loads, of distinct row 8u + l / 8 of dY
     constexpr int kU = kWave * (kExJ / 4) / kWave;  // loads per lane per chunk and matrix
     static_assert(kU == 8, "eight lanes per 128-byte piece of a row");
+    const int nu = (nd + 7) / 8;
     const int pe = l & 7;
     const float* xsrc[kU];
     const float* ysrc[kU];
@@ -1285,7 +1299,7 @@ __global__ __launch_bounds__(kExThreads) void rigl_exact_kernel(
     for (int u = 0; u < kU; ++u) {
         const int src = 8 * u + (l >> 3);
         xsrc[u] = X + static_cast<int64_t>(__shfl(my_col, src)) * N;
-        ysrc[u] = dY + static_cast<int64_t>(__shfl(my_row, src)) * N;
+        ysrc[u] = dY + static_cast<int64_t>(drow[w][src < nd ? src : nd - 1]) * N;
     }
     const int64_t nch = ceil_div(N, kExJ);
     f32x4 rx[2][kU], ry[2][kU];
@@ -1298,7 +1312,7 @@ __global__ __launch_bounds__(kExThreads) void rigl_exact_kernel(
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
             rx[set][u] = *reinterpret_cast<const f32x4*>(xsrc[u] + j);
-            ry[set][u] = *reinterpret_cast<const f32x4*>(ysrc[u] + j);
+            if (u < nu) ry[set][u] = *reinterpret_cast<const f32x4*>(ysrc[u] + j);
         }
     };
     float acc = 0.0f;
@@ -1308,16 +1322,16 @@ __global__ __launch_bounds__(kExThreads) void rigl_exact_kernel(
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
             xs[w][8 * u + (l >> 3)][pe] = rx[set][u];
-            ys[w][8 * u + (l >> 3)][pe] = ry[set][u];
+            if (u < nu) ys[w][8 * u + (l >> 3)][pe] = ry[set][u];
         }
         __syncthreads();
         load(set, ch + 2);
-        const int64_t left = N - ch * kExJ;  // workgroup-uniform
-        const int terms = left <= 0 ? 0 : left < kExJ ? static_cast<int>(left) : kExJ;
+        const int64_t left_j = N - ch * kExJ;  // workgroup-uniform
+        const int terms = left_j <= 0 ? 0 : left_j < kExJ ? static_cast<int>(left_j) : kExJ;
 #pragma unroll
         for (int q = 0; q < kExJ / 4; ++q) {
             if (4 * q < terms) {
-                const f32x4 a = ys[w][l][q];
+                const f32x4 a = ys[w][rank][q];
                 const f32x4 b = xs[w][l][q];
                 acc = acc + a[0] * b[0];
                 acc = acc + a[1] * b[1];
