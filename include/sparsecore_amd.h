@@ -473,6 +473,23 @@ SLK_API int slk_backward_narrow(const slk_csr* W, const float* dYt, int64_t N, c
                                 int64_t X_rows, float* dW, float* dbias, float* dX, int order,
                                 void* stream);
 
+/* Backward of a small layer in one launch (the caller chooses it where the
+ * three kernels are each a few microseconds of latency), from the row-major
+ * output gradient dY (M x N) and the layer input X (K x N):
+ *   dW    — as slk_sddmm in the SIMD order (live slots; padding 0);
+ *   dbias — as slk_sddmm_bias's dbias (M floats), if not NULL;
+ *   dX    — W^T·dY, K x N row-major, bit-identical to slk_spmm(WT, dY) after
+ *           slk_transpose_refresh: WT is W's transpose from
+ *           slk_transpose_fill (its structure: row_start, row_nnz,
+ *           col_indices; its values are not read) and perm its slot map
+ *           (WT slot s holds W slot perm[s]); W's values are read through
+ *           perm, so no refresh is needed first.
+ * Replaces, for such layers, the dW call, the transpose-cache refresh and
+ * spmm(WT, dY) of the reference backward (sparselab/ops.py:160-210).       */
+SLK_API int slk_backward_fused(const slk_csr* W, const slk_csr* WT, const int64_t* perm,
+                               const float* dY, const float* X, int64_t N, float* dW,
+                               float* dbias, float* dX, void* stream);
+
 /* Length of the segment arrays slk_seg_list_build needs for W, block_cols
  * and seg_slots (an upper bound on the padded segment count, so the list can
  * be built without reading anything back to the host); 0 on bad arguments. */

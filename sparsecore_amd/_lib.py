@@ -49,6 +49,7 @@ EXPORTS = (
     "slk_transpose_dense",
     "slk_spmm_t",
     "slk_backward_narrow",
+    "slk_backward_fused",
     "slk_seg_list_capacity",
     "slk_seg_list_workspace_bytes",
     "slk_seg_list_build",
@@ -149,6 +150,7 @@ def _declare(lib) -> None:
     lib.slk_dense_grad.argtypes = [_vp, _vp, _i64, _i64, _i64, ctypes.c_int, _vp, _vp]
     lib.slk_transpose_dense.argtypes = [_vp, _i64, _i64, _i64, _vp, _vp]
     lib.slk_spmm_t.argtypes = [_csrp, _vp, _i64, _i64, _vp, _vp, _vp]
+    lib.slk_backward_fused.argtypes = [_csrp, _csrp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp]
     lib.slk_backward_narrow.argtypes = [_csrp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, ctypes.c_int,
                                         _vp]
     lib.slk_seg_list_capacity.restype = _i64
@@ -353,6 +355,20 @@ def backward_narrow(view: CsrView, dYt: torch.Tensor, X: torch.Tensor,
     lib = load()
     rc = lib.slk_backward_narrow(ctypes.byref(view), ptr(dYt), dYt.shape[0], ptr(X), X.shape[0],
                                  ptr(dW), ptr(dbias), ptr(dX), int(order), stream_of(dYt))
+    if rc:
+        _raise(rc)
+
+
+def backward_fused(view: CsrView, viewT: CsrView, perm: torch.Tensor, dY: torch.Tensor,
+                   X: torch.Tensor, dW: torch.Tensor, dbias: torch.Tensor | None,
+                   dX: torch.Tensor) -> None:
+    """dW (SIMD order), dbias and dX = Wᵀ·dY of a small layer in one launch;
+    viewT is the transpose's structure and perm its slot map, W's values read
+    through it (slk_backward_fused)."""
+    lib = load()
+    rc = lib.slk_backward_fused(ctypes.byref(view), ctypes.byref(viewT), ptr(perm), ptr(dY),
+                                ptr(X), dY.shape[1], ptr(dW), ptr(dbias), ptr(dX),
+                                stream_of(dY))
     if rc:
         _raise(rc)
 

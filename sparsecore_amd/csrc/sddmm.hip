@@ -55,9 +55,11 @@ __device__ __forceinline__ void load4(const float* p, float& a, float& b, float&
     }
 }
 
+// One wave of sddmm_simd_kernel: the 16-slot group wid (wid >= slot_waves: a
+// bias-gradient wave).
 template <bool V4>
-__global__ __launch_bounds__(kBlock) void sddmm_simd_kernel(
-    int64_t M, int64_t N, int64_t cap_total,
+__device__ __forceinline__ void sddmm_simd_wave(
+    int64_t wid, int64_t M, int64_t N, int64_t cap_total,
     const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
     const int32_t* __restrict__ col, const float* __restrict__ dY,
     const float* __restrict__ X, float* __restrict__ dW, float* __restrict__ dbias,
@@ -65,7 +67,6 @@ __global__ __launch_bounds__(kBlock) void sddmm_simd_kernel(
     const int lane = threadIdx.x & (kWave - 1);
     const int g = lane >> 2;  // slot within the wave
     const int q = lane & 3;   // owns virtual lanes 4q..4q+3
-    const int64_t wid = wave_id();
     if (wid >= slot_waves) {  // wave-uniform: a bias-gradient wave
         if (dbias != nullptr) bias_row_sum(dY, M, N, wid - slot_waves, dbias, N, 1);
         return;
@@ -136,6 +137,82 @@ __global__ __launch_bounds__(kBlock) void sddmm_simd_kernel(
         } else {
             dW[slot] = 0.0f;
         }
+    }
+}
+
+template <bool V4>
+__global__ __launch_bounds__(kBlock) void sddmm_simd_kernel(
+    int64_t M, int64_t N, int64_t cap_total,
+    const int32_t* __restrict__ row_start, const int32_t* __restrict__ row_nnz,
+    const int32_t* __restrict__ col, const float* __restrict__ dY,
+    const float* __restrict__ X, float* __restrict__ dW, float* __restrict__ dbias,
+    int64_t slot_waves) {
+    sddmm_simd_wave<V4>(wave_id(), M, N, cap_total, row_start, row_nnz, col, dY, X, dW, dbias,
+                        slot_waves);
+}
+
+// Small layers: the whole backward in one launch (slk_backward_fused). The
+// first dx_items waves compute dX = WT·dY, one (WT row, 64-column tile) per
+// wave and one column per lane: the fma chain over the row's slots in slot
+// order from +0.0 — the bits of spmm on WT — with WT's values read as W's
+// through perm, so no refresh launch comes first. A 32-slot piece of the row
+// at a time: its columns and perm entries, then all its gathers of dY before
+// the values through perm, then the fmas. The gathers take no branch (lanes
+// past the piece repeat its last slot, columns past N load column N - 1 and
+// are not stored): a branch per gather makes the compiler wait for each
+// gather before the next. The remaining waves are sddmm_simd_kernel's (dW in
+// the SIMD order, and the bias-gradient waves). No barriers: a workgroup may
+// hold waves of both.
+constexpr int kPermPiece = 32;  // slots per piece: x[] within 64 VGPRs for the whole kernel
+__device__ __forceinline__ void spmm_perm_wave(int64_t item, int64_t R, int64_t N,
+                                               const int32_t* __restrict__ rs,
+                                               const int32_t* __restrict__ nz,
+                                               const int32_t* __restrict__ colT,
+                                               const int64_t* __restrict__ perm,
+                                               const float* __restrict__ vals,
+                                               const float* __restrict__ B,
+                                               float* __restrict__ out) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t tile = item / R;
+    const int64_t r = item - tile * R;
+    const int64_t n = tile * kWave + lane;
+    const int64_t nc = n < N ? n : N - 1;  // in bounds; not stored past N
+    const int32_t start = rs[r], nnz = nz[r];
+    float acc = 0.0f;
+    for (int32_t k = 0; k < nnz; k += kPermPiece) {
+        const int32_t m = nnz - k < kPermPiece ? nnz - k : kPermPiece;  // wave-uniform, >= 1
+        const int64_t sl = start + k + (lane < m ? lane : m - 1);
+        const int32_t c = colT[sl];
+        const int64_t ps = perm[sl];
+        float x[kPermPiece];
+#pragma unroll
+        for (int u = 0; u < kPermPiece; ++u)
+            x[u] = B[static_cast<int64_t>(__builtin_amdgcn_readlane(c, u)) * N + nc];
+        const float v = vals[ps];
+#pragma unroll
+        for (int u = 0; u < kPermPiece; ++u)
+            if (u < m)
+                acc = __builtin_fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), u)),
+                                     x[u], acc);
+    }
+    if (n < N) out[r * N + n] = acc;
+}
+
+template <bool V4>
+__global__ __launch_bounds__(kBlock) void backward_fused_kernel(
+    int64_t dx_items, int64_t KT, const int32_t* __restrict__ rsT,
+    const int32_t* __restrict__ nzT, const int32_t* __restrict__ colT,
+    const int64_t* __restrict__ perm, float* __restrict__ dX, int64_t M, int64_t N,
+    int64_t cap_total, const int32_t* __restrict__ row_start,
+    const int32_t* __restrict__ row_nnz, const int32_t* __restrict__ col,
+    const float* __restrict__ vals, const float* __restrict__ dY, const float* __restrict__ X,
+    float* __restrict__ dW, float* __restrict__ dbias, int64_t slot_waves) {
+    const int64_t wid = wave_id();
+    if (wid < dx_items) {
+        spmm_perm_wave(wid, KT, N, rsT, nzT, colT, perm, vals, dY, dX);
+    } else {
+        sddmm_simd_wave<V4>(wid - dx_items, M, N, cap_total, row_start, row_nnz, col, dY, X, dW,
+                            dbias, slot_waves);
     }
 }
 
@@ -758,4 +835,47 @@ extern "C" int slk_sddmm_bias(const slk_csr* W, const float* dY, int64_t dY_rows
         return slk::fail(SLK_EINVAL, "spmm_grad_w: NULL dbias");
     }
     return slk::sddmm_impl(W, dY, dY_rows, X, X_rows, N, dW, dbias, order, stream);
+}
+
+extern "C" int slk_backward_fused(const slk_csr* W, const slk_csr* WT, const int64_t* perm,
+                                  const float* dY, const float* X, int64_t N, float* dW,
+                                  float* dbias, float* dX, void* stream) {
+    using namespace slk;
+    clear_error();
+    const char* who = "backward_fused";
+    if (int rc = validate_csr(W, who)) return rc;
+    if (WT == nullptr) return fail(SLK_EINVAL, "backward_fused: NULL WT");
+    if (WT->nrows != W->ncols || WT->ncols != W->nrows || WT->row_start == nullptr ||
+        WT->row_nnz == nullptr || (WT->total_capacity > 0 && WT->col_indices == nullptr))
+        return fail(SLK_EINVAL, "backward_fused: WT is not W's transpose (shape or arrays)");
+    if (N < 0) return fail(SLK_EINVAL, "backward_fused: negative N");
+    const int64_t M = W->nrows, K = W->ncols, cap = W->total_capacity;
+    if (cap > 0 && (dW == nullptr || W->values == nullptr))
+        return fail(SLK_EINVAL, "backward_fused: NULL dW or W values");
+    if (WT->total_capacity > 0 && perm == nullptr)
+        return fail(SLK_EINVAL, "backward_fused: NULL perm");
+    if (N > 0 && ((M > 0 && dY == nullptr) || (K > 0 && (X == nullptr || dX == nullptr))))
+        return fail(SLK_EINVAL, "backward_fused: NULL dY, X or dX");
+    const int64_t dx_items = N > 0 ? K * ceil_div(N, int64_t{kWave}) : 0;
+    const int64_t slot_waves = ceil_div(cap, int64_t{kSlotsPerWave});
+    const int64_t bias_waves = dbias != nullptr ? M : 0;
+    const int64_t waves = dx_items + slot_waves + bias_waves;
+    if (waves == 0) return SLK_OK;
+    const int64_t blocks = ceil_div(waves, int64_t{kBlock / kWave});
+    if (blocks > INT32_MAX) return fail(SLK_EINVAL, "backward_fused: problem too large");
+    hipStream_t st = as_stream(stream);
+    const bool v4 = (N % 4 == 0) && (reinterpret_cast<uintptr_t>(X) % 16 == 0) &&
+                    (reinterpret_cast<uintptr_t>(dY) % 16 == 0);
+#define SLK_FUSED_ARGS                                                                         \
+    dx_items, K, WT->row_start, WT->row_nnz, WT->col_indices, perm, dX, M, N, cap, W->row_start, \
+        W->row_nnz, W->col_indices, W->values, dY, X, dW, dbias, slot_waves
+    if (v4) {
+        hipLaunchKernelGGL(backward_fused_kernel<true>, dim3(static_cast<unsigned>(blocks)),
+                           dim3(kBlock), 0, st, SLK_FUSED_ARGS);
+    } else {
+        hipLaunchKernelGGL(backward_fused_kernel<false>, dim3(static_cast<unsigned>(blocks)),
+                           dim3(kBlock), 0, st, SLK_FUSED_ARGS);
+    }
+#undef SLK_FUSED_ARGS
+    return check_launch(who);
 }

@@ -61,6 +61,20 @@ def _cached_transpose(W: PaddedCSR) -> PaddedCSR:
     return WT
 
 
+def _cached_transpose_structure(W: PaddedCSR):
+    """(WT, perm) from the transpose cache, rebuilt when W's topology changed
+    (as ``_cached_transpose``) but without refreshing WT's values: for a
+    caller that reads W's values through perm (slk_backward_fused). The next
+    ``_cached_transpose`` refreshes them as on every hit."""
+    key = id(W)
+    cached = _transpose_cache.get(key)
+    if cached is not None and cached[0] == W.topology_version and \
+            cached[1] == (int(W.nrows), int(W.ncols)):
+        return cached[2], cached[3]
+    WT = _cached_transpose(W)
+    return WT, _transpose_cache[key][3]
+
+
 def _rebuild_stale_transposes(Ws) -> None:
     """Rebuilds, in one batch (one device->host read for all), the cached
     transposes of those matrices whose entry exists but whose topology has
@@ -256,11 +270,37 @@ class _SpMMFunction(torch.autograd.Function):
         return dW_values, None, dX, None
 
 
+# Small layers: the backward as one launch (slk_backward_fused) where dW,
+# the transpose refresh and dX would each be a few microseconds of launch
+# latency (a 512 x 784 layer at N = 256: 6.8 + 2.3 + 8.2 us in a graph): up
+# to this many waves in the fused grid, one round of waves on the chip.
+_FUSED_MAX_WAVES = 8192
+
+
+def _fused_backward(W: PaddedCSR, N: int, kernel: str) -> bool:
+    forced = _overrides.get("fused_backward")
+    if forced is not None:
+        return bool(forced) and kernel != "scalar"
+    if kernel == "scalar" or N == 0:
+        return False
+    waves = W.ncols * -(-N // 64) + -(-W.total_capacity // 16)
+    return waves <= _FUSED_MAX_WAVES
+
+
 def _spmm_backward(W: PaddedCSR, X: torch.Tensor, dY_f32: torch.Tensor, kernel: str,
                    need_dw: bool, need_dx: bool, dbias: torch.Tensor | None = None):
     """dW on the live slots (SDDMM) and dX = Wᵀ·dY through the transpose cache
     (ops.py:167-210); a gradient that is not needed is not computed. With
-    ``dbias`` (and dW needed) the dW launch also writes dY's row sums there."""
+    ``dbias`` (and dW needed) the dW launch also writes dY's row sums there.
+    Small layers run both in one launch, W's values read through the
+    transpose's slot map instead of a refresh (same bits)."""
+    if need_dw and need_dx and _fused_backward(W, dY_f32.shape[1], kernel):
+        WT, perm = _cached_transpose_structure(W)
+        X32 = _device_f32(X)
+        dW_values = torch.empty(W.total_capacity, dtype=torch.float32, device=X32.device)
+        dX = torch.empty(W.ncols, dY_f32.shape[1], dtype=torch.float32, device=X32.device)
+        _lib.backward_fused(W._view(), WT._view(), perm, dY_f32, X32, dW_values, dbias, dX)
+        return dW_values, dX
     dW_values = dX = None
     if need_dw:
         dW_values = _launch_sddmm(W, dY_f32, _device_f32(X), kernel, dbias)

@@ -57,7 +57,7 @@ def tune():
     overrides of ops."""
     from sparsecore_amd import _lib, ops
 
-    host_keys = ("spmm_phases", "seg", "bin_shape")
+    host_keys = ("spmm_phases", "seg", "bin_shape", "fused_backward")
     touched = []
 
     def set_(**kw):
