@@ -106,6 +106,11 @@ def bytes_dw(nnz, cap, M, K, N):  # cols, row arrays, dY + X read, dW (all slots
     return 4 * nnz + 8 * M + 4 * M * N + 4 * K * N + 4 * cap
 
 
+def bytes_backward_fused(nnz, cap, M, K, N):  # dW as bytes_dw; dX as the forward on WT,
+    # its values gathered through perm (i64) instead of refreshed first
+    return bytes_dw(nnz, cap, M, K, N) + bytes_fwd(nnz, K, M, N) + 8 * nnz
+
+
 def bytes_refresh(nnz, capT):  # perm (i64) read, gathered values, WT values written
     return 8 * capT + 4 * nnz + 4 * capT
 
@@ -118,6 +123,37 @@ def flops(nnz, N):
 
 KERNEL_WARMUP = 3
 KERNEL_REPS = 30
+
+
+def graph_call_us(fn, calls: int = 20, reps: int = 11) -> float:
+    """Per-call time of `fn` replayed from a HIP graph of `calls` consecutive
+    calls (median over `reps` replays, divided by `calls`): for kernels of a
+    few microseconds, whose one-call event interval is mostly launch
+    overhead. Only for calls that a graph can hold (no host reads)."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(KERNEL_WARMUP):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(calls):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b) * 1e3 / calls)
+    return sorted(ts)[reps // 2]
 
 
 def kernel_time_ms(fn, reps: int | None = None):
@@ -570,7 +606,9 @@ def device_rows_csr(counts, K: int, sigma: float, seed: int, dev, padding_ratio=
 
 class LayerWork:
     """One SparseLinear-shaped layer: Y = W·X, dW = SDDMM(dY, X), dX = Wᵀ·dY via
-    the cached transpose (refresh + SpMM) — the three kernels of the path."""
+    the cached transpose (refresh + SpMM) — the three kernels of the path; a
+    small layer's backward is one launch (dW and dX, W's values read through
+    the transpose's slot map), as ops' backward runs it."""
 
     def __init__(self, name, desc, W, X, dY, rigl: bool = False):
         import torch
@@ -589,13 +627,21 @@ class LayerWork:
         torch.cuda.synchronize()
         self.rebuild_ms = 1e3 * (time.perf_counter() - t0)
 
+    def fused(self) -> bool:
+        """The backward as one launch (slk_backward_fused), as ops' backward
+        chooses it for this layer."""
+        from sparsecore_amd import ops
+
+        return ops._fused_backward(self.W, self.N, "simd")
+
     def body(self):
         from sparsecore_amd import ops
 
         Y = ops._launch_spmm(self.W, self.X)
-        dW = ops._launch_sddmm(self.W, self.dY, self.X, "simd")
-        WT = ops._cached_transpose(self.W)
-        dX = ops._launch_spmm(WT, self.dY)
+        # dW (SIMD order) and dX = Wᵀ·dY as the autograd backward computes
+        # them: separate launches through the transpose cache, or one launch
+        # for a small layer
+        dW, dX = ops._spmm_backward(self.W, self.X, self.dY, "simd", True, True)
         if self.rigl:
             self.topology_update()
         return Y, dW, dX
@@ -621,6 +667,9 @@ class LayerWork:
     def step_bytes(self):
         W, WT = self.W, self._WT()
         M, K, N = self.M, self.K, self.N
+        if self.fused():
+            return bytes_fwd(W.nnz, M, K, N) + bytes_backward_fused(W.nnz, W.total_capacity,
+                                                                    M, K, N)
         return (bytes_fwd(W.nnz, M, K, N) + bytes_dw(W.nnz, W.total_capacity, M, K, N)
                 + bytes_refresh(W.nnz, WT.total_capacity) + bytes_fwd(W.nnz, K, M, N))
 
@@ -640,6 +689,15 @@ class LayerWork:
         dW = torch.empty(W.total_capacity, device=self.dev)
         dX = torch.empty(K, N, device=self.dev)
         v, vT = ops._spmm_view(W, self.X), ops._spmm_view(WT, self.dY)
+        if self.fused():
+            WTs, perm_s = ops._cached_transpose_structure(W)
+            return [
+                ("spmm_fwd", lambda: _lib.spmm(v, self.X, Y), bytes_fwd(W.nnz, M, K, N),
+                 flops(W.nnz, N)),
+                ("backward_fused", lambda: _lib.backward_fused(W._view(), WTs._view(), perm_s,
+                                                               self.dY, self.X, dW, None, dX),
+                 bytes_backward_fused(W.nnz, W.total_capacity, M, K, N), 2 * flops(W.nnz, N)),
+            ] + (self._rigl_kernels() if self.rigl else [])
         return [
             ("spmm_fwd", lambda: _lib.spmm(v, self.X, Y), bytes_fwd(W.nnz, M, K, N),
              flops(W.nnz, N)),
@@ -1200,6 +1258,7 @@ def measure(work, args):
         topo_ms = 1e3 * timed_loop(work.topology_update, reps) / reps
 
     kern = []
+    path_labels = ("spmm_fwd", "sddmm_dw", "transpose_refresh", "spmm_dx", "backward_fused")
     for name, fn, nbytes, nflops in work.kernels():
         stage(f"kernel timing: {name}")
         ms, mean_ms, reps = kernel_time_ms(fn)
@@ -1207,8 +1266,12 @@ def measure(work, args):
                      "mean_us": round(mean_ms * 1e3, 3), "bytes": nbytes,
                      "flops": nflops, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
                      "timed_calls": reps, "warmup_calls": KERNEL_WARMUP})
+        if graph_ok and name in path_labels and ms < 0.1:
+            # microsecond kernels: also the per-call time inside a graph,
+            # which the graph-replayed step pays
+            kern[-1]["graph_us"] = round(graph_call_us(fn), 3)
     # roofline on the path's dominant kernel (forward SpMM, dX SpMM or dW SDDMM)
-    dom = max((k for k in kern if k["kernel"].startswith(("spmm", "sddmm", "backward_narrow"))),
+    dom = max((k for k in kern if k["kernel"].startswith(("spmm", "sddmm", "backward_"))),
               key=lambda k: k["median_us"])
     achieved = dom["bytes"] / (dom["median_us"] * 1e-6) / 1e9
     tflops = dom["flops"] / (dom["median_us"] * 1e-6) / 1e12
@@ -1261,9 +1324,11 @@ def measure(work, args):
             config["graph_refused"] = f"{graph_nodes['memset']} memset nodes"
     else:
         path_k = [k for k in kern if k["kernel"] in ("spmm_fwd", "sddmm_dw", "transpose_refresh",
-                                                      "spmm_dx")]
+                                                      "spmm_dx", "backward_fused")]
         path_us = sum(k["median_us"] for k in path_k)
         path = {"fwd_dw_dx_us": round(path_us, 1),
+                **({"fwd_dw_dx_graph_us": round(sum(k["graph_us"] for k in path_k), 2)}
+                   if path_k and all("graph_us" in k for k in path_k) else {}),
                 "fwd_dw_dx_GBps": round(work.step_bytes() / (path_us * 1e-6) / 1e9, 1),
                 "fwd_dw_dx_GFLOPs": round(work.step_flops() / (path_us * 1e-6) / 1e9, 1),
                 "step_bytes_fwd_dw_dx": work.step_bytes(), "nnz": work.W.nnz}
