@@ -341,24 +341,58 @@ __global__ __launch_bounds__(kTileThreads) void tr_scatter_tile_kernel(
         }
         return a;
     };
-    for (int e = t; e < total; e += kTileThreads) {
-        const int rl = row_of(e);
-        const int64_t s = row_start[r0 + rl] + lo[rl] + (e - pre[rl]);
-        const int32_t c = col[s];
-        atomicOr(&mask[rl / B][c - c0], 1u << (rl % B));
+    // The flat passes take kFlatU slots per thread at a time, every load of
+    // the group issued before the first use (elements past the total repeat
+    // the last one and change nothing), so a thread's slots cost one memory
+    // latency per group instead of one each.
+    constexpr int kFlatU = 4;
+    auto locate = [&](int e, int& rl, int64_t& s) {
+        const int ec = e < total ? e : total - 1;
+        rl = row_of(ec);
+        s = row_start[r0 + rl] + lo[rl] + (ec - pre[rl]);
+    };
+    for (int e0 = t; e0 < total; e0 += kFlatU * kTileThreads) {
+        int rl[kFlatU];
+        int64_t s[kFlatU];
+        int32_t c[kFlatU];
+#pragma unroll
+        for (int q = 0; q < kFlatU; ++q) locate(e0 + q * kTileThreads, rl[q], s[q]);
+#pragma unroll
+        for (int q = 0; q < kFlatU; ++q) c[q] = col[s[q]];
+#pragma unroll
+        for (int q = 0; q < kFlatU; ++q)
+            if (e0 + q * kTileThreads < total) atomicOr(&mask[rl[q] / B][c[q] - c0], 1u << (rl[q] % B));
     }
     __syncthreads();
-    for (int e = t; e < total; e += kTileThreads) {
-        const int rl = row_of(e);
-        const int64_t s = row_start[r0 + rl] + lo[rl] + (e - pre[rl]);
-        const int32_t c = col[s];
-        const int64_t sb = rl / B;
-        const uint32_t below = (1u << (rl % B)) - 1u;
-        const int64_t pos = static_cast<int64_t>(start_t[c]) + bh[(b0 + sb) * K + c] +
-                            __popc(mask[sb][c - c0] & below);
-        perm[pos] = s;
-        col_t[pos] = static_cast<int32_t>(r0 + rl);
-        val_t[pos] = val[s];
+    for (int e0 = t; e0 < total; e0 += kFlatU * kTileThreads) {
+        int rl[kFlatU];
+        int64_t s[kFlatU];
+        int32_t c[kFlatU];
+        float v[kFlatU];
+        int32_t st[kFlatU], bb[kFlatU];
+#pragma unroll
+        for (int q = 0; q < kFlatU; ++q) locate(e0 + q * kTileThreads, rl[q], s[q]);
+#pragma unroll
+        for (int q = 0; q < kFlatU; ++q) {
+            c[q] = col[s[q]];
+            v[q] = val[s[q]];
+        }
+#pragma unroll
+        for (int q = 0; q < kFlatU; ++q) {
+            st[q] = start_t[c[q]];
+            bb[q] = bh[(b0 + rl[q] / B) * K + c[q]];
+        }
+#pragma unroll
+        for (int q = 0; q < kFlatU; ++q) {
+            if (e0 + q * kTileThreads >= total) continue;
+            const int64_t sb = rl[q] / B;
+            const uint32_t below = (1u << (rl[q] % B)) - 1u;
+            const int64_t pos = static_cast<int64_t>(st[q]) + bb[q] +
+                                __popc(mask[sb][c[q] - c0] & below);
+            perm[pos] = s[q];
+            col_t[pos] = static_cast<int32_t>(r0 + rl[q]);
+            val_t[pos] = v[q];
+        }
     }
 }
 

@@ -908,14 +908,25 @@ def to_dense(p: PaddedCSR) -> torch.Tensor:
 #  Transpose (layout.py:307-536) — on the HIP device
 # ─────────────────────────────────────────────────────────────────────
 
+def _capacity_bound(nnz: int, rows: int, padding_ratio: float) -> int:
+    """An upper bound of the total capacity of `rows` rows holding `nnz` live
+    slots under the capacity rule max(1, ceil(n * fl(1 + padding_ratio)))
+    (float64): each row's capacity is at most n·(1 + padding_ratio)·(1 +
+    2^-53) + 2, so the arrays can be sized before the exact total is read."""
+    scaled = float(nnz) * (1.0 + padding_ratio) * (1.0 + 1e-15)
+    return int(np.ceil(scaled)) + 2 * int(rows)
+
+
 def transpose_with_perm(p: PaddedCSR, *, padding_ratio: float = 0.2):
     """(WT, perm): the transpose of p and, for each WT slot, the W slot it copies.
 
     WT is ncols x nrows with capacities max(1, ceil(nnz*(1+padding_ratio))),
     each row listing its source rows in ascending order; perm is int64 with -1
     on padding (layout.py:460-536). Built on the GPU by a counting sort
-    (slk_transpose_count / slk_transpose_fill); one device->host read of the
-    WT capacity sizes the output arrays.
+    (slk_transpose_count / slk_transpose_fill). The slot arrays are sized by
+    a bound of the WT capacity, so the fill is queued right behind the count;
+    the one device->host read of the exact capacity comes after it, and the
+    arrays are trimmed to it (views, no copy).
     """
     if padding_ratio < 0:
         raise ValueError(f"padding_ratio must be >= 0, got {padding_ratio}")
@@ -932,13 +943,23 @@ def transpose_with_perm(p: PaddedCSR, *, padding_ratio: float = 0.2):
     counts = torch.empty(2, dtype=torch.int64, device=dev)
     counts[0:1].copy_(capT_dev)
     _count_heavy(nnz_t, p.nnz, counts[1:2])
+    bound = _capacity_bound(p.nnz, K, padding_ratio)
+    early = bound <= np.iinfo(np.int32).max
+    if early:  # fill first, read the exact capacity after it
+        val_t = torch.empty(bound, dtype=_F32, device=dev)
+        col_t = torch.empty(bound, dtype=_I32, device=dev)
+        perm = torch.empty(bound, dtype=torch.int64, device=dev)
+        _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, bound, val_t, col_t, perm)
     capT, heavy = counts.tolist()
     if capT > np.iinfo(np.int32).max:
         raise ValueError(f"transpose: capacity {capT} exceeds the int32 slot range")
-    val_t = torch.empty(capT, dtype=_F32, device=dev)
-    col_t = torch.empty(capT, dtype=_I32, device=dev)
-    perm = torch.empty(capT, dtype=torch.int64, device=dev)
-    _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, capT, val_t, col_t, perm)
+    if early:
+        val_t, col_t, perm = val_t[:capT], col_t[:capT], perm[:capT]
+    else:
+        val_t = torch.empty(capT, dtype=_F32, device=dev)
+        col_t = torch.empty(capT, dtype=_I32, device=dev)
+        perm = torch.empty(capT, dtype=torch.int64, device=dev)
+        _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, capT, val_t, col_t, perm)
     WT = PaddedCSR._from_parts(K, M, val_t, col_t, rs_t, nnz_t, cap_t, p.nnz)
     WT._heavy_hint = heavy
     WT._cols_skewed = view.n_heavy_rows > 0  # WT's columns are p's rows
@@ -985,16 +1006,29 @@ def transposes_with_perm(ps, *, padding_ratio: float = 0.2):
             _count_heavy(nnz_t, p.nnz, caps[n + i:n + i + 1])
         else:
             caps[n + i:n + i + 1].zero_()
-        staged.append((view, ws, rs_t, nnz_t, cap_t))
+        # the fill right behind the count, into arrays sized by a bound of
+        # the capacity (as transpose_with_perm)
+        bound = _capacity_bound(p.nnz, K, padding_ratio)
+        filled = None
+        if bound <= np.iinfo(np.int32).max:
+            filled = (torch.empty(bound, dtype=_F32, device=dev),
+                      torch.empty(bound, dtype=_I32, device=dev),
+                      torch.empty(bound, dtype=torch.int64, device=dev))
+            _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, bound, *filled)
+        staged.append((view, ws, rs_t, nnz_t, cap_t, filled))
     host = caps.tolist()
     out = []
-    for p, capT, heavy, (view, ws, rs_t, nnz_t, cap_t) in zip(ps, host[:n], host[n:], staged):
+    for p, capT, heavy, (view, ws, rs_t, nnz_t, cap_t, filled) in zip(ps, host[:n], host[n:],
+                                                                       staged):
         if capT > np.iinfo(np.int32).max:
             raise ValueError(f"transpose: capacity {capT} exceeds the int32 slot range")
-        val_t = torch.empty(capT, dtype=_F32, device=dev)
-        col_t = torch.empty(capT, dtype=_I32, device=dev)
-        perm = torch.empty(capT, dtype=torch.int64, device=dev)
-        _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, capT, val_t, col_t, perm)
+        if filled is not None:
+            val_t, col_t, perm = (a[:capT] for a in filled)
+        else:
+            val_t = torch.empty(capT, dtype=_F32, device=dev)
+            col_t = torch.empty(capT, dtype=_I32, device=dev)
+            perm = torch.empty(capT, dtype=torch.int64, device=dev)
+            _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, capT, val_t, col_t, perm)
         WT = PaddedCSR._from_parts(p.ncols, p.nrows, val_t, col_t, rs_t, nnz_t, cap_t, p.nnz)
         WT._heavy_hint = heavy
         WT._cols_skewed = view.n_heavy_rows > 0  # WT's columns are p's rows

@@ -108,6 +108,27 @@ def test_capacity_rule():
                     == oracle.row_capacity([nnz], pr).tolist())
 
 
+@pytest.mark.parametrize("padding_ratio", [0.0, 0.1, 0.2, 0.3, 1.0 / 3.0, 0.7, 1.0, 2.5])
+def test_transpose_capacity_bound_covers_the_rule(padding_ratio):
+    """The transpose sizes its slot arrays by _capacity_bound before it reads
+    the exact capacity: the bound must never undercut the capacity rule, for
+    any split of nnz over the rows (empty rows, one full row, many short rows,
+    random), including padding ratios whose float64 is inexact."""
+    from sparsecore_amd.layout import _capacity_bound
+
+    rng = np.random.default_rng(int(padding_ratio * 1000))
+    for rows, counts in [
+        (1, np.array([0])), (5, np.zeros(5, np.int64)), (3, np.array([0, 0, 1000003])),
+        (1000, np.ones(1000, np.int64)), (1000, rng.integers(0, 50, 1000)),
+        (16384, rng.integers(0, 2000, 16384)), (7, np.array([1, 2, 3, 5, 8, 13, 21])),
+        (4096, rng.zipf(1.3, 4096).clip(0, 100000)),
+    ]:
+        exact = int(_compute_row_capacity(counts, padding_ratio).astype(np.int64).sum())
+        bound = _capacity_bound(int(counts.sum()), rows, padding_ratio)
+        assert bound >= exact, (padding_ratio, rows, bound, exact)
+        assert bound <= exact + 2 * rows + 2  # and not wasteful
+
+
 def test_edge_matrices():
     p = PaddedCSR.from_dense(torch.zeros(5, 5))
     assert p.nnz == 0 and p.row_capacity.tolist() == [1] * 5
