@@ -120,7 +120,12 @@ _PHASE_X_ROWS = 4096
 # 95% layer's input gradient 5.80 -> 5.53 ms at 8 x 2; its forward, whose
 # heavy rows run beside the light ones, 6.0 ms on the two-stream path against
 # 6.43 binned; at 99% the gather kernel (1.79 ms) beats any binned shape
-# (3.5 ms and up: staging all of X per workgroup dominates).
+# (3.5 ms and up: staging all of X per workgroup dominates). Only from
+# _BIN_MIN_NNZ live slots: on the 10M- and 60M-GPT layers (0.1-0.5 M slots)
+# the binned kernel runs no faster than the LDS kernel, while its build (one
+# per topology version; SET rewrites every layer every step) and its view
+# cost step time: 60M-GPT + SET 43.0 -> 46.4 ms/step, 10M-GPT 11.1 -> 11.7.
+_BIN_MIN_NNZ = 4_000_000
 _BIN_MIN_N = 1024
 _BIN_MIN_REUSE = 4.0
 _BIN_MAX_PER_CHUNK = 48
@@ -131,7 +136,7 @@ _BIN_SHAPES = ((8, 2), (4, 2), (2, 2), (8, 1), (4, 1), (1, 2))
 def _bin_shape(W: PaddedCSR, K: int, N: int):
     """(rows per wave, halves) of the binned stream slk_spmm should get for W
     and an N-column X, or None."""
-    if N < _BIN_MIN_N or N % 4 or K == 0:
+    if N < _BIN_MIN_N or N % 4 or K == 0 or W.nnz < _BIN_MIN_NNZ:
         return None
     first, slots = W._bin_coverage()
     rows = W.nrows - first
