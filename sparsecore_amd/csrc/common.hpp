@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <utility>
 #include <string>
 
 #include "sparsecore_amd.h"
@@ -55,5 +56,16 @@ __device__ __forceinline__ int64_t wave_id() {
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// f(std::integral_constant<int, j>{}) for j = 0..N-1, unrolled at compile time
+// (so array indexes derived from j are constants, never private memory).
+template <class F, int... J>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, J...>) {
+    (f(std::integral_constant<int, J>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 }  // namespace slk

@@ -280,7 +280,7 @@ __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64
         stage_to_lds(reg ^ 1, reg ^ 1);
         __syncthreads();
     };
-    static_assert(kAChunk / kAJ == 4, "four stages per chunk below");
+    static_assert((kAChunk / kAJ) % 2 == 0, "whole pairs of stages per chunk below");
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     if (nst > 0) {  // workgroup-uniform
@@ -289,10 +289,10 @@ __global__ __launch_bounds__(kAThreads) void rigl_approx_kernel(int64_t M, int64
         stage_to_lds(0, 0);
         __syncthreads();
         for (int64_t c0 = 0; c0 < nst; c0 += kAChunk / kAJ) {
-            stage(I0{}, c0);
-            stage(I1{}, c0 + 1);
-            stage(I0{}, c0 + 2);
-            stage(I1{}, c0 + 3);
+            for (int k = 0; k < kAChunk / kAJ; k += 2) {
+                stage(I0{}, c0 + k);
+                stage(I1{}, c0 + k + 1);
+            }
             // a chunk done: the running sum's magnitude to pm
 #pragma unroll
             for (int a = 0; a < 2; ++a)
@@ -965,8 +965,11 @@ __global__ __launch_bounds__(kRowThreads) void rigl_count_reg_kernel(
             if (!((cand >> (4 * u + e)) & 1ull)) continue;
             const int cls = classify_col(__uint_as_float(~a[u][e]), cni, nr[u][e], delta, c2,
                                          (cw >> (8 * e)) & 255u, t_in, t_out);
-            if (cls == kGrowIn) in |= 1ull << (4 * u + e);
-            if (cls == kGrowUndecided) amb |= 1ull << (4 * u + e);
+            // (both ORs unconditional: with one under each class the compiler
+            // merged them into a store to a class-indexed array in scratch)
+            const uint64_t bit = 1ull << (4 * u + e);
+            in |= cls == kGrowIn ? bit : 0ull;
+            amb |= cls == kGrowUndecided ? bit : 0ull;
         }
     }
     ri.n_grow = static_cast<int32_t>(n_grow);

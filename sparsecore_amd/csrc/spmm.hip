@@ -618,15 +618,6 @@ __global__ __launch_bounds__(kLdsThreads) void spmm_lds_split_kernel(
 // A chunk whose entries pass the window (more than 64 for the wave: dense
 // rows) takes them one by one from the stream.
 
-template <class F, int... J>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, J...>) {
-    (f(std::integral_constant<int, J>{}), ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 // One wave's share of workgroup lb of a binned launch over positions [0, P)
 // (rows order[p], or p when order is NULL), nrowblk row blocks per column
 // tile; the stream's unit u = (row block) * 16 + wave.
