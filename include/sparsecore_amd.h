@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define SLK_ABI_VERSION 14
+#define SLK_ABI_VERSION 15
 
 #if defined(__GNUC__)
 #define SLK_API __attribute__((visibility("default")))
@@ -138,7 +138,37 @@ typedef struct slk_csr {
     int64_t bin_rw;
     int64_t bin_h;
     int64_t n_bin;
+    /* Optional (0 = none): dense rows. The first n_dense_rows rows of
+     * row_order (which must then be given) are the densest, and slk_spmm
+     * computes them as a dense product on the matrix cores: the row spread
+     * over all ncols columns (0 where no live slot is), and one fp32 K=1
+     * MFMA outer product per column in ascending column order. Each such
+     * product adds w·x to its sum with one rounding, exactly the fma of the
+     * slot-order chain, and an absent column adds 0·x, which leaves the sum
+     * as it is; a non-finite X (0·inf is NaN) is caught and the dense rows
+     * are then recomputed slot by slot. Results equal the reference's under
+     * == (a zero sum may differ in sign). dense_ws is device scratch of at
+     * least slk_dense_rows_workspace_bytes(n_dense_rows, ncols) bytes that
+     * every call overwrites (calls that share it must be ordered on one
+     * stream). Not part of the reference layout: a schedule the caller caches
+     * per topology. */
+    int64_t n_dense_rows;
+    void* dense_ws;
+    /* With a segment list (seg_start ...): the rows order[0 ..
+     * seg_dense_rows) are left out of the list, and slk_sddmm computes their
+     * live slots as dense rows on the matrix cores: per slot the reference's
+     * SIMD-order dot product (16 fma chains, then its add tree), each fma a
+     * K=1 fp32 MFMA step — the same bits. Needs seg_dense_rows ==
+     * n_dense_rows, dense_ws, SLK_DW_SIMD and N a multiple of 64.
+     * slk_seg_list_build reads it too and builds the list without those
+     * rows. 0 = none. */
+    int64_t seg_dense_rows;
 } slk_csr;
+
+/* Bytes of slk_csr.dense_ws for n_dense_rows dense rows of an ncols-column
+ * matrix (the rows spread densely, padded, plus a status word). No
+ * counterpart in the reference; 0 for n_dense_rows <= 0. */
+SLK_API int64_t slk_dense_rows_workspace_bytes(int64_t n_dense_rows, int64_t ncols);
 
 /* Padding unit of a segment list: each column block's segments are padded
  * to a multiple of this. slk_sddmm workgroups take 64 or 128 segments. */
@@ -175,6 +205,8 @@ SLK_API int slk_abi_version(void);
  *   SLK_TUNE_SPMM_G       binned kernel: slots of a row read ahead (1, 2 or 4)
  *   SLK_TUNE_RIGL_TILE    slk_dense_grad_approx: 128 = 128 x 128 tiles staged
  *                         through registers (else 256 x 128 tiles, direct loads)
+ *   SLK_TUNE_DENSE_ROWS   0 = run a view's dense rows (slk_csr.n_dense_rows)
+ *                         with the other rows instead of on the matrix cores
  * Returns SLK_EINVAL for an unknown knob.                                   */
 enum slk_tune_knob {
     SLK_TUNE_SPMM_KERNEL = 0,
@@ -189,7 +221,8 @@ enum slk_tune_knob {
     SLK_TUNE_SPMM_BIN = 9,
     SLK_TUNE_SPMM_G = 10,
     SLK_TUNE_RIGL_TILE = 11,
-    SLK_TUNE_COUNT = 12
+    SLK_TUNE_DENSE_ROWS = 12,
+    SLK_TUNE_COUNT = 13
 };
 SLK_API int slk_set_tuning(int knob, int64_t value);
 
@@ -550,6 +583,19 @@ SLK_API int slk_bin_build(const slk_csr* W, int64_t first, int64_t rw, int64_t h
  * within 2u of its exact value relative to the magnitudes summed).          */
 SLK_API int slk_rigl_mfma_probe(const uint16_t* A, const uint16_t* B, const float* C, float* D,
                                 int64_t n, void* stream);
+
+/* Diagnostic with no counterpart in the reference: n independent fp32
+ * 32 x 32 x 1 (two-block) matrix-core outer products, the instruction the
+ * dense rows of slk_spmm (slk_csr.n_dense_rows) accumulate with, run on
+ * given operands in its register layout: for case t and lane l, A[t*64+l]
+ * and B[t*64+l] are the lane's A and B values and C[(t*64+l)*32+r] its
+ * accumulator register r; D gets the result in the same place. Register r of
+ * lane l holds block b = r/16, row 8((r mod 16)/4) + 4(l/32) + r mod 4 of A's
+ * lanes 32b.., column l mod 32 of B's lanes 32b..: D = fma(A[32b + row],
+ * B[32b + l mod 32], C) there. For checking that the instruction rounds as
+ * one fma.                                                                  */
+SLK_API int slk_dense_mfma_probe(const float* A, const float* B, const float* C, float* D,
+                                 int64_t n, void* stream);
 
 #ifdef __cplusplus
 }

@@ -12,6 +12,8 @@ Contents
       sddmm (simd)    csrc/kernels/spmm_grad_avx2.cpp:108-258
       sddmm (scalar)  csrc/kernels/spmm_grad.cpp:85-108
       dense_grad      csrc/kernels/dense_grad.cpp:57-83
+      fmaf            libm's fmaf elementwise (the reference's fma), for
+                      tests of the device's fma-equivalent instructions
   * ctypes bindings to ``_ref/libslref.so`` — the reference's own kernels,
     when that library was built (``make -C oracle ref``; needs the reference
     checkout, so it exists only where it was built and travels with the tree).
@@ -98,6 +100,7 @@ def _lib():
             getattr(lib, name).argtypes = [_i64, _i32p, _i32p, _i32p, _i64, _f32p, _f32p, _i64,
                                            _i64, _f32p, ctypes.c_int]
         lib.orc_dense_grad.argtypes = [_i64, _i64, _i64, _f32p, _f32p, _f32p, ctypes.c_int]
+        lib.orc_fmaf.argtypes = [_i64, _f32p, _f32p, _f32p, _f32p]
         _oracle = lib
     return _oracle
 
@@ -440,6 +443,15 @@ def dense_grad(dY: np.ndarray, X: np.ndarray, nthreads: int = 0) -> np.ndarray:
     G = np.empty((M, K), dtype=np.float32)
     _lib().orc_dense_grad(M, K, N, _ptr(dY, _f32p), _ptr(X, _f32p), _ptr(G, _f32p), nthreads)
     return G
+
+
+def fmaf(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
+    """Elementwise correctly rounded fmaf(a, b, c) (C libm), float32."""
+    a, b, c = (np.ascontiguousarray(np.broadcast_to(v, np.broadcast(a, b, c).shape),
+                                    dtype=np.float32) for v in (a, b, c))
+    out = np.empty(a.shape, dtype=np.float32)
+    _lib().orc_fmaf(a.size, _ptr(a, _f32p), _ptr(b, _f32p), _ptr(c, _f32p), _ptr(out, _f32p))
+    return out
 
 
 # ─────────────────────── the reference's own build ─────────────────────

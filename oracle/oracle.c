@@ -21,6 +21,9 @@
  *   orc_sddmm_scalar  csrc/kernels/spmm_grad.cpp:85-108: one running sum.
  *   orc_dense_grad    csrc/kernels/dense_grad.cpp:57-83: G = dY·X^T, one
  *                     running sum per element.
+ *   orc_fmaf          out[i] = fmaf(a[i], b[i], c[i]) from libm (correctly
+ *                     rounded): the reference's per-slot fma, elementwise,
+ *                     for tests of the device's fma-equivalent instructions.
  *
  * Scalar running sums `acc += a[j] * b[j]` (the AVX2 kernel's 0..7-element
  * tail and the whole scalar kernels) are not one fma chain in the reference
@@ -139,4 +142,8 @@ void orc_dense_grad(int64_t M, int64_t K, int64_t N, const float* dY, const floa
     num_threads(orc_threads(nthreads))
     for (int64_t i = 0; i < M; ++i)
         for (int64_t k = 0; k < K; ++k) G[i * K + k] = dot_sequential(dY + i * N, X + k * N, N);
+}
+
+void orc_fmaf(int64_t n, const float* a, const float* b, const float* c, float* out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = fmaf(a[i], b[i], c[i]);
 }

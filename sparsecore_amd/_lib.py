@@ -21,7 +21,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libsparsecore_amd.so"
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 SLK_OK, SLK_EINVAL, SLK_EDEVICE = 0, 1, 2
 SLK_DW_SIMD, SLK_DW_SCALAR = 0, 1
@@ -66,6 +66,8 @@ EXPORTS = (
     "slk_bin_sizes",
     "slk_bin_build",
     "slk_rigl_mfma_probe",
+    "slk_dense_rows_workspace_bytes",
+    "slk_dense_mfma_probe",
 )
 
 RIGL_INFO_BYTES = 32  # per row, slk_rigl_count's info
@@ -75,7 +77,7 @@ DROP_GROW_NOALLOC_MAX_SLOTS = 1 << 21  # SLK_DROP_GROW_NOALLOC_MAX_SLOTS
 # Kernel-choice overrides (slk_set_tuning): knob numbers of enum slk_tune_knob.
 TUNE_KNOBS = {"spmm_kernel": 0, "spmm_h": 1, "spmm_rw": 2, "spmm_split": 3, "spmm_vec": 4,
               "sddmm_g": 5, "seg_lean": 6, "seg_group": 7, "transpose_tile": 8, "spmm_bin": 9,
-              "spmm_g": 10, "rigl_tile": 11}
+              "spmm_g": 10, "rigl_tile": 11, "dense_rows": 12}
 
 BIN_MAX_CHUNKS = 960  # SLK_BIN_MAX_CHUNKS
 
@@ -116,6 +118,9 @@ class CsrView(ctypes.Structure):
         ("bin_rw", ctypes.c_int64),
         ("bin_h", ctypes.c_int64),
         ("n_bin", ctypes.c_int64),
+        ("n_dense_rows", ctypes.c_int64),
+        ("dense_ws", ctypes.c_void_p),
+        ("seg_dense_rows", ctypes.c_int64),
     ]
 
 
@@ -153,6 +158,9 @@ def _declare(lib) -> None:
     lib.slk_backward_fused.argtypes = [_csrp, _csrp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp]
     lib.slk_backward_narrow.argtypes = [_csrp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, ctypes.c_int,
                                         _vp]
+    lib.slk_dense_mfma_probe.argtypes = [_vp, _vp, _vp, _vp, _i64, _vp]
+    lib.slk_dense_rows_workspace_bytes.restype = _i64
+    lib.slk_dense_rows_workspace_bytes.argtypes = [_i64, _i64]
     lib.slk_seg_list_capacity.restype = _i64
     lib.slk_seg_list_capacity.argtypes = [_csrp, _i64, _i64]
     lib.slk_seg_list_workspace_bytes.restype = _i64
@@ -396,6 +404,11 @@ def seg_list_build(view: CsrView, block_cols: int, seg_slots: int, device):
     return start, row, count, groups
 
 
+def dense_rows_workspace_bytes(n_dense_rows: int, ncols: int) -> int:
+    """Bytes of slk_csr.dense_ws (slk_dense_rows_workspace_bytes)."""
+    return int(load().slk_dense_rows_workspace_bytes(int(n_dense_rows), int(ncols)))
+
+
 def phase_bounds_build(view: CsrView, n_phases: int, device) -> torch.Tensor:
     """int32 tensor of nrows * (n_phases + 1) entries: for each row the first
     live slot whose column is >= p * ceil(ncols / n_phases), p = 0..n_phases
@@ -435,6 +448,20 @@ def bin_build(view: CsrView, first: int, rw: int, h: int, n_bin: int, device):
     if rc:
         _raise(rc)
     return off, slot, cnt, start
+
+
+def dense_mfma_probe(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, D: torch.Tensor) -> None:
+    """One fp32 32x32x1 two-block MFMA per case (slk_dense_mfma_probe): A, B
+    float32 n x 64 (lane operands), C, D float32 n x 64 x 32 (lane registers)."""
+    n = A.shape[0]
+    if A.shape != (n, 64) or B.shape != (n, 64) or C.shape != (n, 64, 32) or D.shape != (n, 64, 32):
+        raise ValueError("dense_mfma_probe: A, B must be n x 64 and C, D n x 64 x 32")
+    for t in (A, B, C, D):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError("dense_mfma_probe: float32 contiguous tensors expected")
+    rc = load().slk_dense_mfma_probe(ptr(A), ptr(B), ptr(C), ptr(D), n, stream_of(D))
+    if rc:
+        _raise(rc)
 
 
 def rigl_mfma_probe(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, D: torch.Tensor) -> None:

@@ -69,6 +69,18 @@ int validate_csr(const slk_csr* W, const char* who) {
                                     ": a segment list needs seg_row, seg_count, seg_groups, "
                                     "n_seg >= 0, seg_block 64 or 128 and seg_slots 4 or 8");
     }
+    if (W->n_dense_rows < 0 || W->n_dense_rows > W->nrows ||
+        (W->n_dense_rows > 0 && (W->row_order == nullptr || W->dense_ws == nullptr))) {
+        return fail(SLK_EINVAL, std::string(who) + ": n_dense_rows=" +
+                                    std::to_string(W->n_dense_rows) +
+                                    " needs row_order and dense_ws and must lie in [0, nrows]");
+    }
+    if (W->seg_dense_rows < 0 || W->seg_dense_rows > W->nrows ||
+        (W->seg_dense_rows > 0 && W->row_order == nullptr)) {
+        return fail(SLK_EINVAL, std::string(who) + ": seg_dense_rows=" +
+                                    std::to_string(W->seg_dense_rows) +
+                                    " needs row_order and must lie in [0, nrows]");
+    }
     if (W->phase_lo != nullptr && W->n_phases < 1) {
         return fail(SLK_EINVAL, std::string(who) + ": phase_lo needs n_phases >= 1, got " +
                                     std::to_string(W->n_phases));

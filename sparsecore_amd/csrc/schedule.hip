@@ -118,6 +118,18 @@ __global__ __launch_bounds__(kScanBlock) void sl_blkscan_kernel(int64_t nb,
     if (PAD > 1 && t == kScanBlock - 1) groups[0] = part[t] / PAD;
 }
 
+// The rows order[0 .. T) left out of the list: every bound of such a row is
+// its first slot, so all its runs are empty.
+__global__ __launch_bounds__(kSchedThreads) void sl_skip_rows_kernel(
+    int64_t T, int64_t nb, const int32_t* __restrict__ order,
+    const int32_t* __restrict__ row_start, int32_t* __restrict__ lo) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kSchedThreads + threadIdx.x;
+    if (t >= T * (nb + 1)) return;
+    const int64_t p = t / (nb + 1);
+    const int64_t r = order[p];
+    lo[r * (nb + 1) + (t - p * (nb + 1))] = row_start[r];
+}
+
 // Segments of run (r, b): seg_start = first slot, seg_row = r, seg_count <= S.
 template <int S>
 __global__ __launch_bounds__(kSchedThreads) void sg_scatter_kernel(
@@ -260,6 +272,13 @@ extern "C" int slk_seg_list_build(const slk_csr* W, int64_t block_cols, int64_t 
                        dim3(kSchedThreads), 0, st, M, p.nb, block_cols, W->row_start, W->row_nnz,
                        W->col_indices, lo);
     if (int rc = check_launch("seg_list/bounds")) return rc;
+    if (W->seg_dense_rows > 0) {
+        const int64_t n = W->seg_dense_rows * (p.nb + 1);
+        hipLaunchKernelGGL(sl_skip_rows_kernel, dim3(static_cast<unsigned>(ceil_div(n, kSchedThreads))),
+                           dim3(kSchedThreads), 0, st, W->seg_dense_rows, p.nb, W->row_order,
+                           W->row_start, lo);
+        if (int rc = check_launch("seg_list/skip")) return rc;
+    }
     if (seg_slots == 4) {
         hipLaunchKernelGGL(sl_rowscan_kernel<4>, dim3(static_cast<unsigned>(p.nb)), dim3(kScanBlock),
                            0, st, M, p.nb, lo, off, total);

@@ -33,6 +33,7 @@
 // swept through N window by window with dY staged in LDS; large N) and
 // sddmm_scalar_kernel. slk_sddmm_bias appends one wave per row that sums the
 // row of dY (the bias gradient) to the same launch.
+#include "dense_rows.hpp"
 #include "dw_common.hpp"
 
 #include <cstdlib>
@@ -764,6 +765,19 @@ int sddmm_impl(const slk_csr* W, const float* dY, int64_t dY_rows, const float* 
     // A segment list: X through LDS, dY rows in registers.
     // (C·N floats of a band addressed with 32-bit byte offsets)
     if (v4 && W->seg_start != nullptr && N >= 16 && W->seg_block * N * 4 < (int64_t{1} << 32)) {
+        // A list without the dense rows: those on the matrix cores first
+        // (the segment kernel's per-row waves still zero their padding and
+        // sum their dbias).
+        if (W->seg_dense_rows > 0) {
+            if (W->seg_dense_rows != W->n_dense_rows || W->dense_ws == nullptr ||
+                !dense_dw_apply(W->n_dense_rows, W->nrows, W->ncols, N)) {
+                return fail(SLK_EINVAL, std::string(who) +
+                                            ": a segment list without the dense rows needs "
+                                            "seg_dense_rows == n_dense_rows, dense_ws and N a "
+                                            "multiple of 64");
+            }
+            if (int rc = sddmm_dense_rows(W, dY, X, N, dW, st)) return rc;
+        }
         // 128 segments per workgroup on large lists (below, 64: measured on
         // the 60M-GPT layers); SLK_TUNE_SEG_GROUP = 64|128 overrides
         int gs = W->n_seg >= int64_t{128} * kSegGroupMinGroups ? 128 : 64;

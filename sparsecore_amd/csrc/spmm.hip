@@ -31,6 +31,7 @@
 // VEC (floats per lane) is chosen so that small problems still launch
 // enough waves to hide gather latency; large problems use 16-byte gathers.
 #include "common.hpp"
+#include "dense_rows.hpp"
 
 #include <cstdlib>
 #include <mutex>
@@ -1062,6 +1063,12 @@ constexpr int64_t kTargetWaves = 4096;
 // X element (density x rows per workgroup) below which direct gathers are as
 // fast (both measured on the C3/C4/C5 layer shapes).
 constexpr int64_t kLdsMinN = 1024;
+// Dense rows run on the matrix cores in the forward only from this many: each
+// dense wave's chain is K steps long whatever the row count (16384 columns:
+// about 0.5 ms), so a few rows cannot fill the chip, and the dense waves'
+// X reads compete with the gather kernel's for the L2s (16384^2 Zipf(1.1):
+// at 95%, 622 rows, 5.80 -> 5.28 ms; at 99%, 102 rows, 2.50 -> 3.0 ms).
+constexpr int64_t kDenseFwdMinRows = 256;
 constexpr double kLdsMinReuse = 4.0;
 constexpr int64_t kCUs = 256;  // MI355X; one LDS-kernel workgroup per CU at a time
 
@@ -1174,16 +1181,22 @@ SideQueue* side_queue(hipStream_t st) {  // g_side_mu held; nullptr if unavailab
 // caller's stream, the rest on the phased gather kernel on the side stream,
 // concurrently: the heavy rows' workgroups alone leave CUs idle in their last
 // rounds, which the gather launches fill. Rows are disjoint, so the two write
-// disjoint rows of Y. Returns SLK_OK with *done = false if no side queue.
+// disjoint rows of Y. With `dense` (a view whose n_dense_rows rows precede
+// W's in the order), those dense rows run first on the caller's stream, on the
+// matrix cores, beside the gather: the gather's waves use the vector units
+// and leave most registers free, the dense waves the matrix cores. Returns
+// SLK_OK with *done = false if no side queue (nothing launched then).
 int spmm_split_two_queues(const slk_csr* W, int64_t T, const float* X, int64_t N,
-                          const float* bias, float* Y, hipStream_t st, bool* done) {
+                          const float* bias, float* Y, hipStream_t st, bool* done,
+                          const slk_csr* dense = nullptr) {
     std::lock_guard<std::mutex> lock(g_side_mu);
     SideQueue* q = side_queue(st);
     *done = q != nullptr;
     if (q == nullptr) return SLK_OK;
     if (hipEventRecord(q->fork, st) != hipSuccess || hipStreamWaitEvent(q->s, q->fork, 0) != hipSuccess)
         return fail(SLK_EDEVICE, "spmm: fork to the side stream failed");
-    int rc = launch_lds_rw<kHeavyRW, kHeavyH>(W, W->row_order, T, X, N, bias, Y, st);
+    int rc = dense != nullptr ? spmm_dense_rows(dense, X, dense->ncols, N, bias, Y, st) : SLK_OK;
+    if (rc == SLK_OK) rc = launch_lds_rw<kHeavyRW, kHeavyH>(W, W->row_order, T, X, N, bias, Y, st);
     if (rc == SLK_OK) {
         slk_csr rest = *W;
         rest.nrows = W->nrows - T;
@@ -1212,6 +1225,38 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
     if (N > INT32_MAX / 4) return fail(SLK_EINVAL, "spmm: N exceeds the 32-bit lane offset range");
     hipStream_t st = as_stream(stream);
     if (transposed_out) return launch_wave_t(W, X, N, bias, Y, st);
+    // Dense rows (the head of row_order) on the matrix cores, then the rest
+    // of the rows as a view of their own. SLK_TUNE_DENSE_ROWS = 0 keeps them
+    // with the rest.
+    if (W->n_dense_rows >= kDenseFwdMinRows && tuning(SLK_TUNE_DENSE_ROWS) != 0 &&
+        dense_rows_apply(W->n_dense_rows, K, N)) {
+        const int64_t T = W->n_dense_rows;
+        slk_csr rest = *W;
+        rest.nrows = W->nrows - T;
+        rest.row_order = W->row_order + T;
+        rest.n_heavy_rows = W->n_heavy_rows > T ? W->n_heavy_rows - T : 0;
+        rest.n_dense_rows = 0;
+        rest.dense_ws = nullptr;
+        if (rest.bin_off != nullptr) {
+            if (W->bin_first >= T) rest.bin_first = W->bin_first - T;
+            else rest.bin_off = nullptr;  // a stream that covers dense rows is not used
+        }
+        if (rest.nrows == 0) return SLK_OK;
+        // the rest's heavy rows on the LDS kernel beside its light rows on
+        // the phased gather (the two-queue path below): the dense rows join
+        // the caller's stream's side of it, concurrent with the gather
+        const uintptr_t al = reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(Y);
+        if (rest.n_heavy_rows > 0 && rest.n_heavy_rows < rest.nrows && rest.phase_lo != nullptr &&
+            rest.n_phases > 1 && N % 4 == 0 && al % 16 == 0 && N >= kLdsMinN &&
+            tuning(SLK_TUNE_SPMM_SPLIT) < 0 && tuning(SLK_TUNE_SPMM_KERNEL) != 0 &&
+            tuning(SLK_TUNE_SPMM_BIN) <= 0 && rest.bin_off == nullptr) {
+            bool done = false;
+            const int rc = spmm_split_two_queues(&rest, rest.n_heavy_rows, X, N, bias, Y, st, &done, W);
+            if (done || rc != SLK_OK) return rc;
+        }
+        if (int rc = spmm_dense_rows(W, X, K, N, bias, Y, st)) return rc;
+        return spmm_impl(&rest, X, K, N, bias, Y, stream);
+    }
     const uintptr_t align = reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(Y);
     const int64_t M = W->nrows;
     // A binned slot stream (built by the caller where it pays) takes the LDS

@@ -193,6 +193,26 @@ def _check_host(nrows, ncols, values, col, rs, nnz, cap) -> str:
 HEAVY_ROW_FACTOR = 2.0
 
 
+# A row is "dense" for slk_spmm when its live slots cover at least this share
+# of the columns (slk_csr.n_dense_rows): it then runs as a dense row on the
+# matrix cores (an fp32 K=1 MFMA per column, bit-equal to the slot chain),
+# whose time grows with the columns, not the slots. Only matrices with at least
+# DENSE_MIN_COLS columns and DENSE_MIN_ROWS such rows take it.
+DENSE_ROW_FRACTION = 0.25
+DENSE_MIN_COLS = 4096
+DENSE_MIN_ROWS = 32
+
+
+def dense_row_count(row_nnz: np.ndarray, ncols: int) -> int:
+    """Rows with at least DENSE_ROW_FRACTION x ncols live slots (the head of
+    the longest-rows-first order) when there are DENSE_MIN_ROWS of them and
+    ncols >= DENSE_MIN_COLS, else 0."""
+    if ncols < DENSE_MIN_COLS or len(row_nnz) == 0:
+        return 0
+    n = int(np.count_nonzero(np.asarray(row_nnz, dtype=np.float64) >= DENSE_ROW_FRACTION * ncols))
+    return n if n >= DENSE_MIN_ROWS else 0
+
+
 def heavy_row_count(row_nnz: np.ndarray) -> int:
     """Rows with more than HEAVY_ROW_FACTOR x the mean row_nnz: the head of the
     longest-rows-first order that slk_spmm runs as a launch of its own."""
@@ -279,6 +299,7 @@ class PaddedCSR:
         self._cols_skewed = False
         self._host_rows = None  # cached numpy (row_start, row_nnz, row_capacity)
         self._heavy_hint = None  # heavy_row_count(row_nnz) when a builder counted it
+        self._dense_hint = None  # dense_row_count(row_nnz, ncols) likewise
 
     # ─── shape and aggregates (bindings.cpp:631-660) ────────────────
     @property
@@ -366,21 +387,30 @@ class PaddedCSR:
     def _view(self) -> _lib.CsrView:
         v = self._cview
         if v is None:
-            order, n_heavy = None, 0
+            order, n_heavy, n_dense, dws = None, 0, 0, None
             if self._nrows >= self._ORDER_MIN_ROWS and self._on_device():
                 if self._order is None or self._order[0] != self._topology_version:
                     # stable: equal-length rows keep their natural order
-                    heavy = self._heavy_hint
-                    if heavy is None:
-                        heavy = heavy_row_count(self._rows_host()[1])
+                    heavy, dense = self._heavy_hint, self._dense_hint
+                    if heavy is None or dense is None:
+                        nz = self._rows_host()[1]
+                        if heavy is None:
+                            heavy = heavy_row_count(nz)
+                        if dense is None:
+                            dense = dense_row_count(nz, self._ncols)
+                    ws = None
+                    if dense:
+                        ws = torch.empty(_lib.dense_rows_workspace_bytes(dense, self._ncols),
+                                         dtype=torch.uint8, device=self._values.device)
                     self._order = (self._topology_version,
                                    torch.argsort(self._row_nnz, descending=True,
-                                                 stable=True).to(_I32), heavy)
-                order, n_heavy = self._order[1], self._order[2]
+                                                 stable=True).to(_I32), heavy, dense, ws)
+                order, n_heavy, n_dense, dws = self._order[1:5]
             v = _lib.CsrView(self._nrows, self._ncols, self._values.numel(),
                              _lib.ptr(self._values), _lib.ptr(self._col), _lib.ptr(self._rs),
                              _lib.ptr(self._row_nnz), _lib.ptr(self._row_cap), _lib.ptr(order),
-                             n_heavy_rows=n_heavy)
+                             n_heavy_rows=n_heavy, n_dense_rows=n_dense,
+                             dense_ws=_lib.ptr(dws))
             self._cview = v
         return v
 
@@ -390,27 +420,32 @@ class PaddedCSR:
         fields.update(changes)
         return _lib.CsrView(**fields)
 
-    def _view_segmented(self, block_cols: int, seg_slots: int) -> _lib.CsrView:
+    def _view_segmented(self, block_cols: int, seg_slots: int,
+                        skip_dense: bool = False) -> _lib.CsrView:
         """The view plus W's live slots cut into segments of at most seg_slots
         consecutive slots of one row inside one column block (slk_csr.seg_start):
         a schedule for slk_sddmm that keeps each segment's dY row in registers.
-        Built on the device (slk_seg_list_build, six launches, no host read)
-        once per topology. The cached view is rebuilt whenever the base view
-        is (a values rebind, a row-schedule change), so it never carries a
-        stale pointer; the segment arrays survive that as long as the
+        With skip_dense (and dense rows in the view) the list leaves the dense
+        rows out (slk_csr.seg_dense_rows) and slk_sddmm runs them on the
+        matrix cores. Built on the device (slk_seg_list_build, six launches, no
+        host read) once per topology. The cached view is rebuilt whenever the
+        base view is (a values rebind, a row-schedule change), so it never
+        carries a stale pointer; the segment arrays survive that as long as the
         topology does."""
         base = self._view()
-        key = (self._topology_version, int(block_cols), int(seg_slots))
+        skip = int(base.n_dense_rows) if skip_dense else 0
+        key = (self._topology_version, int(block_cols), int(seg_slots), skip)
         c = self._seglist
         if c is None or c[0] != key:
-            arrays = _lib.seg_list_build(base, int(block_cols), int(seg_slots), self.device)
+            arrays = _lib.seg_list_build(self._derived(base, seg_dense_rows=skip), int(block_cols),
+                                         int(seg_slots), self.device)
             c = (key, None, None, arrays)
         if c[1] is not base:
             start, row, count, groups = c[3]
             view = self._derived(base, seg_start=_lib.ptr(start), seg_row=_lib.ptr(row),
                                  seg_count=_lib.ptr(count), seg_groups=_lib.ptr(groups),
                                  n_seg=int(start.numel()), seg_block=int(block_cols),
-                                 seg_slots=int(seg_slots))
+                                 seg_slots=int(seg_slots), seg_dense_rows=skip)
             c = (key, base, view, c[3])
         self._seglist = c
         return c[2]
@@ -582,6 +617,7 @@ class PaddedCSR:
         self._topology_version += 1
         self._cview = None  # the row schedule depends on row_nnz
         self._heavy_hint = None
+        self._dense_hint = None
 
     def _drop_grow(self, k_drop: int, rule: int, G: torch.Tensor | None = None,
                    seed: int = 0) -> None:
@@ -675,6 +711,7 @@ class PaddedCSR:
             self._nnz -= lost
             self._host_rows = None
             self._heavy_hint = None
+            self._dense_hint = None
             self._cview = None
             self._order = None
         elif self._order is not None:
@@ -940,9 +977,9 @@ def transpose_with_perm(p: PaddedCSR, *, padding_ratio: float = 0.2):
     cap_t = torch.empty(K, dtype=_I32, device=dev)
     capT_dev = torch.empty(1, dtype=torch.int64, device=dev)
     _lib.transpose_count(view, padding_ratio, ws, rs_t, nnz_t, cap_t, capT_dev)
-    counts = torch.empty(2, dtype=torch.int64, device=dev)
+    counts = torch.empty(3, dtype=torch.int64, device=dev)
     counts[0:1].copy_(capT_dev)
-    _count_heavy(nnz_t, p.nnz, counts[1:2])
+    _count_rows(nnz_t, p.nnz, M, counts[1:3])
     bound = _capacity_bound(p.nnz, K, padding_ratio)
     early = bound <= np.iinfo(np.int32).max
     if early:  # fill first, read the exact capacity after it
@@ -950,7 +987,7 @@ def transpose_with_perm(p: PaddedCSR, *, padding_ratio: float = 0.2):
         col_t = torch.empty(bound, dtype=_I32, device=dev)
         perm = torch.empty(bound, dtype=torch.int64, device=dev)
         _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, bound, val_t, col_t, perm)
-    capT, heavy = counts.tolist()
+    capT, heavy, dense = counts.tolist()
     if capT > np.iinfo(np.int32).max:
         raise ValueError(f"transpose: capacity {capT} exceeds the int32 slot range")
     if early:
@@ -962,19 +999,27 @@ def transpose_with_perm(p: PaddedCSR, *, padding_ratio: float = 0.2):
         _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, capT, val_t, col_t, perm)
     WT = PaddedCSR._from_parts(K, M, val_t, col_t, rs_t, nnz_t, cap_t, p.nnz)
     WT._heavy_hint = heavy
+    WT._dense_hint = dense
     WT._cols_skewed = view.n_heavy_rows > 0  # WT's columns are p's rows
     return WT, perm
 
 
-def _count_heavy(nnz_t: torch.Tensor, nnz: int, out: torch.Tensor) -> None:
-    """out[0] = heavy_row_count of a WT whose row_nnz is nnz_t and total nnz,
-    counted on the device (read with the capacity, no extra host sync)."""
+def _count_rows(nnz_t: torch.Tensor, nnz: int, ncols: int, out: torch.Tensor) -> None:
+    """out[0] = heavy_row_count and out[1] = dense_row_count of a WT whose
+    row_nnz is nnz_t (total nnz, ncols columns), counted on the device (read
+    with the capacity, no extra host sync)."""
     n = nnz_t.numel()
     if n == 0:
         out.zero_()
         return
+    nz = nnz_t.to(torch.float64)
     bar = HEAVY_ROW_FACTOR * (float(nnz) / n)  # the float64 bar of heavy_row_count
-    out.copy_((nnz_t.to(torch.float64) > bar).sum().view(1))
+    out[0:1].copy_((nz > bar).sum().view(1))
+    if ncols < DENSE_MIN_COLS:
+        out[1:2].zero_()
+    else:
+        d = (nz >= DENSE_ROW_FRACTION * ncols).sum()
+        out[1:2].copy_(torch.where(d >= DENSE_MIN_ROWS, d, torch.zeros_like(d)).view(1))
 
 
 def transposes_with_perm(ps, *, padding_ratio: float = 0.2):
@@ -992,7 +1037,7 @@ def transposes_with_perm(ps, *, padding_ratio: float = 0.2):
     if any(p.device != dev for p in ps):
         raise ValueError("transposes_with_perm: all matrices must be on one device")
     n = len(ps)
-    caps = torch.empty(2 * n, dtype=torch.int64, device=dev)  # capacities, heavy-row counts
+    caps = torch.empty(3 * n, dtype=torch.int64, device=dev)  # capacities, heavy, dense counts
     staged = []
     for i, p in enumerate(ps):
         view = p._view()
@@ -1002,10 +1047,10 @@ def transposes_with_perm(ps, *, padding_ratio: float = 0.2):
         nnz_t = torch.empty(K, dtype=_I32, device=dev)
         cap_t = torch.empty(K, dtype=_I32, device=dev)
         _lib.transpose_count(view, padding_ratio, ws, rs_t, nnz_t, cap_t, caps[i:i + 1])
-        if K >= PaddedCSR._ORDER_MIN_ROWS:  # only scheduled views use the count
-            _count_heavy(nnz_t, p.nnz, caps[n + i:n + i + 1])
+        if K >= PaddedCSR._ORDER_MIN_ROWS:  # only scheduled views use the counts
+            _count_rows(nnz_t, p.nnz, p.nrows, caps[n + 2 * i:n + 2 * i + 2])
         else:
-            caps[n + i:n + i + 1].zero_()
+            caps[n + 2 * i:n + 2 * i + 2].zero_()
         # the fill right behind the count, into arrays sized by a bound of
         # the capacity (as transpose_with_perm)
         bound = _capacity_bound(p.nnz, K, padding_ratio)
@@ -1018,8 +1063,8 @@ def transposes_with_perm(ps, *, padding_ratio: float = 0.2):
         staged.append((view, ws, rs_t, nnz_t, cap_t, filled))
     host = caps.tolist()
     out = []
-    for p, capT, heavy, (view, ws, rs_t, nnz_t, cap_t, filled) in zip(ps, host[:n], host[n:],
-                                                                       staged):
+    for p, capT, heavy, dense, (view, ws, rs_t, nnz_t, cap_t, filled) in zip(
+            ps, host[:n], host[n::2], host[n + 1::2], staged):
         if capT > np.iinfo(np.int32).max:
             raise ValueError(f"transpose: capacity {capT} exceeds the int32 slot range")
         if filled is not None:
@@ -1031,6 +1076,7 @@ def transposes_with_perm(ps, *, padding_ratio: float = 0.2):
             _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, capT, val_t, col_t, perm)
         WT = PaddedCSR._from_parts(p.ncols, p.nrows, val_t, col_t, rs_t, nnz_t, cap_t, p.nnz)
         WT._heavy_hint = heavy
+        WT._dense_hint = dense
         WT._cols_skewed = view.n_heavy_rows > 0  # WT's columns are p's rows
         out.append((WT, perm))
     return out

@@ -212,14 +212,29 @@ def _seg_shape(W: PaddedCSR, K: int, N: int) -> tuple[int, int]:
     return 64, 8 if density * 64 >= 4 else 4
 
 
+# Dense rows (slk_csr.n_dense_rows) of a segmented dW run on the matrix cores
+# where N is a multiple of 64 (the dense kernel's staged columns) and there
+# are at least _DENSE_DW_MIN_ROWS of them: the segment kernel's time follows
+# its (row, column block) pairs more than its slots, so a few dense rows
+# taken out save little (16384^2 Zipf(1.1) x 4096: 95%, 622 dense rows,
+# 5.47 -> 5.22 ms; 99%, 102 rows, 1.86 -> 2.04 ms). "dense_dw" = False in
+# _overrides keeps them in the segment list, True takes any count.
+_DENSE_DW_N = 64
+_DENSE_DW_MIN_ROWS = 256
+
+
 def _sddmm_view(W: PaddedCSR, X: torch.Tensor):
-    """W's view for slk_sddmm: with a segment list where it pays (see above)."""
+    """W's view for slk_sddmm: with a segment list where it pays (see above),
+    without W's dense rows where the dense kernel takes them."""
     K, N = X.shape
+    want = _overrides.get("dense_dw")
+    skip = N % _DENSE_DW_N == 0 and N >= _DENSE_DW_N and want is not False and (
+        want is True or W._view().n_dense_rows >= _DENSE_DW_MIN_ROWS)
     forced = _overrides.get("seg")
     if forced is not None:
-        return W._view_segmented(*forced) if forced else W._view()
+        return W._view_segmented(*forced, skip_dense=skip) if forced else W._view()
     if W.nnz >= _SEG_MIN_NNZ and N >= 1024 and N % 4 == 0:
-        return W._view_segmented(*_seg_shape(W, K, N))
+        return W._view_segmented(*_seg_shape(W, K, N), skip_dense=skip)
     return W._view()
 
 

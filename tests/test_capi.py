@@ -96,24 +96,38 @@ def test_heavy_rows_are_those_far_above_the_mean():
     assert heavy_row_count(counts) == int((counts > 2 * counts.mean()).sum()) > 0
 
 
-@pytest.mark.parametrize("case", ["zipf", "ties", "uniform", "empty-rows", "none"])
-def test_transpose_builders_count_heavy_rows_like_the_host_rule(case):
-    """The transpose builders count a WT's heavy rows on the device (read with
-    its capacity); the count equals heavy_row_count on the host arrays."""
+@pytest.mark.parametrize("case", ["zipf", "ties", "uniform", "empty-rows", "none", "dense",
+                                  "dense-few", "dense-at-bar"])
+@pytest.mark.parametrize("ncols", [4000, 8192])
+def test_transpose_builders_count_rows_like_the_host_rules(case, ncols):
+    """The transpose builders count a WT's heavy and dense rows on the device
+    (read with its capacity); the counts equal heavy_row_count and
+    dense_row_count on the host arrays."""
     import torch
 
     from sparsecore_amd import layout
 
     rng = np.random.default_rng(3)
+    bar = int(np.ceil(layout.DENSE_ROW_FRACTION * ncols))
     nnz = {"zipf": np.minimum(4000, (3000 * np.arange(1, 2501) ** -1.1).astype(np.int32)),
            "ties": np.array([10] * 99 + [4 * 10 + 30], np.int32),
            "uniform": np.full(3000, 17, np.int32),
            "empty-rows": np.concatenate([np.zeros(500, np.int32), rng.integers(0, 50, 2000)]),
-           "none": np.zeros(0, np.int32)}[case].astype(np.int32)
+           "none": np.zeros(0, np.int32),
+           "dense": np.concatenate([rng.integers(bar, ncols, 40), rng.integers(0, 80, 3000)]),
+           "dense-few": np.concatenate([rng.integers(bar, ncols, 31), rng.integers(0, 80, 3000)]),
+           "dense-at-bar": np.concatenate([np.full(32, bar), np.full(32, bar - 1),
+                                           rng.integers(0, 80, 3000)]),
+           }[case].astype(np.int32)
     rng.shuffle(nnz)
-    out = torch.full((1,), -1, dtype=torch.int64)
-    layout._count_heavy(torch.from_numpy(nnz), int(nnz.sum()), out)
-    assert int(out) == layout.heavy_row_count(nnz)
+    out = torch.full((2,), -1, dtype=torch.int64)
+    layout._count_rows(torch.from_numpy(nnz), int(nnz.sum()), ncols, out)
+    assert int(out[0]) == layout.heavy_row_count(nnz)
+    assert int(out[1]) == layout.dense_row_count(nnz, ncols)
+    if case == "dense" and ncols >= layout.DENSE_MIN_COLS:
+        assert int(out[1]) == 40
+    if case in ("dense-few", "uniform"):
+        assert int(out[1]) == 0
 
 
 def test_empty_problems_are_no_ops():

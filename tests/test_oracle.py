@@ -269,3 +269,53 @@ def test_c1_fixture_metadata_is_consistent():
     assert set(meta["outputs_sha256"]) == {"Y", "dW", "dW_scalar", "dX"}
     for k, s in meta["samples"].items():
         assert len(s["index"]) == len(s["value_bits"]) == 64, k
+
+
+def _round_to_f32(q):
+    """The float32 nearest the rational q (ties to even), with gradual underflow
+    and overflow to infinity — IEEE 754 round-to-nearest, from its definition."""
+    from fractions import Fraction
+
+    if q == 0:
+        return np.float32(0.0)
+    sign = -1.0 if q < 0 else 1.0
+    a = abs(q)
+    e = a.numerator.bit_length() - a.denominator.bit_length()  # 2^e <= a < 2^(e+2)
+    while Fraction(2) ** e > a:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= a:
+        e += 1
+    ulp_exp = max(e, -126) - 23  # 24-bit significand; below 2^-126 the spacing stays 2^-149
+    m = a / Fraction(2) ** ulp_exp
+    n = m.numerator // m.denominator
+    rem = m - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    val = float(n) * 2.0 ** ulp_exp  # exact in float64
+    if val >= 2.0 ** 128:
+        return np.float32(sign * np.inf)
+    return np.float32(sign * val)
+
+
+def test_oracle_fmaf_is_the_correctly_rounded_fma():
+    """oracle.fmaf (libm) equals a·b + c rounded once, computed exactly; and it
+    differs from the unfused multiply-add where that rounds twice."""
+    from fractions import Fraction
+
+    rng = np.random.default_rng(0)
+    n = 3000
+    a = np.ldexp(rng.standard_normal(n), rng.integers(-62, 62, n)).astype(np.float32)
+    b = np.ldexp(rng.standard_normal(n), rng.integers(-62, 62, n)).astype(np.float32)
+    p = (a * b).astype(np.float32)
+    c = np.where(rng.random(n) < 0.5, -p, np.ldexp(rng.standard_normal(n), rng.integers(-140, 60, n)))
+    c = c.astype(np.float32)
+    got = oracle.fmaf(a, b, c)
+    for i in range(n):
+        exact = Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i]))
+        want = _round_to_f32(exact)
+        assert got[i].view(np.uint32) == want.view(np.uint32) or (got[i] == 0 and want == 0), i
+    # known answer: (1 + 2^-12)^2 - (1 + 2^-11) = 2^-24 fused, 0 unfused
+    x = np.float32(1 + 2.0 ** -12)
+    y = np.float32(-(1 + 2.0 ** -11))
+    assert oracle.fmaf(x, x, y) == np.float32(2.0 ** -24)
+    assert np.float32(x * x) + y == 0.0
