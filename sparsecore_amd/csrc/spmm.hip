@@ -1196,7 +1196,8 @@ int spmm_split_two_queues(const slk_csr* W, int64_t T, const float* X, int64_t N
     if (hipEventRecord(q->fork, st) != hipSuccess || hipStreamWaitEvent(q->s, q->fork, 0) != hipSuccess)
         return fail(SLK_EDEVICE, "spmm: fork to the side stream failed");
     int rc = dense != nullptr ? spmm_dense_rows(dense, X, dense->ncols, N, bias, Y, st) : SLK_OK;
-    if (rc == SLK_OK) rc = launch_lds_rw<kHeavyRW, kHeavyH>(W, W->row_order, T, X, N, bias, Y, st);
+    if (rc == SLK_OK && T > 0)
+        rc = launch_lds_rw<kHeavyRW, kHeavyH>(W, W->row_order, T, X, N, bias, Y, st);
     if (rc == SLK_OK) {
         slk_csr rest = *W;
         rest.nrows = W->nrows - T;
@@ -1242,14 +1243,18 @@ int spmm_impl(const slk_csr* W, const float* X, int64_t K, int64_t N, const floa
             else rest.bin_off = nullptr;  // a stream that covers dense rows is not used
         }
         if (rest.nrows == 0) return SLK_OK;
-        // the rest's heavy rows on the LDS kernel beside its light rows on
-        // the phased gather (the two-queue path below): the dense rows join
-        // the caller's stream's side of it, concurrent with the gather
+        // With phase bounds (X far beyond the L2s), the dense rows run on the
+        // caller's stream beside the phased gather of the light rows on the
+        // side stream (the two-queue path below; the rest's heavy rows, if
+        // any, on the LDS kernel after the dense ones): the gather waves use
+        // the vector units, the dense waves the matrix cores, and the
+        // longest rows, whose serial chains set each phase's length, leave
+        // the gather.
         const uintptr_t al = reinterpret_cast<uintptr_t>(X) | reinterpret_cast<uintptr_t>(Y);
-        if (rest.n_heavy_rows > 0 && rest.n_heavy_rows < rest.nrows && rest.phase_lo != nullptr &&
-            rest.n_phases > 1 && N % 4 == 0 && al % 16 == 0 && N >= kLdsMinN &&
-            tuning(SLK_TUNE_SPMM_SPLIT) < 0 && tuning(SLK_TUNE_SPMM_KERNEL) != 0 &&
-            tuning(SLK_TUNE_SPMM_BIN) <= 0 && rest.bin_off == nullptr) {
+        if (rest.n_heavy_rows < rest.nrows && rest.phase_lo != nullptr && rest.n_phases > 1 &&
+            N % 4 == 0 && al % 16 == 0 && N >= kLdsMinN && tuning(SLK_TUNE_SPMM_SPLIT) < 0 &&
+            tuning(SLK_TUNE_SPMM_KERNEL) != 0 && tuning(SLK_TUNE_SPMM_BIN) <= 0 &&
+            rest.bin_off == nullptr) {
             bool done = false;
             const int rc = spmm_split_two_queues(&rest, rest.n_heavy_rows, X, N, bias, Y, st, &done, W);
             if (done || rc != SLK_OK) return rc;

@@ -194,6 +194,29 @@ def test_dense_rows_forward_equals_the_oracle(dev, M, K, n_dense, N, bias):
     _assert_equal_values(Y2.cpu().numpy(), want, "Y without dense rows")
 
 
+@pytest.mark.parametrize("n_heavy", [0, 150, 420])
+def test_dense_rows_beside_the_phased_gather(dev, n_heavy):
+    """Phase bounds put the light rows on the phased gather of the side
+    stream: the dense rows run on the caller's stream beside it, and the
+    heavy rows beyond the dense ones (none when n_heavy <= n_dense) on the
+    LDS kernel after them."""
+    M, K, n_dense, N = 2200, 4100, 300, 1024
+    print(f"[dense rows] phased {M}x{K} dense={n_dense} heavy={n_heavy} N={N}", flush=True)
+    c = _matrix(M, K, n_dense, seed=11 + n_heavy)
+    W = from_oracle(c, dev)
+    # the constructor's device check built the row order: rebuild it with the hint
+    W._heavy_hint, W._order, W._cview = n_heavy, None, None
+    v = W._view_phased(3)
+    assert v.n_dense_rows == n_dense and v.n_heavy_rows == n_heavy and v.n_phases == 3
+    rng = np.random.default_rng(n_heavy)
+    X = rng.standard_normal((K, N)).astype(np.float32)
+    b = rng.standard_normal(M).astype(np.float32)
+    want = (oracle.spmm(c, X) + b[:, None]).astype(np.float32)
+    Y = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+    _lib.spmm(v, _t(X, dev), Y, _t(b, dev))
+    _assert_equal_values(Y.cpu().numpy(), want, "Y")
+
+
 @pytest.mark.parametrize("bad", ["inf", "nan", "inf-in-dense-column", "overflow"])
 def test_dense_rows_nonfinite_inputs_take_the_recompute(dev, bad):
     print(f"[dense rows] non-finite {bad}", flush=True)
