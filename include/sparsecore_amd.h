@@ -207,6 +207,10 @@ SLK_API int slk_abi_version(void);
  *                         through registers (else 256 x 128 tiles, direct loads)
  *   SLK_TUNE_DENSE_ROWS   0 = run a view's dense rows (slk_csr.n_dense_rows)
  *                         with the other rows instead of on the matrix cores
+ *   SLK_TUNE_TRANSPOSE_RADIX transpose: 0 = the counting sort (row-block
+ *                         histograms and scatter) everywhere, 1 = the radix
+ *                         sort by column wherever ncols <= 65535 (automatic:
+ *                         there, for total_capacity >= 2^20)
  * Returns SLK_EINVAL for an unknown knob.                                   */
 enum slk_tune_knob {
     SLK_TUNE_SPMM_KERNEL = 0,
@@ -222,7 +226,8 @@ enum slk_tune_knob {
     SLK_TUNE_SPMM_G = 10,
     SLK_TUNE_RIGL_TILE = 11,
     SLK_TUNE_DENSE_ROWS = 12,
-    SLK_TUNE_COUNT = 13
+    SLK_TUNE_TRANSPOSE_RADIX = 13,
+    SLK_TUNE_COUNT = 14
 };
 SLK_API int slk_set_tuning(int knob, int64_t value);
 
@@ -297,6 +302,16 @@ SLK_API int slk_transpose_fill(const slk_csr* W, const void* workspace,
 SLK_API int slk_transpose_refresh(const float* W_values, int64_t W_capacity,
                           const int64_t* perm, int64_t capT,
                           float* WT_values, void* stream);
+
+/* Counts of a row_nnz array (n entries, int32) written to device memory:
+ * out[0] = entries with (double)row_nnz[i] > heavy_bar, out[1] = entries
+ * with (double)row_nnz[i] >= dense_bar, or 0 when fewer than
+ * dense_min_rows. No counterpart in the reference: it computes the heavy-
+ * and dense-row hints of a freshly built transpose (the rules of
+ * layout.heavy_row_count / layout.dense_row_count in this package) on the
+ * device, so the host reads them with the transpose's capacity in one read. */
+SLK_API int slk_row_hints(const int32_t* row_nnz, int64_t n, double heavy_bar,
+                          double dense_bar, int64_t dense_min_rows, int64_t* out, void* stream);
 
 /* Invariant scan of a device PaddedCSR (the checks of
  * csrc/kernels/padded_csr.cpp:79-196, invariants 3-7). Writes

@@ -41,6 +41,7 @@ EXPORTS = (
     "slk_transpose_count",
     "slk_transpose_fill",
     "slk_transpose_refresh",
+    "slk_row_hints",
     "slk_check_invariants",
     "slk_live_abs_kth",
     "slk_drop_grow_workspace_bytes",
@@ -77,7 +78,7 @@ DROP_GROW_NOALLOC_MAX_SLOTS = 1 << 21  # SLK_DROP_GROW_NOALLOC_MAX_SLOTS
 # Kernel-choice overrides (slk_set_tuning): knob numbers of enum slk_tune_knob.
 TUNE_KNOBS = {"spmm_kernel": 0, "spmm_h": 1, "spmm_rw": 2, "spmm_split": 3, "spmm_vec": 4,
               "sddmm_g": 5, "seg_lean": 6, "seg_group": 7, "transpose_tile": 8, "spmm_bin": 9,
-              "spmm_g": 10, "rigl_tile": 11, "dense_rows": 12}
+              "spmm_g": 10, "rigl_tile": 11, "dense_rows": 12, "transpose_radix": 13}
 
 BIN_MAX_CHUNKS = 960  # SLK_BIN_MAX_CHUNKS
 
@@ -146,6 +147,7 @@ def _declare(lib) -> None:
                                         _vp]
     lib.slk_transpose_fill.argtypes = [_csrp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp]
     lib.slk_transpose_refresh.argtypes = [_vp, _i64, _vp, _i64, _vp, _vp]
+    lib.slk_row_hints.argtypes = [_vp, _i64, ctypes.c_double, ctypes.c_double, _i64, _vp, _vp]
     lib.slk_check_invariants.argtypes = [_csrp, _i64, _vp, _vp]
     lib.slk_live_abs_kth.argtypes = [_csrp, _i64, _vp, _i64, _vp, _vp]
     lib.slk_drop_grow_workspace_bytes.restype = _i64
@@ -300,6 +302,18 @@ def transpose_refresh(W_values: torch.Tensor, perm: torch.Tensor, WT_values: tor
     lib = load()
     rc = lib.slk_transpose_refresh(ptr(W_values), W_values.numel(), ptr(perm), perm.numel(),
                                    ptr(WT_values), stream_of(WT_values))
+    if rc:
+        _raise(rc)
+
+
+def row_hints(row_nnz: torch.Tensor, heavy_bar: float, dense_bar: float, dense_min_rows: int,
+              out: torch.Tensor) -> None:
+    """out[0] = rows with row_nnz > heavy_bar, out[1] = rows with row_nnz >=
+    dense_bar (0 if fewer than dense_min_rows); float64 compares, on the
+    device (slk_row_hints)."""
+    lib = load()
+    rc = lib.slk_row_hints(ptr(row_nnz), row_nnz.numel(), float(heavy_bar), float(dense_bar),
+                           int(dense_min_rows), out.data_ptr(), stream_of(out))
     if rc:
         _raise(rc)
 

@@ -975,11 +975,8 @@ def transpose_with_perm(p: PaddedCSR, *, padding_ratio: float = 0.2):
     rs_t = torch.empty(K, dtype=_I32, device=dev)
     nnz_t = torch.empty(K, dtype=_I32, device=dev)
     cap_t = torch.empty(K, dtype=_I32, device=dev)
-    capT_dev = torch.empty(1, dtype=torch.int64, device=dev)
-    _lib.transpose_count(view, padding_ratio, ws, rs_t, nnz_t, cap_t, capT_dev)
-    counts = torch.empty(3, dtype=torch.int64, device=dev)
-    counts[0:1].copy_(capT_dev)
-    _count_rows(nnz_t, p.nnz, M, counts[1:3])
+    counts = torch.empty(3, dtype=torch.int64, device=dev)  # capacity, heavy, dense rows
+    _lib.transpose_count(view, padding_ratio, ws, rs_t, nnz_t, cap_t, counts[0:1])
     bound = _capacity_bound(p.nnz, K, padding_ratio)
     early = bound <= np.iinfo(np.int32).max
     if early:  # fill first, read the exact capacity after it
@@ -987,6 +984,7 @@ def transpose_with_perm(p: PaddedCSR, *, padding_ratio: float = 0.2):
         col_t = torch.empty(bound, dtype=_I32, device=dev)
         perm = torch.empty(bound, dtype=torch.int64, device=dev)
         _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, bound, val_t, col_t, perm)
+    _count_rows(nnz_t, p.nnz, M, counts[1:3])
     capT, heavy, dense = counts.tolist()
     if capT > np.iinfo(np.int32).max:
         raise ValueError(f"transpose: capacity {capT} exceeds the int32 slot range")
@@ -1009,17 +1007,9 @@ def _count_rows(nnz_t: torch.Tensor, nnz: int, ncols: int, out: torch.Tensor) ->
     row_nnz is nnz_t (total nnz, ncols columns), counted on the device (read
     with the capacity, no extra host sync)."""
     n = nnz_t.numel()
-    if n == 0:
-        out.zero_()
-        return
-    nz = nnz_t.to(torch.float64)
-    bar = HEAVY_ROW_FACTOR * (float(nnz) / n)  # the float64 bar of heavy_row_count
-    out[0:1].copy_((nz > bar).sum().view(1))
-    if ncols < DENSE_MIN_COLS:
-        out[1:2].zero_()
-    else:
-        d = (nz >= DENSE_ROW_FRACTION * ncols).sum()
-        out[1:2].copy_(torch.where(d >= DENSE_MIN_ROWS, d, torch.zeros_like(d)).view(1))
+    bar = HEAVY_ROW_FACTOR * (float(nnz) / n) if n else 0.0  # heavy_row_count's float64 bar
+    dense_bar = DENSE_ROW_FRACTION * ncols if ncols >= DENSE_MIN_COLS else float("inf")
+    _lib.row_hints(nnz_t, bar, dense_bar, DENSE_MIN_ROWS, out)
 
 
 def transposes_with_perm(ps, *, padding_ratio: float = 0.2):

@@ -96,13 +96,14 @@ def test_heavy_rows_are_those_far_above_the_mean():
     assert heavy_row_count(counts) == int((counts > 2 * counts.mean()).sum()) > 0
 
 
+@pytest.mark.gpu
 @pytest.mark.parametrize("case", ["zipf", "ties", "uniform", "empty-rows", "none", "dense",
                                   "dense-few", "dense-at-bar"])
 @pytest.mark.parametrize("ncols", [4000, 8192])
-def test_transpose_builders_count_rows_like_the_host_rules(case, ncols):
+def test_transpose_builders_count_rows_like_the_host_rules(dev, case, ncols):
     """The transpose builders count a WT's heavy and dense rows on the device
-    (read with its capacity); the counts equal heavy_row_count and
-    dense_row_count on the host arrays."""
+    (slk_row_hints, read with its capacity); the counts equal heavy_row_count
+    and dense_row_count on the host arrays."""
     import torch
 
     from sparsecore_amd import layout
@@ -120,8 +121,8 @@ def test_transpose_builders_count_rows_like_the_host_rules(case, ncols):
                                            rng.integers(0, 80, 3000)]),
            }[case].astype(np.int32)
     rng.shuffle(nnz)
-    out = torch.full((2,), -1, dtype=torch.int64)
-    layout._count_rows(torch.from_numpy(nnz), int(nnz.sum()), ncols, out)
+    out = torch.full((2,), -1, dtype=torch.int64, device=dev)
+    layout._count_rows(torch.from_numpy(nnz).to(dev), int(nnz.sum()), ncols, out)
     assert int(out[0]) == layout.heavy_row_count(nnz)
     assert int(out[1]) == layout.dense_row_count(nnz, ncols)
     if case == "dense" and ncols >= layout.DENSE_MIN_COLS:

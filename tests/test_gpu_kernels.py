@@ -498,6 +498,37 @@ def test_transpose_tiles_bit_exact(dev, tune, M, K, kind):
         assert_bits_equal(perm.cpu().numpy(), perm_o, f"perm tile={tile}")
 
 
+@pytest.mark.parametrize("M,K,kind", [
+    (300, 200, "uniform"), (5000, 256, "zipf"), (2000, 257, "uniform"), (1300, 3000, "zipf"),
+    (4100, 700, "zipf"), (70, 20000, "uniform"), (40, 40000, "uniform"), (9, 65535, "uniform"),
+    (3000, 5000, "empty-rows"), (64, 3000, "none-live")])
+def test_transpose_radix_bit_exact(dev, tune, M, K, kind):
+    """The radix path (a stable sort by column: one 8-bit pass for ncols <=
+    256, two up to 65535) gives the oracle's WT and perm, and so does the
+    counting sort: one-pass and two-pass column counts, skewed rows, column
+    chunks of the count (ncols > 16384), rows and matrices without live
+    slots, partial tiles."""
+    print(f"[transpose radix] {M}x{K} {kind}", flush=True)
+    if kind == "zipf":
+        c = oracle.zipf_rows(M, K, 0.03, 1.1, seed=M, sigma=1.0)
+    elif kind == "empty-rows":
+        c = oracle.uniform_rows(M, K, 40, seed=M)
+        dense = oracle.to_dense(c)
+        dense[::3] = 0.0  # every third row empty
+        c = oracle.from_dense(dense)
+    elif kind == "none-live":
+        c = oracle.from_dense(np.zeros((M, K), np.float32))
+    else:
+        c = oracle.uniform_rows(M, K, max(1, K // 40), seed=M)
+    W = from_oracle(c, dev)
+    WT_o, perm_o = oracle.transpose_with_perm(c)
+    for radix in (1, 0):
+        tune(transpose_radix=radix)
+        WT, perm = layout.transpose_with_perm(W)
+        csr_arrays_equal(to_oracle(WT), WT_o, f"WT radix={radix}")
+        assert_bits_equal(perm.cpu().numpy(), perm_o, f"perm radix={radix}")
+
+
 def test_transpose_wide_matrix_uses_column_chunks(dev):
     """ncols > 16384 exercises the multi-pass (column-chunked) LDS counters."""
     c = oracle.uniform_rows(40, 40000, 300, seed=4)
