@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define SLK_ABI_VERSION 15
+#define SLK_ABI_VERSION 16
 
 #if defined(__GNUC__)
 #define SLK_API __attribute__((visibility("default")))
