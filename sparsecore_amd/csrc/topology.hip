@@ -76,12 +76,25 @@ __global__ __launch_bounds__(kSelThreads) void kth_hist_kernel(
     const uint32_t mask = (1u << sel_width(pass)) - 1u;
     const uint32_t prefix = st->prefix;
     const int hi = shift + sel_width(pass);
+    // kSelUnroll slots per thread at a time, all loads issued before any use
+    constexpr int kSelUnroll = 8;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kSelThreads;
-    for (int64_t s = static_cast<int64_t>(blockIdx.x) * kSelThreads + threadIdx.x; s < cap;
-         s += stride) {
-        if (col[s] < 0) continue;  // padding
-        const uint32_t u = __float_as_uint(fabsf(val[s]));
-        if (pass == 0 || (u >> hi) == prefix) atomicAdd(&h[(u >> shift) & mask], 1u);
+    for (int64_t s0 = static_cast<int64_t>(blockIdx.x) * kSelThreads + threadIdx.x; s0 < cap;
+         s0 += kSelUnroll * stride) {
+        int32_t c[kSelUnroll];
+        float v[kSelUnroll];
+#pragma unroll
+        for (int q = 0; q < kSelUnroll; ++q) {
+            const int64_t s = s0 + q * stride;
+            c[q] = s < cap ? col[s] : -1;
+            v[q] = s < cap ? val[s] : 0.0f;
+        }
+#pragma unroll
+        for (int q = 0; q < kSelUnroll; ++q) {
+            if (c[q] < 0) continue;  // padding (or past the end)
+            const uint32_t u = __float_as_uint(fabsf(v[q]));
+            if (pass == 0 || (u >> hi) == prefix) atomicAdd(&h[(u >> shift) & mask], 1u);
+        }
     }
     __syncthreads();
     for (int b = threadIdx.x; b < kSelBins; b += kSelThreads)
@@ -363,7 +376,7 @@ extern "C" int slk_live_abs_kth(const slk_csr* W, int64_t k, void* workspace,
     SelState* s = static_cast<SelState*>(workspace);
     hipLaunchKernelGGL(kth_init_kernel, dim3(1), dim3(kSelThreads), 0, st, s, k);
     const int64_t cap = W->total_capacity;
-    int64_t blocks = ceil_div(cap, int64_t{kSelThreads} * 8);
+    int64_t blocks = ceil_div(cap, int64_t{kSelThreads} * 16);
     if (blocks > 2048) blocks = 2048;
     if (blocks < 1) blocks = 1;
     for (int pass = 0; pass < 3; ++pass) {
