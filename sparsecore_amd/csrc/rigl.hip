@@ -1420,6 +1420,9 @@ __global__ __launch_bounds__(kRowThreads) void rigl_select_kernel(
     const int t = threadIdx.x;
     const RowInfo ri = info[i];
     if (ri.flags & kRowKeep) return;
+    // more undecided columns than the lists hold: no row is rewritten (the
+    // caller reads the count afterwards and takes the exact path instead)
+    if (amb_off[gridDim.x] > amb_cap) return;
     const int32_t n_live = row_nnz[i];
     const int32_t start = row_start[i];
     for (int64_t w = t; w < Kw; w += kRowThreads) keep[w] = grow[w] = 0;

@@ -659,7 +659,7 @@ class PaddedCSR:
         (slk_rigl_norms, slk_dense_grad_approx, slk_rigl_count,
         slk_rigl_finish). The rows come out exactly as
         ``_drop_grow(k_drop, SLK_GROW_GRADIENT, dense_grad(dY, X))`` writes
-        them. Two device reads: the undecided count and the removed slots.
+        them. One device read: the undecided count with the removed slots.
         """
         self._require_device("rigl")
         if not 1 <= k_drop <= self._nnz:
@@ -683,7 +683,8 @@ class PaddedCSR:
         _lib.dense_grad_approx(dY, X, Gp, Gc)
         info = torch.empty(M * _lib.RIGL_INFO_BYTES, dtype=torch.uint8, device=dev)
         amb_off = torch.empty(2 * M + 1, dtype=torch.int64, device=dev)
-        total = torch.empty(1, dtype=torch.int64, device=dev)
+        counts = torch.empty(2, dtype=torch.int64, device=dev)  # undecided, removed
+        total, removed = counts[0:1], counts[1:2]
         # the undecided-column lists, sized for the most the certified path
         # takes (the count writes them where it holds rows in registers)
         cap = max(1, int(self._RIGL_EXACT_SHARE * max(1, M * K - self._nnz)))
@@ -691,16 +692,19 @@ class PaddedCSR:
         stage = torch.empty(_lib.drop_grow_workspace_bytes(view), dtype=torch.uint8, device=dev)
         _lib.rigl_count(view, thr, Gp, Gc, nrm_dY, nrm_X, dY.shape[1], info, amb_off, total,
                         amb, stage)
-        n_amb = int(total.item())
+        # queued right behind the count: its exact step covers the lists'
+        # capacity and reads the count on the device, and its row rewrite
+        # leaves every row alone when the count exceeds that capacity, so the
+        # undecided count and the removed slots are read together afterwards
+        _lib.rigl_finish(view, thr, Gp, Gc, nrm_dY, nrm_X, dY, X, info, amb_off, amb, stage,
+                         removed)
+        n_amb, lost = counts.tolist()
         if n_amb > cap:
             del Gp, Gc, amb, stage
             from .ops import dense_grad
             self._drop_grow(k_drop, _lib.SLK_GROW_GRADIENT, dense_grad(dY, X))
             return
-        removed = torch.empty(1, dtype=torch.int64, device=dev)
-        _lib.rigl_finish(view, thr, Gp, Gc, nrm_dY, nrm_X, dY, X, info, amb_off, amb, stage,
-                         removed)
-        self._after_topology_pass(int(removed.item()))
+        self._after_topology_pass(int(lost))
 
     def _after_topology_pass(self, lost: int) -> None:
         """Bookkeeping after a drop/grow pass: the version bump, and where rows

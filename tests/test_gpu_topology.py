@@ -607,6 +607,29 @@ def test_rigl_certified_matches_exact_drop_grow(dev, name, df):
         assert 0 < n_amb <= W._RIGL_EXACT_SHARE * (c.nrows * c.ncols - c.nnz), n_amb
 
 
+@pytest.mark.parametrize("name", ["cancel", "cancel-k16", "ties", "zipf-k16"])
+def test_rigl_list_overflow_rewrites_no_row_and_takes_the_exact_path(dev, name):
+    """The finish is queued before the undecided count is read. With lists too
+    small for the count (a capacity of one pair here), its row rewrite leaves
+    every row alone, and the exact-G drop/grow the host then runs gives the
+    exact path's rows."""
+    c, N, kind = _rigl_case(name)
+    print(f"[rigl overflow] {name} {c.nrows}x{c.ncols} N={N}", flush=True)
+    dY_np, X_np = _rigl_inputs(c.nrows, c.ncols, N, 40 + c.nrows, kind)
+    dY, X = torch.from_numpy(dY_np).to(dev), torch.from_numpy(X_np).to(dev)
+    k = max(1, int(0.3 * c.nnz))
+    W_exact, W_cert = from_oracle(c, dev), from_oracle(c, dev)
+    W_exact._drop_grow(k, _lib.SLK_GROW_GRADIENT, ops.dense_grad(dY, X))
+    W_cert._RIGL_EXACT_SHARE = 1e-30  # lists of one pair: every case here has more
+    took_exact = []
+    inner = W_cert._drop_grow
+    W_cert._drop_grow = lambda *a: (took_exact.append(1), inner(*a))[1]
+    W_cert._rigl_update(k, dY, X)
+    assert took_exact, "the count fit the one-pair lists: the case does not test the overflow"
+    csr_arrays_equal(to_oracle(W_cert), to_oracle(W_exact), f"{name} overflow vs exact")
+    assert W_cert.nnz == W_exact.nnz and W_cert.topology_version == 1
+
+
 def _bf16_bits(x: np.ndarray) -> np.ndarray:
     """float32 -> bf16 bits, round to nearest even (finite inputs)."""
     b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
