@@ -31,6 +31,10 @@
 // Integer atomics appear only in T1's LDS histogram (counts are
 // order-independent). Columns are processed in chunks of kColChunk so the LDS
 // footprint stays bounded for any ncols.
+//
+// For ncols <= 65535 and 2^20+ slots the same arrays come from a stable
+// radix sort by column instead (the radix path, further below), which needs
+// no searches.
 #include "common.hpp"
 
 namespace slk {
