@@ -2,6 +2,7 @@
 #include "common.hpp"
 
 #include <atomic>
+#include <mutex>
 
 namespace slk {
 
@@ -20,6 +21,44 @@ Tuning g_tuning;
 }
 
 int64_t tuning(int knob) { return g_tuning.v[knob].load(std::memory_order_relaxed); }
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_side_mu;
+SideQueue g_side[kMaxDevices];
+}  // namespace
+
+std::mutex& side_mutex() { return g_side_mu; }
+
+SideQueue* side_queue(hipStream_t st) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    SideQueue& q = g_side[dev];
+    if (q.s != nullptr) return &q;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    hipStream_t s = nullptr;
+    hipEvent_t f = nullptr, j = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        if (j != nullptr) (void)hipEventDestroy(j);
+        if (f != nullptr) (void)hipEventDestroy(f);
+        if (s != nullptr) (void)hipStreamDestroy(s);
+        return nullptr;
+    }
+    q.s = s;
+    q.fork = f;
+    q.join = j;
+    return &q;
+}
 
 int fail(int code, const std::string& msg) {
     g_last_error = msg;

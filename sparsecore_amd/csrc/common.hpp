@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 #include <utility>
 #include <string>
 
@@ -32,6 +33,22 @@ int64_t tuning(int knob);
 
 // Validates the parts of a CSR view every kernel relies on.
 int validate_csr(const slk_csr* W, const char* who);
+
+// A second queue per device, for launchers that run two independent parts
+// of one call concurrently (slk_spmm's split forward, slk_sddmm's dense rows):
+// one stream (default priority) and the two events that fork it from and join
+// it back to the caller's stream. Created on the first such call on the device
+// that is not made under graph capture (until then such calls keep to one
+// stream) and kept until the process ends. side_mutex() is held from the fork
+// to the join, so calls from several host threads cannot interleave their
+// event records; side_queue() is called with it held and returns nullptr if no
+// queue is available.
+struct SideQueue {
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+std::mutex& side_mutex();
+SideQueue* side_queue(hipStream_t st);
 
 // MI355X has 8 XCDs (each with its own L2); the dispatcher hands workgroup b
 // to XCD (b mod 8). This renumbers workgroups so that every XCD receives one

@@ -1133,50 +1133,6 @@ int launch_phased4(const slk_csr* W, const float* X, int64_t N, const float* bia
     return SLK_OK;
 }
 
-// A second queue per device for the split forward below: one stream (default
-// priority) and the two events that fork it from and join it back to the
-// caller's stream. Created on the first such call on the device that is not
-// made under graph capture (until then the call keeps to one stream), and
-// kept until the process ends; g_side_mu is held from the fork to the join,
-// so calls from several host threads cannot interleave their event records.
-struct SideQueue {
-    hipStream_t s = nullptr;
-    hipEvent_t fork = nullptr, join = nullptr;
-};
-constexpr int kMaxDevices = 64;
-std::mutex g_side_mu;
-SideQueue g_side[kMaxDevices];
-
-SideQueue* side_queue(hipStream_t st) {  // g_side_mu held; nullptr if unavailable
-    int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-        (void)hipGetLastError();
-        return nullptr;
-    }
-    SideQueue& q = g_side[dev];
-    if (q.s != nullptr) return &q;
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
-        (void)hipGetLastError();
-        return nullptr;
-    }
-    hipStream_t s = nullptr;
-    hipEvent_t f = nullptr, j = nullptr;
-    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&f, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&j, hipEventDisableTiming) != hipSuccess) {
-        (void)hipGetLastError();
-        if (j != nullptr) (void)hipEventDestroy(j);
-        if (f != nullptr) (void)hipEventDestroy(f);
-        if (s != nullptr) (void)hipStreamDestroy(s);
-        return nullptr;
-    }
-    q.s = s;
-    q.fork = f;
-    q.join = j;
-    return &q;
-}
-
 // Heavy rows (positions [0, T) of W->row_order) on the LDS kernel on the
 // caller's stream, the rest on the phased gather kernel on the side stream,
 // concurrently: the heavy rows' workgroups alone leave CUs idle in their last
@@ -1189,7 +1145,7 @@ SideQueue* side_queue(hipStream_t st) {  // g_side_mu held; nullptr if unavailab
 int spmm_split_two_queues(const slk_csr* W, int64_t T, const float* X, int64_t N,
                           const float* bias, float* Y, hipStream_t st, bool* done,
                           const slk_csr* dense = nullptr) {
-    std::lock_guard<std::mutex> lock(g_side_mu);
+    std::lock_guard<std::mutex> lock(side_mutex());
     SideQueue* q = side_queue(st);
     *done = q != nullptr;
     if (q == nullptr) return SLK_OK;
