@@ -653,8 +653,8 @@ class LayerWork:
         transpose on the device."""
         from sparsecore_amd import ops
 
-        self.W._rigl_update(max(1, int(0.3 * self.W.nnz)), self.dY, self.X)
-        ops._cached_transpose(self.W)
+        # the rewrite and the rebuild of the cached transpose, one host read
+        ops._rigl_update_cached(self.W, max(1, int(0.3 * self.W.nnz)), self.dY, self.X)
 
     def params(self):
         return []

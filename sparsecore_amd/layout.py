@@ -649,7 +649,8 @@ class PaddedCSR:
     # than recomputing the undecided ones one by one.
     _RIGL_EXACT_SHARE = 0.125
 
-    def _rigl_update(self, k_drop: int, dY: torch.Tensor, X: torch.Tensor) -> None:
+    def _rigl_update(self, k_drop: int, dY: torch.Tensor, X: torch.Tensor,
+                     then=None) -> None:
         """One RigL drop-and-grow pass, grows ranked by |G|, G = dY·Xᵀ with the
         reference's dense_grad arithmetic, without computing G everywhere.
 
@@ -660,6 +661,13 @@ class PaddedCSR:
         slk_rigl_finish). The rows come out exactly as
         ``_drop_grow(k_drop, SLK_GROW_GRADIENT, dense_grad(dY, X))`` writes
         them. One device read: the undecided count with the removed slots.
+
+        ``then`` (optional) is called once the rewrite is queued, before that
+        read, to queue more device work on the rewritten rows: it returns
+        (device int64 tensor, finish); the tensor is read together with the
+        RigL counts, and finish(host values) runs after the bookkeeping if the
+        certified path rewrote the rows, else (the exact path taken instead)
+        finish(None).
         """
         self._require_device("rigl")
         if not 1 <= k_drop <= self._nnz:
@@ -698,13 +706,19 @@ class PaddedCSR:
         # undecided count and the removed slots are read together afterwards
         _lib.rigl_finish(view, thr, Gp, Gc, nrm_dY, nrm_X, dY, X, info, amb_off, amb, stage,
                          removed)
-        n_amb, lost = counts.tolist()
+        more, finish = then() if then is not None else (None, None)
+        host = (torch.cat([counts, more]) if more is not None else counts).tolist()
+        n_amb, lost = host[0], host[1]
         if n_amb > cap:
             del Gp, Gc, amb, stage
             from .ops import dense_grad
             self._drop_grow(k_drop, _lib.SLK_GROW_GRADIENT, dense_grad(dY, X))
+            if finish is not None:
+                finish(None)
             return
         self._after_topology_pass(int(lost))
+        if finish is not None:
+            finish(host[2:])
 
     def _after_topology_pass(self, lost: int) -> None:
         """Bookkeeping after a drop/grow pass: the version bump, and where rows
@@ -969,6 +983,16 @@ def transpose_with_perm(p: PaddedCSR, *, padding_ratio: float = 0.2):
     the one device->host read of the exact capacity comes after it, and the
     arrays are trimmed to it (views, no copy).
     """
+    staged = _transpose_queue(p, padding_ratio, p.nnz)
+    return _transpose_take(p, staged, staged["counts"].tolist(), p.nnz)
+
+
+def _transpose_queue(p: PaddedCSR, padding_ratio: float, nnz_bound: int) -> dict:
+    """Queues transpose_with_perm's device work for p: the count, the fill
+    (into arrays sized by a capacity bound from nnz_bound, at least p's live
+    slots, when the bound fits int32) and the row hints. `counts` (int64
+    capacity, heavy rows, dense rows) is for the caller to read, alone or
+    with other device values, and to hand to _transpose_take."""
     if padding_ratio < 0:
         raise ValueError(f"padding_ratio must be >= 0, got {padding_ratio}")
     p._require_device("transpose")
@@ -981,28 +1005,40 @@ def transpose_with_perm(p: PaddedCSR, *, padding_ratio: float = 0.2):
     cap_t = torch.empty(K, dtype=_I32, device=dev)
     counts = torch.empty(3, dtype=torch.int64, device=dev)  # capacity, heavy, dense rows
     _lib.transpose_count(view, padding_ratio, ws, rs_t, nnz_t, cap_t, counts[0:1])
-    bound = _capacity_bound(p.nnz, K, padding_ratio)
-    early = bound <= np.iinfo(np.int32).max
-    if early:  # fill first, read the exact capacity after it
-        val_t = torch.empty(bound, dtype=_F32, device=dev)
-        col_t = torch.empty(bound, dtype=_I32, device=dev)
-        perm = torch.empty(bound, dtype=torch.int64, device=dev)
-        _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, bound, val_t, col_t, perm)
-    _count_rows(nnz_t, p.nnz, M, counts[1:3])
-    capT, heavy, dense = counts.tolist()
+    bound = _capacity_bound(nnz_bound, K, padding_ratio)
+    filled = None
+    if bound <= np.iinfo(np.int32).max:  # fill first, read the exact capacity after it
+        filled = (torch.empty(bound, dtype=_F32, device=dev),
+                  torch.empty(bound, dtype=_I32, device=dev),
+                  torch.empty(bound, dtype=torch.int64, device=dev))
+        _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, bound, *filled)
+    _count_rows(nnz_t, nnz_bound, M, counts[1:3])
+    return {"view": view, "ws": ws, "rs_t": rs_t, "nnz_t": nnz_t, "cap_t": cap_t,
+            "counts": counts, "filled": filled, "nnz_bound": nnz_bound}
+
+
+def _transpose_take(p: PaddedCSR, staged: dict, host_counts, nnz: int):
+    """(WT, perm) from _transpose_queue's work and its counts read on the host;
+    nnz = p's live slots. Hints counted against another bound than nnz are
+    dropped (WT recounts them from its rows when it needs them)."""
+    capT, heavy, dense = (int(x) for x in host_counts)
     if capT > np.iinfo(np.int32).max:
         raise ValueError(f"transpose: capacity {capT} exceeds the int32 slot range")
-    if early:
-        val_t, col_t, perm = val_t[:capT], col_t[:capT], perm[:capT]
+    dev = p.device
+    if staged["filled"] is not None:
+        val_t, col_t, perm = (a[:capT] for a in staged["filled"])
     else:
         val_t = torch.empty(capT, dtype=_F32, device=dev)
         col_t = torch.empty(capT, dtype=_I32, device=dev)
         perm = torch.empty(capT, dtype=torch.int64, device=dev)
-        _lib.transpose_fill(view, ws, rs_t, nnz_t, cap_t, capT, val_t, col_t, perm)
-    WT = PaddedCSR._from_parts(K, M, val_t, col_t, rs_t, nnz_t, cap_t, p.nnz)
-    WT._heavy_hint = heavy
-    WT._dense_hint = dense
-    WT._cols_skewed = view.n_heavy_rows > 0  # WT's columns are p's rows
+        _lib.transpose_fill(staged["view"], staged["ws"], staged["rs_t"], staged["nnz_t"],
+                            staged["cap_t"], capT, val_t, col_t, perm)
+    WT = PaddedCSR._from_parts(p.ncols, p.nrows, val_t, col_t, staged["rs_t"],
+                               staged["nnz_t"], staged["cap_t"], nnz)
+    exact = staged["nnz_bound"] == nnz
+    WT._heavy_hint = heavy if exact else None
+    WT._dense_hint = dense if exact else None
+    WT._cols_skewed = staged["view"].n_heavy_rows > 0  # WT's columns are p's rows
     return WT, perm
 
 

@@ -23,7 +23,7 @@ import weakref
 
 import torch
 
-from . import _lib
+from . import _lib, layout
 from .layout import PaddedCSR, transpose_with_perm, transposes_with_perm
 
 __all__ = ["spmm", "dense_grad"]
@@ -59,6 +59,33 @@ def _cached_transpose(W: PaddedCSR) -> PaddedCSR:
         weakref.finalize(W, _drop_entry, key)
     _transpose_cache[key] = (cur_version, cur_shape, WT, perm)
     return WT
+
+
+def _rigl_update_cached(W: PaddedCSR, k_drop: int, dY: torch.Tensor, X: torch.Tensor) -> None:
+    """``W._rigl_update(k_drop, dY, X)``, then W's cached transpose rebuilt for
+    the new topology, as ``_cached_transpose`` would on its next call, with one
+    host read for both: the rebuild is queued right behind the row rewrite,
+    its slot arrays sized from the live slots before the update (rows only
+    shrink), and its capacity read with the RigL counts. Without a cached
+    transpose of W this is ``W._rigl_update``."""
+    key = id(W)
+    if key not in _transpose_cache:
+        W._rigl_update(k_drop, dY, X)
+        return
+    staged = {}
+
+    def then():
+        staged["t"] = layout._transpose_queue(W, 0.2, W.nnz)
+        return staged["t"]["counts"], finish
+
+    def finish(host):
+        if host is None:  # the exact path rewrote W after the queued rebuild
+            _cached_transpose(W)
+            return
+        WT, perm = layout._transpose_take(W, staged["t"], host, W.nnz)
+        _transpose_cache[key] = (W.topology_version, (int(W.nrows), int(W.ncols)), WT, perm)
+
+    W._rigl_update(k_drop, dY, X, then=then)
 
 
 def _cached_transpose_structure(W: PaddedCSR):

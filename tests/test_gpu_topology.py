@@ -630,6 +630,39 @@ def test_rigl_list_overflow_rewrites_no_row_and_takes_the_exact_path(dev, name):
     assert W_cert.nnz == W_exact.nnz and W_cert.topology_version == 1
 
 
+@pytest.mark.parametrize("name,share", [("zipf-k16", None), ("nonfinite-rows-k16", None),
+                                        ("nonfinite-rows", None), ("cancel-k16", 1e-30)])
+def test_rigl_update_with_cached_rebuild_matches_separate_calls(dev, name, share):
+    """ops._rigl_update_cached (the rebuild queued behind the rewrite, one host
+    read) leaves W and its cached transpose exactly as _rigl_update followed
+    by _cached_transpose: rows that shrink (NaN rows), and the exact path taken
+    when the undecided lists overflow."""
+    c, N, kind = _rigl_case(name)
+    print(f"[rigl+rebuild] {name} share={share}", flush=True)
+    dY_np, X_np = _rigl_inputs(c.nrows, c.ncols, N, 40 + c.nrows, kind)
+    dY, X = torch.from_numpy(dY_np).to(dev), torch.from_numpy(X_np).to(dev)
+    k = max(1, int(0.3 * c.nnz))
+    A, B = from_oracle(c, dev), from_oracle(c, dev)
+    for W in (A, B):
+        if share is not None:
+            W._RIGL_EXACT_SHARE = share
+        ops._cached_transpose(W)
+    A._rigl_update(k, dY, X)
+    WT_a = ops._cached_transpose(A)
+    ops._rigl_update_cached(B, k, dY, X)
+    entry = ops._transpose_cache[id(B)]
+    assert entry[0] == B.topology_version == A.topology_version
+    WT_b = ops._cached_transpose(B)  # a hit: the entry the merged call stored
+    assert WT_b is entry[2]
+    csr_arrays_equal(to_oracle(B), to_oracle(A), f"{name} W")
+    assert B.nnz == A.nnz and WT_b.nnz == WT_a.nnz == A.nnz
+    csr_arrays_equal(to_oracle(WT_b), to_oracle(WT_a), f"{name} WT")
+    assert torch.equal(entry[3], ops._transpose_cache[id(A)][3])
+    assert WT_b._view().n_heavy_rows == WT_a._view().n_heavy_rows
+    if name.startswith("nonfinite-rows"):
+        assert A.nnz < c.nnz  # rows shrank
+
+
 def _bf16_bits(x: np.ndarray) -> np.ndarray:
     """float32 -> bf16 bits, round to nearest even (finite inputs)."""
     b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
