@@ -237,6 +237,107 @@ __global__ __launch_bounds__(kScanThreads) void tr_scan_kernel(
     }
 }
 
+// T3 / R3 for ncols <= kScanLdsMax: the same outputs as tr_scan_kernel from
+// one round of coalesced loads into LDS; thread t then scans its 16
+// consecutive columns there, the per-thread sums go through one workgroup
+// scan (wave shuffles, then the 16 wave totals), and the results leave LDS
+// by coalesced stores.
+constexpr int kScanLdsMax = 16384;
+
+__global__ __launch_bounds__(kScanThreads) void tr_scan_lds_kernel(
+    int64_t K, const int32_t* __restrict__ cap_t, int32_t* __restrict__ start_t,
+    int64_t* __restrict__ cap_total, const int32_t* __restrict__ nnz_t,
+    int32_t* __restrict__ off, int64_t* __restrict__ nlive) {
+    constexpr int kWaves = kScanThreads / kWave;
+    constexpr int kPer = kScanLdsMax / kScanThreads;
+    __shared__ int32_t sc[kScanLdsMax], sn[kScanLdsMax];
+    __shared__ int64_t wc[kWaves], wn[kWaves];
+    const int t = threadIdx.x, lane = t & (kWave - 1), w = t >> 6;
+    const bool two = nnz_t != nullptr;
+#pragma unroll
+    for (int h = 0; h < kPer; h += kPer / 2) {  // two halves of loads, each issued at once
+        int32_t a[kPer / 2], b[kPer / 2];
+#pragma unroll
+        for (int q = 0; q < kPer / 2; ++q) {
+            const int64_t c = (h + q) * kScanThreads + t;
+            a[q] = c < K ? cap_t[c] : 0;
+            b[q] = (two && c < K) ? nnz_t[c] : 0;
+        }
+#pragma unroll
+        for (int q = 0; q < kPer / 2; ++q) {
+            sc[(h + q) * kScanThreads + t] = a[q];
+            sn[(h + q) * kScanThreads + t] = b[q];
+        }
+    }
+    __syncthreads();
+    int64_t s1 = 0, s2 = 0;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+        s1 += sc[t * kPer + q];
+        s2 += sn[t * kPer + q];
+    }
+    int64_t x1 = s1, x2 = s2;  // inclusive scans over the wave
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int64_t u1 = __shfl_up(x1, o), u2 = __shfl_up(x2, o);
+        if (lane >= o) {
+            x1 += u1;
+            x2 += u2;
+        }
+    }
+    if (lane == kWave - 1) {
+        wc[w] = x1;
+        wn[w] = x2;
+    }
+    __syncthreads();
+    if (t == 0) {  // the wave totals become exclusive prefixes
+        int64_t a1 = 0, a2 = 0;
+        for (int q = 0; q < kWaves; ++q) {
+            const int64_t y1 = wc[q], y2 = wn[q];
+            wc[q] = a1;
+            wn[q] = a2;
+            a1 += y1;
+            a2 += y2;
+        }
+        *cap_total = a1;
+        if (two) *nlive = a2;
+    }
+    __syncthreads();
+    int64_t r1 = wc[w] + x1 - s1, r2 = wn[w] + x2 - s2;
+    // each thread's columns become their start and padding offset, in place
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+        const int i = t * kPer + q;
+        const int32_t c1 = sc[i], c2 = sn[i];
+        sc[i] = static_cast<int32_t>(r1);
+        sn[i] = static_cast<int32_t>(r1 - r2);
+        r1 += c1;
+        r2 += c2;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+        const int64_t c = q * kScanThreads + t;
+        if (c < K) {
+            start_t[c] = sc[c];
+            if (two) off[c] = sn[c];
+        }
+    }
+}
+
+// The capacity scan: the LDS kernel where the columns fit, else the
+// two-pass one.
+void launch_scan(int64_t K, const int32_t* cap_t, int32_t* start_t, int64_t* cap_total,
+                 const int32_t* nnz_t, int32_t* off, int64_t* nlive, hipStream_t st) {
+    if (K <= kScanLdsMax) {
+        hipLaunchKernelGGL(tr_scan_lds_kernel, dim3(1), dim3(kScanThreads), 0, st, K, cap_t,
+                           start_t, cap_total, nnz_t, off, nlive);
+    } else {
+        hipLaunchKernelGGL(tr_scan_kernel, dim3(1), dim3(kScanThreads), 0, st, K, cap_t, start_t,
+                           cap_total, nnz_t, off, nlive);
+    }
+}
+
 // T4: one wave per WT row; lanes write consecutive padding slots.
 __global__ __launch_bounds__(256) void tr_pad_kernel(int64_t K, const int32_t* __restrict__ start_t,
                                                      const int32_t* __restrict__ nnz_t,
@@ -956,10 +1057,9 @@ int rx_count(const slk_csr* W, double padding_ratio, void* workspace, int64_t wo
                        dim3(kColScanWaves * kWave), 0, st, K, x.nsb, 1.0 + padding_ratio, colpart,
                        WT_row_nnz, WT_row_capacity, false);
     if (int rc = check_launch("transpose_count/colscan")) return rc;
-    hipLaunchKernelGGL(tr_scan_kernel, dim3(1), dim3(kScanThreads), 0, st, K, WT_row_capacity,
-                       WT_row_start, capT_dev, WT_row_nnz,
-                       reinterpret_cast<int32_t*>(ws + x.o_off),
-                       reinterpret_cast<int64_t*>(ws + x.o_nlive));
+    launch_scan(K, WT_row_capacity, WT_row_start, capT_dev, WT_row_nnz,
+                reinterpret_cast<int32_t*>(ws + x.o_off),
+                reinterpret_cast<int64_t*>(ws + x.o_nlive), st);
     return check_launch("transpose_count/rx_scan");
 }
 
@@ -1098,8 +1198,7 @@ extern "C" int slk_transpose_count(const slk_csr* W, double padding_ratio, void*
                        dim3(kColScanWaves * kWave), 0, st, K, p.nblk, 1.0 + padding_ratio, bh,
                        WT_row_nnz, WT_row_capacity, true);
     if (int rc = check_launch("transpose_count/colscan")) return rc;
-    hipLaunchKernelGGL(tr_scan_kernel, dim3(1), dim3(kScanThreads), 0, st, K, WT_row_capacity,
-                       WT_row_start, capT_dev, nullptr, nullptr, nullptr);
+    launch_scan(K, WT_row_capacity, WT_row_start, capT_dev, nullptr, nullptr, nullptr, st);
     return check_launch("transpose_count/scan");
 }
 
